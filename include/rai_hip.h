@@ -1,0 +1,250 @@
+/*
+ * rai_hip.h -- C ABI of the MI355X (gfx950) prompt-lookup / W4A8 library.
+ *
+ * This library re-implements, for one MI355X GPU, the hot path of
+ * Classevelabs/rai's `rai_infer` crate: prompt-lookup speculative decoding,
+ * the (k+1)-token verify forward pass, greedy acceptance with KV rollback,
+ * and the W4A8 GEMV/GEMM beneath them.  Each entry point below names the
+ * reference interface it replaces (rai-infer/src/<file>:<line>).  A Rust
+ * `extern "C"` crate can bind these symbols one-to-one.
+ *
+ * Conventions
+ *   - Every function returns an rai_status (0 = RAI_OK).  On failure the
+ *     thread's last error text is available from rai_last_error().  Where the
+ *     reference panics on a shape/buffer violation (gemm.rs:1169-1213,
+ *     layers.rs:1109-1168, kv_cache.rs:143-204), this ABI returns
+ *     RAI_E_SHAPE / RAI_E_WATERMARK instead; where it returns anyhow::Err it
+ *     returns the matching status.
+ *   - Handles are opaque and owned by the library; free them with the
+ *     matching *_free.  A handle is not re-entrant: one host thread at a time.
+ *   - Token ids are uint32.  Sizes are size_t.  No torch types appear here.
+ *   - Host-pointer entry points copy in/out and synchronise before returning.
+ *     Device-pointer entry points (suffix _dev) take a hipStream_t passed as
+ *     void* (NULL = the null stream) and are asynchronous.
+ *   - Arithmetic is bit-identical to the reference's AVX2 path on the same
+ *     inputs: integer accumulators, f32 outputs, logits and token streams.
+ */
+#ifndef RAI_HIP_H
+#define RAI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum rai_status {
+  RAI_OK = 0,
+  RAI_E_ARG = -1,         /* invalid argument / configuration */
+  RAI_E_SHAPE = -2,       /* buffer or dimension violation (reference: assert!) */
+  RAI_E_FORMAT = -3,      /* malformed or hostile .raimodel file */
+  RAI_E_OOM = -4,         /* host or device allocation failed */
+  RAI_E_HIP = -5,         /* HIP runtime error */
+  RAI_E_WATERMARK = -6,   /* KV store gap or read above the filled watermark */
+  RAI_E_UNSUPPORTED = -7, /* a capability this build does not implement */
+  RAI_E_IO = -8,          /* file could not be read */
+  RAI_E_RANGE = -9        /* token id / position outside the model's range */
+} rai_status;
+
+typedef struct rai_model rai_model;
+typedef struct rai_kv rai_kv;
+typedef struct rai_lookup rai_lookup;
+
+/* ModelConfig (format.rs:162-265), the fields this build implements. */
+typedef struct rai_model_config {
+  uint32_t hidden_size, num_layers, num_heads, num_kv_heads, head_dim;
+  uint32_t intermediate_size, vocab_size, max_context;
+  float rope_theta, norm_eps;
+  uint32_t group_size, embed_group_size, version;
+  uint32_t tied;              /* 1 = lm_head tied to the 8-bit embedding */
+  uint32_t num_experts;       /* 0 = dense MLP */
+  uint32_t experts_per_token;
+  uint32_t norm_topk_prob;
+  float embed_scale, attn_scale; /* attn_scale is the effective multiplier */
+} rai_model_config;
+
+/* LookupConfig (lookup.rs:64-89).  temperature <= 1e-6 selects greedy
+ * acceptance (argmax == draft), the T->0 limit of lookup.rs:359-403; the
+ * sampled mode (T > 0) is not implemented in this build (RAI_E_UNSUPPORTED). */
+typedef struct rai_lookup_config {
+  size_t max_draft;   /* K */
+  size_t max_ngram;
+  size_t min_ngram;   /* >= 1 */
+  float temperature;  /* <= 1e-6: greedy */
+} rai_lookup_config;
+
+/* LookupMatch (lookup.rs:91-109). */
+typedef struct rai_lookup_match {
+  size_t ngram, start, len;
+} rai_lookup_match;
+
+/* LookupMetrics (lookup.rs:112-119); matched_ngram == 0 means no match. */
+typedef struct rai_lookup_metrics {
+  size_t accepted, drafted, produced, matched_ngram;
+  float accept_rate;
+} rai_lookup_metrics;
+
+/* Aggregate statistics of rai_lookup_generate (the `rai run` stats,
+ * cli/run.rs:623-633). */
+typedef struct rai_generate_stats {
+  size_t prompt_tokens, generated, steps, steps_with_draft, drafted, accepted;
+  double prefill_seconds, decode_seconds;
+} rai_generate_stats;
+
+/* ---------------------------------------------------------------- errors -- */
+const char *rai_last_error(void);
+/* HIP device the library runs on (reads HIP_VISIBLE_DEVICES semantics). */
+int rai_device_info(char *name, size_t name_len, int *compute_units);
+
+/* ----------------------------------------------------------------- model -- */
+/* RaiModel::load (model.rs:97-181) + RaiModelFile::open (format.rs:557-637):
+ * reads and validates the whole file with the reference's rules
+ * (format.rs:1098-1521), then uploads it to HBM.  max_groups replaces the
+ * reference's MAX_GROUPS = 128 (gemm.rs:1167); pass 0 for the reference value
+ * 128, or a larger bound for group-32 models with K > 4096. */
+int rai_model_open(const char *path, int max_groups, rai_model **out);
+/* Same, from a caller-owned in-memory .raimodel image (copied). */
+int rai_model_from_buffer(const void *data, size_t len, int max_groups, rai_model **out);
+void rai_model_free(rai_model *model);
+int rai_model_get_config(const rai_model *model, rai_model_config *out);
+/* Bytes of quantized weights one decode step streams (linears + lm_head). */
+int rai_model_weight_bytes(const rai_model *model, uint64_t *out);
+
+/* --------------------------------------------------------------- KV cache -- */
+/* RaiModel::create_kv_cache (model.rs:350) / KVCache::new (kv_cache.rs:232).
+ * f32 [layer][kv_head][max_ctx][head_dim] in HBM, allocated up front. */
+int rai_kv_create(rai_model *model, size_t max_ctx, rai_kv **out);
+void rai_kv_free(rai_kv *kv);
+/* KVCache::truncate (kv_cache.rs:300-304): filled = min(filled, len). */
+int rai_kv_truncate(rai_kv *kv, size_t len);
+/* KVCache::filled (kv_cache.rs:292). */
+int rai_kv_filled(const rai_kv *kv, size_t layer, size_t *out);
+/* KVCache::clear (kv_cache.rs:316). */
+int rai_kv_clear(rai_kv *kv);
+/* Copy one cached K or V row [head_dim] (kv_cache.rs:179-204 get_k/get_v);
+ * which = 0 for K, 1 for V.  Reads at or above the watermark fail. */
+int rai_kv_read(const rai_kv *kv, size_t layer, size_t head, size_t pos, int which, float *out);
+
+/* ---------------------------------------------------------- forward pass -- */
+/* RaiModel::embed_token (model.rs:371-403). */
+int rai_embed_token(rai_model *model, size_t token, float *out);
+/* RaiModel::forward_from_hidden (model.rs:407-499); store_kv must be 1. */
+int rai_forward_from_hidden(rai_model *model, rai_kv *kv, float *hidden, size_t pos, int store_kv);
+/* RaiModel::forward_batch (model.rs:692-963): hiddens [batch][hidden] in/out,
+ * positions strictly consecutive. */
+int rai_forward_batch(rai_model *model, rai_kv *kv, float *hiddens, const size_t *positions,
+                      size_t batch);
+/* RaiModel::hidden_to_logits_into (model.rs:504-548). */
+int rai_hidden_to_logits(rai_model *model, const float *hidden, float *logits);
+/* RaiModel::hidden_to_logits_batch (model.rs:966-1033). */
+int rai_hidden_to_logits_batch(rai_model *model, const float *hiddens, float *logits,
+                               size_t batch);
+
+/* ------------------------------------------------------- kernels (device) -- */
+/* w4a8_matmul (gemm.rs:1774-1919); m == 1 is w4a8_matvec (gemm.rs:1336-1384).
+ * out[t*rows + r], x[t*cols + c]; weights in the .raimodel linear layout:
+ * nibbles [rows][cols/2] (low nibble = even column) and params
+ * [rows][ceil(cols/gs)] x (f16 scale, f16 zero).  All pointers are device
+ * pointers. */
+int rai_w4a8_matmul_dev(float *out, const uint8_t *nibbles, const uint8_t *params,
+                        const float *x, size_t rows, size_t cols, size_t m, size_t group_size,
+                        void *stream);
+/* Debug companion (no reference counterpart): the integer accumulators of
+ * matvec_chunk_i8 (gemm.rs:458-525) per (token, row, group) as 12 int32:
+ * [0..8) the 64-column-chunk lanes, [8..12) the trailing 32-column block. */
+int rai_w4a8_lane_sums_dev(int32_t *out, const uint8_t *nibbles, const float *x, size_t rows,
+                           size_t cols, size_t m, size_t group_size, void *stream);
+/* Host-pointer convenience wrapper of rai_w4a8_matmul_dev (copies in/out). */
+int rai_w4a8_matmul(float *out, const uint8_t *nibbles, const uint8_t *params, const float *x,
+                    size_t rows, size_t cols, size_t m, size_t group_size);
+/* tied_lm_head (gemm.rs:1981-2076), device pointers. */
+int rai_tied_lm_head_dev(float *logits, const float *hidden, const uint8_t *codes,
+                         const uint8_t *params, size_t vocab, size_t hidden_size,
+                         size_t group_size, void *stream);
+/* embed_lookup (gemm.rs:1926-1970), device pointers, one token. */
+int rai_embed_lookup_dev(float *out, size_t token, const uint8_t *codes, const uint8_t *params,
+                         size_t vocab, size_t hidden_size, size_t group_size, void *stream);
+
+/* ------------------------------------------------ layer kernels (device) -- */
+/* rms_norm (layers.rs:154-183, 325-376) over m rows of n. */
+int rai_rms_norm_dev(float *out, const float *x, const float *weight, size_t m, size_t n,
+                     float eps, void *stream);
+/* silu_mul_inplace (layers.rs:824-883) over m rows of n: gate = silu(gate)*up. */
+int rai_silu_mul_dev(float *gate, const float *up, size_t m, size_t n, void *stream);
+/* RoPETable::apply (layers.rs:643-726) of one position's cos/sin rows
+ * ([head_dim/2] each) to heads [num_heads][head_dim], in place. */
+int rai_rope_apply_dev(float *heads, size_t num_heads, size_t head_dim, const float *cos_row,
+                       const float *sin_row, void *stream);
+/* attention_head (layers.rs:1266-1452) for one query head over cached rows
+ * k[t][head_dim], v[t][head_dim], t in 0..=pos (softcap disabled). */
+int rai_attention_head_dev(float *out, const float *q, const float *k, const float *v, size_t pos,
+                           size_t head_dim, float scale, void *stream);
+
+/* ----------------------------------------------------- prompt-lookup path -- */
+/* find_ngram_draft (lookup.rs:131-171), evaluated by the GPU search kernel.
+ * *found = 0 when there is no match. */
+int rai_find_ngram_draft(const uint32_t *tokens, size_t len, size_t min_ngram, size_t max_ngram,
+                         size_t max_draft, rai_lookup_match *out, int *found);
+/* LookupDecoder::new (lookup.rs:192-212). */
+int rai_lookup_create(rai_model *model, size_t max_ctx, rai_lookup **out);
+void rai_lookup_free(rai_lookup *dec);
+/* The decoder's `pub kv_cache` (lookup.rs:176): borrowed, do not free. */
+int rai_lookup_kv(rai_lookup *dec, rai_kv **out);
+/* LookupDecoder::prefill (lookup.rs:219-247): forward over prompt[0..n-1]. */
+int rai_lookup_prefill(rai_lookup *dec, const uint32_t *prompt, size_t n, size_t *pos_out);
+/* LookupDecoder::step (lookup.rs:260-425).  context[len-1] lives at pos.
+ * Writes metrics->produced tokens into out_tokens (capacity >= max_draft+1). */
+int rai_lookup_step(rai_lookup *dec, size_t pos, const uint32_t *context, size_t len,
+                    const rai_lookup_config *cfg, uint32_t *out_tokens, size_t out_cap,
+                    rai_lookup_metrics *metrics);
+/* The `rai run --lookup-k` loop (cli/run.rs:517-633) without the tokenizer:
+ * prefill, then steps until max_tokens are generated.  out_tokens receives
+ * the generated ids (capacity >= max_tokens + max_draft). */
+int rai_lookup_generate(rai_lookup *dec, const uint32_t *prompt, size_t n, size_t max_tokens,
+                        const rai_lookup_config *cfg, uint32_t *out_tokens, size_t out_cap,
+                        size_t *n_out, rai_generate_stats *stats);
+/* Plain greedy decode (sampler.rs:61-64 argmax after decode_one), used for the
+ * token-identity check: prefill, then `steps` single-token steps. */
+int rai_greedy_generate(rai_lookup *dec, const uint32_t *prompt, size_t n, size_t steps,
+                        uint32_t *out_tokens);
+
+/* ------------------------------------------------------------------ misc -- */
+/* Synthetic .raimodel writer (the build's stand-in for the exporter).
+ * mode 0: symmetric int4 RTN (code = q+8, zero = -8*scale) of N(0, std)
+ * weights from `seed`; mode 1: the reference exporter's asymmetric min/max RTN
+ * (raimodel.py:257-303) over the same weights.  Norm vectors are 1.0.
+ * Writes to `path`, or, when path is NULL, returns a malloc'ed image in
+ * *image / *image_len (free with rai_free_image). */
+typedef struct rai_synth_config {
+  uint32_t hidden_size, num_layers, num_heads, num_kv_heads, head_dim;
+  uint32_t intermediate_size, vocab_size, max_context;
+  float rope_theta, norm_eps;
+  uint32_t group_size, embed_group_size, tied;
+  uint32_t num_experts, experts_per_token, norm_topk_prob;
+  float weight_std;
+  uint32_t mode;
+} rai_synth_config;
+int rai_synth_model(const rai_synth_config *cfg, uint64_t seed, const char *path, uint8_t **image,
+                    size_t *image_len);
+void rai_free_image(uint8_t *image);
+
+/* Device-memory plumbing for harnesses that bind only this ABI. */
+int rai_dev_malloc(size_t bytes, void **out);
+int rai_dev_free(void *ptr);
+int rai_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int rai_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int rai_device_synchronize(void);
+/* Stream/event helpers for timing from a harness (HIP events). */
+int rai_stream_create(void **out);
+int rai_stream_destroy(void *stream);
+int rai_event_create(void **out);
+int rai_event_destroy(void *ev);
+int rai_event_record(void *ev, void *stream);
+int rai_event_elapsed_ms(void *start, void *stop, float *ms);
+int rai_stream_synchronize(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RAI_HIP_H */

@@ -1,0 +1,123 @@
+/*
+ * CPU oracle for the prompt-lookup / W4A8 hot path.  TEST INFRASTRUCTURE ONLY.
+ *
+ * This is a C++ restatement of Classevelabs/rai's AVX2 CPU path (rai-infer),
+ * written with the same AVX2/FMA/F16C intrinsic sequences, lane structure and
+ * accumulation order, so that its f32 results are bit-identical to the
+ * reference's AVX2 build.  It exists to check the HIP implementation and to
+ * time the CPU baseline; nothing in the shipped library links, loads or calls
+ * it.  Only tests, the smoke check and the bench's CPU-baseline leg use it.
+ *
+ * Parity notes (each pinned by tests under tests/):
+ *   - MAX_GROUPS (gemm.rs:1167, 128) is a validation-time parameter here
+ *     (ora_model_open's max_groups); the arithmetic is unchanged.
+ *   - Greedy prompt-lookup acceptance (argmax == draft) is the T->0 limit of
+ *     lookup.rs:359-403; the reference itself rejects T <= 1e-6.
+ *   - Only the Llama-shaped capability subset is implemented (v1 headers, and
+ *     v2 headers whose only capabilities are embed_scale, attn_scale and MoE).
+ *
+ * All functions return 0 on success and a negative code on failure.
+ */
+#ifndef RAI_ORACLE_H
+#define RAI_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ora_model ora_model;
+typedef struct ora_kv ora_kv;
+typedef struct ora_lookup ora_lookup;
+
+typedef struct ora_config {
+  uint32_t hidden_size, num_layers, num_heads, num_kv_heads, head_dim;
+  uint32_t intermediate_size, vocab_size, max_context;
+  float rope_theta, norm_eps;
+  uint32_t group_size, embed_group_size, version, tied;
+  uint32_t num_experts, experts_per_token, norm_topk_prob;
+  float embed_scale, attn_scale;
+} ora_config;
+
+typedef struct ora_metrics {
+  int32_t accepted, drafted, produced, matched_ngram; /* matched_ngram 0 = none */
+} ora_metrics;
+
+void ora_set_threads(int n);
+int ora_get_threads(void);
+const char *ora_last_error(void);
+
+/* ---- kernel-level (gemm.rs) ---- */
+int ora_quantize_split(const float *x, int cols, int gs, int8_t *q_even,
+                       int8_t *q_odd, float *scales);
+int ora_input_sums(const float *x, int cols, int gs, float *sums);
+int ora_w4a8_matvec(float *out, const uint8_t *nib, const uint8_t *params,
+                    const float *x, int rows, int cols, int gs);
+int ora_w4a8_matmul(float *out, const uint8_t *nib, const uint8_t *params,
+                    const float *x, int rows, int cols, int m, int gs);
+/* Per (token, row, group) integer lane sums: 12 int32 per group,
+ * [0..8) = 64-column-chunk lanes (zero when the group has no 64 chunk),
+ * [8..12) = trailing 32-column block lanes (zero when absent). */
+int ora_w4a8_lane_sums(int32_t *out, const uint8_t *nib, const float *x,
+                       int rows, int cols, int m, int gs);
+int ora_tied_lm_head(float *logits, const float *hidden, const uint8_t *codes,
+                     const uint8_t *params, int vocab, int hidden_size, int gs);
+int ora_embed_lookup(float *out, int token, const uint8_t *codes,
+                     const uint8_t *params, int vocab, int hidden_size, int gs);
+
+/* ---- layer-level (layers.rs) ---- */
+int ora_rms_norm(float *out, const float *x, const float *w, int n, float eps);
+int ora_rms_norm_residual(float *normed, float *residual, const float *x,
+                          const float *w, int n, float eps);
+int ora_silu_mul(float *gate, const float *up, int n);
+int ora_rope_tables(float *cos_t, float *sin_t, int head_dim, int max_ctx,
+                    float theta);
+int ora_rope_apply(float *heads, int num_heads, int head_dim, const float *cos_row,
+                   const float *sin_row);
+/* One query head over cached K/V rows k[t*hd], v[t*hd] for t in 0..=pos. */
+int ora_attention_head(const float *q, const float *k, const float *v, int pos,
+                       int head_dim, float scale, float *out);
+float ora_expf(float x);
+float ora_schraudolph(float x);
+
+/* ---- sampler / lookup (sampler.rs, lookup.rs) ---- */
+int64_t ora_argmax(const float *values, int64_t n);
+/* returns 1 and fills {ngram, start, len} on a match, 0 when none */
+int ora_find_ngram_draft(const int32_t *tokens, int64_t len, int64_t min_ngram,
+                         int64_t max_ngram, int64_t max_draft, int64_t *match3);
+
+/* ---- model (format.rs, model.rs, kv_cache.rs) ---- */
+int ora_model_open(const uint8_t *buf, size_t len, int max_groups, ora_model **out);
+void ora_model_free(ora_model *m);
+int ora_model_config(const ora_model *m, ora_config *out);
+int ora_kv_create(const ora_model *m, int max_ctx, ora_kv **out);
+void ora_kv_free(ora_kv *kv);
+int ora_kv_truncate(ora_kv *kv, int len);
+int ora_kv_filled(const ora_kv *kv, int layer);
+int ora_embed_token(const ora_model *m, int token, float *out);
+int ora_forward_from_hidden(const ora_model *m, ora_kv *kv, float *hidden, int pos,
+                            int store_kv);
+int ora_forward_batch(const ora_model *m, ora_kv *kv, float *hiddens,
+                      const int32_t *positions, int batch);
+int ora_hidden_to_logits(const ora_model *m, const float *hidden, float *logits);
+int ora_hidden_to_logits_batch(const ora_model *m, const float *hiddens,
+                               float *logits, int batch);
+
+/* ---- decoders ---- */
+int ora_lookup_create(const ora_model *m, int max_ctx, ora_lookup **out);
+void ora_lookup_free(ora_lookup *d);
+int ora_lookup_prefill(ora_lookup *d, const int32_t *prompt, int n, int *pos_out);
+int ora_lookup_step_greedy(ora_lookup *d, int pos, const int32_t *context, int len,
+                           int max_draft, int min_ngram, int max_ngram,
+                           int32_t *out_tokens, ora_metrics *metrics);
+int ora_lookup_kv_filled(const ora_lookup *d);
+/* Plain greedy decode: prefill prompt[0..n-1], then `steps` decode_one calls. */
+int ora_greedy_generate(const ora_model *m, const int32_t *prompt, int n, int steps,
+                        int max_ctx, int32_t *out_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,540 @@
+"""rai_amd: MI355X (gfx950) prompt-lookup decoding and W4A8 kernels.
+
+Python mirror of the `rai_infer` library API for this path (RaiModel,
+KVCache, LookupDecoder, LookupConfig, find_ngram_draft, w4a8_matvec,
+w4a8_matmul), bound over the C ABI in include/rai_hip.h.  All compute runs in
+the HIP library (rai_amd/lib/librai_hip.so); there is no CPU fallback: if the
+library is missing or no GPU is present, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_size_t, c_uint32, c_uint64, c_void_p
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "librai_hip.so")
+
+RAI_OK = 0
+_STATUS = {
+    -1: "RAI_E_ARG", -2: "RAI_E_SHAPE", -3: "RAI_E_FORMAT", -4: "RAI_E_OOM", -5: "RAI_E_HIP",
+    -6: "RAI_E_WATERMARK", -7: "RAI_E_UNSUPPORTED", -8: "RAI_E_IO", -9: "RAI_E_RANGE",
+}
+
+
+class RaiError(RuntimeError):
+    """A failed C-ABI call; `.status` holds the rai_status name."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{_STATUS.get(status, status)}: {message}")
+        self.status = _STATUS.get(status, str(status))
+
+
+class ModelConfig(ctypes.Structure):
+    _fields_ = [(n, c_uint32) for n in (
+        "hidden_size", "num_layers", "num_heads", "num_kv_heads", "head_dim",
+        "intermediate_size", "vocab_size", "max_context")] + [
+        ("rope_theta", c_float), ("norm_eps", c_float)] + [
+        (n, c_uint32) for n in ("group_size", "embed_group_size", "version", "tied",
+                                "num_experts", "experts_per_token", "norm_topk_prob")] + [
+        ("embed_scale", c_float), ("attn_scale", c_float)]
+
+
+class _LookupConfig(ctypes.Structure):
+    _fields_ = [("max_draft", c_size_t), ("max_ngram", c_size_t), ("min_ngram", c_size_t),
+                ("temperature", c_float)]
+
+
+class _LookupMatch(ctypes.Structure):
+    _fields_ = [("ngram", c_size_t), ("start", c_size_t), ("len", c_size_t)]
+
+
+class _LookupMetrics(ctypes.Structure):
+    _fields_ = [("accepted", c_size_t), ("drafted", c_size_t), ("produced", c_size_t),
+                ("matched_ngram", c_size_t), ("accept_rate", c_float)]
+
+
+class _GenerateStats(ctypes.Structure):
+    _fields_ = [(n, c_size_t) for n in ("prompt_tokens", "generated", "steps",
+                                        "steps_with_draft", "drafted", "accepted")] + [
+        ("prefill_seconds", c_double), ("decode_seconds", c_double)]
+
+
+class SynthConfig(ctypes.Structure):
+    _fields_ = [(n, c_uint32) for n in (
+        "hidden_size", "num_layers", "num_heads", "num_kv_heads", "head_dim",
+        "intermediate_size", "vocab_size", "max_context")] + [
+        ("rope_theta", c_float), ("norm_eps", c_float)] + [
+        (n, c_uint32) for n in ("group_size", "embed_group_size", "tied", "num_experts",
+                                "experts_per_token", "norm_topk_prob")] + [
+        ("weight_std", c_float), ("mode", c_uint32)]
+
+
+_lib = None
+
+
+def lib():
+    """Load the in-tree HIP library (raises if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: run `python -m rai_amd.build` "
+                           "(there is no CPU fallback)")
+    L = ctypes.CDLL(LIB_PATH)
+    P = c_void_p
+    S = c_size_t
+    sig = {
+        "rai_last_error": (c_char_p, []),
+        "rai_device_info": (c_int, [c_char_p, S, POINTER(c_int)]),
+        "rai_model_open": (c_int, [c_char_p, c_int, POINTER(c_void_p)]),
+        "rai_model_from_buffer": (c_int, [P, S, c_int, POINTER(c_void_p)]),
+        "rai_model_free": (None, [P]),
+        "rai_model_get_config": (c_int, [P, POINTER(ModelConfig)]),
+        "rai_model_weight_bytes": (c_int, [P, POINTER(c_uint64)]),
+        "rai_kv_create": (c_int, [P, S, POINTER(c_void_p)]),
+        "rai_kv_free": (None, [P]),
+        "rai_kv_truncate": (c_int, [P, S]),
+        "rai_kv_filled": (c_int, [P, S, POINTER(c_size_t)]),
+        "rai_kv_clear": (c_int, [P]),
+        "rai_kv_read": (c_int, [P, S, S, S, c_int, P]),
+        "rai_embed_token": (c_int, [P, S, P]),
+        "rai_forward_from_hidden": (c_int, [P, P, P, S, c_int]),
+        "rai_forward_batch": (c_int, [P, P, P, P, S]),
+        "rai_hidden_to_logits": (c_int, [P, P, P]),
+        "rai_hidden_to_logits_batch": (c_int, [P, P, P, S]),
+        "rai_w4a8_matmul_dev": (c_int, [P, P, P, P, S, S, S, S, P]),
+        "rai_w4a8_lane_sums_dev": (c_int, [P, P, P, S, S, S, S, P]),
+        "rai_w4a8_matmul": (c_int, [P, P, P, P, S, S, S, S]),
+        "rai_tied_lm_head_dev": (c_int, [P, P, P, P, S, S, S, P]),
+        "rai_embed_lookup_dev": (c_int, [P, S, P, P, S, S, S, P]),
+        "rai_rms_norm_dev": (c_int, [P, P, P, S, S, c_float, P]),
+        "rai_silu_mul_dev": (c_int, [P, P, S, S, P]),
+        "rai_rope_apply_dev": (c_int, [P, S, S, P, P, P]),
+        "rai_attention_head_dev": (c_int, [P, P, P, P, S, S, c_float, P]),
+        "rai_find_ngram_draft": (c_int, [P, S, S, S, S, POINTER(_LookupMatch), POINTER(c_int)]),
+        "rai_lookup_create": (c_int, [P, S, POINTER(c_void_p)]),
+        "rai_lookup_free": (None, [P]),
+        "rai_lookup_kv": (c_int, [P, POINTER(c_void_p)]),
+        "rai_lookup_prefill": (c_int, [P, P, S, POINTER(c_size_t)]),
+        "rai_lookup_step": (c_int, [P, S, P, S, POINTER(_LookupConfig), P, S,
+                                    POINTER(_LookupMetrics)]),
+        "rai_lookup_generate": (c_int, [P, P, S, S, POINTER(_LookupConfig), P, S,
+                                        POINTER(c_size_t), POINTER(_GenerateStats)]),
+        "rai_greedy_generate": (c_int, [P, P, S, S, P]),
+        "rai_synth_model": (c_int, [POINTER(SynthConfig), c_uint64, c_char_p,
+                                    POINTER(c_void_p), POINTER(c_size_t)]),
+        "rai_free_image": (None, [P]),
+        "rai_dev_malloc": (c_int, [S, POINTER(c_void_p)]),
+        "rai_dev_free": (c_int, [P]),
+        "rai_memcpy_h2d": (c_int, [P, P, S]),
+        "rai_memcpy_d2h": (c_int, [P, P, S]),
+        "rai_device_synchronize": (c_int, []),
+        "rai_stream_create": (c_int, [POINTER(c_void_p)]),
+        "rai_stream_destroy": (c_int, [P]),
+        "rai_event_create": (c_int, [POINTER(c_void_p)]),
+        "rai_event_destroy": (c_int, [P]),
+        "rai_event_record": (c_int, [P, P]),
+        "rai_event_elapsed_ms": (c_int, [P, P, POINTER(c_float)]),
+        "rai_stream_synchronize": (c_int, [P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != RAI_OK:
+        raise RaiError(rc, lib().rai_last_error().decode())
+
+
+def _ptr(a: np.ndarray) -> int:
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("array must be C-contiguous")
+    return a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def device_info() -> tuple[str, int]:
+    buf = ctypes.create_string_buffer(256)
+    cus = c_int()
+    _check(lib().rai_device_info(buf, 256, ctypes.byref(cus)))
+    return buf.value.decode(), cus.value
+
+
+# ---------------------------------------------------------------- device mem --
+
+class DeviceArray:
+    """A device allocation owned from Python (plumbing for kernel-level calls)."""
+
+    def __init__(self, nbytes: int):
+        p = c_void_p()
+        _check(lib().rai_dev_malloc(max(1, nbytes), ctypes.byref(p)))
+        self.ptr = p.value
+        self.nbytes = nbytes
+
+    @classmethod
+    def from_host(cls, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.nbytes)
+        if a.nbytes:
+            _check(lib().rai_memcpy_h2d(d.ptr, _ptr(a), a.nbytes))
+        return d
+
+    def to_host(self, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype)
+        if out.nbytes:
+            _check(lib().rai_memcpy_d2h(_ptr(out), self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().rai_dev_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- kernels --
+
+def w4a8_matmul(nibbles, params, x, rows: int, cols: int, num_tokens: int,
+                group_size: int) -> np.ndarray:
+    """w4a8_matmul (gemm.rs:1774-1919): returns out[num_tokens][rows]."""
+    nib = np.ascontiguousarray(nibbles, np.uint8)
+    par = np.ascontiguousarray(params, np.uint8)
+    x = _f32(x)
+    out = np.zeros(num_tokens * rows, np.float32)
+    _check(lib().rai_w4a8_matmul(_ptr(out), _ptr(nib), _ptr(par), _ptr(x), rows, cols,
+                                 num_tokens, group_size))
+    return out.reshape(num_tokens, rows)
+
+
+def w4a8_matvec(nibbles, params, x, rows: int, cols: int, group_size: int) -> np.ndarray:
+    """w4a8_matvec (gemm.rs:1336-1384)."""
+    return w4a8_matmul(nibbles, params, x, rows, cols, 1, group_size)[0]
+
+
+def w4a8_lane_sums(nibbles, x, rows: int, cols: int, num_tokens: int,
+                   group_size: int) -> np.ndarray:
+    """Integer accumulators of the W4A8 kernel: [tokens][rows][groups][12]."""
+    groups = -(-cols // group_size)
+    dn = DeviceArray.from_host(np.ascontiguousarray(nibbles, np.uint8))
+    dx = DeviceArray.from_host(_f32(x))
+    do = DeviceArray(num_tokens * rows * groups * 12 * 4)
+    _check(lib().rai_w4a8_lane_sums_dev(do.ptr, dn.ptr, dx.ptr, rows, cols, num_tokens,
+                                        group_size, None))
+    return do.to_host(np.int32, num_tokens * rows * groups * 12).reshape(
+        num_tokens, rows, groups, 12)
+
+
+def tied_lm_head(hidden, codes, params, vocab: int, group_size: int) -> np.ndarray:
+    """tied_lm_head (gemm.rs:1981-2076)."""
+    h = _f32(hidden)
+    dh = DeviceArray.from_host(h)
+    dc = DeviceArray.from_host(np.ascontiguousarray(codes, np.uint8))
+    dp = DeviceArray.from_host(np.ascontiguousarray(params, np.uint8))
+    do = DeviceArray(vocab * 4)
+    _check(lib().rai_tied_lm_head_dev(do.ptr, dh.ptr, dc.ptr, dp.ptr, vocab, h.size,
+                                      group_size, None))
+    return do.to_host(np.float32, vocab)
+
+
+def embed_lookup(token: int, codes, params, vocab: int, hidden: int, group_size: int):
+    """embed_lookup (gemm.rs:1926-1970)."""
+    dc = DeviceArray.from_host(np.ascontiguousarray(codes, np.uint8))
+    dp = DeviceArray.from_host(np.ascontiguousarray(params, np.uint8))
+    do = DeviceArray(hidden * 4)
+    _check(lib().rai_embed_lookup_dev(do.ptr, token, dc.ptr, dp.ptr, vocab, hidden,
+                                      group_size, None))
+    return do.to_host(np.float32, hidden)
+
+
+def rms_norm(x, weight, eps: float) -> np.ndarray:
+    """rms_norm (layers.rs:154-183) of each row of x."""
+    x = np.atleast_2d(_f32(x))
+    dx, dw = DeviceArray.from_host(x), DeviceArray.from_host(_f32(weight))
+    do = DeviceArray(x.nbytes)
+    _check(lib().rai_rms_norm_dev(do.ptr, dx.ptr, dw.ptr, x.shape[0], x.shape[1], eps, None))
+    _check(lib().rai_device_synchronize())
+    return do.to_host(np.float32, x.size).reshape(x.shape)
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    """silu_mul_inplace (layers.rs:824-883) of each row."""
+    g = np.atleast_2d(_f32(gate))
+    dg, du = DeviceArray.from_host(g), DeviceArray.from_host(np.atleast_2d(_f32(up)))
+    _check(lib().rai_silu_mul_dev(dg.ptr, du.ptr, g.shape[0], g.shape[1], None))
+    _check(lib().rai_device_synchronize())
+    return dg.to_host(np.float32, g.size).reshape(g.shape)
+
+
+def rope_apply(heads, num_heads: int, head_dim: int, cos_row, sin_row) -> np.ndarray:
+    """RoPETable::apply (layers.rs:643-726) for one position."""
+    h = _f32(heads)
+    dh = DeviceArray.from_host(h)
+    dc, ds = DeviceArray.from_host(_f32(cos_row)), DeviceArray.from_host(_f32(sin_row))
+    _check(lib().rai_rope_apply_dev(dh.ptr, num_heads, head_dim, dc.ptr, ds.ptr, None))
+    _check(lib().rai_device_synchronize())
+    return dh.to_host(np.float32, h.size)
+
+
+def attention_head(q, k, v, pos: int, head_dim: int, scale: float) -> np.ndarray:
+    """attention_head (layers.rs:1266-1452) over rows 0..=pos of k and v."""
+    dq = DeviceArray.from_host(_f32(q))
+    dk = DeviceArray.from_host(_f32(k))
+    dv = DeviceArray.from_host(_f32(v))
+    do = DeviceArray(head_dim * 4)
+    _check(lib().rai_attention_head_dev(do.ptr, dq.ptr, dk.ptr, dv.ptr, pos, head_dim, scale, None))
+    _check(lib().rai_device_synchronize())
+    return do.to_host(np.float32, head_dim)
+
+
+@dataclass
+class LookupMatch:
+    """LookupMatch (lookup.rs:91-109)."""
+    ngram: int
+    start: int
+    len: int
+
+    def draft(self, tokens):
+        return list(tokens[self.start:self.start + self.len])
+
+
+def find_ngram_draft(tokens, min_ngram: int, max_ngram: int, max_draft: int):
+    """find_ngram_draft (lookup.rs:131-171), evaluated by the GPU search kernel."""
+    t = _u32(tokens)
+    m = _LookupMatch()
+    found = c_int()
+    _check(lib().rai_find_ngram_draft(_ptr(t) if t.size else None, t.size, min_ngram,
+                                      max_ngram, max_draft, ctypes.byref(m),
+                                      ctypes.byref(found)))
+    return LookupMatch(m.ngram, m.start, m.len) if found.value else None
+
+
+# ------------------------------------------------------------------ model --
+
+def synth_model(hidden_size, num_layers, num_heads, num_kv_heads, head_dim,
+                intermediate_size, vocab_size, max_context, *, rope_theta=10000.0,
+                norm_eps=1e-5, group_size=32, embed_group_size=64, tied=False,
+                num_experts=0, experts_per_token=0, norm_topk_prob=False, weight_std=0.02,
+                mode=0, seed=0, path: str | None = None) -> bytes | int:
+    """Write a random-init .raimodel (see rai_synth_model in include/rai_hip.h).
+
+    Returns the image bytes, or the file size when `path` is given."""
+    c = SynthConfig(hidden_size, num_layers, num_heads, num_kv_heads, head_dim,
+                    intermediate_size, vocab_size, max_context, rope_theta, norm_eps,
+                    group_size, embed_group_size, int(tied), num_experts, experts_per_token,
+                    int(norm_topk_prob), weight_std, mode)
+    img = c_void_p()
+    n = c_size_t()
+    _check(lib().rai_synth_model(ctypes.byref(c), seed, path.encode() if path else None,
+                                 ctypes.byref(img), ctypes.byref(n)))
+    if path:
+        return n.value
+    try:
+        return ctypes.string_at(img.value, n.value)
+    finally:
+        lib().rai_free_image(img)
+
+
+class RaiModel:
+    """RaiModel (model.rs:97-1033) resident in HBM."""
+
+    def __init__(self, handle: int):
+        self.h = handle
+        cfg = ModelConfig()
+        _check(lib().rai_model_get_config(self.h, ctypes.byref(cfg)))
+        self.config = cfg
+
+    @classmethod
+    def load(cls, path: str, max_groups: int = 0) -> "RaiModel":
+        h = c_void_p()
+        _check(lib().rai_model_open(path.encode(), max_groups, ctypes.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def from_bytes(cls, data: bytes, max_groups: int = 0) -> "RaiModel":
+        buf = np.frombuffer(data, np.uint8)
+        h = c_void_p()
+        _check(lib().rai_model_from_buffer(_ptr(buf), buf.size, max_groups, ctypes.byref(h)))
+        return cls(h.value)
+
+    def close(self):
+        if self.h:
+            lib().rai_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weight_bytes(self) -> int:
+        v = c_uint64()
+        _check(lib().rai_model_weight_bytes(self.h, ctypes.byref(v)))
+        return v.value
+
+    def create_kv_cache(self, max_ctx: int) -> "KVCache":
+        h = c_void_p()
+        _check(lib().rai_kv_create(self.h, max_ctx, ctypes.byref(h)))
+        return KVCache(h.value, owner=self)
+
+    def embed_token(self, token_id: int) -> np.ndarray:
+        out = np.zeros(self.config.hidden_size, np.float32)
+        _check(lib().rai_embed_token(self.h, token_id, _ptr(out)))
+        return out
+
+    def forward_from_hidden(self, hidden, pos: int, kv: "KVCache", store_kv: bool = True):
+        h = _f32(hidden).copy()
+        _check(lib().rai_forward_from_hidden(self.h, kv.h, _ptr(h), pos, int(store_kv)))
+        return h
+
+    def forward_batch(self, hiddens, positions, kv: "KVCache") -> np.ndarray:
+        h = _f32(hiddens).copy()
+        p = np.ascontiguousarray(positions, np.uint64)
+        _check(lib().rai_forward_batch(self.h, kv.h, _ptr(h), _ptr(p), p.size))
+        return h
+
+    def hidden_to_logits(self, hidden) -> np.ndarray:
+        out = np.zeros(self.config.vocab_size, np.float32)
+        _check(lib().rai_hidden_to_logits(self.h, _ptr(_f32(hidden)), _ptr(out)))
+        return out
+
+    def hidden_to_logits_batch(self, hiddens, batch: int) -> np.ndarray:
+        out = np.zeros(batch * self.config.vocab_size, np.float32)
+        _check(lib().rai_hidden_to_logits_batch(self.h, _ptr(_f32(hiddens)), _ptr(out), batch))
+        return out.reshape(batch, self.config.vocab_size)
+
+
+class KVCache:
+    """KVCache (kv_cache.rs:232-330) in HBM."""
+
+    def __init__(self, handle: int, owner=None, borrowed: bool = False):
+        self.h = handle
+        self._owner = owner
+        self._borrowed = borrowed
+
+    def truncate(self, length: int):
+        _check(lib().rai_kv_truncate(self.h, length))
+
+    def filled(self, layer: int = 0) -> int:
+        v = c_size_t()
+        _check(lib().rai_kv_filled(self.h, layer, ctypes.byref(v)))
+        return v.value
+
+    def clear(self):
+        _check(lib().rai_kv_clear(self.h))
+
+    def get_k(self, layer: int, head: int, pos: int, head_dim: int) -> np.ndarray:
+        out = np.zeros(head_dim, np.float32)
+        _check(lib().rai_kv_read(self.h, layer, head, pos, 0, _ptr(out)))
+        return out
+
+    def get_v(self, layer: int, head: int, pos: int, head_dim: int) -> np.ndarray:
+        out = np.zeros(head_dim, np.float32)
+        _check(lib().rai_kv_read(self.h, layer, head, pos, 1, _ptr(out)))
+        return out
+
+    def __del__(self):
+        try:
+            if self.h and not self._borrowed:
+                lib().rai_kv_free(self.h)
+        except Exception:
+            pass
+
+
+@dataclass
+class LookupConfig:
+    """LookupConfig (lookup.rs:64-89).  temperature <= 1e-6 is greedy."""
+    max_draft: int = 10
+    max_ngram: int = 3
+    min_ngram: int = 1
+    temperature: float = 0.0
+
+    def _c(self) -> _LookupConfig:
+        return _LookupConfig(self.max_draft, self.max_ngram, self.min_ngram, self.temperature)
+
+
+@dataclass
+class LookupMetrics:
+    """LookupMetrics (lookup.rs:112-119)."""
+    accepted: int
+    drafted: int
+    produced: int
+    accept_rate: float
+    matched_ngram: int | None
+
+
+class LookupDecoder:
+    """LookupDecoder (lookup.rs:174-455): drafts by n-gram lookup on the GPU,
+    verifies [last, draft...] in one batched forward, accepts greedily."""
+
+    def __init__(self, model: RaiModel, max_ctx: int):
+        h = c_void_p()
+        _check(lib().rai_lookup_create(model.h, max_ctx, ctypes.byref(h)))
+        self.h = h.value
+        self.model = model
+        kv = c_void_p()
+        _check(lib().rai_lookup_kv(self.h, ctypes.byref(kv)))
+        self.kv_cache = KVCache(kv.value, owner=self, borrowed=True)
+
+    def prefill(self, prompt_tokens) -> int:
+        p = _u32(prompt_tokens)
+        pos = c_size_t()
+        _check(lib().rai_lookup_prefill(self.h, _ptr(p), p.size, ctypes.byref(pos)))
+        return pos.value
+
+    def step(self, pos: int, context, config: LookupConfig):
+        c = _u32(context)
+        out = np.zeros(config.max_draft + 1, np.uint32)
+        met = _LookupMetrics()
+        cfg = config._c()
+        _check(lib().rai_lookup_step(self.h, pos, _ptr(c), c.size, ctypes.byref(cfg), _ptr(out),
+                                     out.size, ctypes.byref(met)))
+        metrics = LookupMetrics(met.accepted, met.drafted, met.produced, met.accept_rate,
+                                met.matched_ngram or None)
+        return out[:met.produced].tolist(), metrics
+
+    def generate(self, prompt, max_tokens: int, config: LookupConfig):
+        """Prefill + step loop in the library (the `rai run` lookup loop)."""
+        p = _u32(prompt)
+        out = np.zeros(max_tokens + config.max_draft + 1, np.uint32)
+        n = c_size_t()
+        st = _GenerateStats()
+        cfg = config._c()
+        _check(lib().rai_lookup_generate(self.h, _ptr(p), p.size, max_tokens, ctypes.byref(cfg),
+                                         _ptr(out), out.size, ctypes.byref(n), ctypes.byref(st)))
+        stats = {f: getattr(st, f) for f, _ in _GenerateStats._fields_}
+        return out[:n.value].tolist(), stats
+
+    def greedy_generate(self, prompt, steps: int):
+        p = _u32(prompt)
+        out = np.zeros(steps, np.uint32)
+        _check(lib().rai_greedy_generate(self.h, _ptr(p), p.size, steps, _ptr(out)))
+        return out.tolist()
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().rai_lookup_free(self.h)
+                self.h = None
+        except Exception:
+            pass

@@ -1,0 +1,77 @@
+// Launchers for the gfx950 kernels (kernels.hip).  All launchers are
+// asynchronous on `stream` and validate nothing: callers check shapes.
+#ifndef RAI_KERNELS_H
+#define RAI_KERNELS_H
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace rai {
+
+// Per-token activation quantization of gemm.rs:147-374 for K-column rows:
+// q_nat [m][K] int8 in natural column order; q_split [m][K] int8 in
+// 8-column blocks of (4 even columns, 4 odd columns) when K % 8 == 0 (else
+// unused, may be null); scales/sums [m][groups].
+void launch_quantize(const float *x, int m, int k, int gs, int8_t *q_nat, int8_t *q_split,
+                     float *scales, float *sums, hipStream_t s);
+
+// w4a8 matmul over already-quantized activations (see gemm.rs:1774-1919).
+void launch_w4a8(float *out, const uint8_t *nib, const uint8_t *params, const float *x,
+                 const int8_t *q_nat, const int8_t *q_split, const float *scales,
+                 const float *sums, int rows, int cols, int m, int gs, hipStream_t s);
+// True when launch_w4a8 takes the tiled fast path for this shape.
+bool w4a8_fast_path(int cols, int gs);
+
+void launch_lane_sums(int32_t *out, const uint8_t *nib, const int8_t *q_nat, int rows, int cols,
+                      int m, int gs, hipStream_t s);
+
+// Tied 8-bit lm_head (gemm.rs:804-1047, 1981-2076) for m tokens.
+void launch_tied_lm_head(float *logits, const float *hidden, const uint8_t *codes,
+                         const uint8_t *params, int vocab, int n, int gs, int m, int8_t *hq,
+                         float *hscales, float *hsums, hipStream_t s);
+
+// Embedding rows (gemm.rs:1926-1970, model.rs:371-403) for token ids read
+// from `tokens` (device), or, when tokens == null, from
+// ctx[last] followed by ctx[start .. start+m-1) (the lookup verify batch).
+void launch_embed(const uint32_t *tokens, const uint32_t *ctx, int last, int start, int m,
+                  const uint8_t *codes, const uint8_t *params, int vocab, int hidden, int egs,
+                  float embed_scale, float *out, int *err, hipStream_t s);
+
+void launch_rmsnorm(const float *x, const float *w, float *out, float *resid, int m, int n,
+                    float eps, hipStream_t s);
+void launch_vec_add(float *h, const float *r, const float *a, size_t n, hipStream_t s);
+void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s);
+// RoPE on q [m][nh*hd] and k [m][nkv*hd] at positions pos0.., then K/V store
+// into the layer's cache [nkv][cap][hd].
+void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
+                       int pos0, int m, int nh, int nkv, int hd, float *kc, float *vc, int cap,
+                       hipStream_t s);
+// attention_head_avx2 for every (token, query head).
+void launch_attention(const float *q, const float *kc, const float *vc, int cap, int pos0, int m,
+                      int nh, int nkv, int hd, float scale, float *out, hipStream_t s);
+// Standalone RoPE of one position (layers.rs:643-726) on heads [nh][hd].
+void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,
+                       hipStream_t s);
+void launch_argmax(const float *logits, int m, int vocab, uint32_t *out, hipStream_t s);
+// find_ngram_draft over ctx[0..len): res = {ngram, start, len}; ngram 0 = none.
+void launch_ngram(const uint32_t *ctx, int len, int min_n, int max_n, int max_draft, int *res,
+                  hipStream_t s);
+// Greedy acceptance: argmax[0..nd] vs ctx[start..start+nd); writes the
+// produced tokens to ctx[len..] and res2 = {accepted, produced}.
+void launch_accept(const uint32_t *argmax, uint32_t *ctx, int len, int start, int nd, int *res2,
+                   hipStream_t s);
+
+// MoE (layers.rs:1808-1870, model.rs:208-261): router probabilities and
+// top-k selection per token.
+void launch_router(const float *x, const float *router, int m, int hidden, int experts, int topk,
+                   int norm_topk, int *sel, float *wts, hipStream_t s);
+// out[t] += w * eo[t] for the m tokens (per-token weight array w[t]).
+void launch_moe_accumulate(float *out, const float *eo, const float *w, int m, int n,
+                           hipStream_t s);
+void launch_fill(float *p, float v, size_t n, hipStream_t s);
+
+}  // namespace rai
+
+#endif

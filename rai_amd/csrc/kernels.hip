@@ -1,0 +1,964 @@
+// gfx950 kernels for the prompt-lookup / W4A8 hot path.
+//
+// Every kernel reproduces the f32 operation order of rai's AVX2 CPU path
+// (rai-infer/src/gemm.rs, layers.rs), so outputs are bit-identical to it:
+// the library is built with -ffp-contract=off and fuses a multiply-add only
+// where the reference uses an FMA intrinsic.  Integer dot products use
+// v_dot4 (exact int32).  Wavefronts are 64 lanes.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+
+#include "exact_math.h"
+#include "kernels.h"
+
+namespace rai {
+
+namespace {
+
+__device__ __forceinline__ float f16bits(uint16_t b) { return __half2float(__ushort_as_half(b)); }
+
+// IEEE division, correctly rounded (HIP compiles `/` that way by default;
+// the helper only names the intent at the call sites that need it).
+__device__ __forceinline__ float __fdiv_exact(float a, float b) { return a / b; }
+
+// _mm256 horizontal sum order of gemm.rs:527-533 / layers.rs:1303-1310.
+__device__ __forceinline__ float hsum8(const float *a) {
+  return ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]));
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Integer dot of one 8-column block: low nibbles (even columns) against the
+// 4 even activations, high nibbles against the 4 odd ones
+// (the PMADDUBSW pairing of gemm.rs:470-476).
+__device__ __forceinline__ int block_dot(uint32_t codes, uint32_t q_even, uint32_t q_odd, int acc) {
+  const uint32_t lo = codes & 0x0F0F0F0Fu;
+  const uint32_t hi = (codes >> 4) & 0x0F0F0F0Fu;
+  return dot4(hi, q_odd, dot4(lo, q_even, acc));
+}
+
+// Column c of a block-split row: 8-column block b holds its even columns at
+// 8b+0..3 and its odd columns at 8b+4..7.
+__device__ __forceinline__ int split_index(int c) {
+  const int j = c & 7;
+  return (c & ~7) + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
+}
+
+// ------------------------------------------------------------ quantize --
+
+// One thread per (token, group): absmax, scale, int8 codes (RNE on the
+// 8-wide body, half-away on the pair tail), and the 8-lane input sum
+// (gemm.rs:172-212, 280-374).
+__global__ void k_quantize(const float *__restrict__ x, int m, int k, int gs, int groups,
+                           int8_t *__restrict__ q_nat, int8_t *__restrict__ q_split,
+                           float *__restrict__ scales, float *__restrict__ sums) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.y;
+  if (g >= groups || t >= m) return;
+  const float *row = x + (size_t)t * k;
+  const int start = g * gs;
+  const int end = min(start + gs, k);
+  const int len = end - start;
+  const int c8 = len / 8;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float absmax = 0.0f;
+  for (int i = 0; i < c8; ++i)
+    for (int j = 0; j < 8; ++j) {
+      const float v = row[start + i * 8 + j];
+      acc[j] = acc[j] + v;
+      absmax = fmaxf(absmax, fabsf(v));
+    }
+  float total = hsum8(acc);
+  for (int i = c8 * 8; i < len; ++i) {
+    const float v = row[start + i];
+    total = total + v;
+    const float a = fabsf(v);
+    if (a > absmax) absmax = a;
+  }
+  sums[(size_t)t * groups + g] = total;
+  const float scale = absmax > 1e-10f ? __fdiv_exact(absmax, 127.0f) : 1.0f;
+  const float inv = __fdiv_exact(1.0f, scale);
+  scales[(size_t)t * groups + g] = scale;
+  int8_t *qn = q_nat + (size_t)t * k;
+  int8_t *qs = q_split ? q_split + (size_t)t * k : nullptr;
+  for (int i = 0; i < len; ++i) {
+    const float v = row[start + i] * inv;
+    float r = (i < c8 * 8) ? rintf(v) : roundf(v);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    const int8_t q = (int8_t)(int)r;
+    qn[start + i] = q;
+    if (qs) qs[split_index(start + i)] = q;
+  }
+}
+
+// ---------------------------------------------------------- w4a8 simple --
+
+// One thread per (row, token), the full reference order for any even group
+// size, partial last group and unquantized f32 tail (gemm.rs:401-539).
+__global__ void k_w4a8_simple(float *__restrict__ out, const uint8_t *__restrict__ nib,
+                              const uint8_t *__restrict__ params, const float *__restrict__ x,
+                              const int8_t *__restrict__ q_nat, const float *__restrict__ scales,
+                              const float *__restrict__ sums, int rows, int cols, int m, int gs,
+                              int groups) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.y;
+  if (r >= rows || t >= m) return;
+  const uint8_t *nrow = nib + (size_t)r * (cols / 2);
+  const uint8_t *prow = params + (size_t)r * groups * 4;
+  const int8_t *q = q_nat + (size_t)t * cols;
+  const float *xr = x + (size_t)t * cols;
+  float f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float zc = 0.0f;
+  for (int g = 0; g < groups; ++g) {
+    const uint16_t sb = (uint16_t)(prow[g * 4] | (prow[g * 4 + 1] << 8));
+    const uint16_t zb = (uint16_t)(prow[g * 4 + 2] | (prow[g * 4 + 3] << 8));
+    const float ws = f16bits(sb), wz = f16bits(zb);
+    zc = zc + wz * sums[(size_t)t * groups + g];
+    const float cs = ws * scales[(size_t)t * groups + g];
+    const int col0 = g * gs;
+    const int ags = min(gs, cols - col0);
+    const int c64 = ags / 64;
+    int s64[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int c = 0; c < c64; ++c)
+      for (int l = 0; l < 8; ++l)
+        for (int j = 0; j < 8; ++j) {
+          const int col = col0 + 64 * c + 8 * l + j;
+          const uint8_t b = nrow[col >> 1];
+          const int code = (col & 1) ? (b >> 4) : (b & 15);
+          s64[l] += code * (int)q[col];
+        }
+    for (int l = 0; l < 8; ++l) f[l] = f[l] + (float)s64[l] * cs;
+    const int done = c64 * 64;
+    const bool has32 = done + 32 <= ags;
+    if (has32) {
+      for (int l = 0; l < 4; ++l) {
+        int s = 0;
+        for (int j = 0; j < 8; ++j) {
+          const int col = col0 + done + 8 * l + j;
+          const uint8_t b = nrow[col >> 1];
+          const int code = (col & 1) ? (b >> 4) : (b & 15);
+          s += code * (int)q[col];
+        }
+        f[l] = f[l] + (float)s * cs;
+      }
+    }
+    const int done2 = done + (has32 ? 32 : 0);
+    if (done2 < ags) {
+      float tacc = 0.0f;
+      for (int tc = done2; tc + 1 < ags; tc += 2) {
+        const uint8_t b = nrow[(col0 + tc) >> 1];
+        const float a0 = (float)(b & 15) * xr[col0 + tc];
+        const float a1 = (float)(b >> 4) * xr[col0 + tc + 1];
+        tacc = tacc + (a0 + a1);
+      }
+      f[0] = f[0] + ws * tacc;
+    }
+  }
+  out[(size_t)t * rows + r] = hsum8(f) + zc;
+}
+
+// ------------------------------------------------------------ w4a8 fast --
+
+// Tiled kernel for group sizes 32, 64 and 128 with full groups.
+// A block owns kRows weight rows and all m (<= MT) tokens and walks K in
+// tiles of GT groups.  Phase 1: every (row, group) item computes, for each
+// token, the per-lane products fl(float(S_lane) * fl(ws*as)) and the zero
+// term fl(z * xsum) into LDS.  Phase 2: each (token, chain, row) accumulator
+// adds its products in group order, which is exactly the reference's
+// sequential per-lane f32 accumulation.  NL = reference lanes that receive
+// products (4 for group 32, 8 for groups 64/128); chain NL is the zero term.
+constexpr int kRows = 16;
+constexpr int kThreads = 256;
+
+template <int GS, int MT>
+struct FastCfg {
+  static constexpr int NL = (GS == 32) ? 4 : 8;
+  static constexpr int NC = NL + 1;
+  // Groups per K tile, chosen to keep the product tile within 40 KB of LDS.
+  static constexpr int GT = (GS == 32) ? (MT >= 16 ? 8 : 16) : (MT >= 16 ? 4 : 8);
+  static constexpr int CPT = (MT * NC * kRows + kThreads - 1) / kThreads;
+};
+
+template <int GS, int MT>
+__global__ __launch_bounds__(kThreads) void k_w4a8_fast(
+    float *__restrict__ out, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
+    const int8_t *__restrict__ q_split, const float *__restrict__ scales,
+    const float *__restrict__ sums, int rows, int cols, int m_total, int groups) {
+  using C = FastCfg<GS, MT>;
+  constexpr int NL = C::NL, NC = C::NC, GT = C::GT, CPT = C::CPT;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int t0 = blockIdx.y * MT;
+  const int m = min(MT, m_total - t0);
+  const int row0 = blockIdx.x * kRows;
+  const int tid = threadIdx.x;
+  // LDS carve-up: q tile [MT][GT*GS] bytes, scale/sum [MT][GT], products
+  // [MT][NC][kRows][GT], final chain values reuse the product area.
+  int8_t *qsh = reinterpret_cast<int8_t *>(smem);
+  float *ash = reinterpret_cast<float *>(smem + MT * GT * GS);
+  float *ssh = ash + MT * GT;
+  float *psh = ssh + MT * GT;
+
+  float acc[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) acc[j] = 0.0f;
+
+  const int ktiles = (groups + GT - 1) / GT;
+  const size_t row_bytes = (size_t)cols / 2;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int g0 = kt * GT;
+    const int gcount = min(GT, groups - g0);
+    // Stage the activation tile.
+    {
+      const int tile_bytes = gcount * GS;  // per token, multiple of 16
+      const int vec_per_tok = tile_bytes / 16;
+      for (int i = tid; i < m * vec_per_tok; i += kThreads) {
+        const int t = i / vec_per_tok, v = i % vec_per_tok;
+        const uint4 val = *reinterpret_cast<const uint4 *>(q_split + (size_t)(t0 + t) * cols +
+                                                           (size_t)g0 * GS + v * 16);
+        *reinterpret_cast<uint4 *>(qsh + t * GT * GS + v * 16) = val;
+      }
+      for (int i = tid; i < m * gcount; i += kThreads) {
+        const int t = i / gcount, g = i % gcount;
+        ash[t * GT + g] = scales[(size_t)(t0 + t) * groups + g0 + g];
+        ssh[t * GT + g] = sums[(size_t)(t0 + t) * groups + g0 + g];
+      }
+    }
+    __syncthreads();
+    // Phase 1: products.
+    if (tid < kRows * GT) {
+      const int r = tid / GT, g = tid % GT;
+      const int row = row0 + r;
+      if (row < rows && g < gcount) {
+        const uint8_t *pp = params + ((size_t)row * groups + g0 + g) * 4;
+        const uint32_t pw = *reinterpret_cast<const uint32_t *>(pp);
+        const float ws = f16bits((uint16_t)(pw & 0xFFFF));
+        const float wz = f16bits((uint16_t)(pw >> 16));
+        constexpr int NW = GS / 8;  // 8-column blocks (code dwords) per group
+        uint32_t cw[NW];
+        const uint8_t *cp = nib + (size_t)row * row_bytes + (size_t)(g0 + g) * (GS / 2);
+#pragma unroll
+        for (int v = 0; v < NW / 4; ++v) {
+          const uint4 u = *reinterpret_cast<const uint4 *>(cp + v * 16);
+          cw[v * 4 + 0] = u.x;
+          cw[v * 4 + 1] = u.y;
+          cw[v * 4 + 2] = u.z;
+          cw[v * 4 + 3] = u.w;
+        }
+        for (int t = 0; t < m; ++t) {
+          const uint32_t *qw = reinterpret_cast<const uint32_t *>(qsh + t * GT * GS + g * GS);
+          int s[NL];
+#pragma unroll
+          for (int l = 0; l < NL; ++l) s[l] = 0;
+#pragma unroll
+          for (int b = 0; b < NW; ++b) s[b % NL] = block_dot(cw[b], qw[2 * b], qw[2 * b + 1], s[b % NL]);
+          const float cs = ws * ash[t * GT + g];
+          float *pt = psh + ((t * NC) * kRows + r) * GT + g;
+#pragma unroll
+          for (int l = 0; l < NL; ++l) pt[l * kRows * GT] = (float)s[l] * cs;
+          pt[NL * kRows * GT] = wz * ssh[t * GT + g];
+        }
+      }
+    }
+    __syncthreads();
+    // Phase 2: ordered accumulation.
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int c = tid + j * kThreads;
+      if (c < m * NC * kRows) {
+        const float *p = psh + c * GT;
+        float a = acc[j];
+        for (int g = 0; g < gcount; ++g) a = a + p[g];
+        acc[j] = a;
+      }
+    }
+    __syncthreads();
+  }
+  // Epilogue: lane reduction in the reference's order, plus the zero term.
+  float *fin = psh;  // [m][NC][kRows]
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = tid + j * kThreads;
+    if (c < m * NC * kRows) fin[c] = acc[j];
+  }
+  __syncthreads();
+  if (tid < m * kRows) {
+    const int t = tid / kRows, r = tid % kRows;
+    const int row = row0 + r;
+    if (row < rows) {
+      float f[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) f[l] = (l < NL) ? fin[(t * NC + l) * kRows + r] : 0.0f;
+      const float zc = fin[(t * NC + NL) * kRows + r];
+      out[(size_t)(t0 + t) * rows + row] = hsum8(f) + zc;
+    }
+  }
+}
+
+template <int GS, int MT>
+size_t fast_smem() {
+  using C = FastCfg<GS, MT>;
+  return (size_t)MT * C::GT * GS + 2 * sizeof(float) * MT * C::GT +
+         sizeof(float) * (size_t)MT * C::NC * kRows * C::GT;
+}
+
+template <int GS, int MT>
+void launch_fast_t(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                   const float *scales, const float *sums, int rows, int cols, int m, int groups,
+                   hipStream_t s) {
+  const size_t smem = fast_smem<GS, MT>();
+  static bool configured = false;
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_fast<GS, MT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = true;
+  }
+  dim3 grid((rows + kRows - 1) / kRows, (m + MT - 1) / MT);
+  hipLaunchKernelGGL((k_w4a8_fast<GS, MT>), grid, dim3(kThreads), smem, s, out, nib, params,
+                     q_split, scales, sums, rows, cols, m, groups);
+}
+
+template <int GS>
+void launch_fast_gs(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                    const float *scales, const float *sums, int rows, int cols, int m, int groups,
+                    hipStream_t s) {
+  if (m <= 1)
+    launch_fast_t<GS, 1>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+  else if (m <= 2)
+    launch_fast_t<GS, 2>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+  else if (m <= 4)
+    launch_fast_t<GS, 4>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+  else if (m <= 8)
+    launch_fast_t<GS, 8>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+  else
+    launch_fast_t<GS, 16>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+}
+
+// --------------------------------------------------------- lane sums dbg --
+
+__global__ void k_lane_sums(int32_t *__restrict__ out, const uint8_t *__restrict__ nib,
+                            const int8_t *__restrict__ q_nat, int rows, int cols, int m, int gs,
+                            int groups) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.y;
+  if (idx >= rows * groups || t >= m) return;
+  const int r = idx / groups, g = idx % groups;
+  const uint8_t *nrow = nib + (size_t)r * (cols / 2);
+  const int8_t *q = q_nat + (size_t)t * cols;
+  int32_t *o = out + (((size_t)t * rows + r) * groups + g) * 12;
+  const int col0 = g * gs;
+  const int ags = min(gs, cols - col0);
+  const int c64 = ags / 64;
+  for (int l = 0; l < 8; ++l) {
+    int s = 0;
+    for (int c = 0; c < c64; ++c)
+      for (int j = 0; j < 8; ++j) {
+        const int col = col0 + 64 * c + 8 * l + j;
+        const uint8_t b = nrow[col >> 1];
+        s += ((col & 1) ? (b >> 4) : (b & 15)) * (int)q[col];
+      }
+    o[l] = s;
+  }
+  const int done = c64 * 64;
+  for (int l = 0; l < 4; ++l) {
+    int s = 0;
+    if (done + 32 <= ags)
+      for (int j = 0; j < 8; ++j) {
+        const int col = col0 + done + 8 * l + j;
+        const uint8_t b = nrow[col >> 1];
+        s += ((col & 1) ? (b >> 4) : (b & 15)) * (int)q[col];
+      }
+    o[8 + l] = s;
+  }
+}
+
+// -------------------------------------------------------- tied lm_head --
+
+// quantize_hidden_i8 (gemm.rs:924-1047): +-63 per group, plus input sums.
+__global__ void k_quantize63(const float *__restrict__ x, int m, int n, int gs, int groups,
+                             int8_t *__restrict__ q, float *__restrict__ scales,
+                             float *__restrict__ sums) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.y;
+  if (g >= groups || t >= m) return;
+  const float *row = x + (size_t)t * n;
+  const int start = g * gs, end = min(start + gs, n), len = end - start, c8 = len / 8;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float absmax = 0.0f;
+  for (int i = 0; i < c8; ++i)
+    for (int j = 0; j < 8; ++j) {
+      const float v = row[start + i * 8 + j];
+      acc[j] = acc[j] + v;
+      absmax = fmaxf(absmax, fabsf(v));
+    }
+  float total = hsum8(acc);
+  for (int i = c8 * 8; i < len; ++i) {
+    total = total + row[start + i];
+    const float a = fabsf(row[start + i]);
+    if (a > absmax) absmax = a;
+  }
+  sums[(size_t)t * groups + g] = total;
+  const float scale = absmax > 1e-10f ? __fdiv_exact(absmax, 63.0f) : 1.0f;
+  const float inv = __fdiv_exact(1.0f, scale);
+  scales[(size_t)t * groups + g] = scale;
+  for (int i = 0; i < len; ++i) {
+    const float v = row[start + i] * inv;
+    float r = (i < c8 * 8) ? rintf(v) : roundf(v);
+    r = fminf(fmaxf(r, -63.0f), 63.0f);
+    q[(size_t)t * n + start + i] = (int8_t)(int)r;
+  }
+}
+
+// lm_head_chunk_i8 (gemm.rs:804-915): 8 lanes of 4 consecutive codes per
+// 32-column chunk, scalar tail on the quantized hidden into lane 0.
+__global__ void k_tied_head(float *__restrict__ logits, const uint8_t *__restrict__ codes,
+                            const uint8_t *__restrict__ params, const int8_t *__restrict__ hq,
+                            const float *__restrict__ hscales, const float *__restrict__ hsums,
+                            int vocab, int n, int gs, int groups, int m) {
+  const int v = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.y;
+  if (v >= vocab || t >= m) return;
+  const uint8_t *row = codes + (size_t)v * n;
+  const uint8_t *prow = params + (size_t)v * groups * 4;
+  const int8_t *h = hq + (size_t)t * n;
+  float zc = 0.0f;
+  for (int g = 0; g < groups; ++g) {
+    const float wz = f16bits((uint16_t)(prow[g * 4 + 2] | (prow[g * 4 + 3] << 8)));
+    zc = zc + wz * hsums[(size_t)t * groups + g];
+  }
+  float f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int g = 0; g < groups; ++g) {
+    const float ws = f16bits((uint16_t)(prow[g * 4] | (prow[g * 4 + 1] << 8)));
+    const float hs = hscales[(size_t)t * groups + g];
+    const int col0 = g * gs, ags = min(gs, n - col0), c32 = ags / 32;
+    int s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int c = 0; c < c32; ++c)
+      for (int l = 0; l < 8; ++l)
+        for (int j = 0; j < 4; ++j) {
+          const int col = col0 + 32 * c + 4 * l + j;
+          s[l] += (int)row[col] * (int)h[col];
+        }
+    const float cs = ws * hs;
+    for (int l = 0; l < 8; ++l) f[l] = f[l] + (float)s[l] * cs;
+    if (c32 * 32 < ags) {
+      float tail = 0.0f;
+      for (int i = c32 * 32; i < ags; ++i) tail = tail + (float)row[col0 + i] * (float)h[col0 + i];
+      f[0] = f[0] + (ws * hs) * tail;
+    }
+  }
+  logits[(size_t)t * vocab + v] = hsum8(f) + zc;
+}
+
+// --------------------------------------------------------------- embed --
+
+__global__ void k_embed(const uint32_t *__restrict__ tokens, const uint32_t *__restrict__ ctx,
+                        int last, int start, const uint8_t *__restrict__ codes,
+                        const uint8_t *__restrict__ params, int vocab, int hidden, int egs,
+                        int egroups, float embed_scale, float *__restrict__ out, int *err) {
+  const int t = blockIdx.x;
+  uint32_t tok = tokens ? tokens[t] : (t == 0 ? ctx[last] : ctx[start + t - 1]);
+  float *o = out + (size_t)t * hidden;
+  if (tok >= (uint32_t)vocab) {
+    if (threadIdx.x == 0) atomicExch(err, 1);
+    for (int c = threadIdx.x; c < hidden; c += blockDim.x) o[c] = 0.0f;
+    return;
+  }
+  const uint8_t *row = codes + (size_t)tok * hidden;
+  const uint8_t *prow = params + (size_t)tok * egroups * 4;
+  for (int c = threadIdx.x; c < hidden; c += blockDim.x) {
+    const int g = c / egs;
+    const float s = f16bits((uint16_t)(prow[g * 4] | (prow[g * 4 + 1] << 8)));
+    const float z = f16bits((uint16_t)(prow[g * 4 + 2] | (prow[g * 4 + 3] << 8)));
+    float v = (float)row[c] * s + z;
+    if (embed_scale != 1.0f) v = v * embed_scale;
+    o[c] = v;
+  }
+}
+
+// ------------------------------------------------------------- rmsnorm --
+
+// rms_norm_avx2 (layers.rs:325-376): 16 FMA chains (sq0 lanes 0-7 over
+// elements 16i+j and the trailing 8-block, sq1 lanes over 16i+8+j), lane-wise
+// sq0+sq1, horizontal reduce, scalar tail, inv = 1/sqrt(sum/n + eps),
+// out = (x*inv)*w.  One 64-lane wavefront per token.
+__global__ void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w,
+                          float *__restrict__ out, float *__restrict__ resid, int n, float eps) {
+  const int t = blockIdx.x;
+  const float *row = x + (size_t)t * n;
+  __shared__ float chains[16];
+  __shared__ float inv_sh;
+  const int lane = threadIdx.x;
+  const int c16 = (n / 8) / 2;
+  const bool extra8 = 16 * c16 + 8 <= n;
+  if (lane < 16) {
+    const int j = lane & 7;
+    const int off = (lane < 8) ? 0 : 8;
+    float a = 0.0f;
+    for (int i = 0; i < c16; ++i) {
+      const float v = row[16 * i + off + j];
+      a = __fmaf_rn(v, v, a);
+    }
+    if (lane < 8 && extra8) {
+      const float v = row[16 * c16 + j];
+      a = __fmaf_rn(v, v, a);
+    }
+    chains[lane] = a;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    float s[8];
+    for (int j = 0; j < 8; ++j) s[j] = chains[j] + chains[8 + j];
+    float sum = hsum8(s);
+    for (int i = 16 * c16 + (extra8 ? 8 : 0); i < n; ++i) sum = sum + row[i] * row[i];
+    // Correctly rounded sqrt and divide (the reference's sqrtss / divss).
+    // HIP's __fsqrt_rn maps to the approximate native sqrt unless OCML
+    // rounded operations are enabled, so the builtin is used instead.
+    inv_sh = 1.0f / __builtin_sqrtf(sum / (float)n + eps);
+  }
+  __syncthreads();
+  const float inv = inv_sh;
+  float *o = out + (size_t)t * n;
+  float *rr = resid ? resid + (size_t)t * n : nullptr;
+  for (int i = lane; i < n; i += blockDim.x) {
+    const float v = row[i];
+    o[i] = (v * inv) * w[i];
+    if (rr) rr[i] = v;
+  }
+}
+
+__global__ void k_vec_add(float *__restrict__ h, const float *__restrict__ r,
+                          const float *__restrict__ a, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) h[i] = r[i] + a[i];
+}
+
+// silu_mul_avx2 (layers.rs:850-883) per token row of n.
+__global__ void k_silu_mul(float *__restrict__ gate, const float *__restrict__ up, int m, int n) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n || t >= m) return;
+  const size_t idx = (size_t)t * n + i;
+  const float x = gate[idx];
+  float r;
+  if (i < (n / 8) * 8) {
+    const float e = rai_exact::schraudolph(x * -1.0f);
+    r = __fdiv_exact(x, 1.0f + e) * up[idx];
+  } else {
+    r = __fdiv_exact(x, 1.0f + rai_exact::expf_glibc(-x)) * up[idx];
+  }
+  gate[idx] = r;
+}
+
+// RoPETable::apply_avx2 (layers.rs:689-726) for q and k, then the KV store
+// (kv_cache.rs:143-172).
+__global__ void k_rope_store(float *__restrict__ q, float *__restrict__ k,
+                             const float *__restrict__ v, const float *__restrict__ cos_t,
+                             const float *__restrict__ sin_t, int pos0, int nh, int nkv, int hd,
+                             float *__restrict__ kc, float *__restrict__ vc, int cap) {
+  const int t = blockIdx.x;
+  const int pos = pos0 + t;
+  const int half = hd / 2;
+  const int body = (half / 8) * 8;
+  const float *cr = cos_t + (size_t)pos * half;
+  const float *sr = sin_t + (size_t)pos * half;
+  const int total = (nh + nkv) * half;
+  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    const int h = idx / half, i = idx % half;
+    float *b = (h < nh) ? q + ((size_t)t * nh + h) * hd : k + ((size_t)t * nkv + (h - nh)) * hd;
+    const float x0 = b[i], x1 = b[half + i], c = cr[i], s = sr[i];
+    float r0, r1;
+    if (i < body) {
+      r0 = __fmaf_rn(x0, c, -(x1 * s));
+      r1 = __fmaf_rn(x1, c, x0 * s);
+    } else {
+      r0 = x0 * c - x1 * s;
+      r1 = x1 * c + x0 * s;
+    }
+    b[i] = r0;
+    b[half + i] = r1;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < nkv * hd; idx += blockDim.x) {
+    const int h = idx / hd, d = idx % hd;
+    const size_t dst = ((size_t)h * cap + pos) * hd + d;
+    kc[dst] = k[((size_t)t * nkv + h) * hd + d];
+    vc[dst] = v[((size_t)t * nkv + h) * hd + d];
+  }
+}
+
+__global__ void k_rope_apply(float *__restrict__ heads, int nh, int hd,
+                             const float *__restrict__ cr, const float *__restrict__ sr) {
+  const int half = hd / 2;
+  const int body = (half / 8) * 8;
+  for (int idx = threadIdx.x; idx < nh * half; idx += blockDim.x) {
+    const int h = idx / half, i = idx % half;
+    float *b = heads + (size_t)h * hd;
+    const float x0 = b[i], x1 = b[half + i], c = cr[i], s = sr[i];
+    if (i < body) {
+      b[i] = __fmaf_rn(x0, c, -(x1 * s));
+      b[half + i] = __fmaf_rn(x1, c, x0 * s);
+    } else {
+      b[i] = x0 * c - x1 * s;
+      b[half + i] = x1 * c + x0 * s;
+    }
+  }
+}
+
+// ----------------------------------------------------------- attention --
+
+// attention_head_avx2 (layers.rs:1266-1380) for one (token, query head):
+// 8-lane FMA score dots, Schraudolph exp over the 8-aligned body and glibc
+// expf on the tail, 8-lane sum, p = e * (1/sum), out[d] = fma(p_t, v_t[d],
+// out[d]) sequentially over t.
+__global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q,
+                                                   const float *__restrict__ kc,
+                                                   const float *__restrict__ vc, int cap, int pos0,
+                                                   int nh, int nkv, int hd, float scale,
+                                                   float *__restrict__ out) {
+  extern __shared__ float sc[];  // [pos+1] scores, then 8 partial sums
+  __shared__ float red[256];
+  __shared__ float bcast;
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int pos = pos0 + t;
+  const int n = pos + 1;
+  const int kvh = h / (nh / nkv);
+  const float *qh = q + ((size_t)t * nh + h) * hd;
+  const float *kb = kc + (size_t)kvh * cap * hd;
+  const float *vb = vc + (size_t)kvh * cap * hd;
+  const int tid = threadIdx.x;
+  const int c8 = hd / 8;
+  float mx = -INFINITY;
+  for (int s = tid; s < n; s += blockDim.x) {
+    const float *kr = kb + (size_t)s * hd;
+    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int c = 0; c < c8; ++c)
+      for (int j = 0; j < 8; ++j) a[j] = __fmaf_rn(qh[c * 8 + j], kr[c * 8 + j], a[j]);
+    const float v = hsum8(a) * scale;
+    sc[s] = v;
+    mx = fmaxf(mx, v);
+  }
+  red[tid] = mx;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+    __syncthreads();
+  }
+  mx = red[0];
+  const int n8 = n / 8;
+  for (int s = tid; s < n; s += blockDim.x) {
+    const float d = sc[s] - mx;
+    sc[s] = (s < n8 * 8) ? rai_exact::schraudolph(d) : rai_exact::expf_glibc(d);
+  }
+  __syncthreads();
+  if (tid < 8) {
+    float a = 0.0f;
+    for (int i = 0; i < n8; ++i) a = a + sc[i * 8 + tid];
+    red[tid] = a;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float sum = hsum8(red);
+    for (int s = n8 * 8; s < n; ++s) sum = sum + sc[s];
+    bcast = __fdiv_exact(1.0f, sum);
+  }
+  __syncthreads();
+  const float inv = bcast;
+  for (int s = tid; s < n; s += blockDim.x) sc[s] = sc[s] * inv;
+  __syncthreads();
+  float *o = out + ((size_t)t * nh + h) * hd;
+  for (int d = tid; d < hd; d += blockDim.x) {
+    float a = 0.0f;
+    for (int s = 0; s < n; ++s) a = __fmaf_rn(sc[s], vb[(size_t)s * hd + d], a);
+    o[d] = a;
+  }
+}
+
+// -------------------------------------------------------------- argmax --
+
+__device__ __forceinline__ long long argmax_key(float f, int idx) {
+  if (f != f) f = -INFINITY;  // sampler.rs:55-59 NaN -> -inf
+  int32_t b = (int32_t)__float_as_uint(f);
+  b ^= (int32_t)(((uint32_t)(b >> 31)) >> 1);  // f32::total_cmp ordering
+  return ((long long)b << 32) | (long long)(uint32_t)idx;
+}
+
+// sampler.rs:201-208: max by total_cmp, the last maximal index wins.
+__global__ void k_argmax(const float *__restrict__ logits, int vocab, uint32_t *__restrict__ out) {
+  const int t = blockIdx.x;
+  const float *row = logits + (size_t)t * vocab;
+  long long best = LLONG_MIN;
+  for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
+    const long long k = argmax_key(row[i], i);
+    best = k > best ? k : best;
+  }
+  __shared__ long long red[1024];
+  red[threadIdx.x] = best;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] > red[threadIdx.x + w] ? red[threadIdx.x] : red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[t] = (uint32_t)(red[0] & 0xFFFFFFFFll);
+}
+
+// ------------------------------------------------------- n-gram search --
+
+// find_ngram_draft (lookup.rs:131-171): for n = hi..lo, the largest start
+// <= len-n-1 whose n tokens equal the suffix; draft = min(max_draft,
+// len-start-n) tokens after it.  One 1024-thread block.
+__global__ void k_ngram(const uint32_t *__restrict__ ctx, int len, int min_n, int max_n,
+                        int max_draft, int *__restrict__ res) {
+  __shared__ int best;
+  __shared__ int done;
+  if (threadIdx.x == 0) {
+    done = 0;
+    res[0] = 0;
+    res[1] = 0;
+    res[2] = 0;
+  }
+  __syncthreads();
+  if (max_draft <= 0 || len < 2) return;
+  const int hi = min(max_n, len - 1);
+  const int lo = max(min_n, 1);
+  for (int n = hi; n >= lo; --n) {
+    if (threadIdx.x == 0) best = -1;
+    __syncthreads();
+    const uint32_t *suf = ctx + len - n;
+    for (int s = threadIdx.x; s <= len - n - 1; s += blockDim.x) {
+      bool eq = true;
+      for (int i = 0; i < n && eq; ++i) eq = ctx[s + i] == suf[i];
+      if (eq) atomicMax(&best, s);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && best >= 0) {
+      const int ds = best + n;
+      const int dl = min(max_draft, len - ds);
+      if (dl > 0) {
+        res[0] = n;
+        res[1] = ds;
+        res[2] = dl;
+        done = 1;
+      }
+    }
+    __syncthreads();
+    if (done) return;
+  }
+}
+
+// Greedy acceptance (the T -> 0 limit of lookup.rs:359-403).
+__global__ void k_accept(const uint32_t *__restrict__ am, uint32_t *__restrict__ ctx, int len,
+                         int start, int nd, int *__restrict__ res) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int acc = 0, prod = 0;
+  for (int i = 0; i < nd; ++i) {
+    const uint32_t a = am[i];
+    ctx[len + prod++] = a;
+    if (a != ctx[start + i]) break;
+    ++acc;
+  }
+  if (acc == nd) ctx[len + prod++] = am[nd];
+  res[0] = acc;
+  res[1] = prod;
+}
+
+// --------------------------------------------------------------- MoE --
+
+// route_experts (layers.rs:1808-1870) for one token per block: router dot
+// products (scalar sequential, sum starting at -0.0), max, glibc expf, sum,
+// divide, top-k by strict > (lowest index on ties), optional renormalise.
+__global__ void k_router(const float *__restrict__ x, const float *__restrict__ router, int hidden,
+                         int experts, int topk, int norm_topk, int *__restrict__ sel,
+                         float *__restrict__ wts) {
+  extern __shared__ float probs[];
+  const int t = blockIdx.x;
+  const float *xr = x + (size_t)t * hidden;
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) {
+    const float *rr = router + (size_t)e * hidden;
+    float s = -0.0f;
+    for (int i = 0; i < hidden; ++i) s = s + rr[i] * xr[i];
+    probs[e] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float mx = -INFINITY;
+    for (int e = 0; e < experts; ++e) mx = fmaxf(mx, probs[e]);
+    float sum = 0.0f;
+    for (int e = 0; e < experts; ++e) {
+      const float v = rai_exact::expf_glibc(probs[e] - mx);
+      probs[e] = v;
+      sum = sum + v;
+    }
+    for (int e = 0; e < experts; ++e) probs[e] = __fdiv_exact(probs[e], sum);
+    float total = -0.0f;
+    int cnt = 0;
+    for (int k = 0; k < topk; ++k) {
+      int best = -1;
+      float bv = -INFINITY;
+      for (int e = 0; e < experts; ++e) {
+        bool taken = false;
+        for (int j = 0; j < cnt; ++j) taken |= sel[t * topk + j] == e;
+        if (!taken && probs[e] > bv) {
+          bv = probs[e];
+          best = e;
+        }
+      }
+      if (best < 0) break;
+      sel[t * topk + cnt] = best;
+      wts[t * topk + cnt] = bv;
+      total = total + bv;
+      ++cnt;
+    }
+    for (int k = cnt; k < topk; ++k) {
+      sel[t * topk + k] = -1;
+      wts[t * topk + k] = 0.0f;
+    }
+    if (norm_topk && total > 0.0f)
+      for (int k = 0; k < cnt; ++k) wts[t * topk + k] = __fdiv_exact(wts[t * topk + k], total);
+  }
+}
+
+__global__ void k_moe_acc(float *__restrict__ out, const float *__restrict__ eo,
+                          const float *__restrict__ w, int m, int n) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n || t >= m) return;
+  out[(size_t)t * n + i] = out[(size_t)t * n + i] + w[t] * eo[(size_t)t * n + i];
+}
+
+__global__ void k_fill(float *p, float v, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ launchers --
+
+void launch_quantize(const float *x, int m, int k, int gs, int8_t *q_nat, int8_t *q_split,
+                     float *scales, float *sums, hipStream_t s) {
+  const int groups = (k + gs - 1) / gs;
+  dim3 grid((groups + 63) / 64, m);
+  hipLaunchKernelGGL(k_quantize, grid, dim3(64), 0, s, x, m, k, gs, groups, q_nat,
+                     (k % 8 == 0) ? q_split : nullptr, scales, sums);
+}
+
+bool w4a8_fast_path(int cols, int gs) {
+  return (gs == 32 || gs == 64 || gs == 128) && cols % gs == 0;
+}
+
+void launch_w4a8(float *out, const uint8_t *nib, const uint8_t *params, const float *x,
+                 const int8_t *q_nat, const int8_t *q_split, const float *scales,
+                 const float *sums, int rows, int cols, int m, int gs, hipStream_t s) {
+  const int groups = (cols + gs - 1) / gs;
+  if (w4a8_fast_path(cols, gs)) {
+    if (gs == 32)
+      launch_fast_gs<32>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    else if (gs == 64)
+      launch_fast_gs<64>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    else
+      launch_fast_gs<128>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    return;
+  }
+  dim3 grid((rows + 127) / 128, m);
+  hipLaunchKernelGGL(k_w4a8_simple, grid, dim3(128), 0, s, out, nib, params, x, q_nat, scales,
+                     sums, rows, cols, m, gs, groups);
+}
+
+void launch_lane_sums(int32_t *out, const uint8_t *nib, const int8_t *q_nat, int rows, int cols,
+                      int m, int gs, hipStream_t s) {
+  const int groups = (cols + gs - 1) / gs;
+  dim3 grid((rows * groups + 127) / 128, m);
+  hipLaunchKernelGGL(k_lane_sums, grid, dim3(128), 0, s, out, nib, q_nat, rows, cols, m, gs,
+                     groups);
+}
+
+void launch_tied_lm_head(float *logits, const float *hidden, const uint8_t *codes,
+                         const uint8_t *params, int vocab, int n, int gs, int m, int8_t *hq,
+                         float *hscales, float *hsums, hipStream_t s) {
+  const int groups = (n + gs - 1) / gs;
+  hipLaunchKernelGGL(k_quantize63, dim3((groups + 63) / 64, m), dim3(64), 0, s, hidden, m, n, gs,
+                     groups, hq, hscales, hsums);
+  hipLaunchKernelGGL(k_tied_head, dim3((vocab + 127) / 128, m), dim3(128), 0, s, logits, codes,
+                     params, hq, hscales, hsums, vocab, n, gs, groups, m);
+}
+
+void launch_embed(const uint32_t *tokens, const uint32_t *ctx, int last, int start, int m,
+                  const uint8_t *codes, const uint8_t *params, int vocab, int hidden, int egs,
+                  float embed_scale, float *out, int *err, hipStream_t s) {
+  const int egroups = (hidden + egs - 1) / egs;
+  hipLaunchKernelGGL(k_embed, dim3(m), dim3(256), 0, s, tokens, ctx, last, start, codes, params,
+                     vocab, hidden, egs, egroups, embed_scale, out, err);
+}
+
+void launch_rmsnorm(const float *x, const float *w, float *out, float *resid, int m, int n,
+                    float eps, hipStream_t s) {
+  hipLaunchKernelGGL(k_rmsnorm, dim3(m), dim3(64), 0, s, x, w, out, resid, n, eps);
+}
+
+void launch_vec_add(float *h, const float *r, const float *a, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(k_vec_add, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, h, r, a, n);
+}
+
+void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s) {
+  hipLaunchKernelGGL(k_silu_mul, dim3((n + 255) / 256, m), dim3(256), 0, s, gate, up, m, n);
+}
+
+void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
+                       int pos0, int m, int nh, int nkv, int hd, float *kc, float *vc, int cap,
+                       hipStream_t s) {
+  hipLaunchKernelGGL(k_rope_store, dim3(m), dim3(256), 0, s, q, k, v, cos_t, sin_t, pos0, nh, nkv,
+                     hd, kc, vc, cap);
+}
+
+void launch_attention(const float *q, const float *kc, const float *vc, int cap, int pos0, int m,
+                      int nh, int nkv, int hd, float scale, float *out, hipStream_t s) {
+  const size_t smem = sizeof(float) * (size_t)(pos0 + m);
+  static size_t configured = 0;
+  if (smem > 48 * 1024 && smem > configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attention),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = smem;
+  }
+  hipLaunchKernelGGL(k_attention, dim3(nh, m), dim3(256), smem, s, q, kc, vc, cap, pos0, nh, nkv,
+                     hd, scale, out);
+}
+
+void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,
+                       hipStream_t s) {
+  hipLaunchKernelGGL(k_rope_apply, dim3(1), dim3(256), 0, s, heads, nh, hd, cos_row, sin_row);
+}
+
+void launch_argmax(const float *logits, int m, int vocab, uint32_t *out, hipStream_t s) {
+  hipLaunchKernelGGL(k_argmax, dim3(m), dim3(1024), 0, s, logits, vocab, out);
+}
+
+void launch_ngram(const uint32_t *ctx, int len, int min_n, int max_n, int max_draft, int *res,
+                  hipStream_t s) {
+  hipLaunchKernelGGL(k_ngram, dim3(1), dim3(1024), 0, s, ctx, len, min_n, max_n, max_draft, res);
+}
+
+void launch_accept(const uint32_t *am, uint32_t *ctx, int len, int start, int nd, int *res2,
+                   hipStream_t s) {
+  hipLaunchKernelGGL(k_accept, dim3(1), dim3(64), 0, s, am, ctx, len, start, nd, res2);
+}
+
+void launch_router(const float *x, const float *router, int m, int hidden, int experts, int topk,
+                   int norm_topk, int *sel, float *wts, hipStream_t s) {
+  hipLaunchKernelGGL(k_router, dim3(m), dim3(64), sizeof(float) * experts, s, x, router, hidden,
+                     experts, topk, norm_topk, sel, wts);
+}
+
+void launch_moe_accumulate(float *out, const float *eo, const float *w, int m, int n,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(k_moe_acc, dim3((n + 255) / 256, m), dim3(256), 0, s, out, eo, w, m, n);
+}
+
+void launch_fill(float *p, float v, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(k_fill, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, v, n);
+}
+
+}  // namespace rai

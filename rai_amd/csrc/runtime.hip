@@ -1,0 +1,1088 @@
+// Host runtime and C ABI: device model, KV cache, forward passes, the
+// prompt-lookup decoder.  Mirrors rai-infer/src/{model,kv_cache,lookup}.rs.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "format.h"
+#include "kernels.h"
+
+namespace rai {
+
+static thread_local std::string g_last_error;
+void set_last_error(const std::string &m) { g_last_error = m; }
+
+#define HIP_CHECK(expr)                                                                  \
+  do {                                                                                   \
+    hipError_t e_ = (expr);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      fail(e_ == hipErrorOutOfMemory ? RAI_E_OOM : RAI_E_HIP,                            \
+           std::string(#expr) + ": " + hipGetErrorString(e_));                           \
+  } while (0)
+
+// Largest attention context the LDS-resident score buffer handles.
+constexpr size_t kMaxAttnContext = 16384;
+// Tokens per forward chunk (prefill is split into chunks of this size; the
+// per-token arithmetic does not depend on the split).
+constexpr int kChunk = 256;
+
+struct DevBuf {
+  void *p = nullptr;
+  DevBuf() = default;
+  DevBuf(const DevBuf &) = delete;
+  DevBuf &operator=(const DevBuf &) = delete;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  void alloc(size_t n) {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    if (n == 0) n = 256;
+    HIP_CHECK(hipMalloc(&p, n));
+  }
+  template <class T>
+  T *as() const {
+    return reinterpret_cast<T *>(p);
+  }
+};
+
+struct DLinear {
+  int rows = 0, cols = 0, gs = 0;
+  const uint8_t *nib = nullptr, *params = nullptr;
+};
+
+struct DLayer {
+  DLinear lin[7];
+  std::vector<DLinear> experts;  // all experts, 3 linears each (expert 0 = lin[4..6])
+  const float *router = nullptr;
+  const float *in_norm = nullptr, *post_norm = nullptr;
+};
+
+struct Workspace;
+
+}  // namespace rai
+
+using namespace rai;
+
+struct rai_model {
+  rai_model_config cfg{};
+  ModelView view;
+  DevBuf arena;
+  std::vector<DLayer> layers;
+  const uint8_t *emb_params = nullptr, *emb_codes = nullptr;
+  const float *final_norm = nullptr;
+  DLinear lm_head;
+  bool tied = false;
+  const float *rope_cos = nullptr, *rope_sin = nullptr;
+  float attn_scale = 1.0f;
+  uint64_t weight_bytes = 0;
+  hipStream_t stream = nullptr;
+  std::unique_ptr<Workspace> ws;  // for the model-level host-buffer API
+  ~rai_model();
+};
+
+struct rai_kv {
+  rai_model *model = nullptr;
+  int layers = 0, nkv = 0, hd = 0;
+  size_t cap = 0;
+  DevBuf k, v;  // [layer][nkv][cap][hd]
+  std::vector<size_t> filled;
+  float *kc(int l) const { return k.as<float>() + (size_t)l * nkv * cap * hd; }
+  float *vc(int l) const { return v.as<float>() + (size_t)l * nkv * cap * hd; }
+};
+
+namespace rai {
+
+// Per-context scratch for up to `maxm` tokens.
+struct Workspace {
+  int maxm = 0;
+  DevBuf hid, normed, resid, qb, kb, vb, att, ob, gb, ub, mo, logits, am;
+  DevBuf q_nat, q_split, qscale, qsum, hq;
+  DevBuf err;
+  // MoE
+  DevBuf sel, wts, eo, xg, yg, gg, ug, idx, wcol;
+  int logit_rows = 0;
+  void init(const rai_model &m, int maxm_, int logit_rows_) {
+    const rai_model_config &c = m.cfg;
+    maxm = maxm_;
+    logit_rows = logit_rows_;
+    const size_t H = c.hidden_size, F = c.intermediate_size, qd = (size_t)c.num_heads * c.head_dim;
+    const size_t kvd = (size_t)c.num_kv_heads * c.head_dim, V = c.vocab_size;
+    const size_t K = std::max(std::max(H, F), qd);
+    const size_t G = ceil_div(K, std::min(c.group_size, c.embed_group_size)) + 1;
+    auto f = [&](DevBuf &b, size_t n) { b.alloc(n * sizeof(float) * maxm); };
+    f(hid, H);
+    f(normed, H);
+    f(resid, H);
+    f(qb, qd);
+    f(kb, kvd);
+    f(vb, kvd);
+    f(att, qd);
+    f(ob, H);
+    f(gb, F);
+    f(ub, F);
+    f(mo, H);
+    logits.alloc(sizeof(float) * V * std::max(1, logit_rows));
+    am.alloc(sizeof(uint32_t) * maxm);
+    q_nat.alloc(K * maxm);
+    q_split.alloc(K * maxm);
+    hq.alloc(H * maxm);
+    qscale.alloc(sizeof(float) * G * maxm);
+    qsum.alloc(sizeof(float) * G * maxm);
+    err.alloc(sizeof(int) * 4);
+    HIP_CHECK(hipMemset(err.p, 0, sizeof(int) * 4));
+    if (c.num_experts > 0) {
+      sel.alloc(sizeof(int) * maxm * c.experts_per_token);
+      wts.alloc(sizeof(float) * maxm * c.experts_per_token);
+      eo.alloc(sizeof(float) * maxm * c.experts_per_token * H);
+      xg.alloc(sizeof(float) * maxm * H);
+      yg.alloc(sizeof(float) * maxm * H);
+      gg.alloc(sizeof(float) * maxm * F);
+      ug.alloc(sizeof(float) * maxm * F);
+      idx.alloc(sizeof(int) * maxm * c.experts_per_token);
+      wcol.alloc(sizeof(float) * maxm);
+    }
+  }
+};
+
+}  // namespace rai
+
+rai_model::~rai_model() {
+  ws.reset();
+  if (stream) (void)hipStreamDestroy(stream);
+}
+
+namespace rai {
+
+// ------------------------------------------------------------- loading --
+
+static void upload_model(rai_model &m, const uint8_t *img, size_t len, int max_groups) {
+  m.view = parse_model(img, len, max_groups);
+  const ModelView &v = m.view;
+  m.cfg = v.cfg;
+  m.tied = v.tied;
+  m.attn_scale = v.attention_scale;
+  const rai_model_config &c = m.cfg;
+  if (c.max_context == 0) fail(RAI_E_FORMAT, "max_context is zero");
+  // Arena layout: every piece 256-byte aligned, in the reference's byte layout.
+  struct Piece {
+    size_t src, len, dst;
+  };
+  std::vector<Piece> pieces;
+  size_t total = 0;
+  auto add = [&](size_t src, size_t n) {
+    total = (total + 255) & ~size_t(255);
+    pieces.push_back({src, n, total});
+    total += n;
+    return pieces.size() - 1;
+  };
+  const size_t H = c.hidden_size;
+  const size_t eg = ceil_div(H, c.embed_group_size);
+  const size_t pe = add(v.emb_params_off, (size_t)c.vocab_size * eg * 4);
+  const size_t ce = add(v.emb_codes_off, (size_t)c.vocab_size * H);
+  struct LinIdx {
+    size_t p, n;
+  };
+  std::vector<std::vector<LinIdx>> lidx(c.num_layers);
+  std::vector<size_t> router_idx(c.num_layers), n1_idx(c.num_layers), n2_idx(c.num_layers);
+  uint64_t wbytes = 0;
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    const LayerView &L = v.layers[l];
+    for (int p = 0; p < 7; ++p) {
+      lidx[l].push_back({add(L.lin[p].params_off, L.lin[p].params_len), add(L.lin[p].nib_off, L.lin[p].nib_len)});
+      wbytes += L.lin[p].params_len + L.lin[p].nib_len;
+    }
+    for (const LinearView &e : L.experts) lidx[l].push_back({add(e.params_off, e.params_len), add(e.nib_off, e.nib_len)});
+    if (c.num_experts > 0) router_idx[l] = add(L.router_off, (size_t)c.num_experts * H * 4);
+    n1_idx[l] = add(L.in_norm_off, H * 4);
+    n2_idx[l] = add(L.post_norm_off, H * 4);
+  }
+  const size_t fn = add(v.final_norm_off, H * 4);
+  size_t lmp = 0, lmn = 0;
+  if (!m.tied) {
+    lmp = add(v.lm_head.params_off, v.lm_head.params_len);
+    lmn = add(v.lm_head.nib_off, v.lm_head.nib_len);
+    wbytes += v.lm_head.params_len + v.lm_head.nib_len;
+  } else {
+    wbytes += (size_t)c.vocab_size * (H + eg * 4);
+  }
+  // RoPE tables: RoPETable::with_scaling (layers.rs:561-633) on the host with
+  // the C library's powf/cosf/sinf, exactly as the reference computes them.
+  const size_t half = c.head_dim / 2;
+  std::vector<float> cosv((size_t)c.max_context * half), sinv((size_t)c.max_context * half);
+  {
+    std::vector<float> inv(half);
+    for (size_t i = 0; i < half; ++i)
+      inv[i] = 1.0f / std::pow(c.rope_theta, (2.0f * (float)i) / (float)c.head_dim);
+    for (size_t p = 0; p < c.max_context; ++p)
+      for (size_t i = 0; i < half; ++i) {
+        const float ang = (float)p * inv[i];
+        cosv[p * half + i] = std::cos(ang);
+        sinv[p * half + i] = std::sin(ang);
+      }
+  }
+  total = (total + 255) & ~size_t(255);
+  const size_t rope_off = total;
+  total += 2 * cosv.size() * sizeof(float) + 256;
+  m.arena.alloc(total);
+  uint8_t *base = m.arena.as<uint8_t>();
+  // Stage through a pinned buffer in 64 MiB slices.
+  const size_t slice = 64ull << 20;
+  uint8_t *pin = nullptr;
+  HIP_CHECK(hipHostMalloc((void **)&pin, slice, hipHostMallocDefault));
+  try {
+    for (const Piece &pc : pieces) {
+      for (size_t o = 0; o < pc.len; o += slice) {
+        const size_t n = std::min(slice, pc.len - o);
+        std::memcpy(pin, img + pc.src + o, n);
+        HIP_CHECK(hipMemcpy(base + pc.dst + o, pin, n, hipMemcpyHostToDevice));
+      }
+    }
+  } catch (...) {
+    (void)hipHostFree(pin);
+    throw;
+  }
+  HIP_CHECK(hipHostFree(pin));
+  HIP_CHECK(hipMemcpy(base + rope_off, cosv.data(), cosv.size() * 4, hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(base + rope_off + cosv.size() * 4, sinv.data(), sinv.size() * 4,
+                      hipMemcpyHostToDevice));
+  m.rope_cos = reinterpret_cast<const float *>(base + rope_off);
+  m.rope_sin = reinterpret_cast<const float *>(base + rope_off + cosv.size() * 4);
+  m.emb_params = base + pieces[pe].dst;
+  m.emb_codes = base + pieces[ce].dst;
+  const int qd = c.num_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
+  const int dims[7][2] = {{qd, (int)H}, {kvd, (int)H}, {kvd, (int)H}, {(int)H, qd},
+                          {(int)c.intermediate_size, (int)H}, {(int)c.intermediate_size, (int)H},
+                          {(int)H, (int)c.intermediate_size}};
+  m.layers.resize(c.num_layers);
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    DLayer &D = m.layers[l];
+    auto mk = [&](size_t k, int p) {
+      DLinear d;
+      d.rows = dims[p][0];
+      d.cols = dims[p][1];
+      d.gs = c.group_size;
+      d.params = base + pieces[lidx[l][k].p].dst;
+      d.nib = base + pieces[lidx[l][k].n].dst;
+      return d;
+    };
+    for (int p = 0; p < 7; ++p) D.lin[p] = mk(p, p);
+    if (c.num_experts > 0) {
+      D.experts.push_back(D.lin[4]);
+      D.experts.push_back(D.lin[5]);
+      D.experts.push_back(D.lin[6]);
+      for (size_t k = 7; k < lidx[l].size(); ++k) D.experts.push_back(mk(k, 4 + (int)((k - 7) % 3)));
+      D.router = reinterpret_cast<const float *>(base + pieces[router_idx[l]].dst);
+      // Expert bytes a decode step streams: experts_per_token of them.
+      wbytes += (uint64_t)(c.experts_per_token - 1) *
+                (v.layers[l].lin[4].params_len + v.layers[l].lin[4].nib_len +
+                 v.layers[l].lin[5].params_len + v.layers[l].lin[5].nib_len +
+                 v.layers[l].lin[6].params_len + v.layers[l].lin[6].nib_len);
+    }
+    D.in_norm = reinterpret_cast<const float *>(base + pieces[n1_idx[l]].dst);
+    D.post_norm = reinterpret_cast<const float *>(base + pieces[n2_idx[l]].dst);
+  }
+  m.final_norm = reinterpret_cast<const float *>(base + pieces[fn].dst);
+  if (!m.tied) {
+    m.lm_head.rows = c.vocab_size;
+    m.lm_head.cols = H;
+    m.lm_head.gs = c.group_size;
+    m.lm_head.params = base + pieces[lmp].dst;
+    m.lm_head.nib = base + pieces[lmn].dst;
+  }
+  m.weight_bytes = wbytes;
+  HIP_CHECK(hipStreamCreateWithFlags(&m.stream, hipStreamNonBlocking));
+}
+
+// ------------------------------------------------------------- forward --
+
+static void linear(const DLinear &L, const float *x, const Workspace &w, float *out, int m,
+                   hipStream_t s) {
+  launch_w4a8(out, L.nib, L.params, x, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
+              w.qscale.as<float>(), w.qsum.as<float>(), L.rows, L.cols, m, L.gs, s);
+}
+
+static void quantize(const rai_model &md, const float *x, int m, int k, const Workspace &w,
+                     hipStream_t s) {
+  launch_quantize(x, m, k, md.cfg.group_size, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
+                  w.qscale.as<float>(), w.qsum.as<float>(), s);
+}
+
+// The MLP of a sparse layer: mlp_block's MoE arm (model.rs:208-261) for
+// every token, grouping each expert's tokens into one GEMV batch (each
+// token's arithmetic is the M = 1 arithmetic: matmul == matvec).
+static void moe_block(const rai_model &md, const DLayer &L, Workspace &w, int m, hipStream_t s) {
+  const rai_model_config &c = md.cfg;
+  const int H = c.hidden_size, F = c.intermediate_size, E = c.num_experts, K = c.experts_per_token;
+  launch_router(w.normed.as<float>(), L.router, m, H, E, K, c.norm_topk_prob, w.sel.as<int>(),
+                w.wts.as<float>(), s);
+  std::vector<int> sel((size_t)m * K);
+  HIP_CHECK(hipMemcpyAsync(sel.data(), w.sel.p, sel.size() * sizeof(int), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  std::vector<std::vector<int>> tok(E), slot(E);
+  for (int t = 0; t < m; ++t)
+    for (int k = 0; k < K; ++k)
+      if (sel[(size_t)t * K + k] >= 0) {
+        tok[sel[(size_t)t * K + k]].push_back(t);
+        slot[sel[(size_t)t * K + k]].push_back(k);
+      }
+  float *eo = w.eo.as<float>();
+  for (int e = 0; e < E; ++e) {
+    const int me = (int)tok[e].size();
+    if (me == 0) continue;
+    for (int i = 0; i < me; ++i)
+      HIP_CHECK(hipMemcpyAsync(w.xg.as<float>() + (size_t)i * H, w.normed.as<float>() + (size_t)tok[e][i] * H,
+                               sizeof(float) * H, hipMemcpyDeviceToDevice, s));
+    const DLinear *ex = &L.experts[(size_t)e * 3];
+    quantize(md, w.xg.as<float>(), me, H, w, s);
+    linear(ex[0], w.xg.as<float>(), w, w.gg.as<float>(), me, s);
+    linear(ex[1], w.xg.as<float>(), w, w.ug.as<float>(), me, s);
+    launch_silu_mul(w.gg.as<float>(), w.ug.as<float>(), me, F, s);
+    quantize(md, w.gg.as<float>(), me, F, w, s);
+    linear(ex[2], w.gg.as<float>(), w, w.yg.as<float>(), me, s);
+    for (int i = 0; i < me; ++i)
+      HIP_CHECK(hipMemcpyAsync(eo + ((size_t)tok[e][i] * K + slot[e][i]) * H, w.yg.as<float>() + (size_t)i * H,
+                               sizeof(float) * H, hipMemcpyDeviceToDevice, s));
+  }
+  // output.fill(0) then out += weight * value in selection order.
+  launch_fill(w.mo.as<float>(), 0.0f, (size_t)m * H, s);
+  std::vector<float> wt((size_t)m * K);
+  HIP_CHECK(hipMemcpyAsync(wt.data(), w.wts.p, wt.size() * sizeof(float), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  for (int k = 0; k < K; ++k) {
+    // Gather slot k of every token into contiguous rows, then accumulate.
+    std::vector<float> col(m);
+    for (int t = 0; t < m; ++t) col[t] = sel[(size_t)t * K + k] >= 0 ? wt[(size_t)t * K + k] : 0.0f;
+    HIP_CHECK(hipMemcpyAsync(w.wcol.p, col.data(), sizeof(float) * m, hipMemcpyHostToDevice, s));
+    for (int t = 0; t < m; ++t)
+      HIP_CHECK(hipMemcpyAsync(w.yg.as<float>() + (size_t)t * H, eo + ((size_t)t * K + k) * H, sizeof(float) * H,
+                               hipMemcpyDeviceToDevice, s));
+    bool any = false;
+    for (int t = 0; t < m; ++t) any |= sel[(size_t)t * K + k] >= 0;
+    if (any) launch_moe_accumulate(w.mo.as<float>(), w.yg.as<float>(), w.wcol.as<float>(), m, H, s);
+    HIP_CHECK(hipStreamSynchronize(s));  // `col` is reused next iteration
+  }
+}
+
+// forward_batch (model.rs:692-963) for m tokens at positions pos0.. whose
+// hidden states are in w.hid; updates the KV watermark.
+static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0, hipStream_t s) {
+  const rai_model_config &c = md.cfg;
+  const int H = c.hidden_size, F = c.intermediate_size, hd = c.head_dim;
+  const int nh = c.num_heads, nkv = c.num_kv_heads, qd = nh * hd;
+  if (m <= 0 || m > w.maxm) fail(RAI_E_SHAPE, "batch size exceeds the workspace");
+  if (pos0 + m > c.max_context || pos0 + m > kv.cap) fail(RAI_E_RANGE, "batch position exceeds model context");
+  if (pos0 + m > kMaxAttnContext) fail(RAI_E_UNSUPPORTED, "context beyond 16384 positions is not supported");
+  for (int l = 0; l < kv.layers; ++l)
+    if (pos0 > kv.filled[l])
+      fail(RAI_E_WATERMARK, "KV store at position " + std::to_string(pos0) + " would leave a gap (filled " +
+                                std::to_string(kv.filled[l]) + ")");
+  float *hid = w.hid.as<float>(), *normed = w.normed.as<float>(), *resid = w.resid.as<float>();
+  for (int li = 0; li < (int)c.num_layers; ++li) {
+    const DLayer &L = md.layers[li];
+    launch_rmsnorm(hid, L.in_norm, normed, resid, m, H, c.norm_eps, s);
+    quantize(md, normed, m, H, w, s);
+    linear(L.lin[0], normed, w, w.qb.as<float>(), m, s);
+    linear(L.lin[1], normed, w, w.kb.as<float>(), m, s);
+    linear(L.lin[2], normed, w, w.vb.as<float>(), m, s);
+    launch_rope_store(w.qb.as<float>(), w.kb.as<float>(), w.vb.as<float>(), md.rope_cos, md.rope_sin, (int)pos0,
+                      m, nh, nkv, hd, kv.kc(li), kv.vc(li), (int)kv.cap, s);
+    launch_attention(w.qb.as<float>(), kv.kc(li), kv.vc(li), (int)kv.cap, (int)pos0, m, nh, nkv, hd,
+                     md.attn_scale, w.att.as<float>(), s);
+    quantize(md, w.att.as<float>(), m, qd, w, s);
+    linear(L.lin[3], w.att.as<float>(), w, w.ob.as<float>(), m, s);
+    launch_vec_add(hid, resid, w.ob.as<float>(), (size_t)m * H, s);
+    launch_rmsnorm(hid, L.post_norm, normed, resid, m, H, c.norm_eps, s);
+    if (c.num_experts > 0) {
+      moe_block(md, L, w, m, s);
+    } else {
+      quantize(md, normed, m, H, w, s);
+      linear(L.lin[4], normed, w, w.gb.as<float>(), m, s);
+      linear(L.lin[5], normed, w, w.ub.as<float>(), m, s);
+      launch_silu_mul(w.gb.as<float>(), w.ub.as<float>(), m, F, s);
+      quantize(md, w.gb.as<float>(), m, F, w, s);
+      linear(L.lin[6], w.gb.as<float>(), w, w.mo.as<float>(), m, s);
+    }
+    launch_vec_add(hid, resid, w.mo.as<float>(), (size_t)m * H, s);
+  }
+  for (int l = 0; l < kv.layers; ++l) kv.filled[l] = std::max(kv.filled[l], pos0 + m);
+}
+
+// hidden_to_logits_batch (model.rs:966-1033) for the m rows of w.hid.
+static void logits(rai_model &md, Workspace &w, int m, hipStream_t s) {
+  const rai_model_config &c = md.cfg;
+  const int H = c.hidden_size, V = c.vocab_size;
+  if (m > w.logit_rows) fail(RAI_E_SHAPE, "logit rows exceed the workspace");
+  launch_rmsnorm(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), nullptr, m, H, c.norm_eps, s);
+  if (!md.tied) {
+    quantize(md, w.normed.as<float>(), m, H, w, s);
+    linear(md.lm_head, w.normed.as<float>(), w, w.logits.as<float>(), m, s);
+  } else {
+    launch_tied_lm_head(w.logits.as<float>(), w.normed.as<float>(), md.emb_codes, md.emb_params, V, H,
+                        c.embed_group_size, m, w.hq.as<int8_t>(), w.qscale.as<float>(), w.qsum.as<float>(), s);
+  }
+}
+
+static void check_tokens(const rai_model &md, const uint32_t *t, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    if (t[i] >= md.cfg.vocab_size) fail(RAI_E_RANGE, "token id is out of model vocabulary");
+}
+
+static void embed_tokens(rai_model &md, Workspace &w, const uint32_t *dev_tokens, int m, hipStream_t s) {
+  const rai_model_config &c = md.cfg;
+  launch_embed(dev_tokens, nullptr, 0, 0, m, md.emb_codes, md.emb_params, c.vocab_size, c.hidden_size,
+               c.embed_group_size, c.embed_scale, w.hid.as<float>(), w.err.as<int>(), s);
+}
+
+static void check_kernel_error(Workspace &w, hipStream_t s) {
+  int e = 0;
+  HIP_CHECK(hipMemcpyAsync(&e, w.err.p, sizeof(int), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  if (e) {
+    HIP_CHECK(hipMemsetAsync(w.err.p, 0, sizeof(int), s));
+    fail(RAI_E_RANGE, "token id is out of model vocabulary");
+  }
+}
+
+Workspace &model_ws(rai_model &m) {
+  if (!m.ws) {
+    m.ws = std::make_unique<Workspace>();
+    m.ws->init(m, kChunk, 64);
+  }
+  return *m.ws;
+}
+
+}  // namespace rai
+
+// -------------------------------------------------------- lookup decoder --
+
+struct rai_lookup {
+  rai_model *model = nullptr;
+  rai_kv kv;
+  size_t max_ctx = 0;
+  rai::Workspace ws;
+  DevBuf ctx;             // device context [max_ctx + 64]
+  std::vector<uint32_t> ctx_host;  // mirror of ctx[0..ctx_len)
+  size_t ctx_len = 0;
+  DevBuf res;             // int[8]: ngram result + accept result
+  int *pin = nullptr;     // pinned host mirror of res + tokens
+  hipStream_t stream = nullptr;
+  ~rai_lookup() {
+    if (pin) (void)hipHostFree(pin);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+namespace rai {
+
+static void kv_init(rai_kv &kv, rai_model &m, size_t max_ctx) {
+  const rai_model_config &c = m.cfg;
+  if (max_ctx == 0) fail(RAI_E_ARG, "KV cache context must be non-zero");
+  kv.model = &m;
+  kv.layers = c.num_layers;
+  kv.nkv = c.num_kv_heads;
+  kv.hd = c.head_dim;
+  kv.cap = std::min<size_t>(max_ctx, c.max_context);
+  const size_t bytes = (size_t)kv.layers * kv.nkv * kv.cap * kv.hd * sizeof(float);
+  kv.k.alloc(bytes);
+  kv.v.alloc(bytes);
+  HIP_CHECK(hipMemset(kv.k.p, 0, bytes));
+  HIP_CHECK(hipMemset(kv.v.p, 0, bytes));
+  kv.filled.assign(kv.layers, 0);
+}
+
+// Bring the device context in line with the caller's host context: only the
+// suffix that differs from the device copy is uploaded.
+static void sync_context(rai_lookup &d, const uint32_t *ctx, size_t len) {
+  if (len > d.max_ctx) fail(RAI_E_RANGE, "context exceeds the prompt-lookup window");
+  size_t same = 0;
+  const size_t lim = std::min(len, d.ctx_len);
+  while (same < lim && d.ctx_host[same] == ctx[same]) ++same;
+  if (same < len) {
+    check_tokens(*d.model, ctx + same, len - same);
+    HIP_CHECK(hipMemcpyAsync(d.ctx.as<uint32_t>() + same, ctx + same, (len - same) * sizeof(uint32_t),
+                             hipMemcpyHostToDevice, d.stream));
+    std::copy(ctx + same, ctx + len, d.ctx_host.begin() + same);
+  }
+  d.ctx_len = len;
+}
+
+// One decode step: LookupDecoder::step (lookup.rs:260-425) in greedy mode.
+static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size_t len,
+                        const rai_lookup_config &cfg, uint32_t *out, size_t cap, rai_lookup_metrics &met) {
+  rai_model &md = *d.model;
+  const rai_model_config &c = md.cfg;
+  // validate_lookup_config (lookup.rs:457-475), greedy variant.
+  if (cfg.max_draft == 0) fail(RAI_E_ARG, "prompt-lookup max_draft must be non-zero");
+  if (cfg.min_ngram < 1 || cfg.min_ngram > cfg.max_ngram)
+    fail(RAI_E_ARG, "prompt-lookup requires 1 <= min_ngram <= max_ngram");
+  if (!(cfg.temperature <= 1e-6f))
+    fail(RAI_E_UNSUPPORTED, "sampled acceptance (temperature > 0) is not implemented; use greedy");
+  // The device context keeps 64 slots past max_ctx for the accepted tokens
+  // and the workspace holds 64 logit rows: the verify batch is at most 64.
+  if (cfg.max_draft > 63) fail(RAI_E_ARG, "max_draft above 63 is not supported");
+  if (len == 0) fail(RAI_E_ARG, "prompt-lookup step requires a non-empty context");
+  if (pos >= d.max_ctx) fail(RAI_E_RANGE, "decode position exceeds the context window");
+  if (cap < cfg.max_draft + 1) fail(RAI_E_SHAPE, "output buffer must hold max_draft + 1 tokens");
+  if (len > d.max_ctx) fail(RAI_E_RANGE, "context exceeds the prompt-lookup window");
+  sync_context(d, context, len);
+  hipStream_t s = d.stream;
+  const size_t budget = d.max_ctx > pos + 1 ? d.max_ctx - pos - 1 : 0;
+  int *res = d.res.as<int>();
+  int nd = 0, start = 0, ngram = 0;
+  if (budget > 0) {
+    launch_ngram(d.ctx.as<uint32_t>(), (int)len, (int)cfg.min_ngram, (int)cfg.max_ngram,
+                 (int)std::min(cfg.max_draft, budget), res, s);
+    HIP_CHECK(hipMemcpyAsync(d.pin, res, 3 * sizeof(int), hipMemcpyDeviceToHost, s));
+    HIP_CHECK(hipStreamSynchronize(s));
+    ngram = d.pin[0];
+    start = d.pin[1];
+    nd = ngram ? d.pin[2] : 0;
+  }
+  const int m = nd + 1;  // verify [last, draft...] or the single decode_one token
+  launch_embed(nullptr, d.ctx.as<uint32_t>(), (int)len - 1, start, m, md.emb_codes, md.emb_params, c.vocab_size,
+               c.hidden_size, c.embed_group_size, c.embed_scale, d.ws.hid.as<float>(), d.ws.err.as<int>(), s);
+  forward(md, d.kv, d.ws, m, pos, s);
+  logits(md, d.ws, m, s);
+  launch_argmax(d.ws.logits.as<float>(), m, c.vocab_size, d.ws.am.as<uint32_t>(), s);
+  launch_accept(d.ws.am.as<uint32_t>(), d.ctx.as<uint32_t>(), (int)len, start, nd, res + 4, s);
+  HIP_CHECK(hipMemcpyAsync(d.pin + 4, res + 4, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipMemcpyAsync(d.pin + 8, d.ctx.as<uint32_t>() + len, (size_t)m * sizeof(uint32_t),
+                           hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  int kerr = 0;
+  HIP_CHECK(hipMemcpy(&kerr, d.ws.err.p, sizeof(int), hipMemcpyDeviceToHost));
+  if (kerr) {
+    HIP_CHECK(hipMemset(d.ws.err.p, 0, sizeof(int)));
+    fail(RAI_E_RANGE, "context contains a token outside the model vocabulary");
+  }
+  const int acc = d.pin[4], prod = d.pin[5];
+  for (int i = 0; i < prod; ++i) out[i] = (uint32_t)d.pin[8 + i];
+  // The accept kernel already appended the produced tokens to the device
+  // context; mirror that so the caller's extended context needs no upload.
+  for (int i = 0; i < prod; ++i) d.ctx_host[len + i] = out[i];
+  d.ctx_len = len + prod;
+  // kv_cache.truncate(pos + produced) (lookup.rs:411).
+  for (auto &f : d.kv.filled) f = std::min(f, pos + (size_t)prod);
+  met.accepted = nd ? acc : 0;
+  met.drafted = nd;
+  met.produced = prod;
+  met.matched_ngram = ngram;
+  met.accept_rate = nd ? (float)acc / (float)nd : 0.0f;
+}
+
+static void lookup_prefill(rai_lookup &d, const uint32_t *prompt, size_t n, size_t &pos_out) {
+  rai_model &md = *d.model;
+  if (n == 0) fail(RAI_E_ARG, "prompt must contain at least one token");
+  if (n > d.max_ctx) fail(RAI_E_RANGE, "prompt exceeds the prompt-lookup context window");
+  check_tokens(md, prompt, n);
+  sync_context(d, prompt, n);
+  const size_t cnt = n - 1;
+  for (size_t p = 0; p < cnt; p += kChunk) {
+    const int m = (int)std::min<size_t>(kChunk, cnt - p);
+    launch_embed(d.ctx.as<uint32_t>() + p, nullptr, 0, 0, m, md.emb_codes, md.emb_params, md.cfg.vocab_size,
+                 md.cfg.hidden_size, md.cfg.embed_group_size, md.cfg.embed_scale, d.ws.hid.as<float>(),
+                 d.ws.err.as<int>(), d.stream);
+    forward(md, d.kv, d.ws, m, p, d.stream);
+  }
+  HIP_CHECK(hipStreamSynchronize(d.stream));
+  pos_out = cnt;
+}
+
+}  // namespace rai
+
+// ================================================================ C ABI ==
+
+extern "C" {
+
+const char *rai_last_error(void) { return rai::g_last_error.c_str(); }
+
+int rai_device_info(char *name, size_t name_len, int *cus) {
+  RAI_API_BODY({
+    hipDeviceProp_t p;
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    HIP_CHECK(hipGetDeviceProperties(&p, dev));
+    if (name && name_len) {
+      std::snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+    }
+    if (cus) *cus = p.multiProcessorCount;
+  });
+}
+
+int rai_model_from_buffer(const void *data, size_t len, int max_groups, rai_model **out) {
+  RAI_API_BODY({
+    if (!data || !out) rai::fail(RAI_E_ARG, "null argument");
+    auto m = std::make_unique<rai_model>();
+    rai::upload_model(*m, (const uint8_t *)data, len, max_groups);
+    *out = m.release();
+  });
+}
+
+int rai_model_open(const char *path, int max_groups, rai_model **out) {
+  RAI_API_BODY({
+    if (!path || !out) rai::fail(RAI_E_ARG, "null argument");
+    std::ifstream f(path, std::ios::binary | std::ios::ate);
+    if (!f) rai::fail(RAI_E_IO, std::string("opening ") + path);
+    const std::streamsize n = f.tellg();
+    if (n < 0) rai::fail(RAI_E_IO, std::string("stat ") + path);
+    if ((uint64_t)n > (64ull << 30)) rai::fail(RAI_E_FORMAT, "model file is too large");
+    std::vector<uint8_t> buf((size_t)n);
+    f.seekg(0);
+    if (!f.read((char *)buf.data(), n)) rai::fail(RAI_E_IO, std::string("reading ") + path);
+    auto m = std::make_unique<rai_model>();
+    rai::upload_model(*m, buf.data(), buf.size(), max_groups);
+    *out = m.release();
+  });
+}
+
+void rai_model_free(rai_model *m) { delete m; }
+
+int rai_model_get_config(const rai_model *m, rai_model_config *out) {
+  RAI_API_BODY({
+    if (!m || !out) rai::fail(RAI_E_ARG, "null argument");
+    *out = m->cfg;
+  });
+}
+
+int rai_model_weight_bytes(const rai_model *m, uint64_t *out) {
+  RAI_API_BODY({
+    if (!m || !out) rai::fail(RAI_E_ARG, "null argument");
+    *out = m->weight_bytes;
+  });
+}
+
+int rai_kv_create(rai_model *m, size_t max_ctx, rai_kv **out) {
+  RAI_API_BODY({
+    if (!m || !out) rai::fail(RAI_E_ARG, "null argument");
+    auto kv = std::make_unique<rai_kv>();
+    rai::kv_init(*kv, *m, max_ctx);
+    *out = kv.release();
+  });
+}
+
+void rai_kv_free(rai_kv *kv) { delete kv; }
+
+int rai_kv_truncate(rai_kv *kv, size_t len) {
+  RAI_API_BODY({
+    if (!kv) rai::fail(RAI_E_ARG, "null argument");
+    for (auto &f : kv->filled) f = std::min(f, len);
+  });
+}
+
+int rai_kv_filled(const rai_kv *kv, size_t layer, size_t *out) {
+  RAI_API_BODY({
+    if (!kv || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (layer >= kv->filled.size()) rai::fail(RAI_E_ARG, "layer index out of range");
+    *out = kv->filled[layer];
+  });
+}
+
+int rai_kv_clear(rai_kv *kv) {
+  RAI_API_BODY({
+    if (!kv) rai::fail(RAI_E_ARG, "null argument");
+    const size_t bytes = (size_t)kv->layers * kv->nkv * kv->cap * kv->hd * sizeof(float);
+    HIP_CHECK(hipMemset(kv->k.p, 0, bytes));
+    HIP_CHECK(hipMemset(kv->v.p, 0, bytes));
+    std::fill(kv->filled.begin(), kv->filled.end(), 0);
+  });
+}
+
+int rai_kv_read(const rai_kv *kv, size_t layer, size_t head, size_t pos, int which, float *out) {
+  RAI_API_BODY({
+    if (!kv || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (layer >= (size_t)kv->layers || head >= (size_t)kv->nkv) rai::fail(RAI_E_ARG, "KV cache head is out of range");
+    if (pos >= kv->filled[layer])
+      rai::fail(RAI_E_WATERMARK, "KV read at unwritten position " + std::to_string(pos) + " (filled " +
+                                     std::to_string(kv->filled[layer]) + ")");
+    const float *base = which == 0 ? kv->kc((int)layer) : kv->vc((int)layer);
+    HIP_CHECK(hipMemcpy(out, base + (head * kv->cap + pos) * kv->hd, kv->hd * sizeof(float), hipMemcpyDeviceToHost));
+  });
+}
+
+int rai_embed_token(rai_model *m, size_t token, float *out) {
+  RAI_API_BODY({
+    if (!m || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (token >= m->cfg.vocab_size) rai::fail(RAI_E_RANGE, "token id is out of model vocabulary");
+    rai::Workspace &w = rai::model_ws(*m);
+    const uint32_t t = (uint32_t)token;
+    HIP_CHECK(hipMemcpyAsync(w.am.p, &t, 4, hipMemcpyHostToDevice, m->stream));
+    rai::embed_tokens(*m, w, w.am.as<uint32_t>(), 1, m->stream);
+    HIP_CHECK(hipMemcpyAsync(out, w.hid.p, sizeof(float) * m->cfg.hidden_size, hipMemcpyDeviceToHost, m->stream));
+    rai::check_kernel_error(w, m->stream);
+  });
+}
+
+int rai_forward_batch(rai_model *m, rai_kv *kv, float *hiddens, const size_t *positions, size_t batch) {
+  RAI_API_BODY({
+    if (!m || !kv || !hiddens || !positions) rai::fail(RAI_E_ARG, "null argument");
+    if (kv->model != m) rai::fail(RAI_E_ARG, "KV cache belongs to another model");
+    if (batch == 0) rai::fail(RAI_E_ARG, "batch must contain at least one token");
+    for (size_t b = 0; b < batch; ++b) {
+      if (positions[b] >= m->cfg.max_context) rai::fail(RAI_E_RANGE, "batch position exceeds model context");
+      if (b && positions[b] != positions[b - 1] + 1)
+        rai::fail(RAI_E_ARG, "batch positions must be strictly consecutive and ascending");
+    }
+    rai::Workspace &w = rai::model_ws(*m);
+    const size_t H = m->cfg.hidden_size;
+    for (size_t b0 = 0; b0 < batch; b0 += rai::kChunk) {
+      const int mm = (int)std::min<size_t>(rai::kChunk, batch - b0);
+      HIP_CHECK(hipMemcpyAsync(w.hid.p, hiddens + b0 * H, sizeof(float) * H * mm, hipMemcpyHostToDevice, m->stream));
+      rai::forward(*m, *kv, w, mm, positions[b0], m->stream);
+      HIP_CHECK(hipMemcpyAsync(hiddens + b0 * H, w.hid.p, sizeof(float) * H * mm, hipMemcpyDeviceToHost, m->stream));
+    }
+    HIP_CHECK(hipStreamSynchronize(m->stream));
+  });
+}
+
+int rai_forward_from_hidden(rai_model *m, rai_kv *kv, float *hidden, size_t pos, int store_kv) {
+  if (!store_kv) {
+    rai::set_last_error("probe passes (store_kv = 0) are not part of the lookup path");
+    return RAI_E_UNSUPPORTED;
+  }
+  return rai_forward_batch(m, kv, hidden, &pos, 1);
+}
+
+int rai_hidden_to_logits_batch(rai_model *m, const float *hiddens, float *out, size_t batch) {
+  RAI_API_BODY({
+    if (!m || !hiddens || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (batch == 0) rai::fail(RAI_E_ARG, "batch must contain at least one token");
+    rai::Workspace &w = rai::model_ws(*m);
+    const size_t H = m->cfg.hidden_size, V = m->cfg.vocab_size;
+    for (size_t b0 = 0; b0 < batch; b0 += (size_t)w.logit_rows) {
+      const int mm = (int)std::min<size_t>(w.logit_rows, batch - b0);
+      HIP_CHECK(hipMemcpyAsync(w.hid.p, hiddens + b0 * H, sizeof(float) * H * mm, hipMemcpyHostToDevice, m->stream));
+      rai::logits(*m, w, mm, m->stream);
+      HIP_CHECK(hipMemcpyAsync(out + b0 * V, w.logits.p, sizeof(float) * V * mm, hipMemcpyDeviceToHost, m->stream));
+    }
+    HIP_CHECK(hipStreamSynchronize(m->stream));
+  });
+}
+
+int rai_hidden_to_logits(rai_model *m, const float *hidden, float *out) {
+  return rai_hidden_to_logits_batch(m, hidden, out, 1);
+}
+
+int rai_w4a8_matmul_dev(float *out, const uint8_t *nib, const uint8_t *params, const float *x, size_t rows,
+                        size_t cols, size_t m, size_t gs, void *stream) {
+  RAI_API_BODY({
+    // validate_weight_buffers (gemm.rs:1169-1213).
+    if (!out || !nib || !params || !x) rai::fail(RAI_E_ARG, "null argument");
+    if (rows == 0) rai::fail(RAI_E_SHAPE, "rows must be non-zero");
+    if (cols == 0 || cols % 2) rai::fail(RAI_E_SHAPE, "cols must be non-zero and even");
+    if (gs == 0 || gs % 2) rai::fail(RAI_E_SHAPE, "group_size must be non-zero and even");
+    if (m == 0) rai::fail(RAI_E_SHAPE, "num_tokens must be non-zero");
+    if (rows > INT32_MAX || cols > INT32_MAX || m > INT32_MAX) rai::fail(RAI_E_SHAPE, "dimensions overflow");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t groups = rai::ceil_div(cols, gs);
+    rai::DevBuf qn, qs, sc, su;
+    qn.alloc(m * cols);
+    qs.alloc(m * cols);
+    sc.alloc(m * groups * 4);
+    su.alloc(m * groups * 4);
+    rai::launch_quantize(x, (int)m, (int)cols, (int)gs, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
+                         su.as<float>(), s);
+    rai::launch_w4a8(out, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(), su.as<float>(),
+                     (int)rows, (int)cols, (int)m, (int)gs, s);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipStreamSynchronize(s));  // scratch is freed on return
+  });
+}
+
+int rai_w4a8_lane_sums_dev(int32_t *out, const uint8_t *nib, const float *x, size_t rows, size_t cols, size_t m,
+                           size_t gs, void *stream) {
+  RAI_API_BODY({
+    if (!out || !nib || !x) rai::fail(RAI_E_ARG, "null argument");
+    if (rows == 0 || cols == 0 || cols % 2 || gs == 0 || gs % 2 || m == 0) rai::fail(RAI_E_SHAPE, "invalid shape");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t groups = rai::ceil_div(cols, gs);
+    rai::DevBuf qn, sc, su;
+    qn.alloc(m * cols);
+    sc.alloc(m * groups * 4);
+    su.alloc(m * groups * 4);
+    rai::launch_quantize(x, (int)m, (int)cols, (int)gs, qn.as<int8_t>(), nullptr, sc.as<float>(), su.as<float>(), s);
+    rai::launch_lane_sums(out, nib, qn.as<int8_t>(), (int)rows, (int)cols, (int)m, (int)gs, s);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipStreamSynchronize(s));
+  });
+}
+
+int rai_w4a8_matmul(float *out, const uint8_t *nib, const uint8_t *params, const float *x, size_t rows, size_t cols,
+                    size_t m, size_t gs) {
+  RAI_API_BODY({
+    if (!out || !nib || !params || !x) rai::fail(RAI_E_ARG, "null argument");
+    if (rows == 0 || cols == 0 || cols % 2 || gs == 0 || gs % 2 || m == 0) rai::fail(RAI_E_SHAPE, "invalid shape");
+    const size_t groups = rai::ceil_div(cols, gs);
+    rai::DevBuf dn, dp, dx, dout;
+    dn.alloc(rows * cols / 2);
+    dp.alloc(rows * groups * 4);
+    dx.alloc(m * cols * 4);
+    dout.alloc(m * rows * 4);
+    HIP_CHECK(hipMemcpy(dn.p, nib, rows * cols / 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dp.p, params, rows * groups * 4, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dx.p, x, m * cols * 4, hipMemcpyHostToDevice));
+    const int rc = rai_w4a8_matmul_dev(dout.as<float>(), dn.as<uint8_t>(), dp.as<uint8_t>(), dx.as<float>(), rows,
+                                       cols, m, gs, nullptr);
+    if (rc != RAI_OK) return rc;
+    HIP_CHECK(hipMemcpy(out, dout.p, m * rows * 4, hipMemcpyDeviceToHost));
+  });
+}
+
+int rai_tied_lm_head_dev(float *logits, const float *hidden, const uint8_t *codes, const uint8_t *params,
+                         size_t vocab, size_t n, size_t gs, void *stream) {
+  RAI_API_BODY({
+    if (!logits || !hidden || !codes || !params) rai::fail(RAI_E_ARG, "null argument");
+    if (gs == 0) rai::fail(RAI_E_SHAPE, "group_size must be non-zero");
+    if (n == 0 || n % 2) rai::fail(RAI_E_SHAPE, "hidden_size must be non-zero and even");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t groups = rai::ceil_div(n, gs);
+    rai::DevBuf hq, sc, su;
+    hq.alloc(n);
+    sc.alloc(groups * 4);
+    su.alloc(groups * 4);
+    rai::launch_tied_lm_head(logits, hidden, codes, params, (int)vocab, (int)n, (int)gs, 1, hq.as<int8_t>(),
+                             sc.as<float>(), su.as<float>(), s);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipStreamSynchronize(s));
+  });
+}
+
+int rai_embed_lookup_dev(float *out, size_t token, const uint8_t *codes, const uint8_t *params, size_t vocab,
+                         size_t hidden, size_t gs, void *stream) {
+  RAI_API_BODY({
+    if (!out || !codes || !params) rai::fail(RAI_E_ARG, "null argument");
+    if (gs == 0) rai::fail(RAI_E_SHAPE, "group_size must be non-zero");
+    if (token >= vocab) rai::fail(RAI_E_RANGE, "token id is out of range");
+    hipStream_t s = (hipStream_t)stream;
+    rai::DevBuf tok, err;
+    tok.alloc(4);
+    err.alloc(4);
+    const uint32_t t = (uint32_t)token;
+    HIP_CHECK(hipMemcpyAsync(tok.p, &t, 4, hipMemcpyHostToDevice, s));
+    HIP_CHECK(hipMemsetAsync(err.p, 0, 4, s));
+    rai::launch_embed(tok.as<uint32_t>(), nullptr, 0, 0, 1, codes, params, (int)vocab, (int)hidden, (int)gs, 1.0f,
+                      out, err.as<int>(), s);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipStreamSynchronize(s));
+  });
+}
+
+int rai_rms_norm_dev(float *out, const float *x, const float *w, size_t m, size_t n, float eps, void *stream) {
+  RAI_API_BODY({
+    if (!out || !x || !w) rai::fail(RAI_E_ARG, "null argument");
+    if (n == 0 || m == 0) rai::fail(RAI_E_SHAPE, "RMSNorm input must not be empty");
+    if (!std::isfinite(eps) || eps <= 0.0f) rai::fail(RAI_E_ARG, "RMSNorm epsilon must be finite and positive");
+    rai::launch_rmsnorm(x, w, out, nullptr, (int)m, (int)n, eps, (hipStream_t)stream);
+    HIP_CHECK(hipGetLastError());
+  });
+}
+
+int rai_silu_mul_dev(float *gate, const float *up, size_t m, size_t n, void *stream) {
+  RAI_API_BODY({
+    if (!gate || !up) rai::fail(RAI_E_ARG, "null argument");
+    if (n == 0 || m == 0) return RAI_OK;
+    rai::launch_silu_mul(gate, up, (int)m, (int)n, (hipStream_t)stream);
+    HIP_CHECK(hipGetLastError());
+  });
+}
+
+int rai_rope_apply_dev(float *heads, size_t nh, size_t hd, const float *c, const float *s, void *stream) {
+  RAI_API_BODY({
+    if (!heads || !c || !s) rai::fail(RAI_E_ARG, "null argument");
+    if (hd == 0 || hd % 2) rai::fail(RAI_E_SHAPE, "RoPE head_dim must be positive and even");
+    rai::launch_rope_apply(heads, (int)nh, (int)hd, c, s, (hipStream_t)stream);
+    HIP_CHECK(hipGetLastError());
+  });
+}
+
+int rai_attention_head_dev(float *out, const float *q, const float *k, const float *v, size_t pos, size_t hd,
+                           float scale, void *stream) {
+  RAI_API_BODY({
+    if (!out || !q || !k || !v) rai::fail(RAI_E_ARG, "null argument");
+    if (hd == 0 || hd % 8 || hd > 256) rai::fail(RAI_E_SHAPE, "head_dim must be a multiple of 8 up to 256");
+    if (pos + 1 > rai::kMaxAttnContext) rai::fail(RAI_E_UNSUPPORTED, "context beyond 16384 positions");
+    // One head: q [hd], cache rows [pos+1][hd] viewed as one kv head with cap = pos+1.
+    rai::launch_attention(q, k, v, (int)(pos + 1), (int)pos, 1, 1, 1, (int)hd, scale, out, (hipStream_t)stream);
+    HIP_CHECK(hipGetLastError());
+  });
+}
+
+int rai_find_ngram_draft(const uint32_t *tokens, size_t len, size_t min_ngram, size_t max_ngram, size_t max_draft,
+                         rai_lookup_match *out, int *found) {
+  RAI_API_BODY({
+    if (!out || !found || (len && !tokens)) rai::fail(RAI_E_ARG, "null argument");
+    *found = 0;
+    if (max_draft == 0 || len < 2) return RAI_OK;
+    if (len > INT32_MAX) rai::fail(RAI_E_SHAPE, "context too long");
+    rai::DevBuf dt, dr;
+    dt.alloc(len * 4);
+    dr.alloc(16);
+    HIP_CHECK(hipMemcpy(dt.p, tokens, len * 4, hipMemcpyHostToDevice));
+    const int mx = (int)std::min<size_t>(max_ngram, INT32_MAX), mn = (int)std::min<size_t>(min_ngram, INT32_MAX);
+    rai::launch_ngram(dt.as<uint32_t>(), (int)len, mn, mx, (int)std::min<size_t>(max_draft, INT32_MAX),
+                      dr.as<int>(), nullptr);
+    int r[3];
+    HIP_CHECK(hipMemcpy(r, dr.p, sizeof(r), hipMemcpyDeviceToHost));
+    if (r[0]) {
+      *found = 1;
+      out->ngram = r[0];
+      out->start = r[1];
+      out->len = r[2];
+    }
+  });
+}
+
+int rai_lookup_create(rai_model *m, size_t max_ctx, rai_lookup **out) {
+  RAI_API_BODY({
+    if (!m || !out) rai::fail(RAI_E_ARG, "null argument");
+    auto d = std::make_unique<rai_lookup>();
+    d->model = m;
+    d->max_ctx = std::min<size_t>(max_ctx, m->cfg.max_context);
+    if (d->max_ctx == 0) rai::fail(RAI_E_ARG, "prompt-lookup context must be non-zero");
+    rai::kv_init(d->kv, *m, d->max_ctx);
+    d->ws.init(*m, rai::kChunk, 64);
+    d->ctx.alloc((d->max_ctx + 64) * sizeof(uint32_t));
+    d->ctx_host.assign(d->max_ctx + 64, 0);
+    d->res.alloc(64);
+    HIP_CHECK(hipHostMalloc((void **)&d->pin, 4096, hipHostMallocDefault));
+    HIP_CHECK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+    *out = d.release();
+  });
+}
+
+void rai_lookup_free(rai_lookup *d) { delete d; }
+
+int rai_lookup_kv(rai_lookup *d, rai_kv **out) {
+  RAI_API_BODY({
+    if (!d || !out) rai::fail(RAI_E_ARG, "null argument");
+    *out = &d->kv;
+  });
+}
+
+int rai_lookup_prefill(rai_lookup *d, const uint32_t *prompt, size_t n, size_t *pos_out) {
+  RAI_API_BODY({
+    if (!d || !pos_out || (n && !prompt)) rai::fail(RAI_E_ARG, "null argument");
+    rai::lookup_prefill(*d, prompt, n, *pos_out);
+  });
+}
+
+int rai_lookup_step(rai_lookup *d, size_t pos, const uint32_t *context, size_t len, const rai_lookup_config *cfg,
+                    uint32_t *out_tokens, size_t out_cap, rai_lookup_metrics *metrics) {
+  RAI_API_BODY({
+    if (!d || !cfg || !out_tokens || !metrics || (len && !context)) rai::fail(RAI_E_ARG, "null argument");
+    rai::lookup_step(*d, pos, context, len, *cfg, out_tokens, out_cap, *metrics);
+  });
+}
+
+int rai_lookup_generate(rai_lookup *d, const uint32_t *prompt, size_t n, size_t max_tokens,
+                        const rai_lookup_config *cfg, uint32_t *out, size_t out_cap, size_t *n_out,
+                        rai_generate_stats *st) {
+  RAI_API_BODY({
+    if (!d || !prompt || !cfg || !out || !n_out) rai::fail(RAI_E_ARG, "null argument");
+    if (out_cap < max_tokens + cfg->max_draft) rai::fail(RAI_E_SHAPE, "output buffer too small");
+    rai_generate_stats s{};
+    s.prompt_tokens = n;
+    auto t0 = std::chrono::steady_clock::now();
+    size_t pos = 0;
+    rai::lookup_prefill(*d, prompt, n, pos);
+    auto t1 = std::chrono::steady_clock::now();
+    std::vector<uint32_t> ctx(prompt, prompt + n);
+    ctx.reserve(n + max_tokens + cfg->max_draft + 1);
+    std::vector<uint32_t> step_out(cfg->max_draft + 1);
+    size_t gen = 0;
+    while (gen < max_tokens && pos < d->max_ctx) {
+      rai_lookup_metrics met{};
+      rai::lookup_step(*d, pos, ctx.data(), ctx.size(), *cfg, step_out.data(), step_out.size(), met);
+      for (size_t i = 0; i < met.produced; ++i) {
+        out[gen++] = step_out[i];
+        ctx.push_back(step_out[i]);
+      }
+      pos += met.produced;
+      s.steps++;
+      if (met.drafted) s.steps_with_draft++;
+      s.drafted += met.drafted;
+      s.accepted += met.accepted;
+    }
+    auto t2 = std::chrono::steady_clock::now();
+    s.generated = gen;
+    s.prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
+    s.decode_seconds = std::chrono::duration<double>(t2 - t1).count();
+    *n_out = gen;
+    if (st) *st = s;
+  });
+}
+
+int rai_greedy_generate(rai_lookup *d, const uint32_t *prompt, size_t n, size_t steps, uint32_t *out) {
+  RAI_API_BODY({
+    if (!d || !prompt || !out) rai::fail(RAI_E_ARG, "null argument");
+    size_t pos = 0;
+    rai::lookup_prefill(*d, prompt, n, pos);
+    std::vector<uint32_t> ctx(prompt, prompt + n);
+    rai_model &md = *d->model;
+    for (size_t i = 0; i < steps; ++i) {
+      if (pos >= d->max_ctx) rai::fail(RAI_E_RANGE, "generation exceeds the context window");
+      // decode_one (lookup.rs:428-455) with argmax sampling.
+      rai::sync_context(*d, ctx.data(), ctx.size());
+      launch_embed(nullptr, d->ctx.as<uint32_t>(), (int)ctx.size() - 1, 0, 1, md.emb_codes, md.emb_params,
+                   md.cfg.vocab_size, md.cfg.hidden_size, md.cfg.embed_group_size, md.cfg.embed_scale,
+                   d->ws.hid.as<float>(), d->ws.err.as<int>(), d->stream);
+      rai::forward(md, d->kv, d->ws, 1, pos, d->stream);
+      rai::logits(md, d->ws, 1, d->stream);
+      launch_argmax(d->ws.logits.as<float>(), 1, md.cfg.vocab_size, d->ws.am.as<uint32_t>(), d->stream);
+      uint32_t tok = 0;
+      HIP_CHECK(hipMemcpyAsync(&tok, d->ws.am.p, 4, hipMemcpyDeviceToHost, d->stream));
+      HIP_CHECK(hipStreamSynchronize(d->stream));
+      out[i] = tok;
+      ctx.push_back(tok);
+      ++pos;
+    }
+  });
+}
+
+int rai_dev_malloc(size_t bytes, void **out) {
+  RAI_API_BODY({
+    if (!out) rai::fail(RAI_E_ARG, "null argument");
+    HIP_CHECK(hipMalloc(out, bytes ? bytes : 1));
+  });
+}
+int rai_dev_free(void *p) { RAI_API_BODY(HIP_CHECK(hipFree(p))); }
+int rai_memcpy_h2d(void *dst, const void *src, size_t n) {
+  RAI_API_BODY(HIP_CHECK(hipMemcpy(dst, src, n, hipMemcpyHostToDevice)));
+}
+int rai_memcpy_d2h(void *dst, const void *src, size_t n) {
+  RAI_API_BODY(HIP_CHECK(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost)));
+}
+int rai_device_synchronize(void) { RAI_API_BODY(HIP_CHECK(hipDeviceSynchronize())); }
+int rai_stream_create(void **out) {
+  RAI_API_BODY({
+    hipStream_t s;
+    HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *out = s;
+  });
+}
+int rai_stream_destroy(void *s) { RAI_API_BODY(HIP_CHECK(hipStreamDestroy((hipStream_t)s))); }
+int rai_event_create(void **out) {
+  RAI_API_BODY({
+    hipEvent_t e;
+    HIP_CHECK(hipEventCreate(&e));
+    *out = e;
+  });
+}
+int rai_event_destroy(void *e) { RAI_API_BODY(HIP_CHECK(hipEventDestroy((hipEvent_t)e))); }
+int rai_event_record(void *e, void *s) { RAI_API_BODY(HIP_CHECK(hipEventRecord((hipEvent_t)e, (hipStream_t)s))); }
+int rai_event_elapsed_ms(void *a, void *b, float *ms) {
+  RAI_API_BODY(HIP_CHECK(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b)));
+}
+int rai_stream_synchronize(void *s) { RAI_API_BODY(HIP_CHECK(hipStreamSynchronize((hipStream_t)s))); }
+
+}  // extern "C"

@@ -1,0 +1,120 @@
+"""GPU parity of the kernel-level C ABI against the CPU oracle.
+
+Bar: bit-exact.  Integer lane sums and f32 outputs must equal the oracle's
+(which reproduces the reference's AVX2 path) bit for bit.
+"""
+import numpy as np
+import pytest
+
+from rai_amd.workload import gemv_operands
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _f16b(v):
+    return np.frombuffer(np.float16(v).tobytes(), np.uint8)
+
+
+def test_known_answers(rai):
+    """gemm.rs:2088-2148 through the HIP library."""
+    p = np.concatenate([_f16b(1.0), _f16b(0.0)] * 2)
+    out = rai.w4a8_matvec(np.full(4, 0x11, np.uint8), p, np.ones(4), 2, 4, 4)
+    assert np.all(np.abs(out - 4.0) < 0.05)
+    p = np.concatenate([_f16b(0.5), _f16b(-1.0)])
+    out = rai.w4a8_matvec(np.array([0x55], np.uint8), p, [2.0, 3.0], 1, 2, 2)
+    assert abs(out[0] - 7.5) < 0.05
+
+
+# (rows, cols, gs): the fast tiled path (gs 32/64/128, full groups) and the
+# general path (tiny groups, partial last group, unquantized tails).
+SHAPES = [(64, 256, 32), (48, 256, 64), (40, 512, 128), (33, 160, 32), (16, 96, 32),
+          (24, 100, 36), (8, 8, 4), (8, 70, 64), (17, 320, 96)]
+
+
+@pytest.mark.parametrize("rows,cols,gs", SHAPES)
+@pytest.mark.parametrize("m", [1, 2, 5, 9, 17])
+def test_w4a8_matmul_bit_exact(rai, ora, rows, cols, gs, m):
+    nib, params, x = gemv_operands(rows, cols, m, gs, seed=rows * 7 + cols + m)
+    want = ora.w4a8_matmul(nib, params, x, rows, cols, m, gs)
+    got = rai.w4a8_matmul(nib, params, x, rows, cols, m, gs)
+    assert np.array_equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("rows,cols,gs", SHAPES[:6])
+def test_lane_sums_bit_exact(rai, ora, rows, cols, gs):
+    nib, _, x = gemv_operands(rows, cols, 3, gs, seed=cols)
+    assert np.array_equal(rai.w4a8_lane_sums(nib, x, rows, cols, 3, gs),
+                          ora.lane_sums(nib, x, rows, cols, 3, gs))
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (14336, 4096), (4096, 14336), (32000, 4096)])
+def test_gemv_sweep_shapes_bit_exact(rai, ora, rows, cols):
+    """The W4A8 sweep shapes at full size, g32, M in {1, 9}: f32 outputs and,
+    for a row slice, the int32 accumulators."""
+    for m in (1, 9):
+        nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + m)
+        want = ora.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+        got = rai.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+        assert np.array_equal(_bits(got), _bits(want)), (rows, cols, m)
+    nib, _, x = gemv_operands(256, cols, 2, 32, seed=cols)
+    assert np.array_equal(rai.w4a8_lane_sums(nib, x, 256, cols, 2, 32),
+                          ora.lane_sums(nib, x, 256, cols, 2, 32))
+
+
+def test_tied_lm_head_bit_exact(rai, ora):
+    rng = np.random.default_rng(3)
+    for vocab, n, gs in ((96, 64, 64), (500, 256, 64), (77, 100, 36)):
+        codes = rng.integers(0, 256, vocab * n, dtype=np.uint8)
+        g = -(-n // gs)
+        params = np.stack([np.abs(rng.normal(0, 0.01, vocab * g)) + 1e-3,
+                           rng.normal(0, 0.1, vocab * g)], axis=1).astype(np.float16)
+        params = params.view(np.uint8).reshape(-1)
+        h = rng.normal(size=n).astype(np.float32)
+        want = ora.tied_lm_head(h, codes, params, vocab, gs)
+        got = rai.tied_lm_head(h, codes, params, vocab, gs)
+        assert np.array_equal(_bits(got), _bits(want))
+
+
+def test_embed_lookup_bit_exact(rai, ora):
+    rng = np.random.default_rng(4)
+    vocab, n, gs = 50, 128, 64
+    codes = rng.integers(0, 256, vocab * n, dtype=np.uint8)
+    params = np.stack([np.abs(rng.normal(0, 0.01, vocab * 2)) + 1e-3,
+                       rng.normal(0, 0.1, vocab * 2)], axis=1).astype(np.float16).view(np.uint8).reshape(-1)
+    for t in (0, 17, 49):
+        assert np.array_equal(_bits(rai.embed_lookup(t, codes, params, vocab, n, gs)),
+                              _bits(ora.embed_lookup(t, codes, params, vocab, n, gs)))
+    with pytest.raises(rai.RaiError) as e:
+        rai.embed_lookup(vocab, codes, params, vocab, n, gs)
+    assert e.value.status == "RAI_E_RANGE"
+
+
+def test_ngram_kernel_known_answers(rai):
+    """lookup.rs:486-571 known answers through the GPU search kernel."""
+    from test_cpu_oracle import NGRAM_CASES
+    for tokens, mn, mx, k, want in NGRAM_CASES:
+        m = rai.find_ngram_draft(tokens, mn, mx, k)
+        assert (None if m is None else (m.ngram, m.start, m.len)) == want, tokens
+
+
+def test_ngram_kernel_matches_oracle(rai, ora):
+    rng = np.random.default_rng(5)
+    for i in range(60):
+        n = int(rng.integers(2, 3000 if i % 10 == 0 else 60))
+        t = rng.integers(0, 3 if i % 2 else 50, size=n).tolist()
+        mn = int(rng.integers(1, 4))
+        mx = int(rng.integers(mn, 6))
+        k = int(rng.integers(1, 9))
+        m = rai.find_ngram_draft(t, mn, mx, k)
+        assert (None if m is None else (m.ngram, m.start, m.len)) == ora.find_ngram_draft(t, mn, mx, k)
+
+
+def test_shape_errors(rai):
+    """validate_weight_buffers (gemm.rs:1169-1213) panics become RAI_E_SHAPE."""
+    with pytest.raises(rai.RaiError) as e:
+        rai.w4a8_matmul(np.zeros(2, np.uint8), np.zeros(4, np.uint8), np.ones(3), 1, 3, 1, 3)
+    assert e.value.status == "RAI_E_SHAPE"
