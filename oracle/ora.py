@@ -242,7 +242,7 @@ class Model:
     """Oracle counterpart of RaiModel (model.rs) over an in-memory .raimodel."""
 
     def __init__(self, data: bytes | np.ndarray, max_groups: int = 0):
-        buf = np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray) else data
+        buf = data if isinstance(data, np.ndarray) else np.frombuffer(bytes(data), np.uint8)
         buf = np.ascontiguousarray(buf, np.uint8)
         h = c_void_p()
         _check(lib().ora_model_open(_ptr(buf), buf.size, max_groups, ctypes.byref(h)))

@@ -109,6 +109,7 @@ def lib():
         "rai_w4a8_matmul_dev": (c_int, [P, P, P, P, S, S, S, S, P]),
         "rai_w4a8_lane_sums_dev": (c_int, [P, P, P, S, S, S, S, P]),
         "rai_w4a8_matmul": (c_int, [P, P, P, P, S, S, S, S]),
+        "rai_w4a8_time_dev": (c_int, [P, P, P, P, S, S, S, S, c_int, POINTER(c_float)]),
         "rai_tied_lm_head_dev": (c_int, [P, P, P, P, S, S, S, P]),
         "rai_embed_lookup_dev": (c_int, [P, S, P, P, S, S, S, P]),
         "rai_rms_norm_dev": (c_int, [P, P, P, S, S, c_float, P]),
@@ -231,6 +232,19 @@ def w4a8_matvec(nibbles, params, x, rows: int, cols: int, group_size: int) -> np
     return w4a8_matmul(nibbles, params, x, rows, cols, 1, group_size)[0]
 
 
+def w4a8_time(nibbles, params, x, rows: int, cols: int, num_tokens: int, group_size: int,
+              iters: int = 50) -> float:
+    """Average device time (ms) of one W4A8 kernel launch (HIP events)."""
+    dn = DeviceArray.from_host(np.ascontiguousarray(nibbles, np.uint8))
+    dp = DeviceArray.from_host(np.ascontiguousarray(params, np.uint8))
+    dx = DeviceArray.from_host(_f32(x))
+    do = DeviceArray(num_tokens * rows * 4)
+    ms = c_float()
+    _check(lib().rai_w4a8_time_dev(do.ptr, dn.ptr, dp.ptr, dx.ptr, rows, cols, num_tokens,
+                                   group_size, iters, ctypes.byref(ms)))
+    return ms.value
+
+
 def w4a8_lane_sums(nibbles, x, rows: int, cols: int, num_tokens: int,
                    group_size: int) -> np.ndarray:
     """Integer accumulators of the W4A8 kernel: [tokens][rows][groups][12]."""
@@ -334,10 +348,10 @@ def synth_model(hidden_size, num_layers, num_heads, num_kv_heads, head_dim,
                 intermediate_size, vocab_size, max_context, *, rope_theta=10000.0,
                 norm_eps=1e-5, group_size=32, embed_group_size=64, tied=False,
                 num_experts=0, experts_per_token=0, norm_topk_prob=False, weight_std=0.02,
-                mode=0, seed=0, path: str | None = None) -> bytes | int:
+                mode=0, seed=0, path: str | None = None) -> np.ndarray | int:
     """Write a random-init .raimodel (see rai_synth_model in include/rai_hip.h).
 
-    Returns the image bytes, or the file size when `path` is given."""
+    Returns the image as a uint8 array, or the file size when `path` is given."""
     c = SynthConfig(hidden_size, num_layers, num_heads, num_kv_heads, head_dim,
                     intermediate_size, vocab_size, max_context, rope_theta, norm_eps,
                     group_size, embed_group_size, int(tied), num_experts, experts_per_token,
@@ -349,7 +363,11 @@ def synth_model(hidden_size, num_layers, num_heads, num_kv_heads, head_dim,
     if path:
         return n.value
     try:
-        return ctypes.string_at(img.value, n.value)
+        # numpy buffer filled with memmove (size_t); ctypes.string_at takes a
+        # C int size and cannot return images of 2 GiB or more.
+        out = np.empty(n.value, np.uint8)
+        ctypes.memmove(out.ctypes.data, img.value, n.value)
+        return out
     finally:
         lib().rai_free_image(img)
 
@@ -370,8 +388,9 @@ class RaiModel:
         return cls(h.value)
 
     @classmethod
-    def from_bytes(cls, data: bytes, max_groups: int = 0) -> "RaiModel":
-        buf = np.frombuffer(data, np.uint8)
+    def from_bytes(cls, data, max_groups: int = 0) -> "RaiModel":
+        buf = data if isinstance(data, np.ndarray) else np.frombuffer(data, np.uint8)
+        buf = np.ascontiguousarray(buf, np.uint8)
         h = c_void_p()
         _check(lib().rai_model_from_buffer(_ptr(buf), buf.size, max_groups, ctypes.byref(h)))
         return cls(h.value)

@@ -799,6 +799,43 @@ int rai_w4a8_matmul_dev(float *out, const uint8_t *nib, const uint8_t *params, c
   });
 }
 
+int rai_w4a8_time_dev(float *out, const uint8_t *nib, const uint8_t *params, const float *x, size_t rows,
+                      size_t cols, size_t m, size_t gs, int iters, float *avg_ms) {
+  RAI_API_BODY({
+    if (!out || !nib || !params || !x || !avg_ms) rai::fail(RAI_E_ARG, "null argument");
+    if (rows == 0 || cols == 0 || cols % 2 || gs == 0 || gs % 2 || m == 0 || iters <= 0)
+      rai::fail(RAI_E_SHAPE, "invalid shape");
+    const size_t groups = rai::ceil_div(cols, gs);
+    rai::DevBuf qn, qs, sc, su;
+    qn.alloc(m * cols);
+    qs.alloc(m * cols);
+    sc.alloc(m * groups * 4);
+    su.alloc(m * groups * 4);
+    hipStream_t s;
+    HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    hipEvent_t e0, e1;
+    HIP_CHECK(hipEventCreate(&e0));
+    HIP_CHECK(hipEventCreate(&e1));
+    rai::launch_quantize(x, (int)m, (int)cols, (int)gs, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
+                         su.as<float>(), s);
+    auto run = [&] {
+      rai::launch_w4a8(out, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(), su.as<float>(),
+                       (int)rows, (int)cols, (int)m, (int)gs, s);
+    };
+    run();  // warm-up
+    HIP_CHECK(hipEventRecord(e0, s));
+    for (int i = 0; i < iters; ++i) run();
+    HIP_CHECK(hipEventRecord(e1, s));
+    HIP_CHECK(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+    *avg_ms = ms / iters;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipStreamDestroy(s);
+  });
+}
+
 int rai_w4a8_lane_sums_dev(int32_t *out, const uint8_t *nib, const float *x, size_t rows, size_t cols, size_t m,
                            size_t gs, void *stream) {
   RAI_API_BODY({
