@@ -48,9 +48,14 @@ void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s);
 void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
                        int pos0, int m, int nh, int nkv, int hd, float *kc, float *vc, int cap,
                        hipStream_t s);
-// attention_head_avx2 for every (token, query head).
+// attention_head_avx2 for every (token, query head).  `scores` is scratch of
+// attention_scores_floats(m, nh, pos0 + m) floats; tokens are processed in
+// groups of kAttnTokens.
+constexpr int kAttnTokens = 64;
+size_t attention_scores_floats(int m, int nh, int ctx);
 void launch_attention(const float *q, const float *kc, const float *vc, int cap, int pos0, int m,
-                      int nh, int nkv, int hd, float scale, float *out, hipStream_t s);
+                      int nh, int nkv, int hd, float scale, float *out, float *scores,
+                      hipStream_t s);
 // Standalone RoPE of one position (layers.rs:643-726) on heads [nh][hd].
 void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,
                        hipStream_t s);

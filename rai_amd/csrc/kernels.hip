@@ -8,6 +8,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 
@@ -338,6 +339,418 @@ void launch_fast_gs(float *out, const uint8_t *nib, const uint8_t *params, const
     launch_fast_t<GS, 16>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
 }
 
+// ------------------------------------------------------ w4a8 small-M v2 --
+
+// Small-M (<= 16 tokens) W4A8 kernel for group sizes 32/64/128 with full
+// groups, same two-phase arithmetic as k_w4a8_fast:
+//   phase 1: item (row r, group g) -> per-token lane products
+//            fl(float(S_lane) * fl(ws*as)) and zero terms fl(z*xsum) in LDS;
+//   phase 2: each (token, chain, row) accumulator adds its tile's products in
+//            group order (the reference's sequential per-lane f32 sums).
+// A block owns R rows; a K tile holds GT = 256/R groups, one item per thread.
+// Weights are prefetched PD tiles ahead in a register ring so the block
+// keeps PD tiles of HBM traffic in flight.  Activations (int8, block-split),
+// scales and sums are staged in LDS once per block when they fit (WHOLE),
+// else one tile at a time with a one-tile register prefetch.  LDS strides are
+// padded against bank conflicts.
+template <int GS, int MT, int R, int PD, bool WHOLE>
+struct SmallCfg {
+  static constexpr int NL = (GS == 32) ? 4 : 8;
+  static constexpr int NC = NL + 1;
+  static constexpr int NW = GS / 8;          // code dwords per group
+  static constexpr int GT = kThreads / R;    // groups per K tile
+  static constexpr int PSTR = GT + 1;        // padded product stride
+  static constexpr int QSTR = GS + 8;        // padded per-group q stride (bytes)
+  static constexpr int CPT = (MT * NC * R + kThreads - 1) / kThreads;
+  static constexpr int QV = (MT * GT * NW + kThreads - 1) / kThreads;  // uint2 per thread per tile
+};
+
+template <int GS, int MT, int R, int PD, bool WHOLE>
+__global__ __launch_bounds__(kThreads) void k_w4a8_small(
+    float *__restrict__ out, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
+    const int8_t *__restrict__ q_split, const float *__restrict__ scales,
+    const float *__restrict__ sums, int rows, int cols, int m_total, int groups) {
+  using C = SmallCfg<GS, MT, R, PD, WHOLE>;
+  constexpr int NL = C::NL, NC = C::NC, NW = C::NW, GT = C::GT, PSTR = C::PSTR, QSTR = C::QSTR;
+  constexpr int CPT = C::CPT, QV = C::QV;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int t0 = blockIdx.y * MT;
+  const int m = min(MT, m_total - t0);
+  const int row0 = blockIdx.x * R;
+  const int tid = threadIdx.x;
+  const int ktiles = (groups + GT - 1) / GT;
+  const int gstage = WHOLE ? groups : GT;  // groups held per staged q buffer
+  const int nbuf = WHOLE ? 1 : 2;
+  // LDS: q [nbuf][MT][gstage][QSTR] bytes | scale, sum [nbuf][MT][gstage] f32
+  //      | products [MT][NC][R][PSTR] f32
+  // Sized by the launch's token count m (<= MT), see small_smem().
+  const size_t qbytes = (size_t)nbuf * m * gstage * QSTR;
+  int8_t *qsh = reinterpret_cast<int8_t *>(smem);
+  float *ash = reinterpret_cast<float *>(smem + ((qbytes + 15) & ~size_t(15)));
+  float *ssh = ash + nbuf * m * gstage;
+  float *psh = ssh + nbuf * m * gstage;
+
+  const int r_item = tid / GT, g_item = tid % GT;
+  const int row_item = row0 + r_item;
+  const bool row_ok = row_item < rows;
+  const size_t row_bytes = (size_t)cols / 2;
+  const uint8_t *nrow = nib + (size_t)(row_ok ? row_item : 0) * row_bytes;
+  const uint8_t *prow = params + (size_t)(row_ok ? row_item : 0) * groups * 4;
+
+  // Weight ring: tile kt lives in slot kt % PD.
+  uint32_t ring_c[PD][NW];
+  uint32_t ring_p[PD];
+  auto load_tile = [&](int kt, uint32_t (&c)[NW], uint32_t &p) {
+    const int gi = kt * GT + g_item;
+    if (row_ok && gi < groups) {
+      const uint4 *cp = reinterpret_cast<const uint4 *>(nrow + (size_t)gi * (GS / 2));
+#pragma unroll
+      for (int v = 0; v < NW / 4; ++v) {
+        const uint4 u = cp[v];
+        c[4 * v + 0] = u.x;
+        c[4 * v + 1] = u.y;
+        c[4 * v + 2] = u.z;
+        c[4 * v + 3] = u.w;
+      }
+      p = *reinterpret_cast<const uint32_t *>(prow + (size_t)gi * 4);
+    }
+  };
+  // Stage activations for groups [g0, g0+gn) of tokens t0.. into buffer b.
+  auto stage_direct = [&](int b, int g0, int gn) {
+    int8_t *qb = qsh + (size_t)b * m * gstage * QSTR;
+    const int per_tok = gn * NW;  // uint2 per token
+    for (int i = tid; i < m * per_tok; i += kThreads) {
+      const int t = i / per_tok, rem = i % per_tok, g = rem / NW, w = rem % NW;
+      const uint2 v = *reinterpret_cast<const uint2 *>(q_split + (size_t)(t0 + t) * cols +
+                                                       (size_t)(g0 + g) * GS + w * 8);
+      *reinterpret_cast<uint2 *>(qb + ((size_t)t * gstage + g) * QSTR + w * 8) = v;
+    }
+    for (int i = tid; i < m * gn; i += kThreads) {
+      const int t = i / gn, g = i % gn;
+      ash[(b * m + t) * gstage + g] = scales[(size_t)(t0 + t) * groups + g0 + g];
+      ssh[(b * m + t) * gstage + g] = sums[(size_t)(t0 + t) * groups + g0 + g];
+    }
+  };
+
+  float acc[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) acc[j] = 0.0f;
+
+#pragma unroll
+  for (int j = 0; j < PD; ++j)
+    if (j < ktiles) load_tile(j, ring_c[j], ring_p[j]);
+  stage_direct(0, 0, WHOLE ? groups : min(GT, groups));
+  __syncthreads();
+
+  uint2 qn[QV];
+  float an = 0.0f, sn = 0.0f;
+  for (int kt0 = 0; kt0 < ktiles; kt0 += PD) {
+#pragma unroll
+    for (int j = 0; j < PD; ++j) {
+      const int kt = kt0 + j;
+      if (kt >= ktiles) break;
+      const int g0 = kt * GT;
+      const int gcount = min(GT, groups - g0);
+      const int buf = WHOLE ? 0 : (kt & 1);
+      const int gbase = WHOLE ? g0 : 0;
+      // Prefetch the next tile's activations (per-tile staging only).
+      const int gn_next = (kt + 1 < ktiles) ? min(GT, groups - (kt + 1) * GT) : 0;
+      if (!WHOLE && gn_next > 0) {
+#pragma unroll
+        for (int v = 0; v < QV; ++v) {
+          const int i = tid + v * kThreads;
+          if (i < m * gn_next * NW) {
+            const int t = i / (gn_next * NW), rem = i % (gn_next * NW), g = rem / NW, w = rem % NW;
+            qn[v] = *reinterpret_cast<const uint2 *>(q_split + (size_t)(t0 + t) * cols +
+                                                     (size_t)((kt + 1) * GT + g) * GS + w * 8);
+          }
+        }
+        if (tid < m * gn_next) {
+          const int t = tid / gn_next, g = tid % gn_next;
+          an = scales[(size_t)(t0 + t) * groups + (kt + 1) * GT + g];
+          sn = sums[(size_t)(t0 + t) * groups + (kt + 1) * GT + g];
+        }
+      }
+      // Phase 1: products of this thread's (row, group) item.
+      if (row_ok && g_item < gcount) {
+        const uint32_t pw = ring_p[j];
+        const float ws = f16bits((uint16_t)(pw & 0xFFFF));
+        const float wz = f16bits((uint16_t)(pw >> 16));
+        const int gq = gbase + g_item;
+        for (int t = 0; t < m; ++t) {
+          const int8_t *qg = qsh + ((size_t)(buf * m + t) * gstage + gq) * QSTR;
+          int sl[NL];
+#pragma unroll
+          for (int l = 0; l < NL; ++l) sl[l] = 0;
+#pragma unroll
+          for (int b = 0; b < NW; ++b) {
+            const uint2 qv = *reinterpret_cast<const uint2 *>(qg + 8 * b);
+            sl[b % NL] = block_dot(ring_c[j][b], qv.x, qv.y, sl[b % NL]);
+          }
+          const float cs = ws * ash[(buf * m + t) * gstage + gq];
+          float *pt = psh + ((size_t)(t * NC) * R + r_item) * PSTR + g_item;
+#pragma unroll
+          for (int l = 0; l < NL; ++l) pt[(size_t)l * R * PSTR] = (float)sl[l] * cs;
+          pt[(size_t)NL * R * PSTR] = wz * ssh[(buf * m + t) * gstage + gq];
+        }
+      }
+      // Refill this ring slot with tile kt + PD.
+      if (kt + PD < ktiles) load_tile(kt + PD, ring_c[j], ring_p[j]);
+      // Publish the next tile's activations into the other buffer.
+      if (!WHOLE && gn_next > 0) {
+        int8_t *qb = qsh + (size_t)((kt + 1) & 1) * m * gstage * QSTR;
+#pragma unroll
+        for (int v = 0; v < QV; ++v) {
+          const int i = tid + v * kThreads;
+          if (i < m * gn_next * NW) {
+            const int t = i / (gn_next * NW), rem = i % (gn_next * NW), g = rem / NW, w = rem % NW;
+            *reinterpret_cast<uint2 *>(qb + ((size_t)t * gstage + g) * QSTR + w * 8) = qn[v];
+          }
+        }
+        if (tid < m * gn_next) {
+          const int t = tid / gn_next, g = tid % gn_next;
+          ash[(((kt + 1) & 1) * m + t) * gstage + g] = an;
+          ssh[(((kt + 1) & 1) * m + t) * gstage + g] = sn;
+        }
+      }
+      __syncthreads();
+      // Phase 2: ordered accumulation.
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const int ch = tid + c * kThreads;
+        if (ch < m * NC * R) {
+          const float *p = psh + (size_t)ch * PSTR;
+          float a = acc[c];
+          for (int g = 0; g < gcount; ++g) a = a + p[g];
+          acc[c] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  float *fin = psh;  // [m][NC][R]
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int ch = tid + c * kThreads;
+    if (ch < m * NC * R) fin[ch] = acc[c];
+  }
+  __syncthreads();
+  if (tid < m * R) {
+    const int t = tid / R, r = tid % R;
+    const int row = row0 + r;
+    if (row < rows) {
+      float f[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) f[l] = (l < NL) ? fin[(t * NC + l) * R + r] : 0.0f;
+      out[(size_t)(t0 + t) * rows + row] = hsum8(f) + fin[(t * NC + NL) * R + r];
+    }
+  }
+}
+
+// LDS bytes for a launch whose token tiles hold at most m tokens.
+template <int GS, int MT, int R, int PD, bool WHOLE>
+size_t small_smem(int groups, int m) {
+  using C = SmallCfg<GS, MT, R, PD, WHOLE>;
+  const int gstage = WHOLE ? groups : C::GT;
+  const int nbuf = WHOLE ? 1 : 2;
+  const size_t qbytes = (((size_t)nbuf * m * gstage * C::QSTR) + 15) & ~size_t(15);
+  return qbytes + 2 * sizeof(float) * (size_t)nbuf * m * gstage +
+         sizeof(float) * (size_t)m * C::NC * R * C::PSTR;
+}
+
+template <int GS, int MT, int R, int PD, bool WHOLE>
+void launch_small_t(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                    const float *scales, const float *sums, int rows, int cols, int m, int groups,
+                    hipStream_t s) {
+  const size_t smem = small_smem<GS, MT, R, PD, WHOLE>(groups, std::min(m, MT));
+  static size_t configured = 0;
+  if (smem > configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_small<GS, MT, R, PD, WHOLE>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = smem;
+  }
+  dim3 grid((rows + R - 1) / R, (m + MT - 1) / MT);
+  hipLaunchKernelGGL((k_w4a8_small<GS, MT, R, PD, WHOLE>), grid, dim3(kThreads), smem, s, out, nib,
+                     params, q_split, scales, sums, rows, cols, m, groups);
+}
+
+// ---------------------------------------------------------- w4a8 M = 1 --
+
+// (row, group) items each thread of the M = 1 kernel holds in registers.
+constexpr int m1_items_per_thread(int gs) { return gs == 128 ? 4 : 8; }
+
+// Single-token W4A8 kernel (decode), group sizes 32/64/128 with full groups.
+// A block owns R rows and the whole K: its R*G (row, group) items are split
+// over the 256 threads (up to IPT each) and every weight load is issued up
+// front, so one HBM round trip covers the block.  Phase 1 writes each item's
+// lane products fl(float(S_lane) * fl(ws*as)) and zero term fl(z*xsum) to
+// LDS; phase 2 runs the NC*R sequential accumulators over all groups in
+// order; the epilogue applies the reference's lane reduction.
+template <int GS, int R, int IPT>
+__global__ __launch_bounds__(kThreads) void k_w4a8_m1(
+    float *__restrict__ out, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
+    const int8_t *__restrict__ q_split, const float *__restrict__ scales,
+    const float *__restrict__ sums, int rows, int cols, int groups) {
+  constexpr int NL = (GS == 32) ? 4 : 8;
+  constexpr int NC = NL + 1;
+  constexpr int NW = GS / 8;
+  static_assert(NC * R <= kThreads, "one thread per accumulator chain");
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x;
+  const int row0 = blockIdx.x * R;
+  const int pstr = groups + 1;  // padded product stride
+  // LDS: q [K] (block-split) | scale, sum [G] | products [NC][R][G+1]
+  int8_t *qsh = reinterpret_cast<int8_t *>(smem);
+  float *ash = reinterpret_cast<float *>(smem + ((cols + 15) & ~15));
+  float *ssh = ash + groups;
+  float *psh = ssh + groups;
+  const int items = R * groups;
+  uint32_t cw[IPT][NW];
+  uint32_t pw[IPT];
+  int ir[IPT], ig[IPT];
+#pragma unroll
+  for (int j = 0; j < IPT; ++j) {
+    const int i = tid + j * kThreads;
+    ir[j] = i / groups;
+    ig[j] = i - ir[j] * groups;
+    const int row = row0 + ir[j];
+    if (i < items && row < rows) {
+      const uint4 *cp = reinterpret_cast<const uint4 *>(nib + (size_t)row * (cols / 2) + ig[j] * (GS / 2));
+#pragma unroll
+      for (int v = 0; v < NW / 4; ++v) {
+        const uint4 u = cp[v];
+        cw[j][4 * v + 0] = u.x;
+        cw[j][4 * v + 1] = u.y;
+        cw[j][4 * v + 2] = u.z;
+        cw[j][4 * v + 3] = u.w;
+      }
+      pw[j] = *reinterpret_cast<const uint32_t *>(params + ((size_t)row * groups + ig[j]) * 4);
+    }
+  }
+  for (int i = tid; i < cols / 16; i += kThreads)
+    reinterpret_cast<uint4 *>(qsh)[i] = reinterpret_cast<const uint4 *>(q_split)[i];
+  for (int i = tid; i < groups; i += kThreads) {
+    ash[i] = scales[i];
+    ssh[i] = sums[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < IPT; ++j) {
+    const int i = tid + j * kThreads;
+    if (i < items && row0 + ir[j] < rows) {
+      const float ws = f16bits((uint16_t)(pw[j] & 0xFFFF));
+      const float wz = f16bits((uint16_t)(pw[j] >> 16));
+      const uint2 *qg = reinterpret_cast<const uint2 *>(qsh + ig[j] * GS);
+      int sl[NL];
+#pragma unroll
+      for (int l = 0; l < NL; ++l) sl[l] = 0;
+#pragma unroll
+      for (int b = 0; b < NW; ++b) {
+        const uint2 qv = qg[b];
+        sl[b % NL] = block_dot(cw[j][b], qv.x, qv.y, sl[b % NL]);
+      }
+      const float cs = ws * ash[ig[j]];
+      float *pt = psh + ir[j] * pstr + ig[j];
+#pragma unroll
+      for (int l = 0; l < NL; ++l) pt[l * R * pstr] = (float)sl[l] * cs;
+      pt[NL * R * pstr] = wz * ssh[ig[j]];
+    }
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  if (tid < NC * R) {
+    const float *p = psh + tid * pstr;
+    for (int g = 0; g < groups; ++g) acc = acc + p[g];
+  }
+  __syncthreads();
+  if (tid < NC * R) psh[tid] = acc;  // chain c = l*R + r
+  __syncthreads();
+  if (tid < R && row0 + tid < rows) {
+    float f[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) f[l] = (l < NL) ? psh[l * R + tid] : 0.0f;
+    out[row0 + tid] = hsum8(f) + psh[NL * R + tid];
+  }
+}
+
+template <int GS, int R>
+void launch_m1_t(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                 const float *scales, const float *sums, int rows, int cols, int groups,
+                 hipStream_t s) {
+  constexpr int NC = (GS == 32) ? 5 : 9;
+  constexpr int IPT = m1_items_per_thread(GS);
+  const size_t smem = (size_t)((cols + 15) & ~15) + 8 * (size_t)groups +
+                      4 * (size_t)NC * R * (groups + 1);
+  static size_t configured = 0;
+  if (smem > configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_m1<GS, R, IPT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = smem;
+  }
+  hipLaunchKernelGGL((k_w4a8_m1<GS, R, IPT>), dim3((rows + R - 1) / R), dim3(kThreads), smem, s,
+                     out, nib, params, q_split, scales, sums, rows, cols, groups);
+}
+
+// Rows per block: the largest power of two whose R*G items fit IPT per
+// thread.  Returns false when one row's groups do not fit (very large K).
+template <int GS>
+bool launch_m1(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+               const float *scales, const float *sums, int rows, int cols, int groups,
+               hipStream_t s) {
+  const int cap = m1_items_per_thread(GS) * kThreads;
+  if (groups > cap) return false;
+  // Phase 2 gives each of the NC*R accumulator chains its own thread.
+  constexpr bool allow32 = ((GS == 32) ? 5 : 9) * 32 <= kThreads;
+  if constexpr (allow32) {
+    if (32 * groups <= cap) {
+      launch_m1_t<GS, 32>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+      return true;
+    }
+  }
+  if (16 * groups <= cap)
+    launch_m1_t<GS, 16>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+  else if (8 * groups <= cap)
+    launch_m1_t<GS, 8>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+  else if (4 * groups <= cap)
+    launch_m1_t<GS, 4>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+  else if (2 * groups <= cap)
+    launch_m1_t<GS, 2>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+  else
+    launch_m1_t<GS, 1>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+  return true;
+}
+
+// Activation staging of the whole K fits comfortably in LDS.
+constexpr size_t kWholeStageBytes = 24 * 1024;
+
+template <int GS, int MT>
+void launch_small_mt(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                     const float *scales, const float *sums, int rows, int cols, int m, int groups,
+                     hipStream_t s) {
+  constexpr int R = 16, PD = 4;
+  const size_t whole = (size_t)std::min(m, MT) * groups * (GS + 8 + 8);
+  if (whole <= kWholeStageBytes)
+    launch_small_t<GS, MT, R, PD, true>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+  else
+    launch_small_t<GS, MT, R, PD, false>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+}
+
+template <int GS>
+void launch_small_gs(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                     const float *scales, const float *sums, int rows, int cols, int m, int groups,
+                     hipStream_t s) {
+  if (m <= 1)
+    launch_small_mt<GS, 1>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+  else if (m <= 2)
+    launch_small_mt<GS, 2>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+  else if (m <= 4)
+    launch_small_mt<GS, 4>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+  else if (m <= 8 || GS > 32)  // groups 64/128 carry 9 chains: at most 8 tokens per tile
+    launch_small_mt<GS, 8>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+  else
+    launch_small_mt<GS, 16>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+}
+
 // --------------------------------------------------------- lane sums dbg --
 
 __global__ void k_lane_sums(int32_t *__restrict__ out, const uint8_t *__restrict__ nib,
@@ -610,71 +1023,164 @@ __global__ void k_rope_apply(float *__restrict__ heads, int nh, int hd,
 
 // ----------------------------------------------------------- attention --
 
-// attention_head_avx2 (layers.rs:1266-1380) for one (token, query head):
-// 8-lane FMA score dots, Schraudolph exp over the 8-aligned body and glibc
-// expf on the tail, 8-lane sum, p = e * (1/sum), out[d] = fma(p_t, v_t[d],
-// out[d]) sequentially over t.
-__global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q,
-                                                   const float *__restrict__ kc,
-                                                   const float *__restrict__ vc, int cap, int pos0,
-                                                   int nh, int nkv, int hd, float scale,
-                                                   float *__restrict__ out) {
-  extern __shared__ float sc[];  // [pos+1] scores, then 8 partial sums
-  __shared__ float red[256];
-  __shared__ float bcast;
-  const int h = blockIdx.x, t = blockIdx.y;
-  const int pos = pos0 + t;
-  const int n = pos + 1;
-  const int kvh = h / (nh / nkv);
-  const float *qh = q + ((size_t)t * nh + h) * hd;
-  const float *kb = kc + (size_t)kvh * cap * hd;
-  const float *vb = vc + (size_t)kvh * cap * hd;
-  const int tid = threadIdx.x;
-  const int c8 = hd / 8;
-  float mx = -INFINITY;
-  for (int s = tid; s < n; s += blockDim.x) {
-    const float *kr = kb + (size_t)s * hd;
-    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int c = 0; c < c8; ++c)
-      for (int j = 0; j < 8; ++j) a[j] = __fmaf_rn(qh[c * 8 + j], kr[c * 8 + j], a[j]);
-    const float v = hsum8(a) * scale;
-    sc[s] = v;
-    mx = fmaxf(mx, v);
+// Attention (attention_head_avx2, layers.rs:1266-1380) in three passes over
+// a score buffer S [t][h][sstride]:
+//   scores   S[s] = hsum8(8-lane FMA dot(q, k_s)) * scale, s < n = pos+1;
+//   softmax  mx = max S; e_s = Schraudolph(S_s - mx) on the first 8*(n/8)
+//            positions and expf on the tail; sum = hsum8 of the 8 lane
+//            chains (lane j adds e_{8i+j} in i order) then the tail in order;
+//            S[s] = e_s * (1/sum);
+//   PV       out[d] = fma(p_s, v_s[d], out[d]) for s = 0..n-1 in order.
+// Every position's score and probability is independent, so the first two
+// passes spread positions over threads; the order-dependent parts (the 8
+// sum chains and each output dimension's FMA chain) run as the reference
+// runs them, one chain per lane.
+
+constexpr int kAttnTile = 64;  // positions per score block (one per lane)
+
+// grid (ceil(nmax / 64), nkv), 256 threads.  Lane = position; the four waves
+// share the (head-in-group, token) pairs.  HD > 0: the key row is held in
+// registers and reused for every pair; HD == 0: runtime head_dim.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q,
+                                                     const float *__restrict__ kc, int cap,
+                                                     int pos0, int m, int nh, int nkv, int hd,
+                                                     float scale, float *__restrict__ S,
+                                                     int sstride) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int s0 = (int)blockIdx.x * kAttnTile;
+  const int s = s0 + lane;
+  const int kvh = blockIdx.y;
+  const int G = nh / nkv;
+  const int nmax = pos0 + m;
+  if (s0 >= nmax) return;
+  const int hdim = HD > 0 ? HD : hd;
+  const float *kr = kc + ((size_t)kvh * cap + (s < nmax ? s : 0)) * hdim;
+  float kreg[HD > 0 ? HD : 1];
+  if constexpr (HD > 0) {
+#pragma unroll
+    for (int c = 0; c < HD / 4; ++c) {
+      const float4 v4 = reinterpret_cast<const float4 *>(kr)[c];
+      kreg[4 * c + 0] = v4.x;
+      kreg[4 * c + 1] = v4.y;
+      kreg[4 * c + 2] = v4.z;
+      kreg[4 * c + 3] = v4.w;
+    }
   }
-  red[tid] = mx;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
-    __syncthreads();
+  // Tokens whose causal window ends before this tile contribute nothing:
+  // token t sees positions <= pos0 + t.
+  const int tfirst = s0 > pos0 ? s0 - pos0 : 0;
+  const int pairs = G * (m - tfirst);
+  for (int pi = wave; pi < pairs; pi += 4) {
+    const int t = tfirst + pi / G;
+    const int h = kvh * G + pi % G;
+    if (s > pos0 + t) continue;
+    const float *qh = q + ((size_t)t * nh + h) * hdim;
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if constexpr (HD > 0) {
+#pragma unroll
+      for (int c = 0; c < HD / 8; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = __fmaf_rn(qh[8 * c + j], kreg[8 * c + j], a[j]);
+    } else {
+      for (int c = 0; c < hdim / 8; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = __fmaf_rn(qh[8 * c + j], kr[8 * c + j], a[j]);
+    }
+    S[((size_t)t * nh + h) * sstride + s] = hsum8(a) * scale;
   }
-  mx = red[0];
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// grid (nh, m), 256 threads; dynamic LDS holds the n exponentials.
+__global__ __launch_bounds__(256) void k_attn_softmax(float *__restrict__ S, int pos0, int nh,
+                                                      int sstride) {
+  extern __shared__ float e[];
+  __shared__ float red[8];
+  __shared__ float bc;
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+  const int n = pos0 + t + 1;
   const int n8 = n / 8;
-  for (int s = tid; s < n; s += blockDim.x) {
-    const float d = sc[s] - mx;
-    sc[s] = (s < n8 * 8) ? rai_exact::schraudolph(d) : rai_exact::expf_glibc(d);
+  float *row = S + ((size_t)t * nh + h) * sstride;
+  float mx = -INFINITY;
+  for (int s = tid; s < n; s += 256) mx = fmaxf(mx, row[s]);
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  for (int s = tid; s < n; s += 256) {
+    const float d = row[s] - mx;
+    e[s] = (s < n8 * 8) ? rai_exact::schraudolph(d) : rai_exact::expf_glibc(d);
   }
   __syncthreads();
   if (tid < 8) {
-    float a = 0.0f;
-    for (int i = 0; i < n8; ++i) a = a + sc[i * 8 + tid];
-    red[tid] = a;
+    float acc = 0.0f;
+    int i = 0;
+    for (; i + 8 <= n8; i += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = e[(i + u) * 8 + tid];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = acc + v[u];
+    }
+    for (; i < n8; ++i) acc = acc + e[i * 8 + tid];
+    red[tid] = acc;
   }
   __syncthreads();
   if (tid == 0) {
     float sum = hsum8(red);
-    for (int s = n8 * 8; s < n; ++s) sum = sum + sc[s];
-    bcast = __fdiv_exact(1.0f, sum);
+    for (int s = n8 * 8; s < n; ++s) sum = sum + e[s];
+    bc = __fdiv_exact(1.0f, sum);
   }
   __syncthreads();
-  const float inv = bcast;
-  for (int s = tid; s < n; s += blockDim.x) sc[s] = sc[s] * inv;
-  __syncthreads();
-  float *o = out + ((size_t)t * nh + h) * hd;
-  for (int d = tid; d < hd; d += blockDim.x) {
-    float a = 0.0f;
-    for (int s = 0; s < n; ++s) a = __fmaf_rn(sc[s], vb[(size_t)s * hd + d], a);
-    o[d] = a;
+  const float inv = bc;
+  for (int s = tid; s < n; s += 256) row[s] = e[s] * inv;
+}
+
+// One 64-lane block per 64 consecutive outputs of out [t][h][d].  When
+// head_dim is a multiple of 64 (UNIFORM) a block lies inside one (t, h) row,
+// so its probabilities are wave-uniform loads.
+template <bool UNIFORM>
+__global__ __launch_bounds__(64) void k_attn_pv(const float *__restrict__ P,
+                                                const float *__restrict__ vc, int cap, int pos0,
+                                                int m, int nh, int nkv, int hd, int sstride,
+                                                float *__restrict__ out) {
+  const int G = nh / nkv;
+  const size_t gid = (size_t)blockIdx.x * 64 + threadIdx.x;
+  const size_t total = (size_t)m * nh * hd;
+  int row, d;
+  if constexpr (UNIFORM) {
+    const int per = hd / 64;
+    row = blockIdx.x / per;
+    d = (blockIdx.x - row * per) * 64 + threadIdx.x;
+  } else {
+    if (gid >= total) return;
+    row = (int)(gid / hd);
+    d = (int)(gid - (size_t)row * hd);
   }
+  const int t = row / nh, h = row - t * nh;
+  const int n = pos0 + t + 1;
+  const float *p = P + (size_t)row * sstride;
+  const float *vb = vc + (size_t)(h / G) * cap * hd + d;
+  float acc = 0.0f;
+  int s = 0;
+  for (; s + 8 <= n; s += 8) {
+    float pv[8], vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      pv[u] = p[s + u];
+      vv[u] = vb[(size_t)(s + u) * hd];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = __fmaf_rn(pv[u], vv[u], acc);
+  }
+  for (; s < n; ++s) acc = __fmaf_rn(p[s], vb[(size_t)s * hd], acc);
+  out[(size_t)row * hd + d] = acc;
 }
 
 // -------------------------------------------------------------- argmax --
@@ -854,6 +1360,27 @@ void launch_w4a8(float *out, const uint8_t *nib, const uint8_t *params, const fl
                  const int8_t *q_nat, const int8_t *q_split, const float *scales,
                  const float *sums, int rows, int cols, int m, int gs, hipStream_t s) {
   const int groups = (cols + gs - 1) / gs;
+  // The whole-K kernel wins where few, long rows leave the streaming kernel
+  // with too few blocks (measured on 1024..32000 x 2048..14336, g32).
+  if (w4a8_fast_path(cols, gs) && m == 1 && cols >= 4096 && rows <= cols) {
+    bool done;
+    if (gs == 32)
+      done = launch_m1<32>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+    else if (gs == 64)
+      done = launch_m1<64>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+    else
+      done = launch_m1<128>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+    if (done) return;
+  }
+  if (w4a8_fast_path(cols, gs) && m <= 16) {
+    if (gs == 32)
+      launch_small_gs<32>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    else if (gs == 64)
+      launch_small_gs<64>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    else
+      launch_small_gs<128>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    return;
+  }
   if (w4a8_fast_path(cols, gs)) {
     if (gs == 32)
       launch_fast_gs<32>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
@@ -914,17 +1441,47 @@ void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, c
                      hd, kc, vc, cap);
 }
 
+size_t attention_scores_floats(int m, int nh, int ctx) {
+  return (size_t)std::min(m, kAttnTokens) * nh * (size_t)((ctx + 3) & ~3);
+}
+
 void launch_attention(const float *q, const float *kc, const float *vc, int cap, int pos0, int m,
-                      int nh, int nkv, int hd, float scale, float *out, hipStream_t s) {
-  const size_t smem = sizeof(float) * (size_t)(pos0 + m);
+                      int nh, int nkv, int hd, float scale, float *out, float *scores,
+                      hipStream_t s) {
   static size_t configured = 0;
-  if (smem > 48 * 1024 && smem > configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attention),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    configured = smem;
+  for (int t0 = 0; t0 < m; t0 += kAttnTokens) {
+    const int mt = std::min(kAttnTokens, m - t0);
+    const int p0 = pos0 + t0;
+    const int nmax = p0 + mt;
+    const int sstride = (nmax + 3) & ~3;
+    const float *qt = q + (size_t)t0 * nh * hd;
+    float *ot = out + (size_t)t0 * nh * hd;
+    const dim3 sg((nmax + kAttnTile - 1) / kAttnTile, nkv);
+    const bool vec = (reinterpret_cast<uintptr_t>(kc) & 15) == 0;
+    if (hd == 128 && vec)
+      hipLaunchKernelGGL(k_attn_scores<128>, sg, dim3(256), 0, s, qt, kc, cap, p0, mt, nh, nkv, hd,
+                         scale, scores, sstride);
+    else if (hd == 64 && vec)
+      hipLaunchKernelGGL(k_attn_scores<64>, sg, dim3(256), 0, s, qt, kc, cap, p0, mt, nh, nkv, hd,
+                         scale, scores, sstride);
+    else
+      hipLaunchKernelGGL(k_attn_scores<0>, sg, dim3(256), 0, s, qt, kc, cap, p0, mt, nh, nkv, hd,
+                         scale, scores, sstride);
+    const size_t smem = sizeof(float) * (size_t)nmax;
+    if (smem > 48 * 1024 && smem > configured) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_softmax),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      configured = smem;
+    }
+    hipLaunchKernelGGL(k_attn_softmax, dim3(nh, mt), dim3(256), smem, s, scores, p0, nh, sstride);
+    const size_t total = (size_t)mt * nh * hd;
+    if (hd % 64 == 0)
+      hipLaunchKernelGGL(k_attn_pv<true>, dim3((unsigned)(total / 64)), dim3(64), 0, s, scores, vc,
+                         cap, p0, mt, nh, nkv, hd, sstride, ot);
+    else
+      hipLaunchKernelGGL(k_attn_pv<false>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s,
+                         scores, vc, cap, p0, mt, nh, nkv, hd, sstride, ot);
   }
-  hipLaunchKernelGGL(k_attention, dim3(nh, m), dim3(256), smem, s, q, kc, vc, cap, pos0, nh, nkv,
-                     hd, scale, out);
 }
 
 void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,

@@ -109,6 +109,17 @@ struct Workspace {
   DevBuf hid, normed, resid, qb, kb, vb, att, ob, gb, ub, mo, logits, am;
   DevBuf q_nat, q_split, qscale, qsum, hq;
   DevBuf err;
+  // Attention score/probability rows; grown to the largest KV capacity seen.
+  DevBuf scores;
+  size_t scores_n = 0;
+  float *attn_scores(const rai_model_config &c, size_t cap) {
+    const size_t n = attention_scores_floats(maxm, (int)c.num_heads, (int)cap);
+    if (n > scores_n) {
+      scores.alloc(n * sizeof(float));
+      scores_n = n;
+    }
+    return scores.as<float>();
+  }
   // MoE
   DevBuf sel, wts, eo, xg, yg, gg, ug, idx, wcol;
   int logit_rows = 0;
@@ -388,6 +399,7 @@ static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0,
       fail(RAI_E_WATERMARK, "KV store at position " + std::to_string(pos0) + " would leave a gap (filled " +
                                 std::to_string(kv.filled[l]) + ")");
   float *hid = w.hid.as<float>(), *normed = w.normed.as<float>(), *resid = w.resid.as<float>();
+  float *scores = w.attn_scores(c, kv.cap);
   for (int li = 0; li < (int)c.num_layers; ++li) {
     const DLayer &L = md.layers[li];
     launch_rmsnorm(hid, L.in_norm, normed, resid, m, H, c.norm_eps, s);
@@ -398,7 +410,7 @@ static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0,
     launch_rope_store(w.qb.as<float>(), w.kb.as<float>(), w.vb.as<float>(), md.rope_cos, md.rope_sin, (int)pos0,
                       m, nh, nkv, hd, kv.kc(li), kv.vc(li), (int)kv.cap, s);
     launch_attention(w.qb.as<float>(), kv.kc(li), kv.vc(li), (int)kv.cap, (int)pos0, m, nh, nkv, hd,
-                     md.attn_scale, w.att.as<float>(), s);
+                     md.attn_scale, w.att.as<float>(), scores, s);
     quantize(md, w.att.as<float>(), m, qd, w, s);
     linear(L.lin[3], w.att.as<float>(), w, w.ob.as<float>(), m, s);
     launch_vec_add(hid, resid, w.ob.as<float>(), (size_t)m * H, s);
@@ -949,8 +961,12 @@ int rai_attention_head_dev(float *out, const float *q, const float *k, const flo
     if (hd == 0 || hd % 8 || hd > 256) rai::fail(RAI_E_SHAPE, "head_dim must be a multiple of 8 up to 256");
     if (pos + 1 > rai::kMaxAttnContext) rai::fail(RAI_E_UNSUPPORTED, "context beyond 16384 positions");
     // One head: q [hd], cache rows [pos+1][hd] viewed as one kv head with cap = pos+1.
-    rai::launch_attention(q, k, v, (int)(pos + 1), (int)pos, 1, 1, 1, (int)hd, scale, out, (hipStream_t)stream);
+    rai::DevBuf scores;
+    scores.alloc(sizeof(float) * rai::attention_scores_floats(1, 1, (int)(pos + 1)));
+    rai::launch_attention(q, k, v, (int)(pos + 1), (int)pos, 1, 1, 1, (int)hd, scale, out, scores.as<float>(),
+                          (hipStream_t)stream);
     HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipStreamSynchronize((hipStream_t)stream));
   });
 }
 

@@ -44,6 +44,18 @@ def test_w4a8_matmul_bit_exact(rai, ora, rows, cols, gs, m):
     assert np.array_equal(_bits(got), _bits(want))
 
 
+@pytest.mark.parametrize("rows,cols,gs", [(100, 4096, 64), (77, 8192, 128), (300, 14336, 32),
+                                          (37, 2048, 64), (65, 32768, 128), (9, 65536, 32)])
+@pytest.mark.parametrize("m", [1, 3, 9])
+def test_w4a8_matmul_wide_k_bit_exact(rai, ora, rows, cols, gs, m):
+    """Long rows at every fast-path group size, row counts that leave a
+    partial row block, and K beyond what one block holds in registers."""
+    nib, params, x = gemv_operands(rows, cols, m, gs, seed=rows + cols + m)
+    want = ora.w4a8_matmul(nib, params, x, rows, cols, m, gs)
+    got = rai.w4a8_matmul(nib, params, x, rows, cols, m, gs)
+    assert np.array_equal(_bits(got), _bits(want)), (rows, cols, gs, m)
+
+
 @pytest.mark.parametrize("rows,cols,gs", SHAPES[:6])
 def test_lane_sums_bit_exact(rai, ora, rows, cols, gs):
     nib, _, x = gemv_operands(rows, cols, 3, gs, seed=cols)
