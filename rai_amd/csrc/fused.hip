@@ -1,0 +1,712 @@
+// gfx950 kernels that fuse the elementwise steps of a layer with the
+// per-group activation quantization the next W4A8 projection needs, and the
+// decode/verify attention.  Same bit-exact contract as kernels.hip: every
+// value is produced in the f32 operation order of rai's AVX2 path
+// (rai-infer/src/layers.rs, gemm.rs).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cstdint>
+#include <utility>
+
+#include "exact_math.h"
+#include "kernels.h"
+
+namespace rai {
+
+namespace {
+
+// Column c of a block-split row: 8-column block b holds its even columns at
+// 8b+0..3 and its odd columns at 8b+4..7 (the q_split layout).
+__device__ __forceinline__ int split_col(int c) {
+  const int j = c & 7;
+  return (c & ~7) + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
+}
+
+// A pointer the compiler must treat as lane-varying: loads through it are
+// vector loads (tracked in order by vmcnt) even when every lane reads the
+// same address.  Scalar loads would be waited for all at once (lgkmcnt(0)),
+// which serialises a software pipeline.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T *vector_ptr(const T *p) {
+  uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  asm volatile("" : "+v"(a));
+  return reinterpret_cast<const __attribute__((address_space(1))) T *>(a);
+}
+
+// Quantize one group held by 8 consecutive lanes (lane j owns the columns
+// 8c + j, c = 0..NB-1, of the group) exactly as quantize_input_split_avx2
+// and compute_input_sums do (gemm.rs:182-212, 280-374):
+//   sum   = ((a0+a4)+(a1+a5))+((a2+a6)+(a3+a7)), a_j = sequential sum of the
+//           lane's values in column order;
+//   scale = absmax/127 (1 when absmax <= 1e-10); q = clamp(rne(v/scale)).
+// All 64 lanes of the wave must call this together.
+// Lanes with ok == false take part in the shuffles and store nothing.
+template <int NB>
+__device__ __forceinline__ void quantize_group8(const float (&v)[NB], int j, int col0, bool ok,
+                                                int8_t *__restrict__ qs, int8_t *__restrict__ qn,
+                                                float *__restrict__ scale_out,
+                                                float *__restrict__ sum_out) {
+  float a = 0.0f, amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+    a = a + v[c];
+    amax = fmaxf(amax, fabsf(v[c]));
+  }
+  // hsum8 in the reference's order via 8-lane shuffles.
+  const float a4 = __shfl(a, (j + 4) & 7, 8);
+  const float b = a + a4;  // lanes 0..3: a_j + a_{j+4}
+  const float b1 = __shfl(b, (j + 1) & 7, 8);
+  const float c = b + b1;  // lane 0: b0+b1, lane 2: b2+b3
+  const float c2 = __shfl(c, (j + 2) & 7, 8);
+  const float total = c + c2;  // lane 0
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+  const float scale = amax > 1e-10f ? amax / 127.0f : 1.0f;
+  const float inv = 1.0f / scale;
+  if (!ok) return;
+#pragma unroll
+  for (int c8 = 0; c8 < NB; ++c8) {
+    float r = rintf(v[c8] * inv);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    const int8_t q = (int8_t)(int)r;
+    const int col = col0 + 8 * c8 + j;
+    qs[split_col(col)] = q;
+    if (qn) qn[col] = q;
+  }
+  if (j == 0) {
+    *scale_out = scale;
+    *sum_out = total;
+  }
+}
+
+// ------------------------------------------------------ RMSNorm + quant --
+
+// rms_norm_avx2 (layers.rs:325-376) of one token row followed by the
+// per-group quantization of the normalised row (gemm.rs:147-374).  One
+// 256-thread block per token; the row is staged in LDS.  The sum of squares
+// runs as the reference's 16 FMA chains (lane c: j = c & 7 over the
+// elements 16i + (c < 8 ? 0 : 8) + j, the trailing 8-block into chains
+// 0..7), then lane-wise sq0 + sq1, hsum8 and the scalar tail.
+template <int GS>
+__global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
+                                                    const float *__restrict__ w,
+                                                    float *__restrict__ normed,
+                                                    int8_t *__restrict__ q_split,
+                                                    int8_t *__restrict__ q_nat,
+                                                    float *__restrict__ scales,
+                                                    float *__restrict__ sums, int n, float eps) {
+  extern __shared__ float xs[];  // [n] row, then [n] weights
+  float *ws = xs + n;
+  __shared__ float chains[16];
+  __shared__ float inv_sh;
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float *row = x + (size_t)t * n;
+  const int n4 = (n % 4 == 0) ? n / 4 : 0;  // rows stay 16-byte aligned
+  for (int i = tid; i < n4; i += 256) {
+    reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(row)[i];
+    reinterpret_cast<float4 *>(ws)[i] = reinterpret_cast<const float4 *>(w)[i];
+  }
+  for (int i = n4 * 4 + tid; i < n; i += 256) {
+    xs[i] = row[i];
+    ws[i] = w[i];
+  }
+  __syncthreads();
+  const int c16 = (n / 8) / 2;
+  const bool extra8 = 16 * c16 + 8 <= n;
+  if (tid < 16) {
+    const int j = tid & 7, off = tid < 8 ? 0 : 8;
+    float a = 0.0f;
+    int i = 0;
+    for (; i + 32 <= c16; i += 32) {
+      float v[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) v[u] = xs[16 * (i + u) + off + j];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) a = __fmaf_rn(v[u], v[u], a);
+    }
+    for (; i < c16; ++i) {
+      const float v = xs[16 * i + off + j];
+      a = __fmaf_rn(v, v, a);
+    }
+    if (tid < 8 && extra8) {
+      const float v = xs[16 * c16 + j];
+      a = __fmaf_rn(v, v, a);
+    }
+    chains[tid] = a;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = chains[j] + chains[8 + j];
+    float sum = ((s[0] + s[4]) + (s[1] + s[5])) + ((s[2] + s[6]) + (s[3] + s[7]));
+    for (int i = 16 * c16 + (extra8 ? 8 : 0); i < n; ++i) sum = sum + xs[i] * xs[i];
+    // Correctly rounded sqrt and divide (the reference's sqrtss / divss).
+    inv_sh = 1.0f / __builtin_sqrtf(sum / (float)n + eps);
+  }
+  __syncthreads();
+  const float inv = inv_sh;
+  if constexpr (GS == 0) {
+    // RMSNorm only (rms_norm / rms_norm_with_residual): out = (x*inv)*w.
+    float *nrow = normed + (size_t)t * n;
+    for (int i = tid; i < n; i += 256) nrow[i] = (xs[i] * inv) * ws[i];
+    return;
+  } else {
+  const int groups = n / GS;
+  constexpr int NB = GS / 8;
+  float *nrow = normed ? normed + (size_t)t * n : nullptr;
+  int8_t *qs = q_split + (size_t)t * n;
+  int8_t *qn = q_nat ? q_nat + (size_t)t * n : nullptr;
+  // 8 lanes per group; every lane of a wave iterates the same number of times
+  // so the group shuffles always see all 64 lanes.
+  const int per_pass = 256 / 8;
+  const int passes = (groups + per_pass - 1) / per_pass;
+  for (int p = 0; p < passes; ++p) {
+    const int g = p * per_pass + tid / 8;
+    const int j = tid & 7;
+    const bool ok = g < groups;
+    const int col0 = (ok ? g : 0) * GS;
+    float v[NB];
+#pragma unroll
+    for (int c = 0; c < NB; ++c) {
+      const int col = col0 + 8 * c + j;
+      v[c] = ok ? (xs[col] * inv) * ws[col] : 0.0f;
+      if (ok && nrow) nrow[col] = v[c];
+    }
+    quantize_group8<NB>(v, j, col0, ok, qs, qn, scales + (size_t)t * groups + g,
+                        sums + (size_t)t * groups + g);
+  }
+  }
+}
+
+// silu_mul_avx2 (layers.rs:850-883) on one token's gate/up rows (n a
+// multiple of 8: every element takes the Schraudolph body) followed by the
+// per-group quantization of the product for the down projection.  Grid
+// (ceil(groups / 32), m), 256 threads, 8 lanes per group.
+template <int GS>
+__global__ __launch_bounds__(256) void k_silu_quant(float *__restrict__ gate,
+                                                    const float *__restrict__ up, int n,
+                                                    int8_t *__restrict__ q_split,
+                                                    int8_t *__restrict__ q_nat,
+                                                    float *__restrict__ scales,
+                                                    float *__restrict__ sums) {
+  constexpr int NB = GS / 8;
+  const int t = blockIdx.y;
+  const int groups = n / GS;
+  const int g = blockIdx.x * 32 + threadIdx.x / 8;
+  const int j = threadIdx.x & 7;
+  const bool ok = g < groups;
+  const int col0 = (ok ? g : 0) * GS;
+  float *gr = gate + (size_t)t * n;
+  const float *ur = up + (size_t)t * n;
+  float v[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+    const int col = col0 + 8 * c + j;
+    if (ok) {
+      const float xv = gr[col];
+      const float e = rai_exact::schraudolph(xv * -1.0f);
+      v[c] = (xv / (1.0f + e)) * ur[col];
+      gr[col] = v[c];
+    } else {
+      v[c] = 0.0f;
+    }
+  }
+  int8_t *qs = q_split + (size_t)t * n;
+  int8_t *qn = q_nat ? q_nat + (size_t)t * n : nullptr;
+  quantize_group8<NB>(v, j, col0, ok, qs, qn, scales + (size_t)t * groups + g,
+                      sums + (size_t)t * groups + g);
+}
+
+// Per-group quantization of m rows of n (quantize_input_split +
+// compute_input_sums, gemm.rs:147-374).  Grid (ceil(groups / 32), m).
+template <int GS>
+__global__ __launch_bounds__(256) void k_quant(const float *__restrict__ x, int n,
+                                               int8_t *__restrict__ q_split,
+                                               int8_t *__restrict__ q_nat,
+                                               float *__restrict__ scales,
+                                               float *__restrict__ sums) {
+  constexpr int NB = GS / 8;
+  const int t = blockIdx.y;
+  const int groups = n / GS;
+  const int g = blockIdx.x * 32 + threadIdx.x / 8;
+  const int j = threadIdx.x & 7;
+  const bool ok = g < groups;
+  const int col0 = (ok ? g : 0) * GS;
+  const float *xr = x + (size_t)t * n;
+  float v[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) v[c] = ok ? xr[col0 + 8 * c + j] : 0.0f;
+  int8_t *qs = q_split + (size_t)t * n;
+  int8_t *qn = q_nat ? q_nat + (size_t)t * n : nullptr;
+  quantize_group8<NB>(v, j, col0, ok, qs, qn, scales + (size_t)t * groups + g,
+                      sums + (size_t)t * groups + g);
+}
+
+// -------------------------------------------------------------- attention --
+//
+// attention_head_avx2 (layers.rs:1266-1380) for every (token, query head) in
+// three kernels over a score buffer S [t][h][sstride]:
+//   scores   S[s] = hsum8(8-lane FMA dot(q, k_s)) * scale for s <= pos;
+//   softmax  mx = max S; e_s = Schraudolph(S_s - mx) on the first
+//            8*floor(n/8) positions, expf on the tail; sum = hsum8 of the 8
+//            lane chains (lane j adds e_{8i+j} in i order) plus the tail in
+//            order; S[s] = e_s * (1/sum);
+//   PV       out[d] = fma(p_s, v_s[d], out[d]) for s = 0..n-1 in order.
+
+constexpr int kScoreTile = 64;  // positions per score block (one per lane)
+
+// grid (ceil(nmax / 64), nkv), 256 threads.  The block stages its 64 key
+// rows in LDS (row stride hd + 1: lanes reading the same column of
+// consecutive rows hit distinct banks); each wave takes (token, head) pairs
+// of the kv group, lane = position.  HD > 0: compile-time head_dim.
+template <int HD>
+__global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q,
+                                                const float *__restrict__ kc, int cap, int pos0,
+                                                int m, int nh, int nkv, int hd_rt, float scale,
+                                                float *__restrict__ S, int sstride) {
+  extern __shared__ float ks[];
+  const int hd = HD > 0 ? HD : hd_rt;
+  const int kstride = hd + 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int s0 = (int)blockIdx.x * kScoreTile;
+  const int kvh = blockIdx.y;
+  const int G = nh / nkv;
+  const int nmax = pos0 + m;
+  const int rows = min(kScoreTile, nmax - s0);
+  const float *kb = kc + ((size_t)kvh * cap + s0) * hd;
+  if constexpr (HD > 0) {
+    // All of the thread's loads are issued before the first LDS store.
+    constexpr int NPT = kScoreTile * (HD / 4) / 256;
+    float4 v4[NPT];
+#pragma unroll
+    for (int u = 0; u < NPT; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      const int r = min(i / (HD / 4), rows - 1), c4 = i % (HD / 4);
+      v4[u] = reinterpret_cast<const float4 *>(kb + (size_t)r * HD)[c4];
+    }
+#pragma unroll
+    for (int u = 0; u < NPT; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      const int r = i / (HD / 4), c4 = i % (HD / 4);
+      float *d = ks + r * kstride + 4 * c4;
+      d[0] = v4[u].x;
+      d[1] = v4[u].y;
+      d[2] = v4[u].z;
+      d[3] = v4[u].w;
+    }
+  } else {
+    for (int i = threadIdx.x; i < rows * (hd / 4); i += 256) {
+      const int r = i / (hd / 4), c4 = i - r * (hd / 4);
+      const float4 v4 = reinterpret_cast<const float4 *>(kb + (size_t)r * hd)[c4];
+      float *d = ks + r * kstride + 4 * c4;
+      d[0] = v4.x;
+      d[1] = v4.y;
+      d[2] = v4.z;
+      d[3] = v4.w;
+    }
+  }
+  __syncthreads();
+  const int s = s0 + lane;
+  const float *kr = ks + lane * kstride;
+  // Token t sees positions <= pos0 + t.
+  const int tfirst = s0 > pos0 ? s0 - pos0 : 0;
+  const int pairs = G * (m - tfirst);
+  for (int pi = wave; pi < pairs; pi += 4) {
+    const int t = tfirst + pi / G;
+    const int h = kvh * G + pi % G;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const auto *qh = vector_ptr(reinterpret_cast<const f4 *>(q + ((size_t)t * nh + h) * hd));
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (lane < rows) {
+      for (int c = 0; c < hd / 8; ++c) {
+        const f4 q0 = qh[2 * c];
+        const f4 q1 = qh[2 * c + 1];
+        const float *k8 = kr + 8 * c;
+        a[0] = __fmaf_rn(q0.x, k8[0], a[0]);
+        a[1] = __fmaf_rn(q0.y, k8[1], a[1]);
+        a[2] = __fmaf_rn(q0.z, k8[2], a[2]);
+        a[3] = __fmaf_rn(q0.w, k8[3], a[3]);
+        a[4] = __fmaf_rn(q1.x, k8[4], a[4]);
+        a[5] = __fmaf_rn(q1.y, k8[5], a[5]);
+        a[6] = __fmaf_rn(q1.z, k8[6], a[6]);
+        a[7] = __fmaf_rn(q1.w, k8[7], a[7]);
+      }
+    }
+    if (lane < rows && s <= pos0 + t) {
+      const float d = ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]));
+      S[((size_t)t * nh + h) * sstride + s] = d * scale;
+    }
+  }
+}
+
+__device__ __forceinline__ float block_max256(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return v;
+}
+
+// grid (nh, m), 256 threads; dynamic LDS holds the n exponentials.
+__global__ __launch_bounds__(256) void k_softmax(float *__restrict__ S, int pos0, int nh,
+                                                 int sstride) {
+  extern __shared__ float e[];
+  __shared__ float red[8];
+  __shared__ float bc;
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+  const int n = pos0 + t + 1;
+  const int n8 = n / 8;
+  float *row = S + ((size_t)t * nh + h) * sstride;
+  float mx = -INFINITY;
+  for (int base = 0; base < n; base += 256 * 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = base + 256 * u + tid;
+      v[u] = s < n ? row[s] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = base + 256 * u + tid;
+      if (s < n) e[s] = v[u];
+      mx = fmaxf(mx, v[u]);
+    }
+  }
+  mx = block_max256(mx, red);
+  for (int s = tid; s < n; s += 256) {
+    const float d = e[s] - mx;
+    e[s] = (s < n8 * 8) ? rai_exact::schraudolph(d) : rai_exact::expf_glibc(d);
+  }
+  __syncthreads();
+  if (tid < 8) {
+    // Chain j adds e[8i + j] for i = 0..n8-1 in order; loads run 16 ahead.
+    float acc = 0.0f;
+    int i = 0;
+    float bufA[16], bufB[16];
+    if (n8 >= 16) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) bufA[u] = e[(u)*8 + tid];
+    }
+    for (; i + 32 <= n8; i += 32) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) bufB[u] = e[(i + 16 + u) * 8 + tid];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc = acc + bufA[u];
+      if (i + 48 <= n8) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) bufA[u] = e[(i + 32 + u) * 8 + tid];
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc = acc + bufB[u];
+    }
+    if (i + 16 <= n8) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc = acc + bufA[u];
+      i += 16;
+    }
+    for (; i < n8; ++i) acc = acc + e[i * 8 + tid];
+    red[tid] = acc;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float sum = ((red[0] + red[4]) + (red[1] + red[5])) + ((red[2] + red[6]) + (red[3] + red[7]));
+    for (int s = n8 * 8; s < n; ++s) sum = sum + e[s];
+    bc = 1.0f / sum;
+  }
+  __syncthreads();
+  const float inv = bc;
+  for (int s = tid; s < n; s += 256) row[s] = e[s] * inv;
+}
+
+// PV with the V stream spread over loader waves.  The V cache is d-major
+// ([kv head][head dim][vstride] floats, vstride a multiple of 64), so the
+// positions of one dim in a chunk are contiguous.  One block per (token, kv
+// head, slice of DL head dims) with NCW compute waves and 8 - NCW loader
+// waves.  Compute lane L = 64w + lane owns the chain of query head
+// kvh*G + L/DL, dim d0 + L%DL, so the G heads of the kv group share every V
+// value.  Loader i fetches chunks i, i + NL, ... (CP positions: the V tile
+// [DL][CP] and the G probability rows) with 16-byte coalesced loads, so NL
+// chunks are in flight while the compute waves work.  Each iteration the
+// owner of the next chunk stores it into the free half of a double-buffered
+// LDS tile (probabilities of positions >= n stored as 0: fma(0, v, acc) ==
+// acc for the finite cached v, and acc is never -0), and the compute waves
+// run the reference's sequential FMA chain over the current chunk, reading
+// 4 positions' V values and (wave-broadcast) probabilities per 16-byte LDS
+// read.  One barrier per chunk.
+template <int DL, int G, int CP>
+struct PvCfg {
+  static constexpr int NCW = G * DL / 64;       // compute waves
+  static constexpr int NL = 8 - NCW;            // loader waves
+  static constexpr int NV = DL * CP / 256;      // V float4 per loader lane per chunk
+  static constexpr int NP = (G * CP / 4 + 63) / 64;  // P float4 per loader lane per chunk
+  static constexpr int STR = CP + 4;            // LDS row stride (floats)
+};
+
+template <int DL, int G, int CP>
+__global__ __launch_bounds__(512) void k_pv_stream(const float *__restrict__ P,
+                                                    const float *__restrict__ vt_g, int vstride,
+                                                    int pos0, int nh, int hd, int sstride,
+                                                    float *__restrict__ out) {
+  using C = PvCfg<DL, G, CP>;
+  constexpr int NCW = C::NCW, NL = C::NL, NV = C::NV, NP = C::NP, STR = C::STR;
+  constexpr int Q4 = CP / 4;  // float4 per tile row
+  __shared__ __align__(16) float vt[2][DL * STR];
+  __shared__ __align__(16) float pt[2][G * STR];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slices = hd / DL;
+  const int kvh = blockIdx.x / slices;
+  const int d0 = (blockIdx.x - kvh * slices) * DL;
+  const int t = blockIdx.y;
+  const int n = pos0 + t + 1;
+  const int nchunks = (n + CP - 1) / CP;
+  const float *vbase = vt_g + ((size_t)kvh * hd + d0) * vstride;
+  const float *pbase = P + ((size_t)t * nh + (size_t)kvh * G) * sstride;
+
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 fv[NV], fp[NP];
+#define RAI_PV_ISSUE(k_)                                                                        \
+  do {                                                                                          \
+    const int s0_ = (k_) * CP;                                                                  \
+    _Pragma("unroll") for (int u = 0; u < NV; ++u) {                                            \
+      const int f = 64 * u + lane; /* float4 index in the [DL][CP] tile */                      \
+      const int q0 = min(s0_ + 4 * (f % Q4), vstride - 4);                                      \
+      fv[u] = *reinterpret_cast<const f4 *>(vbase + (size_t)(f / Q4) * vstride + q0);      \
+    }                                                                                           \
+    _Pragma("unroll") for (int r = 0; r < NP; ++r) {                                            \
+      const int f = 64 * r + lane; /* float4 index in the [G][CP] tile */                       \
+      const int gg = min(f / Q4, G - 1);                                                        \
+      const int q0 = min(s0_ + 4 * (f % Q4), sstride - 4);                                      \
+      fp[r] = *reinterpret_cast<const f4 *>(pbase + (size_t)gg * sstride + q0);            \
+    }                                                                                           \
+  } while (0)
+#define RAI_PV_PUBLISH(k_)                                                                      \
+  do {                                                                                          \
+    const int s0_ = (k_) * CP, b_ = (k_) & 1;                                                   \
+    _Pragma("unroll") for (int u = 0; u < NV; ++u) {                                            \
+      const int f = 64 * u + lane;                                                              \
+      *reinterpret_cast<f4 *>(&vt[b_][(f / Q4) * STR + 4 * (f % Q4)]) = fv[u];              \
+    }                                                                                           \
+    _Pragma("unroll") for (int r = 0; r < NP; ++r) {                                            \
+      const int f = 64 * r + lane;                                                              \
+      if (f < G * Q4) {                                                                         \
+        const int q = 4 * (f % Q4);                                                             \
+        f4 v = fp[r];                                                                       \
+        if (s0_ + q + 0 >= n) v.x = 0.0f;                                                       \
+        if (s0_ + q + 1 >= n) v.y = 0.0f;                                                       \
+        if (s0_ + q + 2 >= n) v.z = 0.0f;                                                       \
+        if (s0_ + q + 3 >= n) v.w = 0.0f;                                                       \
+        *reinterpret_cast<f4 *>(&pt[b_][(f / Q4) * STR + q]) = v;                           \
+      }                                                                                         \
+    }                                                                                           \
+  } while (0)
+
+  const int lw = wave - NCW;  // loader index, negative for compute waves
+  if (lw >= 0 && lw < nchunks) {
+    RAI_PV_ISSUE(lw);
+    if (lw == 0) {
+      RAI_PV_PUBLISH(0);
+      if (NL < nchunks) RAI_PV_ISSUE(NL);
+    }
+  }
+  __syncthreads();
+  const int L = wave * 64 + lane;
+  const int g = L / DL, dd = L - g * DL;
+  float acc = 0.0f;
+  for (int k = 0; k < nchunks; ++k) {
+    if (wave < NCW) {
+      const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
+      const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][g * STR]);
+#pragma unroll 8
+      for (int u = 0; u < Q4; ++u) {
+        const float4 v4 = vr[u];
+        const float4 p4 = pr[u];
+        acc = __fmaf_rn(p4.x, v4.x, acc);
+        acc = __fmaf_rn(p4.y, v4.y, acc);
+        acc = __fmaf_rn(p4.z, v4.z, acc);
+        acc = __fmaf_rn(p4.w, v4.w, acc);
+      }
+    } else if (k + 1 < nchunks && lw == (k + 1) % NL) {
+      RAI_PV_PUBLISH(k + 1);
+      if (k + 1 + NL < nchunks) RAI_PV_ISSUE(k + 1 + NL);
+    }
+    __syncthreads();
+  }
+  if (wave < NCW) out[((size_t)t * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc;
+#undef RAI_PV_ISSUE
+#undef RAI_PV_PUBLISH
+}
+
+// PV for any head_dim: thread per output element, same chain order.  V
+// layout: DMAJOR [kv][hd][vstride], else [kv][cap][hd].
+template <bool DMAJOR>
+__global__ __launch_bounds__(64) void k_pv_any(const float *__restrict__ P,
+                                               const float *__restrict__ vc, int cap, int vstride,
+                                               int pos0, int m, int nh, int nkv, int hd,
+                                               int sstride, float *__restrict__ out) {
+  const int G = nh / nkv;
+  const size_t gid = (size_t)blockIdx.x * 64 + threadIdx.x;
+  if (gid >= (size_t)m * nh * hd) return;
+  const int row = (int)(gid / hd), d = (int)(gid - (size_t)row * hd);
+  const int t = row / nh, h = row - t * nh;
+  const int n = pos0 + t + 1;
+  const float *p = P + (size_t)row * sstride;
+  const size_t step = DMAJOR ? 1 : (size_t)hd;
+  const float *vb = DMAJOR ? vc + ((size_t)(h / G) * hd + d) * vstride
+                           : vc + (size_t)(h / G) * cap * hd + d;
+  float acc = 0.0f;
+  int s = 0;
+  for (; s + 8 <= n; s += 8) {
+    float pv[8], vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      pv[u] = p[s + u];
+      vv[u] = vb[(size_t)(s + u) * step];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = __fmaf_rn(pv[u], vv[u], acc);
+  }
+  for (; s < n; ++s) acc = __fmaf_rn(p[s], vb[(size_t)s * step], acc);
+  out[(size_t)row * hd + d] = acc;
+}
+
+template <int GS>
+void launch_norm_quant_t(const float *x, const float *w, float *normed, int m, int n, float eps,
+                         int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
+                         hipStream_t s) {
+  const size_t smem = 2 * sizeof(float) * (size_t)n;
+  static size_t configured = 0;
+  if (smem > 48 * 1024 && smem > configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_norm_quant<GS>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = smem;
+  }
+  hipLaunchKernelGGL(k_norm_quant<GS>, dim3(m), dim3(256), smem, s, x, w, normed, q_split, q_nat,
+                     scales, sums, n, eps);
+}
+
+template <int GS>
+void launch_silu_quant_t(float *gate, const float *up, int m, int n, int8_t *q_split,
+                         int8_t *q_nat, float *scales, float *sums, hipStream_t s) {
+  const int groups = n / GS;
+  hipLaunchKernelGGL(k_silu_quant<GS>, dim3((groups + 31) / 32, m), dim3(256), 0, s, gate, up, n,
+                     q_split, q_nat, scales, sums);
+}
+
+}  // namespace
+
+void launch_rmsnorm(const float *x, const float *w, float *out, float *resid, int m, int n,
+                    float eps, hipStream_t s) {
+  if (resid)
+    (void)hipMemcpyAsync(resid, x, sizeof(float) * (size_t)m * n, hipMemcpyDeviceToDevice, s);
+  launch_norm_quant_t<0>(x, w, out, m, n, eps, nullptr, nullptr, nullptr, nullptr, s);
+}
+
+bool fused_quant_ok(int n, int gs) {
+  return (gs == 32 || gs == 64 || gs == 128) && n % gs == 0 && n % 8 == 0;
+}
+
+void launch_norm_quant(const float *x, const float *w, float *normed, int m, int n, float eps,
+                       int gs, int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
+                       hipStream_t s) {
+  if (gs == 32)
+    launch_norm_quant_t<32>(x, w, normed, m, n, eps, q_split, q_nat, scales, sums, s);
+  else if (gs == 64)
+    launch_norm_quant_t<64>(x, w, normed, m, n, eps, q_split, q_nat, scales, sums, s);
+  else
+    launch_norm_quant_t<128>(x, w, normed, m, n, eps, q_split, q_nat, scales, sums, s);
+}
+
+void launch_quant(const float *x, int m, int n, int gs, int8_t *q_split, int8_t *q_nat,
+                  float *scales, float *sums, hipStream_t s) {
+  const dim3 grid((n / gs + 31) / 32, m);
+  if (gs == 32)
+    hipLaunchKernelGGL(k_quant<32>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums);
+  else if (gs == 64)
+    hipLaunchKernelGGL(k_quant<64>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums);
+  else
+    hipLaunchKernelGGL(k_quant<128>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums);
+}
+
+void launch_silu_quant(float *gate, const float *up, int m, int n, int gs, int8_t *q_split,
+                       int8_t *q_nat, float *scales, float *sums, hipStream_t s) {
+  if (gs == 32)
+    launch_silu_quant_t<32>(gate, up, m, n, q_split, q_nat, scales, sums, s);
+  else if (gs == 64)
+    launch_silu_quant_t<64>(gate, up, m, n, q_split, q_nat, scales, sums, s);
+  else
+    launch_silu_quant_t<128>(gate, up, m, n, q_split, q_nat, scales, sums, s);
+}
+
+size_t attention_scores_floats(int m, int nh, int ctx) {
+  return (size_t)std::min(m, kAttnTokens) * nh * (size_t)((ctx + 3) & ~3);
+}
+
+void launch_attention(const float *q, const float *kc, const float *vc, int cap, int vstride,
+                      int pos0, int m, int nh, int nkv, int hd, float scale, float *out,
+                      float *scores, hipStream_t s) {
+  static size_t sm_configured = 0, sc_configured = 0;
+  for (int t0 = 0; t0 < m; t0 += kAttnTokens) {
+    const int mt = std::min(kAttnTokens, m - t0);
+    const int p0 = pos0 + t0;
+    const int nmax = p0 + mt;
+    const int sstride = (nmax + 3) & ~3;
+    const float *qt = q + (size_t)t0 * nh * hd;
+    float *ot = out + (size_t)t0 * nh * hd;
+    const dim3 sg((nmax + kScoreTile - 1) / kScoreTile, nkv);
+    const size_t ksm = sizeof(float) * (size_t)kScoreTile * (hd + 1);
+    if (ksm > 48 * 1024 && ksm > sc_configured) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_scores<0>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)ksm);
+      sc_configured = ksm;
+    }
+    if (hd == 128)
+      hipLaunchKernelGGL(k_scores<128>, sg, dim3(256), ksm, s, qt, kc, cap, p0, mt, nh, nkv, hd,
+                         scale, scores, sstride);
+    else if (hd == 64)
+      hipLaunchKernelGGL(k_scores<64>, sg, dim3(256), ksm, s, qt, kc, cap, p0, mt, nh, nkv, hd,
+                         scale, scores, sstride);
+    else
+      hipLaunchKernelGGL(k_scores<0>, sg, dim3(256), ksm, s, qt, kc, cap, p0, mt, nh, nkv, hd,
+                         scale, scores, sstride);
+    const size_t smem = sizeof(float) * (size_t)nmax;
+    if (smem > 48 * 1024 && smem > sm_configured) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_softmax),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      sm_configured = smem;
+    }
+    hipLaunchKernelGGL(k_softmax, dim3(nh, mt), dim3(256), smem, s, scores, p0, nh, sstride);
+    const size_t total = (size_t)mt * nh * hd;
+    const int G = nh / nkv;
+    const int DL = (G == 1) ? 64 : (G == 2) ? 32 : 16;
+    const bool stream = vstride > 0 && vstride % 64 == 0 &&
+                        (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && hd % DL == 0;
+    if (stream) {
+      const dim3 pg(nkv * (hd / DL), mt);
+      if (G == 4)
+        hipLaunchKernelGGL((k_pv_stream<16, 4, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+      else if (G == 8)
+        hipLaunchKernelGGL((k_pv_stream<16, 8, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+      else if (G == 16)
+        hipLaunchKernelGGL((k_pv_stream<16, 16, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+      else if (G == 2)
+        hipLaunchKernelGGL((k_pv_stream<32, 2, 128>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+      else
+        hipLaunchKernelGGL((k_pv_stream<64, 1, 64>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+    } else if (vstride > 0) {
+      hipLaunchKernelGGL(k_pv_any<true>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, scores,
+                         vc, cap, vstride, p0, mt, nh, nkv, hd, sstride, ot);
+    } else {
+      hipLaunchKernelGGL(k_pv_any<false>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, scores,
+                         vc, cap, 0, p0, mt, nh, nkv, hd, sstride, ot);
+    }
+  }
+}
+
+}  // namespace rai

@@ -41,21 +41,38 @@ void launch_embed(const uint32_t *tokens, const uint32_t *ctx, int last, int sta
 
 void launch_rmsnorm(const float *x, const float *w, float *out, float *resid, int m, int n,
                     float eps, hipStream_t s);
+
+// Fused kernels (fused.hip).  fused_quant_ok: the row length and group size
+// the fused quantizing kernels handle (group 32/64/128, whole groups).
+bool fused_quant_ok(int n, int gs);
+// RMSNorm of m rows of n (layers.rs:325-376) + per-group quantization of
+// the result (gemm.rs:147-374); `normed` and `q_nat` may be null.
+void launch_norm_quant(const float *x, const float *w, float *normed, int m, int n, float eps,
+                       int gs, int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
+                       hipStream_t s);
+// Per-group quantization of m rows of n into q_split (q_nat may be null).
+void launch_quant(const float *x, int m, int n, int gs, int8_t *q_split, int8_t *q_nat,
+                  float *scales, float *sums, hipStream_t s);
+// silu_mul (layers.rs:850-883) in place on gate [m][n] + quantization of
+// the product; requires n % 8 == 0.
+void launch_silu_quant(float *gate, const float *up, int m, int n, int gs, int8_t *q_split,
+                       int8_t *q_nat, float *scales, float *sums, hipStream_t s);
 void launch_vec_add(float *h, const float *r, const float *a, size_t n, hipStream_t s);
 void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s);
-// RoPE on q [m][nh*hd] and k [m][nkv*hd] at positions pos0.., then K/V store
-// into the layer's cache [nkv][cap][hd].
+// RoPE on q [m][nh*hd] and k [m][nkv*hd] at positions pos0.., then the
+// KV store: K into kc [nkv][cap][hd], V into vc d-major [nkv][hd][vstride].
 void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
                        int pos0, int m, int nh, int nkv, int hd, float *kc, float *vc, int cap,
-                       hipStream_t s);
-// attention_head_avx2 for every (token, query head).  `scores` is scratch of
-// attention_scores_floats(m, nh, pos0 + m) floats; tokens are processed in
-// groups of kAttnTokens.
+                       int vstride, hipStream_t s);
+// attention_head_avx2 for every (token, query head).  K cache [nkv][cap][hd];
+// V cache d-major [nkv][hd][vstride] when vstride > 0, else [nkv][cap][hd].
+// `scores` is scratch of attention_scores_floats(m, nh, pos0 + m) floats;
+// tokens are processed in groups of kAttnTokens.
 constexpr int kAttnTokens = 64;
 size_t attention_scores_floats(int m, int nh, int ctx);
-void launch_attention(const float *q, const float *kc, const float *vc, int cap, int pos0, int m,
-                      int nh, int nkv, int hd, float scale, float *out, float *scores,
-                      hipStream_t s);
+void launch_attention(const float *q, const float *kc, const float *vc, int cap, int vstride,
+                      int pos0, int m, int nh, int nkv, int hd, float scale, float *out,
+                      float *scores, hipStream_t s);
 // Standalone RoPE of one position (layers.rs:643-726) on heads [nh][hd].
 void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,
                        hipStream_t s);

@@ -868,83 +868,33 @@ __global__ void k_tied_head(float *__restrict__ logits, const uint8_t *__restric
 
 // --------------------------------------------------------------- embed --
 
+// embed_lookup (gemm.rs:1926-1970): out = fl(fl(code*scale) + zero), then
+// *embed_scale when it is not 1.  Grid (m, ceil(hidden / 256)).
 __global__ void k_embed(const uint32_t *__restrict__ tokens, const uint32_t *__restrict__ ctx,
                         int last, int start, const uint8_t *__restrict__ codes,
                         const uint8_t *__restrict__ params, int vocab, int hidden, int egs,
                         int egroups, float embed_scale, float *__restrict__ out, int *err) {
   const int t = blockIdx.x;
+  const int c = blockIdx.y * blockDim.x + threadIdx.x;
   uint32_t tok = tokens ? tokens[t] : (t == 0 ? ctx[last] : ctx[start + t - 1]);
+  if (c >= hidden) return;
   float *o = out + (size_t)t * hidden;
   if (tok >= (uint32_t)vocab) {
-    if (threadIdx.x == 0) atomicExch(err, 1);
-    for (int c = threadIdx.x; c < hidden; c += blockDim.x) o[c] = 0.0f;
+    if (c == 0) atomicExch(err, 1);
+    o[c] = 0.0f;
     return;
   }
   const uint8_t *row = codes + (size_t)tok * hidden;
-  const uint8_t *prow = params + (size_t)tok * egroups * 4;
-  for (int c = threadIdx.x; c < hidden; c += blockDim.x) {
-    const int g = c / egs;
-    const float s = f16bits((uint16_t)(prow[g * 4] | (prow[g * 4 + 1] << 8)));
-    const float z = f16bits((uint16_t)(prow[g * 4 + 2] | (prow[g * 4 + 3] << 8)));
-    float v = (float)row[c] * s + z;
-    if (embed_scale != 1.0f) v = v * embed_scale;
-    o[c] = v;
-  }
+  const uint8_t *prow = params + ((size_t)tok * egroups + c / egs) * 4;
+  const float sc = f16bits((uint16_t)(prow[0] | (prow[1] << 8)));
+  const float z = f16bits((uint16_t)(prow[2] | (prow[3] << 8)));
+  float v = (float)row[c] * sc + z;
+  if (embed_scale != 1.0f) v = v * embed_scale;
+  o[c] = v;
 }
 
-// ------------------------------------------------------------- rmsnorm --
-
-// rms_norm_avx2 (layers.rs:325-376): 16 FMA chains (sq0 lanes 0-7 over
-// elements 16i+j and the trailing 8-block, sq1 lanes over 16i+8+j), lane-wise
-// sq0+sq1, horizontal reduce, scalar tail, inv = 1/sqrt(sum/n + eps),
-// out = (x*inv)*w.  One 64-lane wavefront per token.
-__global__ void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w,
-                          float *__restrict__ out, float *__restrict__ resid, int n, float eps) {
-  const int t = blockIdx.x;
-  const float *row = x + (size_t)t * n;
-  __shared__ float chains[16];
-  __shared__ float inv_sh;
-  const int lane = threadIdx.x;
-  const int c16 = (n / 8) / 2;
-  const bool extra8 = 16 * c16 + 8 <= n;
-  if (lane < 16) {
-    const int j = lane & 7;
-    const int off = (lane < 8) ? 0 : 8;
-    float a = 0.0f;
-    for (int i = 0; i < c16; ++i) {
-      const float v = row[16 * i + off + j];
-      a = __fmaf_rn(v, v, a);
-    }
-    if (lane < 8 && extra8) {
-      const float v = row[16 * c16 + j];
-      a = __fmaf_rn(v, v, a);
-    }
-    chains[lane] = a;
-  }
-  __syncthreads();
-  if (lane == 0) {
-    float s[8];
-    for (int j = 0; j < 8; ++j) s[j] = chains[j] + chains[8 + j];
-    float sum = hsum8(s);
-    for (int i = 16 * c16 + (extra8 ? 8 : 0); i < n; ++i) sum = sum + row[i] * row[i];
-    // Correctly rounded sqrt and divide (the reference's sqrtss / divss).
-    // HIP's __fsqrt_rn maps to the approximate native sqrt unless OCML
-    // rounded operations are enabled, so the builtin is used instead.
-    inv_sh = 1.0f / __builtin_sqrtf(sum / (float)n + eps);
-  }
-  __syncthreads();
-  const float inv = inv_sh;
-  float *o = out + (size_t)t * n;
-  float *rr = resid ? resid + (size_t)t * n : nullptr;
-  for (int i = lane; i < n; i += blockDim.x) {
-    const float v = row[i];
-    o[i] = (v * inv) * w[i];
-    if (rr) rr[i] = v;
-  }
-}
-
-__global__ void k_vec_add(float *__restrict__ h, const float *__restrict__ r,
-                          const float *__restrict__ a, size_t n) {
+// vec_add (layers.rs:503-531): h = r + a; h may alias r.
+__global__ void k_vec_add(float *h, const float *r, const float *__restrict__ a, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) h[i] = r[i] + a[i];
 }
@@ -967,39 +917,44 @@ __global__ void k_silu_mul(float *__restrict__ gate, const float *__restrict__ u
 }
 
 // RoPETable::apply_avx2 (layers.rs:689-726) for q and k, then the KV store
-// (kv_cache.rs:143-172).
+// (kv_cache.rs:143-172).  One thread per (token, head, pair i): rotates
+// (i, i + hd/2) of a q or k head; k threads also store the rotated pair and
+// the matching v pair in the cache.  Grid (m, ceil((nh + nkv) * hd/2 / 256)).
 __global__ void k_rope_store(float *__restrict__ q, float *__restrict__ k,
                              const float *__restrict__ v, const float *__restrict__ cos_t,
                              const float *__restrict__ sin_t, int pos0, int nh, int nkv, int hd,
-                             float *__restrict__ kc, float *__restrict__ vc, int cap) {
+                             float *__restrict__ kc, float *__restrict__ vc, int cap,
+                             int vstride) {
   const int t = blockIdx.x;
   const int pos = pos0 + t;
   const int half = hd / 2;
   const int body = (half / 8) * 8;
-  const float *cr = cos_t + (size_t)pos * half;
-  const float *sr = sin_t + (size_t)pos * half;
-  const int total = (nh + nkv) * half;
-  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
-    const int h = idx / half, i = idx % half;
-    float *b = (h < nh) ? q + ((size_t)t * nh + h) * hd : k + ((size_t)t * nkv + (h - nh)) * hd;
-    const float x0 = b[i], x1 = b[half + i], c = cr[i], s = sr[i];
-    float r0, r1;
-    if (i < body) {
-      r0 = __fmaf_rn(x0, c, -(x1 * s));
-      r1 = __fmaf_rn(x1, c, x0 * s);
-    } else {
-      r0 = x0 * c - x1 * s;
-      r1 = x1 * c + x0 * s;
-    }
-    b[i] = r0;
-    b[half + i] = r1;
+  const int idx = blockIdx.y * blockDim.x + threadIdx.x;
+  if (idx >= (nh + nkv) * half) return;
+  const int h = idx / half, i = idx - h * half;
+  const bool isq = h < nh;
+  const int kh = h - nh;
+  float *b = isq ? q + ((size_t)t * nh + h) * hd : k + ((size_t)t * nkv + kh) * hd;
+  const float x0 = b[i], x1 = b[half + i];
+  const float c = cos_t[(size_t)pos * half + i], sn = sin_t[(size_t)pos * half + i];
+  float r0, r1;
+  if (i < body) {
+    r0 = __fmaf_rn(x0, c, -(x1 * sn));
+    r1 = __fmaf_rn(x1, c, x0 * sn);
+  } else {
+    r0 = x0 * c - x1 * sn;
+    r1 = x1 * c + x0 * sn;
   }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < nkv * hd; idx += blockDim.x) {
-    const int h = idx / hd, d = idx % hd;
-    const size_t dst = ((size_t)h * cap + pos) * hd + d;
-    kc[dst] = k[((size_t)t * nkv + h) * hd + d];
-    vc[dst] = v[((size_t)t * nkv + h) * hd + d];
+  b[i] = r0;
+  b[half + i] = r1;
+  if (!isq) {
+    const size_t dst = ((size_t)kh * cap + pos) * hd;
+    kc[dst + i] = r0;
+    kc[dst + half + i] = r1;
+    const float *vr = v + ((size_t)t * nkv + kh) * hd;
+    float *vd = vc + (size_t)kh * hd * vstride + pos;  // d-major V
+    vd[(size_t)i * vstride] = vr[i];
+    vd[(size_t)(half + i) * vstride] = vr[half + i];
   }
 }
 
@@ -1021,168 +976,6 @@ __global__ void k_rope_apply(float *__restrict__ heads, int nh, int hd,
   }
 }
 
-// ----------------------------------------------------------- attention --
-
-// Attention (attention_head_avx2, layers.rs:1266-1380) in three passes over
-// a score buffer S [t][h][sstride]:
-//   scores   S[s] = hsum8(8-lane FMA dot(q, k_s)) * scale, s < n = pos+1;
-//   softmax  mx = max S; e_s = Schraudolph(S_s - mx) on the first 8*(n/8)
-//            positions and expf on the tail; sum = hsum8 of the 8 lane
-//            chains (lane j adds e_{8i+j} in i order) then the tail in order;
-//            S[s] = e_s * (1/sum);
-//   PV       out[d] = fma(p_s, v_s[d], out[d]) for s = 0..n-1 in order.
-// Every position's score and probability is independent, so the first two
-// passes spread positions over threads; the order-dependent parts (the 8
-// sum chains and each output dimension's FMA chain) run as the reference
-// runs them, one chain per lane.
-
-constexpr int kAttnTile = 64;  // positions per score block (one per lane)
-
-// grid (ceil(nmax / 64), nkv), 256 threads.  Lane = position; the four waves
-// share the (head-in-group, token) pairs.  HD > 0: the key row is held in
-// registers and reused for every pair; HD == 0: runtime head_dim.
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q,
-                                                     const float *__restrict__ kc, int cap,
-                                                     int pos0, int m, int nh, int nkv, int hd,
-                                                     float scale, float *__restrict__ S,
-                                                     int sstride) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int s0 = (int)blockIdx.x * kAttnTile;
-  const int s = s0 + lane;
-  const int kvh = blockIdx.y;
-  const int G = nh / nkv;
-  const int nmax = pos0 + m;
-  if (s0 >= nmax) return;
-  const int hdim = HD > 0 ? HD : hd;
-  const float *kr = kc + ((size_t)kvh * cap + (s < nmax ? s : 0)) * hdim;
-  float kreg[HD > 0 ? HD : 1];
-  if constexpr (HD > 0) {
-#pragma unroll
-    for (int c = 0; c < HD / 4; ++c) {
-      const float4 v4 = reinterpret_cast<const float4 *>(kr)[c];
-      kreg[4 * c + 0] = v4.x;
-      kreg[4 * c + 1] = v4.y;
-      kreg[4 * c + 2] = v4.z;
-      kreg[4 * c + 3] = v4.w;
-    }
-  }
-  // Tokens whose causal window ends before this tile contribute nothing:
-  // token t sees positions <= pos0 + t.
-  const int tfirst = s0 > pos0 ? s0 - pos0 : 0;
-  const int pairs = G * (m - tfirst);
-  for (int pi = wave; pi < pairs; pi += 4) {
-    const int t = tfirst + pi / G;
-    const int h = kvh * G + pi % G;
-    if (s > pos0 + t) continue;
-    const float *qh = q + ((size_t)t * nh + h) * hdim;
-    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if constexpr (HD > 0) {
-#pragma unroll
-      for (int c = 0; c < HD / 8; ++c)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = __fmaf_rn(qh[8 * c + j], kreg[8 * c + j], a[j]);
-    } else {
-      for (int c = 0; c < hdim / 8; ++c)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = __fmaf_rn(qh[8 * c + j], kr[8 * c + j], a[j]);
-    }
-    S[((size_t)t * nh + h) * sstride + s] = hsum8(a) * scale;
-  }
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-
-// grid (nh, m), 256 threads; dynamic LDS holds the n exponentials.
-__global__ __launch_bounds__(256) void k_attn_softmax(float *__restrict__ S, int pos0, int nh,
-                                                      int sstride) {
-  extern __shared__ float e[];
-  __shared__ float red[8];
-  __shared__ float bc;
-  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-  const int n = pos0 + t + 1;
-  const int n8 = n / 8;
-  float *row = S + ((size_t)t * nh + h) * sstride;
-  float mx = -INFINITY;
-  for (int s = tid; s < n; s += 256) mx = fmaxf(mx, row[s]);
-  mx = wave_max(mx);
-  if ((tid & 63) == 0) red[tid >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  for (int s = tid; s < n; s += 256) {
-    const float d = row[s] - mx;
-    e[s] = (s < n8 * 8) ? rai_exact::schraudolph(d) : rai_exact::expf_glibc(d);
-  }
-  __syncthreads();
-  if (tid < 8) {
-    float acc = 0.0f;
-    int i = 0;
-    for (; i + 8 <= n8; i += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = e[(i + u) * 8 + tid];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc = acc + v[u];
-    }
-    for (; i < n8; ++i) acc = acc + e[i * 8 + tid];
-    red[tid] = acc;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float sum = hsum8(red);
-    for (int s = n8 * 8; s < n; ++s) sum = sum + e[s];
-    bc = __fdiv_exact(1.0f, sum);
-  }
-  __syncthreads();
-  const float inv = bc;
-  for (int s = tid; s < n; s += 256) row[s] = e[s] * inv;
-}
-
-// One 64-lane block per 64 consecutive outputs of out [t][h][d].  When
-// head_dim is a multiple of 64 (UNIFORM) a block lies inside one (t, h) row,
-// so its probabilities are wave-uniform loads.
-template <bool UNIFORM>
-__global__ __launch_bounds__(64) void k_attn_pv(const float *__restrict__ P,
-                                                const float *__restrict__ vc, int cap, int pos0,
-                                                int m, int nh, int nkv, int hd, int sstride,
-                                                float *__restrict__ out) {
-  const int G = nh / nkv;
-  const size_t gid = (size_t)blockIdx.x * 64 + threadIdx.x;
-  const size_t total = (size_t)m * nh * hd;
-  int row, d;
-  if constexpr (UNIFORM) {
-    const int per = hd / 64;
-    row = blockIdx.x / per;
-    d = (blockIdx.x - row * per) * 64 + threadIdx.x;
-  } else {
-    if (gid >= total) return;
-    row = (int)(gid / hd);
-    d = (int)(gid - (size_t)row * hd);
-  }
-  const int t = row / nh, h = row - t * nh;
-  const int n = pos0 + t + 1;
-  const float *p = P + (size_t)row * sstride;
-  const float *vb = vc + (size_t)(h / G) * cap * hd + d;
-  float acc = 0.0f;
-  int s = 0;
-  for (; s + 8 <= n; s += 8) {
-    float pv[8], vv[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      pv[u] = p[s + u];
-      vv[u] = vb[(size_t)(s + u) * hd];
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) acc = __fmaf_rn(pv[u], vv[u], acc);
-  }
-  for (; s < n; ++s) acc = __fmaf_rn(p[s], vb[(size_t)s * hd], acc);
-  out[(size_t)row * hd + d] = acc;
-}
-
 // -------------------------------------------------------------- argmax --
 
 __device__ __forceinline__ long long argmax_key(float f, int idx) {
@@ -1192,23 +985,43 @@ __device__ __forceinline__ long long argmax_key(float f, int idx) {
   return ((long long)b << 32) | (long long)(uint32_t)idx;
 }
 
-// sampler.rs:201-208: max by total_cmp, the last maximal index wins.
-__global__ void k_argmax(const float *__restrict__ logits, int vocab, uint32_t *__restrict__ out) {
+// sampler.rs:201-208: max by total_cmp, the last maximal index wins (the
+// key puts the index in the low bits, so the larger index wins a tie).
+// One 1024-thread block per token.
+__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logits, int vocab,
+                                                 uint32_t *__restrict__ out) {
   const int t = blockIdx.x;
   const float *row = logits + (size_t)t * vocab;
   long long best = LLONG_MIN;
-  for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
-    const long long k = argmax_key(row[i], i);
-    best = k > best ? k : best;
+  for (int base = 0; base < vocab; base += 8 * (int)blockDim.x) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;
+      v[u] = i < vocab ? row[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;
+      if (i < vocab) {
+        const long long k = argmax_key(v[u], i);
+        best = k > best ? k : best;
+      }
+    }
   }
-  __shared__ long long red[1024];
-  red[threadIdx.x] = best;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const long long other = __shfl_xor(best, o, 64);
+    best = other > best ? other : best;
+  }
+  __shared__ long long red[16];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
   __syncthreads();
-  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-    if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] > red[threadIdx.x + w] ? red[threadIdx.x] : red[threadIdx.x + w];
-    __syncthreads();
+  if (threadIdx.x == 0) {
+    long long b = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) b = red[w] > b ? red[w] : b;
+    out[t] = (uint32_t)(b & 0xFFFFFFFFll);
   }
-  if (threadIdx.x == 0) out[t] = (uint32_t)(red[0] & 0xFFFFFFFFll);
 }
 
 // ------------------------------------------------------- n-gram search --
@@ -1417,13 +1230,8 @@ void launch_embed(const uint32_t *tokens, const uint32_t *ctx, int last, int sta
                   const uint8_t *codes, const uint8_t *params, int vocab, int hidden, int egs,
                   float embed_scale, float *out, int *err, hipStream_t s) {
   const int egroups = (hidden + egs - 1) / egs;
-  hipLaunchKernelGGL(k_embed, dim3(m), dim3(256), 0, s, tokens, ctx, last, start, codes, params,
+  hipLaunchKernelGGL(k_embed, dim3(m, (hidden + 255) / 256), dim3(256), 0, s, tokens, ctx, last, start, codes, params,
                      vocab, hidden, egs, egroups, embed_scale, out, err);
-}
-
-void launch_rmsnorm(const float *x, const float *w, float *out, float *resid, int m, int n,
-                    float eps, hipStream_t s) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(m), dim3(64), 0, s, x, w, out, resid, n, eps);
 }
 
 void launch_vec_add(float *h, const float *r, const float *a, size_t n, hipStream_t s) {
@@ -1436,52 +1244,10 @@ void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s) 
 
 void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
                        int pos0, int m, int nh, int nkv, int hd, float *kc, float *vc, int cap,
-                       hipStream_t s) {
-  hipLaunchKernelGGL(k_rope_store, dim3(m), dim3(256), 0, s, q, k, v, cos_t, sin_t, pos0, nh, nkv,
-                     hd, kc, vc, cap);
-}
-
-size_t attention_scores_floats(int m, int nh, int ctx) {
-  return (size_t)std::min(m, kAttnTokens) * nh * (size_t)((ctx + 3) & ~3);
-}
-
-void launch_attention(const float *q, const float *kc, const float *vc, int cap, int pos0, int m,
-                      int nh, int nkv, int hd, float scale, float *out, float *scores,
-                      hipStream_t s) {
-  static size_t configured = 0;
-  for (int t0 = 0; t0 < m; t0 += kAttnTokens) {
-    const int mt = std::min(kAttnTokens, m - t0);
-    const int p0 = pos0 + t0;
-    const int nmax = p0 + mt;
-    const int sstride = (nmax + 3) & ~3;
-    const float *qt = q + (size_t)t0 * nh * hd;
-    float *ot = out + (size_t)t0 * nh * hd;
-    const dim3 sg((nmax + kAttnTile - 1) / kAttnTile, nkv);
-    const bool vec = (reinterpret_cast<uintptr_t>(kc) & 15) == 0;
-    if (hd == 128 && vec)
-      hipLaunchKernelGGL(k_attn_scores<128>, sg, dim3(256), 0, s, qt, kc, cap, p0, mt, nh, nkv, hd,
-                         scale, scores, sstride);
-    else if (hd == 64 && vec)
-      hipLaunchKernelGGL(k_attn_scores<64>, sg, dim3(256), 0, s, qt, kc, cap, p0, mt, nh, nkv, hd,
-                         scale, scores, sstride);
-    else
-      hipLaunchKernelGGL(k_attn_scores<0>, sg, dim3(256), 0, s, qt, kc, cap, p0, mt, nh, nkv, hd,
-                         scale, scores, sstride);
-    const size_t smem = sizeof(float) * (size_t)nmax;
-    if (smem > 48 * 1024 && smem > configured) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_softmax),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      configured = smem;
-    }
-    hipLaunchKernelGGL(k_attn_softmax, dim3(nh, mt), dim3(256), smem, s, scores, p0, nh, sstride);
-    const size_t total = (size_t)mt * nh * hd;
-    if (hd % 64 == 0)
-      hipLaunchKernelGGL(k_attn_pv<true>, dim3((unsigned)(total / 64)), dim3(64), 0, s, scores, vc,
-                         cap, p0, mt, nh, nkv, hd, sstride, ot);
-    else
-      hipLaunchKernelGGL(k_attn_pv<false>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s,
-                         scores, vc, cap, p0, mt, nh, nkv, hd, sstride, ot);
-  }
+                       int vstride, hipStream_t s) {
+  const int pairs = (nh + nkv) * (hd / 2);
+  hipLaunchKernelGGL(k_rope_store, dim3(m, (pairs + 255) / 256), dim3(256), 0, s, q, k, v, cos_t, sin_t, pos0, nh, nkv,
+                     hd, kc, vc, cap, vstride);
 }
 
 void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,

@@ -95,10 +95,13 @@ struct rai_kv {
   rai_model *model = nullptr;
   int layers = 0, nkv = 0, hd = 0;
   size_t cap = 0;
-  DevBuf k, v;  // [layer][nkv][cap][hd]
+  size_t vstride = 0;  // cap rounded up to 64: the d-major V row length
+  DevBuf k, v;         // K [layer][nkv][cap][hd]; V d-major [layer][nkv][hd][vstride]
   std::vector<size_t> filled;
   float *kc(int l) const { return k.as<float>() + (size_t)l * nkv * cap * hd; }
-  float *vc(int l) const { return v.as<float>() + (size_t)l * nkv * cap * hd; }
+  float *vc(int l) const { return v.as<float>() + (size_t)l * nkv * hd * vstride; }
+  size_t k_bytes() const { return (size_t)layers * nkv * cap * hd * sizeof(float); }
+  size_t v_bytes() const { return (size_t)layers * nkv * hd * vstride * sizeof(float); }
 };
 
 namespace rai {
@@ -106,7 +109,7 @@ namespace rai {
 // Per-context scratch for up to `maxm` tokens.
 struct Workspace {
   int maxm = 0;
-  DevBuf hid, normed, resid, qb, kb, vb, att, ob, gb, ub, mo, logits, am;
+  DevBuf hid, normed, qb, kb, vb, att, ob, gb, ub, mo, logits, am;
   DevBuf q_nat, q_split, qscale, qsum, hq;
   DevBuf err;
   // Attention score/probability rows; grown to the largest KV capacity seen.
@@ -134,7 +137,6 @@ struct Workspace {
     auto f = [&](DevBuf &b, size_t n) { b.alloc(n * sizeof(float) * maxm); };
     f(hid, H);
     f(normed, H);
-    f(resid, H);
     f(qb, qd);
     f(kb, kvd);
     f(vb, kvd);
@@ -325,8 +327,12 @@ static void linear(const DLinear &L, const float *x, const Workspace &w, float *
 
 static void quantize(const rai_model &md, const float *x, int m, int k, const Workspace &w,
                      hipStream_t s) {
-  launch_quantize(x, m, k, md.cfg.group_size, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
-                  w.qscale.as<float>(), w.qsum.as<float>(), s);
+  if (fused_quant_ok(k, md.cfg.group_size))
+    launch_quant(x, m, k, md.cfg.group_size, w.q_split.as<int8_t>(), nullptr, w.qscale.as<float>(),
+                 w.qsum.as<float>(), s);
+  else
+    launch_quantize(x, m, k, md.cfg.group_size, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
+                    w.qscale.as<float>(), w.qsum.as<float>(), s);
 }
 
 // The MLP of a sparse layer: mlp_block's MoE arm (model.rs:208-261) for
@@ -398,34 +404,50 @@ static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0,
     if (pos0 > kv.filled[l])
       fail(RAI_E_WATERMARK, "KV store at position " + std::to_string(pos0) + " would leave a gap (filled " +
                                 std::to_string(kv.filled[l]) + ")");
-  float *hid = w.hid.as<float>(), *normed = w.normed.as<float>(), *resid = w.resid.as<float>();
+  float *hid = w.hid.as<float>(), *normed = w.normed.as<float>();
   float *scores = w.attn_scores(c, kv.cap);
+  const int gs = c.group_size;
+  // enter_block (model.rs:319-337): RMSNorm, then one quantization of the
+  // normalised rows shared by the projections that read them (the
+  // reference re-quantizes per projection; the result is identical).
+  auto norm_then_quant = [&](const float *wn) {
+    if (fused_quant_ok(H, gs)) {
+      launch_norm_quant(hid, wn, normed, m, H, c.norm_eps, gs, w.q_split.as<int8_t>(), nullptr,
+                        w.qscale.as<float>(), w.qsum.as<float>(), s);
+    } else {
+      launch_rmsnorm(hid, wn, normed, nullptr, m, H, c.norm_eps, s);
+      quantize(md, normed, m, H, w, s);
+    }
+  };
   for (int li = 0; li < (int)c.num_layers; ++li) {
     const DLayer &L = md.layers[li];
-    launch_rmsnorm(hid, L.in_norm, normed, resid, m, H, c.norm_eps, s);
-    quantize(md, normed, m, H, w, s);
+    norm_then_quant(L.in_norm);
     linear(L.lin[0], normed, w, w.qb.as<float>(), m, s);
     linear(L.lin[1], normed, w, w.kb.as<float>(), m, s);
     linear(L.lin[2], normed, w, w.vb.as<float>(), m, s);
     launch_rope_store(w.qb.as<float>(), w.kb.as<float>(), w.vb.as<float>(), md.rope_cos, md.rope_sin, (int)pos0,
-                      m, nh, nkv, hd, kv.kc(li), kv.vc(li), (int)kv.cap, s);
-    launch_attention(w.qb.as<float>(), kv.kc(li), kv.vc(li), (int)kv.cap, (int)pos0, m, nh, nkv, hd,
+                      m, nh, nkv, hd, kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, s);
+    launch_attention(w.qb.as<float>(), kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, (int)pos0, m, nh, nkv, hd,
                      md.attn_scale, w.att.as<float>(), scores, s);
     quantize(md, w.att.as<float>(), m, qd, w, s);
     linear(L.lin[3], w.att.as<float>(), w, w.ob.as<float>(), m, s);
-    launch_vec_add(hid, resid, w.ob.as<float>(), (size_t)m * H, s);
-    launch_rmsnorm(hid, L.post_norm, normed, resid, m, H, c.norm_eps, s);
+    launch_vec_add(hid, hid, w.ob.as<float>(), (size_t)m * H, s);
+    norm_then_quant(L.post_norm);
     if (c.num_experts > 0) {
       moe_block(md, L, w, m, s);
     } else {
-      quantize(md, normed, m, H, w, s);
       linear(L.lin[4], normed, w, w.gb.as<float>(), m, s);
       linear(L.lin[5], normed, w, w.ub.as<float>(), m, s);
-      launch_silu_mul(w.gb.as<float>(), w.ub.as<float>(), m, F, s);
-      quantize(md, w.gb.as<float>(), m, F, w, s);
+      if (fused_quant_ok(F, gs)) {
+        launch_silu_quant(w.gb.as<float>(), w.ub.as<float>(), m, F, gs, w.q_split.as<int8_t>(), nullptr,
+                          w.qscale.as<float>(), w.qsum.as<float>(), s);
+      } else {
+        launch_silu_mul(w.gb.as<float>(), w.ub.as<float>(), m, F, s);
+        quantize(md, w.gb.as<float>(), m, F, w, s);
+      }
       linear(L.lin[6], w.gb.as<float>(), w, w.mo.as<float>(), m, s);
     }
-    launch_vec_add(hid, resid, w.mo.as<float>(), (size_t)m * H, s);
+    launch_vec_add(hid, hid, w.mo.as<float>(), (size_t)m * H, s);
   }
   for (int l = 0; l < kv.layers; ++l) kv.filled[l] = std::max(kv.filled[l], pos0 + m);
 }
@@ -435,11 +457,17 @@ static void logits(rai_model &md, Workspace &w, int m, hipStream_t s) {
   const rai_model_config &c = md.cfg;
   const int H = c.hidden_size, V = c.vocab_size;
   if (m > w.logit_rows) fail(RAI_E_SHAPE, "logit rows exceed the workspace");
-  launch_rmsnorm(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), nullptr, m, H, c.norm_eps, s);
   if (!md.tied) {
-    quantize(md, w.normed.as<float>(), m, H, w, s);
+    if (fused_quant_ok(H, c.group_size)) {
+      launch_norm_quant(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), m, H, c.norm_eps, c.group_size,
+                        w.q_split.as<int8_t>(), nullptr, w.qscale.as<float>(), w.qsum.as<float>(), s);
+    } else {
+      launch_rmsnorm(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), nullptr, m, H, c.norm_eps, s);
+      quantize(md, w.normed.as<float>(), m, H, w, s);
+    }
     linear(md.lm_head, w.normed.as<float>(), w, w.logits.as<float>(), m, s);
   } else {
+    launch_rmsnorm(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), nullptr, m, H, c.norm_eps, s);
     launch_tied_lm_head(w.logits.as<float>(), w.normed.as<float>(), md.emb_codes, md.emb_params, V, H,
                         c.embed_group_size, m, w.hq.as<int8_t>(), w.qscale.as<float>(), w.qsum.as<float>(), s);
   }
@@ -505,11 +533,11 @@ static void kv_init(rai_kv &kv, rai_model &m, size_t max_ctx) {
   kv.nkv = c.num_kv_heads;
   kv.hd = c.head_dim;
   kv.cap = std::min<size_t>(max_ctx, c.max_context);
-  const size_t bytes = (size_t)kv.layers * kv.nkv * kv.cap * kv.hd * sizeof(float);
-  kv.k.alloc(bytes);
-  kv.v.alloc(bytes);
-  HIP_CHECK(hipMemset(kv.k.p, 0, bytes));
-  HIP_CHECK(hipMemset(kv.v.p, 0, bytes));
+  kv.vstride = (kv.cap + 63) & ~size_t(63);
+  kv.k.alloc(kv.k_bytes());
+  kv.v.alloc(kv.v_bytes());
+  HIP_CHECK(hipMemset(kv.k.p, 0, kv.k_bytes()));
+  HIP_CHECK(hipMemset(kv.v.p, 0, kv.v_bytes()));
   kv.filled.assign(kv.layers, 0);
 }
 
@@ -703,9 +731,8 @@ int rai_kv_filled(const rai_kv *kv, size_t layer, size_t *out) {
 int rai_kv_clear(rai_kv *kv) {
   RAI_API_BODY({
     if (!kv) rai::fail(RAI_E_ARG, "null argument");
-    const size_t bytes = (size_t)kv->layers * kv->nkv * kv->cap * kv->hd * sizeof(float);
-    HIP_CHECK(hipMemset(kv->k.p, 0, bytes));
-    HIP_CHECK(hipMemset(kv->v.p, 0, bytes));
+    HIP_CHECK(hipMemset(kv->k.p, 0, kv->k_bytes()));
+    HIP_CHECK(hipMemset(kv->v.p, 0, kv->v_bytes()));
     std::fill(kv->filled.begin(), kv->filled.end(), 0);
   });
 }
@@ -717,8 +744,15 @@ int rai_kv_read(const rai_kv *kv, size_t layer, size_t head, size_t pos, int whi
     if (pos >= kv->filled[layer])
       rai::fail(RAI_E_WATERMARK, "KV read at unwritten position " + std::to_string(pos) + " (filled " +
                                      std::to_string(kv->filled[layer]) + ")");
-    const float *base = which == 0 ? kv->kc((int)layer) : kv->vc((int)layer);
-    HIP_CHECK(hipMemcpy(out, base + (head * kv->cap + pos) * kv->hd, kv->hd * sizeof(float), hipMemcpyDeviceToHost));
+    if (which == 0) {
+      const float *base = kv->kc((int)layer);
+      HIP_CHECK(hipMemcpy(out, base + (head * kv->cap + pos) * kv->hd, kv->hd * sizeof(float), hipMemcpyDeviceToHost));
+    } else {
+      // d-major V: the row's hd values are vstride floats apart.
+      const float *base = kv->vc((int)layer) + head * kv->hd * kv->vstride + pos;
+      HIP_CHECK(hipMemcpy2D(out, sizeof(float), base, kv->vstride * sizeof(float), sizeof(float), kv->hd,
+                            hipMemcpyDeviceToHost));
+    }
   });
 }
 
@@ -963,7 +997,7 @@ int rai_attention_head_dev(float *out, const float *q, const float *k, const flo
     // One head: q [hd], cache rows [pos+1][hd] viewed as one kv head with cap = pos+1.
     rai::DevBuf scores;
     scores.alloc(sizeof(float) * rai::attention_scores_floats(1, 1, (int)(pos + 1)));
-    rai::launch_attention(q, k, v, (int)(pos + 1), (int)pos, 1, 1, 1, (int)hd, scale, out, scores.as<float>(),
+    rai::launch_attention(q, k, v, (int)(pos + 1), 0, (int)pos, 1, 1, 1, (int)hd, scale, out, scores.as<float>(),
                           (hipStream_t)stream);
     HIP_CHECK(hipGetLastError());
     HIP_CHECK(hipStreamSynchronize((hipStream_t)stream));
