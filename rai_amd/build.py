@@ -23,7 +23,7 @@ ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall",
           "-I", os.path.join(ROOT, "include"), "-I", CSRC]
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-SOURCES = ["kernels.hip", "fused.hip", "runtime.hip", "format.cpp", "synth.cpp"]
+SOURCES = ["kernels.hip", "fused.hip", "gemv.hip", "runtime.hip", "format.cpp", "synth.cpp"]
 
 
 def _compile(src: str) -> str:

@@ -18,9 +18,24 @@ void launch_quantize(const float *x, int m, int k, int gs, int8_t *q_nat, int8_t
                      float *scales, float *sums, hipStream_t s);
 
 // w4a8 matmul over already-quantized activations (see gemm.rs:1774-1919).
+// `qa` (may be null): the activations packed by launch_qa_pack, which
+// enables the matrix-core kernel for 2..kMfmaMaxTokens tokens at group 32.
 void launch_w4a8(float *out, const uint8_t *nib, const uint8_t *params, const float *x,
                  const int8_t *q_nat, const int8_t *q_split, const float *scales,
-                 const float *sums, int rows, int cols, int m, int gs, hipStream_t s);
+                 const float *sums, int rows, int cols, int m, int gs, hipStream_t s,
+                 const _Float16 *qa = nullptr);
+
+// Matrix-core W4A8 (gemv.hip): group 32, K a multiple of 256, 2..16 tokens.
+constexpr int kMfmaMaxTokens = 16;
+bool w4a8_mfma_path(int rows, int cols, int m, int gs);
+// Halves of the packed activation buffer for m tokens of `cols` columns.
+size_t qa_pack_halves(int m, int cols);
+// Packs block-split int8 activations [m][cols] into the MFMA A-operand
+// layout (f16, zero rows for the padding tokens of the last 4-token group).
+void launch_qa_pack(const int8_t *q_split, int m, int cols, _Float16 *qa, hipStream_t s);
+bool launch_w4a8_mfma(float *out, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
+                      const float *scales, const float *sums, int rows, int cols, int m, int gs,
+                      hipStream_t s);
 // True when launch_w4a8 takes the tiled fast path for this shape.
 bool w4a8_fast_path(int cols, int gs);
 

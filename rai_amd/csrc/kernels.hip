@@ -1171,8 +1171,10 @@ bool w4a8_fast_path(int cols, int gs) {
 
 void launch_w4a8(float *out, const uint8_t *nib, const uint8_t *params, const float *x,
                  const int8_t *q_nat, const int8_t *q_split, const float *scales,
-                 const float *sums, int rows, int cols, int m, int gs, hipStream_t s) {
+                 const float *sums, int rows, int cols, int m, int gs, hipStream_t s,
+                 const _Float16 *qa) {
   const int groups = (cols + gs - 1) / gs;
+  if (launch_w4a8_mfma(out, nib, params, qa, scales, sums, rows, cols, m, gs, s)) return;
   // The whole-K kernel wins where few, long rows leave the streaming kernel
   // with too few blocks (measured on 1024..32000 x 2048..14336, g32).
   if (w4a8_fast_path(cols, gs) && m == 1 && cols >= 4096 && rows <= cols) {

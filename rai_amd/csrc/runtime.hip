@@ -111,6 +111,7 @@ struct Workspace {
   int maxm = 0;
   DevBuf hid, normed, qb, kb, vb, att, ob, gb, ub, mo, logits, am;
   DevBuf q_nat, q_split, qscale, qsum, hq;
+  DevBuf qa;  // activations packed for the matrix-core W4A8 kernel (<= 16 tokens)
   DevBuf err;
   // Attention score/probability rows; grown to the largest KV capacity seen.
   DevBuf scores;
@@ -149,6 +150,7 @@ struct Workspace {
     am.alloc(sizeof(uint32_t) * maxm);
     q_nat.alloc(K * maxm);
     q_split.alloc(K * maxm);
+    qa.alloc(sizeof(_Float16) * qa_pack_halves(std::min(maxm, kMfmaMaxTokens), (int)K));
     hq.alloc(H * maxm);
     qscale.alloc(sizeof(float) * G * maxm);
     qsum.alloc(sizeof(float) * G * maxm);
@@ -322,7 +324,15 @@ static void upload_model(rai_model &m, const uint8_t *img, size_t len, int max_g
 static void linear(const DLinear &L, const float *x, const Workspace &w, float *out, int m,
                    hipStream_t s) {
   launch_w4a8(out, L.nib, L.params, x, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
-              w.qscale.as<float>(), w.qsum.as<float>(), L.rows, L.cols, m, L.gs, s);
+              w.qscale.as<float>(), w.qsum.as<float>(), L.rows, L.cols, m, L.gs, s,
+              w.qa.as<_Float16>());
+}
+
+// After any quantization of m rows of k columns into the workspace: pack
+// the activations for the matrix-core kernel when it applies.
+static void pack_for_mfma(const rai_model &md, int m, int k, const Workspace &w, hipStream_t s) {
+  if (w4a8_mfma_path(1, k, m, md.cfg.group_size))
+    launch_qa_pack(w.q_split.as<int8_t>(), m, k, w.qa.as<_Float16>(), s);
 }
 
 static void quantize(const rai_model &md, const float *x, int m, int k, const Workspace &w,
@@ -333,6 +343,7 @@ static void quantize(const rai_model &md, const float *x, int m, int k, const Wo
   else
     launch_quantize(x, m, k, md.cfg.group_size, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
                     w.qscale.as<float>(), w.qsum.as<float>(), s);
+  pack_for_mfma(md, m, k, w, s);
 }
 
 // The MLP of a sparse layer: mlp_block's MoE arm (model.rs:208-261) for
@@ -414,6 +425,7 @@ static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0,
     if (fused_quant_ok(H, gs)) {
       launch_norm_quant(hid, wn, normed, m, H, c.norm_eps, gs, w.q_split.as<int8_t>(), nullptr,
                         w.qscale.as<float>(), w.qsum.as<float>(), s);
+      pack_for_mfma(md, m, H, w, s);
     } else {
       launch_rmsnorm(hid, wn, normed, nullptr, m, H, c.norm_eps, s);
       quantize(md, normed, m, H, w, s);
@@ -441,6 +453,7 @@ static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0,
       if (fused_quant_ok(F, gs)) {
         launch_silu_quant(w.gb.as<float>(), w.ub.as<float>(), m, F, gs, w.q_split.as<int8_t>(), nullptr,
                           w.qscale.as<float>(), w.qsum.as<float>(), s);
+        pack_for_mfma(md, m, F, w, s);
       } else {
         launch_silu_mul(w.gb.as<float>(), w.ub.as<float>(), m, F, s);
         quantize(md, w.gb.as<float>(), m, F, w, s);
@@ -461,6 +474,7 @@ static void logits(rai_model &md, Workspace &w, int m, hipStream_t s) {
     if (fused_quant_ok(H, c.group_size)) {
       launch_norm_quant(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), m, H, c.norm_eps, c.group_size,
                         w.q_split.as<int8_t>(), nullptr, w.qscale.as<float>(), w.qsum.as<float>(), s);
+      pack_for_mfma(md, m, H, w, s);
     } else {
       launch_rmsnorm(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), nullptr, m, H, c.norm_eps, s);
       quantize(md, w.normed.as<float>(), m, H, w, s);
@@ -838,8 +852,14 @@ int rai_w4a8_matmul_dev(float *out, const uint8_t *nib, const uint8_t *params, c
     su.alloc(m * groups * 4);
     rai::launch_quantize(x, (int)m, (int)cols, (int)gs, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
                          su.as<float>(), s);
+    rai::DevBuf qa;
+    const bool mfma = rai::w4a8_mfma_path((int)rows, (int)cols, (int)m, (int)gs);
+    if (mfma) {
+      qa.alloc(sizeof(_Float16) * rai::qa_pack_halves((int)m, (int)cols));
+      rai::launch_qa_pack(qs.as<int8_t>(), (int)m, (int)cols, qa.as<_Float16>(), s);
+    }
     rai::launch_w4a8(out, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(), su.as<float>(),
-                     (int)rows, (int)cols, (int)m, (int)gs, s);
+                     (int)rows, (int)cols, (int)m, (int)gs, s, mfma ? qa.as<_Float16>() : nullptr);
     HIP_CHECK(hipGetLastError());
     HIP_CHECK(hipStreamSynchronize(s));  // scratch is freed on return
   });
@@ -864,9 +884,15 @@ int rai_w4a8_time_dev(float *out, const uint8_t *nib, const uint8_t *params, con
     HIP_CHECK(hipEventCreate(&e1));
     rai::launch_quantize(x, (int)m, (int)cols, (int)gs, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
                          su.as<float>(), s);
+    rai::DevBuf qa;
+    const bool mfma = rai::w4a8_mfma_path((int)rows, (int)cols, (int)m, (int)gs);
+    if (mfma) {
+      qa.alloc(sizeof(_Float16) * rai::qa_pack_halves((int)m, (int)cols));
+      rai::launch_qa_pack(qs.as<int8_t>(), (int)m, (int)cols, qa.as<_Float16>(), s);
+    }
     auto run = [&] {
       rai::launch_w4a8(out, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(), su.as<float>(),
-                       (int)rows, (int)cols, (int)m, (int)gs, s);
+                       (int)rows, (int)cols, (int)m, (int)gs, s, mfma ? qa.as<_Float16>() : nullptr);
     };
     run();  // warm-up
     HIP_CHECK(hipEventRecord(e0, s));

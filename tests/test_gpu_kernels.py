@@ -56,6 +56,19 @@ def test_w4a8_matmul_wide_k_bit_exact(rai, ora, rows, cols, gs, m):
     assert np.array_equal(_bits(got), _bits(want)), (rows, cols, gs, m)
 
 
+@pytest.mark.parametrize("rows,cols", [(100, 512), (256, 4096), (1000, 2048), (17, 14336)])
+@pytest.mark.parametrize("m", [2, 3, 4, 8, 12, 16])
+def test_w4a8_matrix_core_path_bit_exact(rai, ora, rows, cols, m):
+    """Group 32, K a multiple of 256, 2..16 tokens: the matrix-core kernel
+    (exact integer products in f16 MFMA, reference-order f32 epilogue),
+    including row counts that leave partial 16-row tiles and token counts
+    that leave partial 4-token groups."""
+    nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + 3 * cols + m)
+    want = ora.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    got = rai.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    assert np.array_equal(_bits(got), _bits(want)), (rows, cols, m)
+
+
 @pytest.mark.parametrize("rows,cols,gs", SHAPES[:6])
 def test_lane_sums_bit_exact(rai, ora, rows, cols, gs):
     nib, _, x = gemv_operands(rows, cols, 3, gs, seed=cols)
