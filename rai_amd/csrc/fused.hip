@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
 // (ceil(groups / 32), m), 256 threads, 8 lanes per group.
 template <int GS>
 __global__ __launch_bounds__(256) void k_silu_quant(float *__restrict__ gate,
-                                                    const float *__restrict__ up, int n,
+                                                    const float *__restrict__ up, int n, int ld,
                                                     int8_t *__restrict__ q_split,
                                                     int8_t *__restrict__ q_nat,
                                                     float *__restrict__ scales,
@@ -199,8 +199,8 @@ __global__ __launch_bounds__(256) void k_silu_quant(float *__restrict__ gate,
   const int j = threadIdx.x & 7;
   const bool ok = g < groups;
   const int col0 = (ok ? g : 0) * GS;
-  float *gr = gate + (size_t)t * n;
-  const float *ur = up + (size_t)t * n;
+  float *gr = gate + (size_t)t * ld;
+  const float *ur = up + (size_t)t * ld;
   float v[NB];
 #pragma unroll
   for (int c = 0; c < NB; ++c) {
@@ -263,7 +263,7 @@ constexpr int kScoreTile = 64;  // positions per score block (one per lane)
 // consecutive rows hit distinct banks); each wave takes (token, head) pairs
 // of the kv group, lane = position.  HD > 0: compile-time head_dim.
 template <int HD>
-__global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q,
+__global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int q_ld,
                                                 const float *__restrict__ kc, int cap, int pos0,
                                                 int m, int nh, int nkv, int hd_rt, float scale,
                                                 float *__restrict__ S, int sstride) {
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q,
     const int t = tfirst + pi / G;
     const int h = kvh * G + pi % G;
     typedef float f4 __attribute__((ext_vector_type(4)));
-    const auto *qh = vector_ptr(reinterpret_cast<const f4 *>(q + ((size_t)t * nh + h) * hd));
+    const auto *qh = vector_ptr(reinterpret_cast<const f4 *>(q + (size_t)t * q_ld + (size_t)h * hd));
     float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (lane < rows) {
       for (int c = 0; c < hd / 8; ++c) {
@@ -592,11 +592,11 @@ void launch_norm_quant_t(const float *x, const float *w, float *normed, int m, i
 }
 
 template <int GS>
-void launch_silu_quant_t(float *gate, const float *up, int m, int n, int8_t *q_split,
+void launch_silu_quant_t(float *gate, const float *up, int m, int n, int ld, int8_t *q_split,
                          int8_t *q_nat, float *scales, float *sums, hipStream_t s) {
   const int groups = n / GS;
   hipLaunchKernelGGL(k_silu_quant<GS>, dim3((groups + 31) / 32, m), dim3(256), 0, s, gate, up, n,
-                     q_split, q_nat, scales, sums);
+                     ld, q_split, q_nat, scales, sums);
 }
 
 }  // namespace
@@ -634,30 +634,31 @@ void launch_quant(const float *x, int m, int n, int gs, int8_t *q_split, int8_t 
     hipLaunchKernelGGL(k_quant<128>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums);
 }
 
-void launch_silu_quant(float *gate, const float *up, int m, int n, int gs, int8_t *q_split,
-                       int8_t *q_nat, float *scales, float *sums, hipStream_t s) {
+void launch_silu_quant(float *gate, const float *up, int m, int n, int ld, int gs,
+                       int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
+                       hipStream_t s) {
   if (gs == 32)
-    launch_silu_quant_t<32>(gate, up, m, n, q_split, q_nat, scales, sums, s);
+    launch_silu_quant_t<32>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s);
   else if (gs == 64)
-    launch_silu_quant_t<64>(gate, up, m, n, q_split, q_nat, scales, sums, s);
+    launch_silu_quant_t<64>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s);
   else
-    launch_silu_quant_t<128>(gate, up, m, n, q_split, q_nat, scales, sums, s);
+    launch_silu_quant_t<128>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s);
 }
 
 size_t attention_scores_floats(int m, int nh, int ctx) {
   return (size_t)std::min(m, kAttnTokens) * nh * (size_t)((ctx + 3) & ~3);
 }
 
-void launch_attention(const float *q, const float *kc, const float *vc, int cap, int vstride,
-                      int pos0, int m, int nh, int nkv, int hd, float scale, float *out,
-                      float *scores, hipStream_t s) {
+void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
+                      int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
+                      float *out, float *scores, hipStream_t s) {
   static size_t sm_configured = 0, sc_configured = 0;
   for (int t0 = 0; t0 < m; t0 += kAttnTokens) {
     const int mt = std::min(kAttnTokens, m - t0);
     const int p0 = pos0 + t0;
     const int nmax = p0 + mt;
     const int sstride = (nmax + 3) & ~3;
-    const float *qt = q + (size_t)t0 * nh * hd;
+    const float *qt = q + (size_t)t0 * q_ld;
     float *ot = out + (size_t)t0 * nh * hd;
     const dim3 sg((nmax + kScoreTile - 1) / kScoreTile, nkv);
     const size_t ksm = sizeof(float) * (size_t)kScoreTile * (hd + 1);
@@ -667,13 +668,13 @@ void launch_attention(const float *q, const float *kc, const float *vc, int cap,
       sc_configured = ksm;
     }
     if (hd == 128)
-      hipLaunchKernelGGL(k_scores<128>, sg, dim3(256), ksm, s, qt, kc, cap, p0, mt, nh, nkv, hd,
+      hipLaunchKernelGGL(k_scores<128>, sg, dim3(256), ksm, s, qt, q_ld, kc, cap, p0, mt, nh, nkv, hd,
                          scale, scores, sstride);
     else if (hd == 64)
-      hipLaunchKernelGGL(k_scores<64>, sg, dim3(256), ksm, s, qt, kc, cap, p0, mt, nh, nkv, hd,
+      hipLaunchKernelGGL(k_scores<64>, sg, dim3(256), ksm, s, qt, q_ld, kc, cap, p0, mt, nh, nkv, hd,
                          scale, scores, sstride);
     else
-      hipLaunchKernelGGL(k_scores<0>, sg, dim3(256), ksm, s, qt, kc, cap, p0, mt, nh, nkv, hd,
+      hipLaunchKernelGGL(k_scores<0>, sg, dim3(256), ksm, s, qt, q_ld, kc, cap, p0, mt, nh, nkv, hd,
                          scale, scores, sstride);
     const size_t smem = sizeof(float) * (size_t)nmax;
     if (smem > 48 * 1024 && smem > sm_configured) {

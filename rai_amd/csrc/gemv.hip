@@ -113,7 +113,7 @@ __global__ void k_qa_pack(const int8_t *__restrict__ q_split, int m, int cols, i
 // wait is static.  Requires groups % P == 0.
 template <int TGW, int P, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_gemv_ms(
-    float *__restrict__ out, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
+    float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
     const _Float16 *__restrict__ qa, const float *__restrict__ scales,
     const float *__restrict__ sums, int rows, int cols, int m) {
   typedef float f4 __attribute__((ext_vector_type(4)));
@@ -280,7 +280,11 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv_ms(
 #pragma unroll
     for (int tg = 0; tg < TGW; ++tg) {
       const int t = (tgc * TGW + tg) * 4 + h;
-      if (t < m) out[(size_t)t * rows + row] = ((f[tg][0] + f[tg][1]) + (f[tg][2] + f[tg][3])) + zc[tg];
+      if (t < m) {
+        const size_t oi = (size_t)t * rows + row;
+        const float v = ((f[tg][0] + f[tg][1]) + (f[tg][2] + f[tg][3])) + zc[tg];
+        out[oi] = add ? add[oi] + v : v;
+      }
     }
   }
 }
@@ -288,12 +292,12 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv_ms(
 namespace {
 
 template <int TGW, int P>
-void launch_ms(float *out, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
+void launch_ms(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                const float *scales, const float *sums, int rows, int cols, int m, int ntg,
                hipStream_t s) {
   constexpr int WPB = 4;
   const dim3 grid((rows + 16 * WPB - 1) / (16 * WPB), (ntg + TGW - 1) / TGW);
-  hipLaunchKernelGGL((k_gemv_ms<TGW, P, WPB>), grid, dim3(64 * WPB), 0, s, out, nib, params, qa,
+  hipLaunchKernelGGL((k_gemv_ms<TGW, P, WPB>), grid, dim3(64 * WPB), 0, s, out, add, nib, params, qa,
                      scales, sums, rows, cols, m);
 }
 
@@ -313,7 +317,7 @@ void launch_qa_pack(const int8_t *q_split, int m, int cols, _Float16 *qa, hipStr
   hipLaunchKernelGGL(k_qa_pack, dim3((n + 255) / 256), dim3(256), 0, s, q_split, m, cols, ntg, qa);
 }
 
-bool launch_w4a8_mfma(float *out, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
+bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                       const float *scales, const float *sums, int rows, int cols, int m, int gs,
                       hipStream_t s) {
   if (!qa || !w4a8_mfma_path(rows, cols, m, gs)) return false;
@@ -323,14 +327,14 @@ bool launch_w4a8_mfma(float *out, const uint8_t *nib, const uint8_t *params, con
   // decode are shared); few rows: one token group per wave for more waves
   // (measured on 4096..32000 x 4096..14336, M = 2..16).
   if (rows >= 8192) {
-    if (ntg == 1) launch_ms<1, 8>(out, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (ntg == 2) launch_ms<2, 8>(out, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (ntg == 3) launch_ms<3, 8>(out, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else launch_ms<4, 8>(out, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    if (ntg == 1) launch_ms<1, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (ntg == 2) launch_ms<2, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (ntg == 3) launch_ms<3, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else launch_ms<4, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
   } else if (groups % 16 == 0) {
-    launch_ms<1, 16>(out, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    launch_ms<1, 16>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
   } else {
-    launch_ms<1, 8>(out, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    launch_ms<1, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
   }
   return true;
 }

@@ -18,9 +18,12 @@ void launch_quantize(const float *x, int m, int k, int gs, int8_t *q_nat, int8_t
                      float *scales, float *sums, hipStream_t s);
 
 // w4a8 matmul over already-quantized activations (see gemm.rs:1774-1919).
+// `add` (may be null, may equal `out`): a residual [m][rows] added to each
+// output, out = add + matmul (the reference's vec_add after o_proj/down,
+// layers.rs:503-531, fused into the epilogue).
 // `qa` (may be null): the activations packed by launch_qa_pack, which
 // enables the matrix-core kernel for 2..kMfmaMaxTokens tokens at group 32.
-void launch_w4a8(float *out, const uint8_t *nib, const uint8_t *params, const float *x,
+void launch_w4a8(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const float *x,
                  const int8_t *q_nat, const int8_t *q_split, const float *scales,
                  const float *sums, int rows, int cols, int m, int gs, hipStream_t s,
                  const _Float16 *qa = nullptr);
@@ -33,7 +36,7 @@ size_t qa_pack_halves(int m, int cols);
 // Packs block-split int8 activations [m][cols] into the MFMA A-operand
 // layout (f16, zero rows for the padding tokens of the last 4-token group).
 void launch_qa_pack(const int8_t *q_split, int m, int cols, _Float16 *qa, hipStream_t s);
-bool launch_w4a8_mfma(float *out, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
+bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                       const float *scales, const float *sums, int rows, int cols, int m, int gs,
                       hipStream_t s);
 // True when launch_w4a8 takes the tiled fast path for this shape.
@@ -68,26 +71,29 @@ void launch_norm_quant(const float *x, const float *w, float *normed, int m, int
 // Per-group quantization of m rows of n into q_split (q_nat may be null).
 void launch_quant(const float *x, int m, int n, int gs, int8_t *q_split, int8_t *q_nat,
                   float *scales, float *sums, hipStream_t s);
-// silu_mul (layers.rs:850-883) in place on gate [m][n] + quantization of
-// the product; requires n % 8 == 0.
-void launch_silu_quant(float *gate, const float *up, int m, int n, int gs, int8_t *q_split,
-                       int8_t *q_nat, float *scales, float *sums, hipStream_t s);
+// silu_mul (layers.rs:850-883) in place on gate rows of n (row stride ld,
+// up rows likewise) + quantization of the product; requires n % 8 == 0.
+void launch_silu_quant(float *gate, const float *up, int m, int n, int ld, int gs,
+                       int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
+                       hipStream_t s);
 void launch_vec_add(float *h, const float *r, const float *a, size_t n, hipStream_t s);
 void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s);
 // RoPE on q [m][nh*hd] and k [m][nkv*hd] at positions pos0.., then the
 // KV store: K into kc [nkv][cap][hd], V into vc d-major [nkv][hd][vstride].
+// Rows of q are q_ld floats apart, rows of k and v kv_ld apart.
 void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
                        int pos0, int m, int nh, int nkv, int hd, float *kc, float *vc, int cap,
-                       int vstride, hipStream_t s);
+                       int vstride, int q_ld, int kv_ld, hipStream_t s);
 // attention_head_avx2 for every (token, query head).  K cache [nkv][cap][hd];
 // V cache d-major [nkv][hd][vstride] when vstride > 0, else [nkv][cap][hd].
 // `scores` is scratch of attention_scores_floats(m, nh, pos0 + m) floats;
 // tokens are processed in groups of kAttnTokens.
 constexpr int kAttnTokens = 64;
 size_t attention_scores_floats(int m, int nh, int ctx);
-void launch_attention(const float *q, const float *kc, const float *vc, int cap, int vstride,
-                      int pos0, int m, int nh, int nkv, int hd, float scale, float *out,
-                      float *scores, hipStream_t s);
+// q rows are q_ld floats apart; out is [m][nh * hd].
+void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
+                      int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
+                      float *out, float *scores, hipStream_t s);
 // Standalone RoPE of one position (layers.rs:643-726) on heads [nh][hd].
 void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,
                        hipStream_t s);

@@ -101,7 +101,7 @@ __global__ void k_quantize(const float *__restrict__ x, int m, int k, int gs, in
 
 // One thread per (row, token), the full reference order for any even group
 // size, partial last group and unquantized f32 tail (gemm.rs:401-539).
-__global__ void k_w4a8_simple(float *__restrict__ out, const uint8_t *__restrict__ nib,
+__global__ void k_w4a8_simple(float *out, const float *add, const uint8_t *__restrict__ nib,
                               const uint8_t *__restrict__ params, const float *__restrict__ x,
                               const int8_t *__restrict__ q_nat, const float *__restrict__ scales,
                               const float *__restrict__ sums, int rows, int cols, int m, int gs,
@@ -160,7 +160,9 @@ __global__ void k_w4a8_simple(float *__restrict__ out, const uint8_t *__restrict
       f[0] = f[0] + ws * tacc;
     }
   }
-  out[(size_t)t * rows + r] = hsum8(f) + zc;
+  const size_t oi = (size_t)t * rows + r;
+  const float v = hsum8(f) + zc;
+  out[oi] = add ? add[oi] + v : v;
 }
 
 // ------------------------------------------------------------ w4a8 fast --
@@ -187,7 +189,7 @@ struct FastCfg {
 
 template <int GS, int MT>
 __global__ __launch_bounds__(kThreads) void k_w4a8_fast(
-    float *__restrict__ out, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
+    float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
     const int8_t *__restrict__ q_split, const float *__restrict__ scales,
     const float *__restrict__ sums, int rows, int cols, int m_total, int groups) {
   using C = FastCfg<GS, MT>;
@@ -295,7 +297,9 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_fast(
 #pragma unroll
       for (int l = 0; l < 8; ++l) f[l] = (l < NL) ? fin[(t * NC + l) * kRows + r] : 0.0f;
       const float zc = fin[(t * NC + NL) * kRows + r];
-      out[(size_t)(t0 + t) * rows + row] = hsum8(f) + zc;
+      const size_t oi = (size_t)(t0 + t) * rows + row;
+      const float v = hsum8(f) + zc;
+      out[oi] = add ? add[oi] + v : v;
     }
   }
 }
@@ -308,7 +312,7 @@ size_t fast_smem() {
 }
 
 template <int GS, int MT>
-void launch_fast_t(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+void launch_fast_t(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                    const float *scales, const float *sums, int rows, int cols, int m, int groups,
                    hipStream_t s) {
   const size_t smem = fast_smem<GS, MT>();
@@ -319,24 +323,24 @@ void launch_fast_t(float *out, const uint8_t *nib, const uint8_t *params, const 
     configured = true;
   }
   dim3 grid((rows + kRows - 1) / kRows, (m + MT - 1) / MT);
-  hipLaunchKernelGGL((k_w4a8_fast<GS, MT>), grid, dim3(kThreads), smem, s, out, nib, params,
+  hipLaunchKernelGGL((k_w4a8_fast<GS, MT>), grid, dim3(kThreads), smem, s, out, add, nib, params,
                      q_split, scales, sums, rows, cols, m, groups);
 }
 
 template <int GS>
-void launch_fast_gs(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+void launch_fast_gs(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                     const float *scales, const float *sums, int rows, int cols, int m, int groups,
                     hipStream_t s) {
   if (m <= 1)
-    launch_fast_t<GS, 1>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_fast_t<GS, 1>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
   else if (m <= 2)
-    launch_fast_t<GS, 2>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_fast_t<GS, 2>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
   else if (m <= 4)
-    launch_fast_t<GS, 4>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_fast_t<GS, 4>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
   else if (m <= 8)
-    launch_fast_t<GS, 8>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_fast_t<GS, 8>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
   else
-    launch_fast_t<GS, 16>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_fast_t<GS, 16>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
 }
 
 // ------------------------------------------------------ w4a8 small-M v2 --
@@ -367,7 +371,7 @@ struct SmallCfg {
 
 template <int GS, int MT, int R, int PD, bool WHOLE>
 __global__ __launch_bounds__(kThreads) void k_w4a8_small(
-    float *__restrict__ out, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
+    float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
     const int8_t *__restrict__ q_split, const float *__restrict__ scales,
     const float *__restrict__ sums, int rows, int cols, int m_total, int groups) {
   using C = SmallCfg<GS, MT, R, PD, WHOLE>;
@@ -542,7 +546,9 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_small(
       float f[8];
 #pragma unroll
       for (int l = 0; l < 8; ++l) f[l] = (l < NL) ? fin[(t * NC + l) * R + r] : 0.0f;
-      out[(size_t)(t0 + t) * rows + row] = hsum8(f) + fin[(t * NC + NL) * R + r];
+      const size_t oi = (size_t)(t0 + t) * rows + row;
+      const float v = hsum8(f) + fin[(t * NC + NL) * R + r];
+      out[oi] = add ? add[oi] + v : v;
     }
   }
 }
@@ -559,7 +565,7 @@ size_t small_smem(int groups, int m) {
 }
 
 template <int GS, int MT, int R, int PD, bool WHOLE>
-void launch_small_t(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+void launch_small_t(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                     const float *scales, const float *sums, int rows, int cols, int m, int groups,
                     hipStream_t s) {
   const size_t smem = small_smem<GS, MT, R, PD, WHOLE>(groups, std::min(m, MT));
@@ -570,8 +576,8 @@ void launch_small_t(float *out, const uint8_t *nib, const uint8_t *params, const
     configured = smem;
   }
   dim3 grid((rows + R - 1) / R, (m + MT - 1) / MT);
-  hipLaunchKernelGGL((k_w4a8_small<GS, MT, R, PD, WHOLE>), grid, dim3(kThreads), smem, s, out, nib,
-                     params, q_split, scales, sums, rows, cols, m, groups);
+  hipLaunchKernelGGL((k_w4a8_small<GS, MT, R, PD, WHOLE>), grid, dim3(kThreads), smem, s, out, add,
+                     nib, params, q_split, scales, sums, rows, cols, m, groups);
 }
 
 // ---------------------------------------------------------- w4a8 M = 1 --
@@ -588,7 +594,7 @@ constexpr int m1_items_per_thread(int gs) { return gs == 128 ? 4 : 8; }
 // order; the epilogue applies the reference's lane reduction.
 template <int GS, int R, int IPT>
 __global__ __launch_bounds__(kThreads) void k_w4a8_m1(
-    float *__restrict__ out, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
+    float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
     const int8_t *__restrict__ q_split, const float *__restrict__ scales,
     const float *__restrict__ sums, int rows, int cols, int groups) {
   constexpr int NL = (GS == 32) ? 4 : 8;
@@ -669,12 +675,13 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_m1(
     float f[8];
 #pragma unroll
     for (int l = 0; l < 8; ++l) f[l] = (l < NL) ? psh[l * R + tid] : 0.0f;
-    out[row0 + tid] = hsum8(f) + psh[NL * R + tid];
+    const float v = hsum8(f) + psh[NL * R + tid];
+    out[row0 + tid] = add ? add[row0 + tid] + v : v;
   }
 }
 
 template <int GS, int R>
-void launch_m1_t(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+void launch_m1_t(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                  const float *scales, const float *sums, int rows, int cols, int groups,
                  hipStream_t s) {
   constexpr int NC = (GS == 32) ? 5 : 9;
@@ -688,13 +695,13 @@ void launch_m1_t(float *out, const uint8_t *nib, const uint8_t *params, const in
     configured = smem;
   }
   hipLaunchKernelGGL((k_w4a8_m1<GS, R, IPT>), dim3((rows + R - 1) / R), dim3(kThreads), smem, s,
-                     out, nib, params, q_split, scales, sums, rows, cols, groups);
+                     out, add, nib, params, q_split, scales, sums, rows, cols, groups);
 }
 
 // Rows per block: the largest power of two whose R*G items fit IPT per
 // thread.  Returns false when one row's groups do not fit (very large K).
 template <int GS>
-bool launch_m1(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+bool launch_m1(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                const float *scales, const float *sums, int rows, int cols, int groups,
                hipStream_t s) {
   const int cap = m1_items_per_thread(GS) * kThreads;
@@ -703,20 +710,20 @@ bool launch_m1(float *out, const uint8_t *nib, const uint8_t *params, const int8
   constexpr bool allow32 = ((GS == 32) ? 5 : 9) * 32 <= kThreads;
   if constexpr (allow32) {
     if (32 * groups <= cap) {
-      launch_m1_t<GS, 32>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+      launch_m1_t<GS, 32>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
       return true;
     }
   }
   if (16 * groups <= cap)
-    launch_m1_t<GS, 16>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+    launch_m1_t<GS, 16>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
   else if (8 * groups <= cap)
-    launch_m1_t<GS, 8>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+    launch_m1_t<GS, 8>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
   else if (4 * groups <= cap)
-    launch_m1_t<GS, 4>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+    launch_m1_t<GS, 4>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
   else if (2 * groups <= cap)
-    launch_m1_t<GS, 2>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+    launch_m1_t<GS, 2>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
   else
-    launch_m1_t<GS, 1>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+    launch_m1_t<GS, 1>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
   return true;
 }
 
@@ -724,31 +731,31 @@ bool launch_m1(float *out, const uint8_t *nib, const uint8_t *params, const int8
 constexpr size_t kWholeStageBytes = 24 * 1024;
 
 template <int GS, int MT>
-void launch_small_mt(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+void launch_small_mt(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                      const float *scales, const float *sums, int rows, int cols, int m, int groups,
                      hipStream_t s) {
   constexpr int R = 16, PD = 4;
   const size_t whole = (size_t)std::min(m, MT) * groups * (GS + 8 + 8);
   if (whole <= kWholeStageBytes)
-    launch_small_t<GS, MT, R, PD, true>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_small_t<GS, MT, R, PD, true>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
   else
-    launch_small_t<GS, MT, R, PD, false>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_small_t<GS, MT, R, PD, false>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
 }
 
 template <int GS>
-void launch_small_gs(float *out, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+void launch_small_gs(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                      const float *scales, const float *sums, int rows, int cols, int m, int groups,
                      hipStream_t s) {
   if (m <= 1)
-    launch_small_mt<GS, 1>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_small_mt<GS, 1>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
   else if (m <= 2)
-    launch_small_mt<GS, 2>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_small_mt<GS, 2>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
   else if (m <= 4)
-    launch_small_mt<GS, 4>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_small_mt<GS, 4>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
   else if (m <= 8 || GS > 32)  // groups 64/128 carry 9 chains: at most 8 tokens per tile
-    launch_small_mt<GS, 8>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_small_mt<GS, 8>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
   else
-    launch_small_mt<GS, 16>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+    launch_small_mt<GS, 16>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
 }
 
 // --------------------------------------------------------- lane sums dbg --
@@ -924,7 +931,7 @@ __global__ void k_rope_store(float *__restrict__ q, float *__restrict__ k,
                              const float *__restrict__ v, const float *__restrict__ cos_t,
                              const float *__restrict__ sin_t, int pos0, int nh, int nkv, int hd,
                              float *__restrict__ kc, float *__restrict__ vc, int cap,
-                             int vstride) {
+                             int vstride, int q_ld, int kv_ld) {
   const int t = blockIdx.x;
   const int pos = pos0 + t;
   const int half = hd / 2;
@@ -934,7 +941,7 @@ __global__ void k_rope_store(float *__restrict__ q, float *__restrict__ k,
   const int h = idx / half, i = idx - h * half;
   const bool isq = h < nh;
   const int kh = h - nh;
-  float *b = isq ? q + ((size_t)t * nh + h) * hd : k + ((size_t)t * nkv + kh) * hd;
+  float *b = isq ? q + (size_t)t * q_ld + (size_t)h * hd : k + (size_t)t * kv_ld + (size_t)kh * hd;
   const float x0 = b[i], x1 = b[half + i];
   const float c = cos_t[(size_t)pos * half + i], sn = sin_t[(size_t)pos * half + i];
   float r0, r1;
@@ -951,7 +958,7 @@ __global__ void k_rope_store(float *__restrict__ q, float *__restrict__ k,
     const size_t dst = ((size_t)kh * cap + pos) * hd;
     kc[dst + i] = r0;
     kc[dst + half + i] = r1;
-    const float *vr = v + ((size_t)t * nkv + kh) * hd;
+    const float *vr = v + (size_t)t * kv_ld + (size_t)kh * hd;
     float *vd = vc + (size_t)kh * hd * vstride + pos;  // d-major V
     vd[(size_t)i * vstride] = vr[i];
     vd[(size_t)(half + i) * vstride] = vr[half + i];
@@ -1169,44 +1176,44 @@ bool w4a8_fast_path(int cols, int gs) {
   return (gs == 32 || gs == 64 || gs == 128) && cols % gs == 0;
 }
 
-void launch_w4a8(float *out, const uint8_t *nib, const uint8_t *params, const float *x,
+void launch_w4a8(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const float *x,
                  const int8_t *q_nat, const int8_t *q_split, const float *scales,
                  const float *sums, int rows, int cols, int m, int gs, hipStream_t s,
                  const _Float16 *qa) {
   const int groups = (cols + gs - 1) / gs;
-  if (launch_w4a8_mfma(out, nib, params, qa, scales, sums, rows, cols, m, gs, s)) return;
+  if (launch_w4a8_mfma(out, add, nib, params, qa, scales, sums, rows, cols, m, gs, s)) return;
   // The whole-K kernel wins where few, long rows leave the streaming kernel
   // with too few blocks (measured on 1024..32000 x 2048..14336, g32).
   if (w4a8_fast_path(cols, gs) && m == 1 && cols >= 4096 && rows <= cols) {
     bool done;
     if (gs == 32)
-      done = launch_m1<32>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+      done = launch_m1<32>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
     else if (gs == 64)
-      done = launch_m1<64>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+      done = launch_m1<64>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
     else
-      done = launch_m1<128>(out, nib, params, q_split, scales, sums, rows, cols, groups, s);
+      done = launch_m1<128>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
     if (done) return;
   }
   if (w4a8_fast_path(cols, gs) && m <= 16) {
     if (gs == 32)
-      launch_small_gs<32>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+      launch_small_gs<32>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
     else if (gs == 64)
-      launch_small_gs<64>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+      launch_small_gs<64>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
     else
-      launch_small_gs<128>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+      launch_small_gs<128>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
     return;
   }
   if (w4a8_fast_path(cols, gs)) {
     if (gs == 32)
-      launch_fast_gs<32>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+      launch_fast_gs<32>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
     else if (gs == 64)
-      launch_fast_gs<64>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+      launch_fast_gs<64>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
     else
-      launch_fast_gs<128>(out, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+      launch_fast_gs<128>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
     return;
   }
   dim3 grid((rows + 127) / 128, m);
-  hipLaunchKernelGGL(k_w4a8_simple, grid, dim3(128), 0, s, out, nib, params, x, q_nat, scales,
+  hipLaunchKernelGGL(k_w4a8_simple, grid, dim3(128), 0, s, out, add, nib, params, x, q_nat, scales,
                      sums, rows, cols, m, gs, groups);
 }
 
@@ -1246,10 +1253,10 @@ void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s) 
 
 void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
                        int pos0, int m, int nh, int nkv, int hd, float *kc, float *vc, int cap,
-                       int vstride, hipStream_t s) {
+                       int vstride, int q_ld, int kv_ld, hipStream_t s) {
   const int pairs = (nh + nkv) * (hd / 2);
   hipLaunchKernelGGL(k_rope_store, dim3(m, (pairs + 255) / 256), dim3(256), 0, s, q, k, v, cos_t, sin_t, pos0, nh, nkv,
-                     hd, kc, vc, cap, vstride);
+                     hd, kc, vc, cap, vstride, q_ld, kv_ld);
 }
 
 void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,

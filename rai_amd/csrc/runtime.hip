@@ -63,6 +63,9 @@ struct DLinear {
 
 struct DLayer {
   DLinear lin[7];
+  // q|k|v and gate|up stored back to back (same cols): one GEMV each.
+  // rows == 0 when the pieces could not be placed contiguously.
+  DLinear qkv, gate_up;
   std::vector<DLinear> experts;  // all experts, 3 linears each (expert 0 = lin[4..6])
   const float *router = nullptr;
   const float *in_norm = nullptr, *post_norm = nullptr;
@@ -110,6 +113,7 @@ namespace rai {
 struct Workspace {
   int maxm = 0;
   DevBuf hid, normed, qb, kb, vb, att, ob, gb, ub, mo, logits, am;
+  DevBuf qkvb, gub;  // fused q|k|v and gate|up outputs [m][rows]
   DevBuf q_nat, q_split, qscale, qsum, hq;
   DevBuf qa;  // activations packed for the matrix-core W4A8 kernel (<= 16 tokens)
   DevBuf err;
@@ -146,6 +150,8 @@ struct Workspace {
     f(gb, F);
     f(ub, F);
     f(mo, H);
+    f(qkvb, qd + 2 * kvd);
+    f(gub, 2 * F);
     logits.alloc(sizeof(float) * V * std::max(1, logit_rows));
     am.alloc(sizeof(uint32_t) * maxm);
     q_nat.alloc(K * maxm);
@@ -213,8 +219,19 @@ static void upload_model(rai_model &m, const uint8_t *img, size_t len, int max_g
   uint64_t wbytes = 0;
   for (uint32_t l = 0; l < c.num_layers; ++l) {
     const LayerView &L = v.layers[l];
+    // q, k, v and gate, up: codes back to back, then params back to back,
+    // so each set can run as one matrix.
+    size_t ni[7], pi[7];
+    for (int p : {0, 1, 2}) ni[p] = add(L.lin[p].nib_off, L.lin[p].nib_len);
+    for (int p : {0, 1, 2}) pi[p] = add(L.lin[p].params_off, L.lin[p].params_len);
+    pi[3] = add(L.lin[3].params_off, L.lin[3].params_len);
+    ni[3] = add(L.lin[3].nib_off, L.lin[3].nib_len);
+    for (int p : {4, 5}) ni[p] = add(L.lin[p].nib_off, L.lin[p].nib_len);
+    for (int p : {4, 5}) pi[p] = add(L.lin[p].params_off, L.lin[p].params_len);
+    pi[6] = add(L.lin[6].params_off, L.lin[6].params_len);
+    ni[6] = add(L.lin[6].nib_off, L.lin[6].nib_len);
     for (int p = 0; p < 7; ++p) {
-      lidx[l].push_back({add(L.lin[p].params_off, L.lin[p].params_len), add(L.lin[p].nib_off, L.lin[p].nib_len)});
+      lidx[l].push_back({pi[p], ni[p]});
       wbytes += L.lin[p].params_len + L.lin[p].nib_len;
     }
     for (const LinearView &e : L.experts) lidx[l].push_back({add(e.params_off, e.params_len), add(e.nib_off, e.nib_len)});
@@ -292,6 +309,26 @@ static void upload_model(rai_model &m, const uint8_t *img, size_t len, int max_g
       return d;
     };
     for (int p = 0; p < 7; ++p) D.lin[p] = mk(p, p);
+    auto contiguous = [&](std::initializer_list<int> ps) {
+      int prev = -1;
+      for (int p : ps) {
+        if (prev >= 0) {
+          const Piece &a = pieces[lidx[l][prev].n], &b = pieces[lidx[l][p].n];
+          const Piece &pa = pieces[lidx[l][prev].p], &pb = pieces[lidx[l][p].p];
+          if (a.dst + a.len != b.dst || pa.dst + pa.len != pb.dst) return false;
+        }
+        prev = p;
+      }
+      return true;
+    };
+    if (contiguous({0, 1, 2})) {
+      D.qkv = D.lin[0];
+      D.qkv.rows = D.lin[0].rows + D.lin[1].rows + D.lin[2].rows;
+    }
+    if (c.num_experts == 0 && contiguous({4, 5})) {
+      D.gate_up = D.lin[4];
+      D.gate_up.rows = D.lin[4].rows + D.lin[5].rows;
+    }
     if (c.num_experts > 0) {
       D.experts.push_back(D.lin[4]);
       D.experts.push_back(D.lin[5]);
@@ -322,8 +359,8 @@ static void upload_model(rai_model &m, const uint8_t *img, size_t len, int max_g
 // ------------------------------------------------------------- forward --
 
 static void linear(const DLinear &L, const float *x, const Workspace &w, float *out, int m,
-                   hipStream_t s) {
-  launch_w4a8(out, L.nib, L.params, x, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
+                   hipStream_t s, const float *add = nullptr) {
+  launch_w4a8(out, add, L.nib, L.params, x, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
               w.qscale.as<float>(), w.qsum.as<float>(), L.rows, L.cols, m, L.gs, s,
               w.qa.as<_Float16>());
 }
@@ -434,33 +471,61 @@ static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0,
   for (int li = 0; li < (int)c.num_layers; ++li) {
     const DLayer &L = md.layers[li];
     norm_then_quant(L.in_norm);
-    linear(L.lin[0], normed, w, w.qb.as<float>(), m, s);
-    linear(L.lin[1], normed, w, w.kb.as<float>(), m, s);
-    linear(L.lin[2], normed, w, w.vb.as<float>(), m, s);
-    launch_rope_store(w.qb.as<float>(), w.kb.as<float>(), w.vb.as<float>(), md.rope_cos, md.rope_sin, (int)pos0,
-                      m, nh, nkv, hd, kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, s);
-    launch_attention(w.qb.as<float>(), kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, (int)pos0, m, nh, nkv, hd,
+    float *qp, *kp, *vp;
+    int q_ld, kv_ld;
+    if (L.qkv.rows) {
+      linear(L.qkv, normed, w, w.qkvb.as<float>(), m, s);
+      qp = w.qkvb.as<float>();
+      kp = qp + qd;
+      vp = kp + nkv * hd;
+      q_ld = kv_ld = L.qkv.rows;
+    } else {
+      linear(L.lin[0], normed, w, w.qb.as<float>(), m, s);
+      linear(L.lin[1], normed, w, w.kb.as<float>(), m, s);
+      linear(L.lin[2], normed, w, w.vb.as<float>(), m, s);
+      qp = w.qb.as<float>();
+      kp = w.kb.as<float>();
+      vp = w.vb.as<float>();
+      q_ld = qd;
+      kv_ld = nkv * hd;
+    }
+    launch_rope_store(qp, kp, vp, md.rope_cos, md.rope_sin, (int)pos0, m, nh, nkv, hd, kv.kc(li), kv.vc(li),
+                      (int)kv.cap, (int)kv.vstride, q_ld, kv_ld, s);
+    launch_attention(qp, q_ld, kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, (int)pos0, m, nh, nkv, hd,
                      md.attn_scale, w.att.as<float>(), scores, s);
     quantize(md, w.att.as<float>(), m, qd, w, s);
-    linear(L.lin[3], w.att.as<float>(), w, w.ob.as<float>(), m, s);
-    launch_vec_add(hid, hid, w.ob.as<float>(), (size_t)m * H, s);
+    // o_proj with the first residual add (model.rs:858-863) in its epilogue.
+    linear(L.lin[3], w.att.as<float>(), w, hid, m, s, hid);
     norm_then_quant(L.post_norm);
     if (c.num_experts > 0) {
       moe_block(md, L, w, m, s);
+      launch_vec_add(hid, hid, w.mo.as<float>(), (size_t)m * H, s);
     } else {
-      linear(L.lin[4], normed, w, w.gb.as<float>(), m, s);
-      linear(L.lin[5], normed, w, w.ub.as<float>(), m, s);
+      float *gp, *up;
+      int gu_ld;
+      if (L.gate_up.rows && fused_quant_ok(F, gs)) {
+        linear(L.gate_up, normed, w, w.gub.as<float>(), m, s);
+        gp = w.gub.as<float>();
+        up = gp + F;
+        gu_ld = 2 * F;
+      } else {
+        linear(L.lin[4], normed, w, w.gb.as<float>(), m, s);
+        linear(L.lin[5], normed, w, w.ub.as<float>(), m, s);
+        gp = w.gb.as<float>();
+        up = w.ub.as<float>();
+        gu_ld = F;
+      }
       if (fused_quant_ok(F, gs)) {
-        launch_silu_quant(w.gb.as<float>(), w.ub.as<float>(), m, F, gs, w.q_split.as<int8_t>(), nullptr,
-                          w.qscale.as<float>(), w.qsum.as<float>(), s);
+        launch_silu_quant(gp, up, m, F, gu_ld, gs, w.q_split.as<int8_t>(), nullptr, w.qscale.as<float>(),
+                          w.qsum.as<float>(), s);
         pack_for_mfma(md, m, F, w, s);
       } else {
-        launch_silu_mul(w.gb.as<float>(), w.ub.as<float>(), m, F, s);
-        quantize(md, w.gb.as<float>(), m, F, w, s);
+        launch_silu_mul(gp, up, m, F, s);
+        quantize(md, gp, m, F, w, s);
       }
-      linear(L.lin[6], w.gb.as<float>(), w, w.mo.as<float>(), m, s);
+      // down with the second residual add (model.rs:955-960) in its epilogue.
+      linear(L.lin[6], gp, w, hid, m, s, hid);
     }
-    launch_vec_add(hid, hid, w.mo.as<float>(), (size_t)m * H, s);
   }
   for (int l = 0; l < kv.layers; ++l) kv.filled[l] = std::max(kv.filled[l], pos0 + m);
 }
@@ -858,8 +923,8 @@ int rai_w4a8_matmul_dev(float *out, const uint8_t *nib, const uint8_t *params, c
       qa.alloc(sizeof(_Float16) * rai::qa_pack_halves((int)m, (int)cols));
       rai::launch_qa_pack(qs.as<int8_t>(), (int)m, (int)cols, qa.as<_Float16>(), s);
     }
-    rai::launch_w4a8(out, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(), su.as<float>(),
-                     (int)rows, (int)cols, (int)m, (int)gs, s, mfma ? qa.as<_Float16>() : nullptr);
+    rai::launch_w4a8(out, nullptr, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
+                     su.as<float>(), (int)rows, (int)cols, (int)m, (int)gs, s, mfma ? qa.as<_Float16>() : nullptr);
     HIP_CHECK(hipGetLastError());
     HIP_CHECK(hipStreamSynchronize(s));  // scratch is freed on return
   });
@@ -891,8 +956,8 @@ int rai_w4a8_time_dev(float *out, const uint8_t *nib, const uint8_t *params, con
       rai::launch_qa_pack(qs.as<int8_t>(), (int)m, (int)cols, qa.as<_Float16>(), s);
     }
     auto run = [&] {
-      rai::launch_w4a8(out, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(), su.as<float>(),
-                       (int)rows, (int)cols, (int)m, (int)gs, s, mfma ? qa.as<_Float16>() : nullptr);
+      rai::launch_w4a8(out, nullptr, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
+                       su.as<float>(), (int)rows, (int)cols, (int)m, (int)gs, s, mfma ? qa.as<_Float16>() : nullptr);
     };
     run();  // warm-up
     HIP_CHECK(hipEventRecord(e0, s));
@@ -1023,7 +1088,7 @@ int rai_attention_head_dev(float *out, const float *q, const float *k, const flo
     // One head: q [hd], cache rows [pos+1][hd] viewed as one kv head with cap = pos+1.
     rai::DevBuf scores;
     scores.alloc(sizeof(float) * rai::attention_scores_floats(1, 1, (int)(pos + 1)));
-    rai::launch_attention(q, k, v, (int)(pos + 1), 0, (int)pos, 1, 1, 1, (int)hd, scale, out, scores.as<float>(),
+    rai::launch_attention(q, (int)hd, k, v, (int)(pos + 1), 0, (int)pos, 1, 1, 1, (int)hd, scale, out, scores.as<float>(),
                           (hipStream_t)stream);
     HIP_CHECK(hipGetLastError());
     HIP_CHECK(hipStreamSynchronize((hipStream_t)stream));
