@@ -266,8 +266,10 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int q_ld,
                                                 const float *__restrict__ kc, int cap, int pos0,
                                                 int m, int nh, int nkv, int hd_rt, float scale,
-                                                float *__restrict__ S, int sstride) {
+                                                float *__restrict__ S, int sstride,
+                                                const int *__restrict__ st) {
   extern __shared__ float ks[];
+  if (st) pos0 = st[0];
   const int hd = HD > 0 ? HD : hd_rt;
   const int kstride = hd + 1;
   const int lane = threadIdx.x & 63;
@@ -276,6 +278,7 @@ __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int
   const int kvh = blockIdx.y;
   const int G = nh / nkv;
   const int nmax = pos0 + m;
+  if (s0 >= nmax) return;  // capacity-sized grids (step record) end early
   const int rows = min(kScoreTile, nmax - s0);
   const float *kb = kc + ((size_t)kvh * cap + s0) * hd;
   if constexpr (HD > 0) {
@@ -355,10 +358,11 @@ __device__ __forceinline__ float block_max256(float v, float *red) {
 
 // grid (nh, m), 256 threads; dynamic LDS holds the n exponentials.
 __global__ __launch_bounds__(256) void k_softmax(float *__restrict__ S, int pos0, int nh,
-                                                 int sstride) {
+                                                 int sstride, const int *__restrict__ st) {
   extern __shared__ float e[];
   __shared__ float red[8];
   __shared__ float bc;
+  if (st) pos0 = st[0];
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const int n = pos0 + t + 1;
   const int n8 = n / 8;
@@ -452,8 +456,10 @@ template <int DL, int G, int CP>
 __global__ __launch_bounds__(512) void k_pv_stream(const float *__restrict__ P,
                                                     const float *__restrict__ vt_g, int vstride,
                                                     int pos0, int nh, int hd, int sstride,
-                                                    float *__restrict__ out) {
+                                                    float *__restrict__ out,
+                                                    const int *__restrict__ st) {
   using C = PvCfg<DL, G, CP>;
+  if (st) pos0 = st[0];
   constexpr int NCW = C::NCW, NL = C::NL, NV = C::NV, NP = C::NP, STR = C::STR;
   constexpr int Q4 = CP / 4;  // float4 per tile row
   __shared__ __align__(16) float vt[2][DL * STR];
@@ -549,7 +555,9 @@ template <bool DMAJOR>
 __global__ __launch_bounds__(64) void k_pv_any(const float *__restrict__ P,
                                                const float *__restrict__ vc, int cap, int vstride,
                                                int pos0, int m, int nh, int nkv, int hd,
-                                               int sstride, float *__restrict__ out) {
+                                               int sstride, float *__restrict__ out,
+                                               const int *__restrict__ st) {
+  if (st) pos0 = st[0];
   const int G = nh / nkv;
   const size_t gid = (size_t)blockIdx.x * 64 + threadIdx.x;
   if (gid >= (size_t)m * nh * hd) return;
@@ -651,12 +659,13 @@ size_t attention_scores_floats(int m, int nh, int ctx) {
 
 void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
                       int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
-                      float *out, float *scores, hipStream_t s) {
+                      float *out, float *scores, hipStream_t s, const int *st) {
   static size_t sm_configured = 0, sc_configured = 0;
   for (int t0 = 0; t0 < m; t0 += kAttnTokens) {
     const int mt = std::min(kAttnTokens, m - t0);
     const int p0 = pos0 + t0;
-    const int nmax = p0 + mt;
+    // With a step record the position is on the device: size for capacity.
+    const int nmax = st ? cap : p0 + mt;
     const int sstride = (nmax + 3) & ~3;
     const float *qt = q + (size_t)t0 * q_ld;
     float *ot = out + (size_t)t0 * nh * hd;
@@ -669,20 +678,20 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     }
     if (hd == 128)
       hipLaunchKernelGGL(k_scores<128>, sg, dim3(256), ksm, s, qt, q_ld, kc, cap, p0, mt, nh, nkv, hd,
-                         scale, scores, sstride);
+                         scale, scores, sstride, st);
     else if (hd == 64)
       hipLaunchKernelGGL(k_scores<64>, sg, dim3(256), ksm, s, qt, q_ld, kc, cap, p0, mt, nh, nkv, hd,
-                         scale, scores, sstride);
+                         scale, scores, sstride, st);
     else
       hipLaunchKernelGGL(k_scores<0>, sg, dim3(256), ksm, s, qt, q_ld, kc, cap, p0, mt, nh, nkv, hd,
-                         scale, scores, sstride);
+                         scale, scores, sstride, st);
     const size_t smem = sizeof(float) * (size_t)nmax;
     if (smem > 48 * 1024 && smem > sm_configured) {
       (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_softmax),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
       sm_configured = smem;
     }
-    hipLaunchKernelGGL(k_softmax, dim3(nh, mt), dim3(256), smem, s, scores, p0, nh, sstride);
+    hipLaunchKernelGGL(k_softmax, dim3(nh, mt), dim3(256), smem, s, scores, p0, nh, sstride, st);
     const size_t total = (size_t)mt * nh * hd;
     const int G = nh / nkv;
     const int DL = (G == 1) ? 64 : (G == 2) ? 32 : 16;
@@ -691,21 +700,21 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     if (stream) {
       const dim3 pg(nkv * (hd / DL), mt);
       if (G == 4)
-        hipLaunchKernelGGL((k_pv_stream<16, 4, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+        hipLaunchKernelGGL((k_pv_stream<16, 4, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
       else if (G == 8)
-        hipLaunchKernelGGL((k_pv_stream<16, 8, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+        hipLaunchKernelGGL((k_pv_stream<16, 8, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
       else if (G == 16)
-        hipLaunchKernelGGL((k_pv_stream<16, 16, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+        hipLaunchKernelGGL((k_pv_stream<16, 16, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
       else if (G == 2)
-        hipLaunchKernelGGL((k_pv_stream<32, 2, 128>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+        hipLaunchKernelGGL((k_pv_stream<32, 2, 128>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
       else
-        hipLaunchKernelGGL((k_pv_stream<64, 1, 64>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot);
+        hipLaunchKernelGGL((k_pv_stream<64, 1, 64>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
     } else if (vstride > 0) {
       hipLaunchKernelGGL(k_pv_any<true>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, scores,
-                         vc, cap, vstride, p0, mt, nh, nkv, hd, sstride, ot);
+                         vc, cap, vstride, p0, mt, nh, nkv, hd, sstride, ot, st);
     } else {
       hipLaunchKernelGGL(k_pv_any<false>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, scores,
-                         vc, cap, 0, p0, mt, nh, nkv, hd, sstride, ot);
+                         vc, cap, 0, p0, mt, nh, nkv, hd, sstride, ot, st);
     }
   }
 }

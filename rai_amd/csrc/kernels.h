@@ -53,9 +53,13 @@ void launch_tied_lm_head(float *logits, const float *hidden, const uint8_t *code
 // Embedding rows (gemm.rs:1926-1970, model.rs:371-403) for token ids read
 // from `tokens` (device), or, when tokens == null, from
 // ctx[last] followed by ctx[start .. start+m-1) (the lookup verify batch).
+// Device step record for graph replay: int[4] = {pos0, len, start, nd}.
+// Kernels given one read their position arguments from it (the host
+// arguments are then ignored); null means use the host arguments.
 void launch_embed(const uint32_t *tokens, const uint32_t *ctx, int last, int start, int m,
                   const uint8_t *codes, const uint8_t *params, int vocab, int hidden, int egs,
-                  float embed_scale, float *out, int *err, hipStream_t s);
+                  float embed_scale, float *out, int *err, hipStream_t s,
+                  const int *st = nullptr);
 
 void launch_rmsnorm(const float *x, const float *w, float *out, float *resid, int m, int n,
                     float eps, hipStream_t s);
@@ -83,7 +87,8 @@ void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s);
 // Rows of q are q_ld floats apart, rows of k and v kv_ld apart.
 void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
                        int pos0, int m, int nh, int nkv, int hd, float *kc, float *vc, int cap,
-                       int vstride, int q_ld, int kv_ld, hipStream_t s);
+                       int vstride, int q_ld, int kv_ld, hipStream_t s,
+                       const int *st = nullptr);
 // attention_head_avx2 for every (token, query head).  K cache [nkv][cap][hd];
 // V cache d-major [nkv][hd][vstride] when vstride > 0, else [nkv][cap][hd].
 // `scores` is scratch of attention_scores_floats(m, nh, pos0 + m) floats;
@@ -91,9 +96,12 @@ void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, c
 constexpr int kAttnTokens = 64;
 size_t attention_scores_floats(int m, int nh, int ctx);
 // q rows are q_ld floats apart; out is [m][nh * hd].
+// With a step record `st` (m <= kAttnTokens), grids and the score stride
+// are sized for the whole capacity `cap` so the launch does not depend on
+// the position.
 void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
                       int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
-                      float *out, float *scores, hipStream_t s);
+                      float *out, float *scores, hipStream_t s, const int *st = nullptr);
 // Standalone RoPE of one position (layers.rs:643-726) on heads [nh][hd].
 void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,
                        hipStream_t s);
@@ -104,7 +112,7 @@ void launch_ngram(const uint32_t *ctx, int len, int min_n, int max_n, int max_dr
 // Greedy acceptance: argmax[0..nd] vs ctx[start..start+nd); writes the
 // produced tokens to ctx[len..] and res2 = {accepted, produced}.
 void launch_accept(const uint32_t *argmax, uint32_t *ctx, int len, int start, int nd, int *res2,
-                   hipStream_t s);
+                   hipStream_t s, const int *st = nullptr);
 
 // MoE (layers.rs:1808-1870, model.rs:208-261): router probabilities and
 // top-k selection per token.

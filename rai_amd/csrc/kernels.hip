@@ -880,8 +880,13 @@ __global__ void k_tied_head(float *__restrict__ logits, const uint8_t *__restric
 __global__ void k_embed(const uint32_t *__restrict__ tokens, const uint32_t *__restrict__ ctx,
                         int last, int start, const uint8_t *__restrict__ codes,
                         const uint8_t *__restrict__ params, int vocab, int hidden, int egs,
-                        int egroups, float embed_scale, float *__restrict__ out, int *err) {
+                        int egroups, float embed_scale, float *__restrict__ out, int *err,
+                        const int *__restrict__ st) {
   const int t = blockIdx.x;
+  if (st) {  // device step record {pos0, len, start, nd}
+    last = st[1] - 1;
+    start = st[2];
+  }
   const int c = blockIdx.y * blockDim.x + threadIdx.x;
   uint32_t tok = tokens ? tokens[t] : (t == 0 ? ctx[last] : ctx[start + t - 1]);
   if (c >= hidden) return;
@@ -931,8 +936,9 @@ __global__ void k_rope_store(float *__restrict__ q, float *__restrict__ k,
                              const float *__restrict__ v, const float *__restrict__ cos_t,
                              const float *__restrict__ sin_t, int pos0, int nh, int nkv, int hd,
                              float *__restrict__ kc, float *__restrict__ vc, int cap,
-                             int vstride, int q_ld, int kv_ld) {
+                             int vstride, int q_ld, int kv_ld, const int *__restrict__ st) {
   const int t = blockIdx.x;
+  if (st) pos0 = st[0];
   const int pos = pos0 + t;
   const int half = hd / 2;
   const int body = (half / 8) * 8;
@@ -1077,8 +1083,13 @@ __global__ void k_ngram(const uint32_t *__restrict__ ctx, int len, int min_n, in
 
 // Greedy acceptance (the T -> 0 limit of lookup.rs:359-403).
 __global__ void k_accept(const uint32_t *__restrict__ am, uint32_t *__restrict__ ctx, int len,
-                         int start, int nd, int *__restrict__ res) {
+                         int start, int nd, int *__restrict__ res, const int *__restrict__ st) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  if (st) {
+    len = st[1];
+    start = st[2];
+    nd = st[3];
+  }
   int acc = 0, prod = 0;
   for (int i = 0; i < nd; ++i) {
     const uint32_t a = am[i];
@@ -1237,10 +1248,10 @@ void launch_tied_lm_head(float *logits, const float *hidden, const uint8_t *code
 
 void launch_embed(const uint32_t *tokens, const uint32_t *ctx, int last, int start, int m,
                   const uint8_t *codes, const uint8_t *params, int vocab, int hidden, int egs,
-                  float embed_scale, float *out, int *err, hipStream_t s) {
+                  float embed_scale, float *out, int *err, hipStream_t s, const int *st) {
   const int egroups = (hidden + egs - 1) / egs;
   hipLaunchKernelGGL(k_embed, dim3(m, (hidden + 255) / 256), dim3(256), 0, s, tokens, ctx, last, start, codes, params,
-                     vocab, hidden, egs, egroups, embed_scale, out, err);
+                     vocab, hidden, egs, egroups, embed_scale, out, err, st);
 }
 
 void launch_vec_add(float *h, const float *r, const float *a, size_t n, hipStream_t s) {
@@ -1253,10 +1264,10 @@ void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s) 
 
 void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
                        int pos0, int m, int nh, int nkv, int hd, float *kc, float *vc, int cap,
-                       int vstride, int q_ld, int kv_ld, hipStream_t s) {
+                       int vstride, int q_ld, int kv_ld, hipStream_t s, const int *st) {
   const int pairs = (nh + nkv) * (hd / 2);
   hipLaunchKernelGGL(k_rope_store, dim3(m, (pairs + 255) / 256), dim3(256), 0, s, q, k, v, cos_t, sin_t, pos0, nh, nkv,
-                     hd, kc, vc, cap, vstride, q_ld, kv_ld);
+                     hd, kc, vc, cap, vstride, q_ld, kv_ld, st);
 }
 
 void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,
@@ -1274,8 +1285,8 @@ void launch_ngram(const uint32_t *ctx, int len, int min_n, int max_n, int max_dr
 }
 
 void launch_accept(const uint32_t *am, uint32_t *ctx, int len, int start, int nd, int *res2,
-                   hipStream_t s) {
-  hipLaunchKernelGGL(k_accept, dim3(1), dim3(64), 0, s, am, ctx, len, start, nd, res2);
+                   hipStream_t s, const int *st) {
+  hipLaunchKernelGGL(k_accept, dim3(1), dim3(64), 0, s, am, ctx, len, start, nd, res2, st);
 }
 
 void launch_router(const float *x, const float *router, int m, int hidden, int experts, int topk,

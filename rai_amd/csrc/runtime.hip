@@ -6,6 +6,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <memory>
@@ -439,12 +440,9 @@ static void moe_block(const rai_model &md, const DLayer &L, Workspace &w, int m,
   }
 }
 
-// forward_batch (model.rs:692-963) for m tokens at positions pos0.. whose
-// hidden states are in w.hid; updates the KV watermark.
-static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0, hipStream_t s) {
+// Host-side checks of forward_batch (model.rs:709-725, kv_cache.rs:143-172).
+static void forward_check(const rai_model &md, const rai_kv &kv, const Workspace &w, int m, size_t pos0) {
   const rai_model_config &c = md.cfg;
-  const int H = c.hidden_size, F = c.intermediate_size, hd = c.head_dim;
-  const int nh = c.num_heads, nkv = c.num_kv_heads, qd = nh * hd;
   if (m <= 0 || m > w.maxm) fail(RAI_E_SHAPE, "batch size exceeds the workspace");
   if (pos0 + m > c.max_context || pos0 + m > kv.cap) fail(RAI_E_RANGE, "batch position exceeds model context");
   if (pos0 + m > kMaxAttnContext) fail(RAI_E_UNSUPPORTED, "context beyond 16384 positions is not supported");
@@ -452,6 +450,20 @@ static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0,
     if (pos0 > kv.filled[l])
       fail(RAI_E_WATERMARK, "KV store at position " + std::to_string(pos0) + " would leave a gap (filled " +
                                 std::to_string(kv.filled[l]) + ")");
+}
+
+static void forward_commit(rai_kv &kv, int m, size_t pos0) {
+  for (int l = 0; l < kv.layers; ++l) kv.filled[l] = std::max(kv.filled[l], pos0 + m);
+}
+
+// The launches of forward_batch (model.rs:692-963) for m tokens at positions
+// pos0.. whose hidden states are in w.hid.  With a device step record `st`
+// the position-dependent kernels read pos0 from it (graph replay).
+static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0, hipStream_t s,
+                            const int *st) {
+  const rai_model_config &c = md.cfg;
+  const int H = c.hidden_size, F = c.intermediate_size, hd = c.head_dim;
+  const int nh = c.num_heads, nkv = c.num_kv_heads, qd = nh * hd;
   float *hid = w.hid.as<float>(), *normed = w.normed.as<float>();
   float *scores = w.attn_scores(c, kv.cap);
   const int gs = c.group_size;
@@ -490,9 +502,9 @@ static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0,
       kv_ld = nkv * hd;
     }
     launch_rope_store(qp, kp, vp, md.rope_cos, md.rope_sin, (int)pos0, m, nh, nkv, hd, kv.kc(li), kv.vc(li),
-                      (int)kv.cap, (int)kv.vstride, q_ld, kv_ld, s);
+                      (int)kv.cap, (int)kv.vstride, q_ld, kv_ld, s, st);
     launch_attention(qp, q_ld, kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, (int)pos0, m, nh, nkv, hd,
-                     md.attn_scale, w.att.as<float>(), scores, s);
+                     md.attn_scale, w.att.as<float>(), scores, s, st);
     quantize(md, w.att.as<float>(), m, qd, w, s);
     // o_proj with the first residual add (model.rs:858-863) in its epilogue.
     linear(L.lin[3], w.att.as<float>(), w, hid, m, s, hid);
@@ -527,7 +539,13 @@ static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0,
       linear(L.lin[6], gp, w, hid, m, s, hid);
     }
   }
-  for (int l = 0; l < kv.layers; ++l) kv.filled[l] = std::max(kv.filled[l], pos0 + m);
+}
+
+// forward_batch: checks, launches, KV watermark.
+static void forward(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0, hipStream_t s) {
+  forward_check(md, kv, w, m, pos0);
+  forward_enqueue(md, kv, w, m, pos0, s, nullptr);
+  forward_commit(kv, m, pos0);
 }
 
 // hidden_to_logits_batch (model.rs:966-1033) for the m rows of w.hid.
@@ -594,9 +612,17 @@ struct rai_lookup {
   std::vector<uint32_t> ctx_host;  // mirror of ctx[0..ctx_len)
   size_t ctx_len = 0;
   DevBuf res;             // int[8]: ngram result + accept result
-  int *pin = nullptr;     // pinned host mirror of res + tokens
+  int *pin = nullptr;     // pinned host mirror of res + tokens (+ the step record at pin[512])
   hipStream_t stream = nullptr;
+  // Step graphs: one per verify batch size m (embed, forward, logits,
+  // argmax, accept), replayed with the position in the device step record.
+  DevBuf step;            // int[4] {pos0, len, start, nd}
+  bool graphs = false;
+  std::vector<hipGraphExec_t> graph;
+  std::vector<int> graph_uses;
   ~rai_lookup() {
+    for (hipGraphExec_t g : graph)
+      if (g) (void)hipGraphExecDestroy(g);
     if (pin) (void)hipHostFree(pin);
     if (stream) (void)hipStreamDestroy(stream);
   }
@@ -669,12 +695,44 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
     nd = ngram ? d.pin[2] : 0;
   }
   const int m = nd + 1;  // verify [last, draft...] or the single decode_one token
-  launch_embed(nullptr, d.ctx.as<uint32_t>(), (int)len - 1, start, m, md.emb_codes, md.emb_params, c.vocab_size,
-               c.hidden_size, c.embed_group_size, c.embed_scale, d.ws.hid.as<float>(), d.ws.err.as<int>(), s);
-  forward(md, d.kv, d.ws, m, pos, s);
-  logits(md, d.ws, m, s);
-  launch_argmax(d.ws.logits.as<float>(), m, c.vocab_size, d.ws.am.as<uint32_t>(), s);
-  launch_accept(d.ws.am.as<uint32_t>(), d.ctx.as<uint32_t>(), (int)len, start, nd, res + 4, s);
+  forward_check(md, d.kv, d.ws, m, pos);
+  auto enqueue = [&](const int *st) {
+    launch_embed(nullptr, d.ctx.as<uint32_t>(), (int)len - 1, start, m, md.emb_codes, md.emb_params,
+                 c.vocab_size, c.hidden_size, c.embed_group_size, c.embed_scale, d.ws.hid.as<float>(),
+                 d.ws.err.as<int>(), s, st);
+    forward_enqueue(md, d.kv, d.ws, m, pos, s, st);
+    logits(md, d.ws, m, s);
+    launch_argmax(d.ws.logits.as<float>(), m, c.vocab_size, d.ws.am.as<uint32_t>(), s);
+    launch_accept(d.ws.am.as<uint32_t>(), d.ctx.as<uint32_t>(), (int)len, start, nd, res + 4, s, st);
+  };
+  if (d.graphs && m <= kAttnTokens) {
+    int *sh = d.pin + 512;
+    sh[0] = (int)pos;
+    sh[1] = (int)len;
+    sh[2] = start;
+    sh[3] = nd;
+    HIP_CHECK(hipMemcpyAsync(d.step.p, sh, 4 * sizeof(int), hipMemcpyHostToDevice, s));
+    const int *st = d.step.as<int>();
+    if (d.graph[m]) {
+      HIP_CHECK(hipGraphLaunch(d.graph[m], s));
+    } else if (d.graph_uses[m]++ == 0) {
+      enqueue(st);  // first use: eager (sets kernel attributes, sizes scratch)
+    } else {
+      hipGraph_t g = nullptr;
+      HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      enqueue(st);
+      HIP_CHECK(hipStreamEndCapture(s, &g));
+      hipGraphExec_t ge = nullptr;
+      const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      HIP_CHECK(ie);
+      d.graph[m] = ge;
+      HIP_CHECK(hipGraphLaunch(ge, s));
+    }
+  } else {
+    enqueue(nullptr);
+  }
+  forward_commit(d.kv, m, pos);
   HIP_CHECK(hipMemcpyAsync(d.pin + 4, res + 4, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
   HIP_CHECK(hipMemcpyAsync(d.pin + 8, d.ctx.as<uint32_t>() + len, (size_t)m * sizeof(uint32_t),
                            hipMemcpyDeviceToHost, s));
@@ -1132,8 +1190,15 @@ int rai_lookup_create(rai_model *m, size_t max_ctx, rai_lookup **out) {
     d->ctx.alloc((d->max_ctx + 64) * sizeof(uint32_t));
     d->ctx_host.assign(d->max_ctx + 64, 0);
     d->res.alloc(64);
+    d->step.alloc(64);
     HIP_CHECK(hipHostMalloc((void **)&d->pin, 4096, hipHostMallocDefault));
     HIP_CHECK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+    // Step graphs for dense models (the MoE block synchronises with the
+    // host to group tokens by expert, which a graph cannot hold).
+    const char *env = std::getenv("RAI_STEP_GRAPHS");
+    d->graphs = m->cfg.num_experts == 0 && !(env && env[0] == '0');
+    d->graph.assign(rai::kAttnTokens + 1, nullptr);
+    d->graph_uses.assign(rai::kAttnTokens + 1, 0);
     *out = d.release();
   });
 }

@@ -184,6 +184,25 @@ def test_lookup_generate_loop_matches_greedy(rai):
     assert stats["steps"] <= stats["generated"]
 
 
+def test_step_graph_replay_matches_eager(rai, monkeypatch):
+    """The decode step replayed as a HIP graph (position read from the
+    device step record, capacity-sized attention grids) produces the same
+    token stream and metrics as eager launches, over enough steps that every
+    verify size used is captured and replayed several times."""
+    img = _small_synth(rai, seed=21)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    prompt = copy_heavy_prompt(260, 1000, seed=9)
+    cfg = rai.LookupConfig(max_draft=8, min_ngram=1, max_ngram=3)
+    monkeypatch.setenv("RAI_STEP_GRAPHS", "0")
+    eager_toks, eager_stats = rai.LookupDecoder(gm, 1024).generate(prompt, 120, cfg)
+    monkeypatch.setenv("RAI_STEP_GRAPHS", "1")
+    graph_toks, graph_stats = rai.LookupDecoder(gm, 1024).generate(prompt, 120, cfg)
+    assert graph_toks == eager_toks
+    for key in ("steps", "steps_with_draft", "drafted", "accepted", "generated"):
+        assert graph_stats[key] == eager_stats[key], key
+    assert graph_toks == rai.LookupDecoder(gm, 1024).greedy_generate(prompt, len(graph_toks))
+
+
 def test_lookup_config_errors(rai):
     """validate_lookup_config (lookup.rs:457-475); sampled mode is not built."""
     gm = rai.RaiModel.from_bytes(read_golden("tiny-untied.raimodel"))
