@@ -24,6 +24,10 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall",
           "-I", os.path.join(ROOT, "include"), "-I", CSRC]
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 SOURCES = ["kernels.hip", "fused.hip", "gemv.hip", "runtime.hip", "format.cpp", "synth.cpp"]
+# Per-source device flags: the matrix-core GEMV keeps MFMA results in
+# architectural VGPRs, which its epilogue reads directly (without it the
+# compiler routes them through AGPRs and one copy per value).
+EXTRA = {"gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(src: str) -> str:
@@ -31,7 +35,7 @@ def _compile(src: str) -> str:
     obj = os.path.join(OBJ, src + ".o")
     cmd = [HIPCC] + COMMON
     if src.endswith(".hip"):
-        cmd += DEVICE + ["-x", "hip"]
+        cmd += DEVICE + EXTRA.get(src, []) + ["-x", "hip"]
     cmd += ["-c", path, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # The host pass of hipcc does not know the packed-fp32 feature and says so;

@@ -4,25 +4,31 @@
 // group, the reference's per-lane int8 x int4 sums, gemm.rs:458-525) come
 // from v_mfma_f32_16x16x32_f16 with exact operands: weight codes 0..15 and
 // int8 activations are exact in f16, every product and partial sum is an
-// integer below 2^24, so the f32 accumulators hold S exactly whatever the
-// summation order inside the instruction.
+// integer (or, for codes entered as subnormals, an integer times 2^-24)
+// well inside the f32 significand, so the f32 accumulators hold S exactly
+// whatever the summation order inside the instruction.
 //
 // MFMA operand roles (16x16x32): B = weights, column j = row of the weight
-// tile (16 rows per wave), K = the group's 32 columns in the lane order
-// below.  A = activations, block-diagonal: A row i = 4t + b (token t of the
-// wave's 4-token group, block b), nonzero only on block b's 8 columns.  So
-// D[4t + b][j] = S[row j][token t][block b], and lane l (j = l % 16,
-// h = l / 16) receives S for row j, token h, blocks 0..3 in its 4
-// accumulators: exactly the 4 reference lane chains of one (row, token).
+// tile (16 rows per wave); A = activations, block-diagonal, so that each of
+// the 16 D rows collects one (token, 8-column block) partial sum: lane l
+// (j = l % 16, h = l / 16) receives in its 4 accumulators the S values of
+// row j and token h for 4 (group, block) pairs.  k_gemv_ms spans one group's
+// 4 blocks per instruction, k_gemv_rs block b of 4 consecutive groups.
 //
 // Each lane then runs the reference epilogue for its (row, token) in group
 // order: cs = fl(ws * as); f_b += fl(S_b * cs); zc += fl(wz * xsum), and at
 // the end out = hsum8(f0..f3, 0, 0, 0, 0) + zc (gemm.rs:458-537).  The
-// chains never leave the lane, so no products go through LDS.
+// chains never leave the lane, so no products go through LDS.  That f32
+// epilogue (11 VALU operations per row, token and group) rather than HBM
+// bounds these kernels at 9 tokens.
 //
 // K order inside a block (8 columns c0..c7): f16 element e of the lane's 8
 // is column (0, 4, 1, 5, 2, 6, 3, 7)[e], which is what the nibble unpack
 // (shifts by 0/4/8/12 of a 0x000F000F mask) produces for the weights.
+//
+// Activations for both kernels are packed once per GEMV input by
+// k_qa_pack4 as qa4[tg][q][b][i = 4t + r][8] f16: token 4*tg + t, group
+// 4*q + r, block b.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -73,33 +79,6 @@ __device__ __forceinline__ h8 unpack_codes(uint32_t w) {
 
 }  // namespace
 
-// Activations in the MFMA A-operand layout: qa[tg][g][slot i = 4t + b][8]
-// f16, block b of token 4*tg + t in the K order above (zeros for tokens
-// past m).  One thread per (token slot, group, block).
-__global__ void k_qa_pack(const int8_t *__restrict__ q_split, int m, int cols, int ntg,
-                          _Float16 *__restrict__ qa) {
-  const int groups = cols / 32;
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // over ntg*groups*16
-  if (idx >= ntg * groups * 16) return;
-  const int i = idx & 15, g = (idx >> 4) % groups, tg = (idx >> 4) / groups;
-  const int t = 4 * tg + i / 4, b = i % 4;
-  _Float16 *dst = qa + (size_t)idx * 8;
-  if (t >= m) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dst[e] = (_Float16)0.0f;
-    return;
-  }
-  // q_split block: bytes 0..3 = even columns 0,2,4,6; bytes 4..7 = odd 1,3,5,7.
-  const int8_t *src = q_split + (size_t)t * cols + g * 32 + 8 * b;
-  const int col_of_e[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int c = col_of_e[e];
-    const int sidx = (c & 1) ? 4 + (c >> 1) : (c >> 1);
-    dst[e] = (_Float16)(float)src[sidx];
-  }
-}
-
 // Block-staged version.  A block of WPB waves owns RB = 16*WPB weight rows
 // and TGW token groups (4*TGW tokens); wave w computes rows 16w..16w+15.
 // K runs in tiles of P groups.  All threads of the block cooperatively
@@ -124,7 +103,6 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv_ms(
   constexpr int NW4 = RB * P / NT;         // code float4 per thread per tile
   constexpr int NP4 = (RB * P / 4 + NT - 1) / NT;   // param float4 per thread
   constexpr int NA4 = (TGW * P * 16 + NT - 1) / NT; // activation float4 per thread
-  constexpr int ASLOT = 16 * 8;            // halves per (tg, group) in qa
   static_assert(NW4 * NT == RB * P, "code tile must split evenly");
   __shared__ __align__(16) uint32_t lw[2][RB * WSTR];
   __shared__ uint32_t lp[2][RB * PSTR];
@@ -183,7 +161,10 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv_ms(
     for (int u = 0; u < NA4; ++u) {
       const int i = min(tid + NT * u, TGW * P * 16 - 1);
       const int tg = i / (P * 16), k = i % (P * 16);
-      S.a[u] = reinterpret_cast<const u4 *>(qa + ((size_t)(tgc * TGW + tg) * groups + (size_t)kt * P) * ASLOT)[k];
+      // A row (slot) 4t + b of group p sits at qa4[tg][p / 4][b][4t + p % 4].
+      const int p = kt * P + k / 16, t = (k & 15) >> 2, b = k & 3;
+      S.a[u] = reinterpret_cast<const u4 *>(qa)[(((size_t)(tgc * TGW + tg) * (groups / 4) + p / 4) * 4 + b) * 16 +
+                                                4 * t + (p & 3)];
     }
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
@@ -289,6 +270,248 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv_ms(
   }
 }
 
+// Activations in the register-streamed kernel's A layout:
+// qa4[tg][q][b][i = 4t + r][8] f16 = token 4*tg + t, group 4*q + r, block b
+// in the K order above (zeros for tokens past m).  One thread per
+// (tg, q, b, i).  Requires groups % 4 == 0.
+__global__ void k_qa_pack4(const int8_t *__restrict__ q_split, int m, int cols, int ntg,
+                           _Float16 *__restrict__ qa) {
+  const int groups = cols / 32, nq = groups / 4;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // over ntg*nq*64
+  if (idx >= ntg * nq * 64) return;
+  const int i = idx & 15, b = (idx >> 4) & 3, qq = (idx >> 6) % nq, tg = (idx >> 6) / nq;
+  const int t = 4 * tg + (i >> 2), g = 4 * qq + (i & 3);
+  _Float16 *dst = qa + (size_t)idx * 8;
+  if (t >= m) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[e] = (_Float16)0.0f;
+    return;
+  }
+  const int8_t *src = q_split + (size_t)t * cols + g * 32 + 8 * b;
+  const int col_of_e[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int c = col_of_e[e];
+    const int sidx = (c & 1) ? 4 + (c >> 1) : (c >> 1);
+    dst[e] = (_Float16)(float)src[sidx];
+  }
+}
+
+// Register-streamed version.  MFMA K = 32 covers block b of four
+// consecutive groups 4q..4q+3: B lane (j, h) = row j's codes of group
+// 4q + h, block b (one dword of the 16-byte group it loads); A row
+// i = 4t + r is token t's block b of group 4q + r, nonzero only on K block
+// r.  Lane (j, h) then holds D[4h + r][j] = S[row j][token h][group 4q+r]
+// [block b], so after the four blocks it owns the four lane chains of
+// (row j, token h) for four groups, which it accumulates in group order.
+//
+// Each lane streams its own weight bytes (16 B of codes and 16 B of params
+// per step of four groups) through a register ring NQ steps deep; the
+// first NQ steps of the loop only fill the ring (through the same code, so
+// the loop starts with nothing in flight and every load wait stays
+// static).  The block's activations, scales and input sums go through LDS
+// in chunks of NQ steps, double-buffered: chunk c + 1 is loaded into
+// registers while chunk c is computed and stored behind it, with one barrier
+// per chunk.
+//
+// Codes enter the MFMA either as f16 subnormals n * 2^-24 (SUB: one mask
+// per pair, D = S * 2^-24 exactly, products and partial sums being
+// multiples of 2^-24 below 2^-10) with the weight scale taken as ws * 2^24,
+// or as 1024 + n minus 1024 (D = S).  fl(D * fl(ws*2^24 * as)) equals
+// fl(S * fl(ws * as)) whenever |ws * as| < 2^104 (power-of-two scaling
+// commutes with rounding in the normal range, and ws * as is zero or at
+// least 2^-24 * 1e-10 / 127), which holds when every activation scale is
+// below 2^88 since |ws| <= 65504.  A chunk whose staged scales include a
+// larger finite value is computed in the 1024 + n form.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ h8 unpack_codes_sub(uint32_t w) {
+  const uint32_t m = 0x000F000Fu;
+  const u32x4 d = {w & m, (w >> 4) & m, (w >> 8) & m, (w >> 12) & m};
+  return __builtin_bit_cast(h8, d);
+}
+
+// NQ steps of the main loop on one staged chunk (LDS buffer at la_c, lsc_c,
+// lsu_c); steps q < 0 or q >= nq only refill the ring.
+template <int TGW, bool SUB>
+__device__ __forceinline__ void gemv_rs_step(
+    const u32x4 &rc, const u32x4 &rp, int s, int NQ, const u32x4 *__restrict__ la_c,
+    const f32x4 *__restrict__ lsc_c, const f32x4 *__restrict__ lsu_c, int h, float (&f)[TGW][4],
+    float (&zc)[TGW]) {
+  typedef f32x4 f4;
+  const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 D[TGW][4], as4[TGW], xs4[TGW];
+  float ws[4], wz[4];
+  u32x4 av[TGW][4];
+#pragma unroll
+  for (int tg = 0; tg < TGW; ++tg) {
+    const int base = (tg * NQ + s) * 4;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) av[tg][b] = la_c[(base + b) * 17];
+    as4[tg] = lsc_c[base + h];
+    xs4[tg] = lsu_c[base + h];
+  }
+  h8 bq[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) bq[b] = SUB ? unpack_codes_sub(rc[b]) : unpack_codes(rc[b]);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    ws[r] = SUB ? f16lo(rp[r]) * 16777216.0f : f16lo(rp[r]);
+    wz[r] = f16hi(rp[r]);
+  }
+#pragma unroll
+  for (int tg = 0; tg < TGW; ++tg) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      D[tg][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, av[tg][b]), bq[b], zero4, 0, 0, 0);
+  }
+#pragma unroll
+  for (int tg = 0; tg < TGW; ++tg) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float cs = ws[r] * as4[tg][r];
+      f[tg][0] = f[tg][0] + D[tg][0][r] * cs;
+      f[tg][1] = f[tg][1] + D[tg][1][r] * cs;
+      f[tg][2] = f[tg][2] + D[tg][2][r] * cs;
+      f[tg][3] = f[tg][3] + D[tg][3][r] * cs;
+      zc[tg] = zc[tg] + wz[r] * xs4[tg][r];
+    }
+  }
+}
+
+// NQ steps of the main loop on one staged chunk (LDS buffer at la_c, lsc_c,
+// lsu_c); steps q < 0 or q >= nq only refill the ring.  The compute branch
+// holds no memory loads, so every load wait stays static.
+template <int TGW, int NQ>
+__device__ __forceinline__ void gemv_rs_steps(
+    int q0, bool huge, u32x4 (&rc)[NQ], u32x4 (&rp)[NQ], const u32x4 *__restrict__ cptr,
+    const u32x4 *__restrict__ pptr, const u32x4 *__restrict__ la_c, const f32x4 *__restrict__ lsc_c,
+    const f32x4 *__restrict__ lsu_c, int nq, int h, float (&f)[TGW][4], float (&zc)[TGW]) {
+#pragma unroll
+  for (int s = 0; s < NQ; ++s) {
+    const int q = q0 + s;
+    if (q >= 0 && q < nq) {
+      if (huge)
+        gemv_rs_step<TGW, false>(rc[s], rp[s], s, NQ, la_c, lsc_c, lsu_c, h, f, zc);
+      else
+        gemv_rs_step<TGW, true>(rc[s], rp[s], s, NQ, la_c, lsc_c, lsu_c, h, f, zc);
+    }
+    const int qn = min(q + NQ, nq - 1);
+    rc[s] = cptr[4 * qn];
+    rp[s] = pptr[qn];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int TGW, int NQ, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_gemv_rs(
+    float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
+    const _Float16 *__restrict__ qa, const float *__restrict__ scales,
+    const float *__restrict__ sums, int rows, int cols, int m, int ntg) {
+  typedef u32x4 u4;
+  typedef f32x4 f4;
+  constexpr int NT = 64 * WPB;
+  constexpr int AU = TGW * NQ * 64;       // A u4 per chunk
+  constexpr int SU = TGW * NQ * 4;        // scale / sum f4 per chunk
+  constexpr int NA = (AU + NT - 1) / NT;  // per thread
+  constexpr int NS = (SU + NT - 1) / NT;
+  constexpr int ABUF = TGW * NQ * 68;     // u4 per A buffer, 17 slots per block
+  extern __shared__ __align__(16) unsigned char smem[];
+  // LDS: A [2][TGW][NQ][4 blocks][17 slots] u4 (slot 16 zero) | scales,
+  // sums [2][TGW][NQ][4 tokens] f4 (groups 4q..4q+3).
+  u4 *la = reinterpret_cast<u4 *>(smem);
+  f4 *lsc = reinterpret_cast<f4 *>(la + 2 * ABUF);
+  f4 *lsu = lsc + 2 * SU;
+  const int groups = cols / 32, nq = groups / 4, nch = (nq + NQ - 1) / NQ;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, h = lane >> 4;
+  const int tg0 = blockIdx.y * TGW;
+  const int row = blockIdx.x * (16 * WPB) + 16 * wave + j;
+  const int rowc = min(row, rows - 1);
+  const u4 *cptr = reinterpret_cast<const u4 *>(nib + (size_t)rowc * (cols / 2)) + h;
+  const u4 *pptr = reinterpret_cast<const u4 *>(params + (size_t)rowc * groups * 4);
+  const u4 *qsrc = reinterpret_cast<const u4 *>(qa);
+  for (int i = tid; i < 2 * TGW * NQ * 4; i += NT) la[i * 17 + 16] = u4{0u, 0u, 0u, 0u};
+
+  // Chunk staging.  Token groups past ntg (grid rounding) and steps past nq
+  // load clamped duplicates; their results are never stored.
+  u4 sa[NA];
+  f4 ssc[NS], ssu[NS];
+#define RAI_RS_LOAD(C)                                                                          \
+  {                                                                                             \
+    const int c_ = (C);                                                                         \
+    _Pragma("unroll") for (int u = 0; u < NA; ++u) {                                            \
+      const int i = min(tid + NT * u, AU - 1);                                                  \
+      const int tg = i / (NQ * 64), rem = i - tg * (NQ * 64);                                   \
+      const int qq = min(c_ * NQ + rem / 64, nq - 1);                                           \
+      sa[u] = qsrc[((size_t)min(tg0 + tg, ntg - 1) * nq + qq) * 64 + (rem & 63)];                \
+    }                                                                                           \
+    _Pragma("unroll") for (int u = 0; u < NS; ++u) {                                            \
+      const int i = min(tid + NT * u, SU - 1);                                                  \
+      const int tg = i / (NQ * 4), qq = min(c_ * NQ + (i / 4) % NQ, nq - 1);                     \
+      const int tok = min(4 * (tg0 + tg) + (i & 3), m - 1);                                     \
+      ssc[u] = reinterpret_cast<const f4 *>(scales + (size_t)tok * groups)[qq];                 \
+      ssu[u] = reinterpret_cast<const f4 *>(sums + (size_t)tok * groups)[qq];                   \
+    }                                                                                           \
+  }
+  int huge = 0;
+  float f[TGW][4], zc[TGW];
+#pragma unroll
+  for (int tg = 0; tg < TGW; ++tg) {
+    f[tg][0] = f[tg][1] = f[tg][2] = f[tg][3] = 0.0f;
+    zc[tg] = 0.0f;
+  }
+  const int aslot = (h == (j & 3)) ? j : 16;
+  u32x4 rc[NQ], rp[NQ];
+  for (int c = -1; c < nch; ++c) {
+    RAI_RS_LOAD(min(c + 1, nch - 1))
+    const int b = c & 1;
+    gemv_rs_steps<TGW, NQ>(c * NQ, huge != 0, rc, rp, cptr, pptr, la + b * ABUF + aslot, lsc + b * SU,
+                           lsu + b * SU, nq, h, f, zc);
+    // Store chunk c + 1 into the other buffer (last read by chunk c - 1,
+    // before the previous barrier) and flag huge scales in it.
+    const int bn = (c + 1) & 1;
+    int big = 0;
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+      const int i = tid + NT * u;
+      if (i < AU) la[bn * ABUF + (i >> 4) * 17 + (i & 15)] = sa[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int i = tid + NT * u;
+      if (i < SU) {
+        lsc[bn * SU + i] = ssc[u];
+        lsu[bn * SU + i] = ssu[u];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = fabsf(ssc[u][e]);
+          big |= (v >= 0x1p88f && v < INFINITY) ? 1 : 0;
+        }
+      }
+    }
+    huge = __syncthreads_or(big);
+  }
+#undef RAI_RS_LOAD
+  if (row < rows) {
+#pragma unroll
+    for (int tg = 0; tg < TGW; ++tg) {
+      const int t = 4 * (tg0 + tg) + h;
+      if (t < m) {
+        const size_t oi = (size_t)t * rows + row;
+        const float v = ((f[tg][0] + f[tg][1]) + (f[tg][2] + f[tg][3])) + zc[tg];
+        out[oi] = add ? add[oi] + v : v;
+      }
+    }
+  }
+}
+
+// LDS bytes of k_gemv_rs: two chunk buffers of A blocks, scales and sums.
+size_t gemv_rs_smem(int tgw, int nq_chunk) {
+  return (size_t)2 * tgw * nq_chunk * (68 * 16 + 2 * 4 * 16);
+}
+
 namespace {
 
 template <int TGW, int P>
@@ -313,9 +536,29 @@ size_t qa_pack_halves(int m, int cols) {
 
 void launch_qa_pack(const int8_t *q_split, int m, int cols, _Float16 *qa, hipStream_t s) {
   const int ntg = (m + 3) / 4;
-  const int n = ntg * (cols / 32) * 16;
-  hipLaunchKernelGGL(k_qa_pack, dim3((n + 255) / 256), dim3(256), 0, s, q_split, m, cols, ntg, qa);
+  const int n = ntg * (cols / 128) * 64;
+  hipLaunchKernelGGL(k_qa_pack4, dim3((n + 255) / 256), dim3(256), 0, s, q_split, m, cols, ntg, qa);
 }
+
+namespace {
+
+template <int TGW, int NQ>
+void launch_rs(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
+               const float *scales, const float *sums, int rows, int cols, int m, int ntg, hipStream_t s) {
+  constexpr int WPB = 4;
+  const size_t smem = gemv_rs_smem(TGW, NQ);
+  static bool configured = false;
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_rs<TGW, NQ, WPB>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = true;
+  }
+  const dim3 grid((rows + 16 * WPB - 1) / (16 * WPB), (ntg + TGW - 1) / TGW);
+  hipLaunchKernelGGL((k_gemv_rs<TGW, NQ, WPB>), grid, dim3(64 * WPB), smem, s, out, add, nib, params, qa,
+                     scales, sums, rows, cols, m, ntg);
+}
+
+}  // namespace
 
 bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                       const float *scales, const float *sums, int rows, int cols, int m, int gs,
@@ -323,14 +566,20 @@ bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const ui
   if (!qa || !w4a8_mfma_path(rows, cols, m, gs)) return false;
   const int ntg = (m + 3) / 4;
   const int groups = cols / 32;
-  // Many rows: one wave keeps every token group (the code unpack and param
-  // decode are shared); few rows: one token group per wave for more waves
-  // (measured on 4096..32000 x 4096..14336, M = 2..16).
-  if (rows >= 8192) {
-    if (ntg == 1) launch_ms<1, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (ntg == 2) launch_ms<2, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (ntg == 3) launch_ms<3, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else launch_ms<4, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+  // Kernel and tiling per shape, measured on 4096..32000 x 4096..14336 and
+  // M = 2..16: the register-streamed kernel for many rows (one wave keeps up
+  // to four token groups; past 16384 rows a shallower ring lets two blocks
+  // share a CU), the block-staged kernel with one token group per wave for
+  // fewer rows.
+  if (rows >= 16384) {
+    if (ntg == 1) launch_rs<1, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (ntg == 2) launch_rs<2, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (ntg == 3) launch_rs<3, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else launch_rs<4, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+  } else if (rows >= 8192) {
+    if (ntg == 1) launch_rs<1, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (ntg == 3) launch_rs<3, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else launch_rs<2, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
   } else if (groups % 16 == 0) {
     launch_ms<1, 16>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
   } else {
