@@ -158,10 +158,13 @@ int rai_w4a8_lane_sums_dev(int32_t *out, const uint8_t *nibbles, const float *x,
 /* Kernel timer (the role of the reference's gemm-bench, bin/gemm_bench.rs:9-77):
  * quantizes x once, then launches the W4A8 kernel `iters` times back to back
  * on its own stream between two HIP events; *avg_ms = elapsed / iters.
- * Device pointers. */
+ * nibbles / params hold `copies` >= 1 back-to-back copies of the weights and
+ * launch i reads copy i % copies, so that enough copies (together larger
+ * than the GPU's last-level cache) make every launch stream its weights from
+ * HBM as in a model step.  Device pointers. */
 int rai_w4a8_time_dev(float *out, const uint8_t *nibbles, const uint8_t *params, const float *x,
-                      size_t rows, size_t cols, size_t m, size_t group_size, int iters,
-                      float *avg_ms);
+                      size_t rows, size_t cols, size_t m, size_t group_size, size_t copies,
+                      int iters, float *avg_ms);
 /* Host-pointer convenience wrapper of rai_w4a8_matmul_dev (copies in/out). */
 int rai_w4a8_matmul(float *out, const uint8_t *nibbles, const uint8_t *params, const float *x,
                     size_t rows, size_t cols, size_t m, size_t group_size);

@@ -109,7 +109,7 @@ def lib():
         "rai_w4a8_matmul_dev": (c_int, [P, P, P, P, S, S, S, S, P]),
         "rai_w4a8_lane_sums_dev": (c_int, [P, P, P, S, S, S, S, P]),
         "rai_w4a8_matmul": (c_int, [P, P, P, P, S, S, S, S]),
-        "rai_w4a8_time_dev": (c_int, [P, P, P, P, S, S, S, S, c_int, POINTER(c_float)]),
+        "rai_w4a8_time_dev": (c_int, [P, P, P, P, S, S, S, S, S, c_int, POINTER(c_float)]),
         "rai_tied_lm_head_dev": (c_int, [P, P, P, P, S, S, S, P]),
         "rai_embed_lookup_dev": (c_int, [P, S, P, P, S, S, S, P]),
         "rai_rms_norm_dev": (c_int, [P, P, P, S, S, c_float, P]),
@@ -233,15 +233,23 @@ def w4a8_matvec(nibbles, params, x, rows: int, cols: int, group_size: int) -> np
 
 
 def w4a8_time(nibbles, params, x, rows: int, cols: int, num_tokens: int, group_size: int,
-              iters: int = 50) -> float:
-    """Average device time (ms) of one W4A8 kernel launch (HIP events)."""
-    dn = DeviceArray.from_host(np.ascontiguousarray(nibbles, np.uint8))
-    dp = DeviceArray.from_host(np.ascontiguousarray(params, np.uint8))
+              iters: int = 50, copies: int = 1) -> float:
+    """Average device time (ms) of one W4A8 kernel launch (HIP events).
+    With copies > 1 the launches rotate over that many device copies of the
+    weights (so that, together larger than the last-level cache, every
+    launch reads its weights from HBM)."""
+    nib = np.ascontiguousarray(nibbles, np.uint8)
+    par = np.ascontiguousarray(params, np.uint8)
+    dn = DeviceArray(nib.nbytes * copies)
+    dp = DeviceArray(par.nbytes * copies)
+    for c in range(copies):
+        _check(lib().rai_memcpy_h2d(c_void_p(dn.ptr + c * nib.nbytes), _ptr(nib), nib.nbytes))
+        _check(lib().rai_memcpy_h2d(c_void_p(dp.ptr + c * par.nbytes), _ptr(par), par.nbytes))
     dx = DeviceArray.from_host(_f32(x))
     do = DeviceArray(num_tokens * rows * 4)
     ms = c_float()
     _check(lib().rai_w4a8_time_dev(do.ptr, dn.ptr, dp.ptr, dx.ptr, rows, cols, num_tokens,
-                                   group_size, iters, ctypes.byref(ms)))
+                                   group_size, copies, iters, ctypes.byref(ms)))
     return ms.value
 
 

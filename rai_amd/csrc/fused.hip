@@ -12,17 +12,11 @@
 
 #include "exact_math.h"
 #include "kernels.h"
+#include "quant_dev.h"
 
 namespace rai {
 
 namespace {
-
-// Column c of a block-split row: 8-column block b holds its even columns at
-// 8b+0..3 and its odd columns at 8b+4..7 (the q_split layout).
-__device__ __forceinline__ int split_col(int c) {
-  const int j = c & 7;
-  return (c & ~7) + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
-}
 
 // A pointer the compiler must treat as lane-varying: loads through it are
 // vector loads (tracked in order by vmcnt) even when every lane reads the
@@ -35,50 +29,14 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T *vector_ptr
   return reinterpret_cast<const __attribute__((address_space(1))) T *>(a);
 }
 
-// Quantize one group held by 8 consecutive lanes (lane j owns the columns
-// 8c + j, c = 0..NB-1, of the group) exactly as quantize_input_split_avx2
-// and compute_input_sums do (gemm.rs:182-212, 280-374):
-//   sum   = ((a0+a4)+(a1+a5))+((a2+a6)+(a3+a7)), a_j = sequential sum of the
-//           lane's values in column order;
-//   scale = absmax/127 (1 when absmax <= 1e-10); q = clamp(rne(v/scale)).
-// All 64 lanes of the wave must call this together.
-// Lanes with ok == false take part in the shuffles and store nothing.
+// quantize_group8_to with row pointers: group at columns col0.. of the
+// rows qs (block-split) and qn (natural, may be null).
 template <int NB>
 __device__ __forceinline__ void quantize_group8(const float (&v)[NB], int j, int col0, bool ok,
                                                 int8_t *__restrict__ qs, int8_t *__restrict__ qn,
                                                 float *__restrict__ scale_out,
                                                 float *__restrict__ sum_out) {
-  float a = 0.0f, amax = 0.0f;
-#pragma unroll
-  for (int c = 0; c < NB; ++c) {
-    a = a + v[c];
-    amax = fmaxf(amax, fabsf(v[c]));
-  }
-  // hsum8 in the reference's order via 8-lane shuffles.
-  const float a4 = __shfl(a, (j + 4) & 7, 8);
-  const float b = a + a4;  // lanes 0..3: a_j + a_{j+4}
-  const float b1 = __shfl(b, (j + 1) & 7, 8);
-  const float c = b + b1;  // lane 0: b0+b1, lane 2: b2+b3
-  const float c2 = __shfl(c, (j + 2) & 7, 8);
-  const float total = c + c2;  // lane 0
-#pragma unroll
-  for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
-  const float scale = amax > 1e-10f ? amax / 127.0f : 1.0f;
-  const float inv = 1.0f / scale;
-  if (!ok) return;
-#pragma unroll
-  for (int c8 = 0; c8 < NB; ++c8) {
-    float r = rintf(v[c8] * inv);
-    r = fminf(fmaxf(r, -128.0f), 127.0f);
-    const int8_t q = (int8_t)(int)r;
-    const int col = col0 + 8 * c8 + j;
-    qs[split_col(col)] = q;
-    if (qn) qn[col] = q;
-  }
-  if (j == 0) {
-    *scale_out = scale;
-    *sum_out = total;
-  }
+  quantize_group8_to<NB>(v, j, ok, qs + col0, qn ? qn + col0 : nullptr, scale_out, sum_out);
 }
 
 // ------------------------------------------------------ RMSNorm + quant --
@@ -97,87 +55,67 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
                                                     int8_t *__restrict__ q_nat,
                                                     float *__restrict__ scales,
                                                     float *__restrict__ sums, int n, float eps) {
-  extern __shared__ float xs[];  // [n] row, then [n] weights
-  float *ws = xs + n;
-  __shared__ float chains[16];
-  __shared__ float inv_sh;
+  extern __shared__ float xs[];
   const int t = blockIdx.x, tid = threadIdx.x;
   const float *row = x + (size_t)t * n;
-  const int n4 = (n % 4 == 0) ? n / 4 : 0;  // rows stay 16-byte aligned
-  for (int i = tid; i < n4; i += 256) {
-    reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(row)[i];
-    reinterpret_cast<float4 *>(ws)[i] = reinterpret_cast<const float4 *>(w)[i];
-  }
-  for (int i = n4 * 4 + tid; i < n; i += 256) {
-    xs[i] = row[i];
-    ws[i] = w[i];
-  }
-  __syncthreads();
-  const int c16 = (n / 8) / 2;
-  const bool extra8 = 16 * c16 + 8 <= n;
-  if (tid < 16) {
-    const int j = tid & 7, off = tid < 8 ? 0 : 8;
-    float a = 0.0f;
-    int i = 0;
-    for (; i + 32 <= c16; i += 32) {
-      float v[32];
-#pragma unroll
-      for (int u = 0; u < 32; ++u) v[u] = xs[16 * (i + u) + off + j];
-#pragma unroll
-      for (int u = 0; u < 32; ++u) a = __fmaf_rn(v[u], v[u], a);
-    }
-    for (; i < c16; ++i) {
-      const float v = xs[16 * i + off + j];
-      a = __fmaf_rn(v, v, a);
-    }
-    if (tid < 8 && extra8) {
-      const float v = xs[16 * c16 + j];
-      a = __fmaf_rn(v, v, a);
-    }
-    chains[tid] = a;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float s[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s[j] = chains[j] + chains[8 + j];
-    float sum = ((s[0] + s[4]) + (s[1] + s[5])) + ((s[2] + s[6]) + (s[3] + s[7]));
-    for (int i = 16 * c16 + (extra8 ? 8 : 0); i < n; ++i) sum = sum + xs[i] * xs[i];
-    // Correctly rounded sqrt and divide (the reference's sqrtss / divss).
-    inv_sh = 1.0f / __builtin_sqrtf(sum / (float)n + eps);
-  }
-  __syncthreads();
-  const float inv = inv_sh;
-  if constexpr (GS == 0) {
+  if constexpr (GS > 0) {
+    // n % 8 == 0 and GS | n (fused_quant_ok).
+    const int groups = n / GS;
+    rmsnorm_quant_block<GS>(row, w, n, eps, xs, q_split + (size_t)t * n, GS,
+                            q_nat ? q_nat + (size_t)t * n : nullptr, scales + (size_t)t * groups,
+                            sums + (size_t)t * groups, normed ? normed + (size_t)t * n : nullptr);
+  } else {
     // RMSNorm only (rms_norm / rms_norm_with_residual): out = (x*inv)*w.
+    float *ws = xs + n;  // [n] row, then [n] weights
+    __shared__ float chains[16];
+    __shared__ float inv_sh;
+    const int n4 = (n % 4 == 0) ? n / 4 : 0;  // rows stay 16-byte aligned
+    for (int i = tid; i < n4; i += 256) {
+      reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(row)[i];
+      reinterpret_cast<float4 *>(ws)[i] = reinterpret_cast<const float4 *>(w)[i];
+    }
+    for (int i = n4 * 4 + tid; i < n; i += 256) {
+      xs[i] = row[i];
+      ws[i] = w[i];
+    }
+    __syncthreads();
+    const int c16 = (n / 8) / 2;
+    const bool extra8 = 16 * c16 + 8 <= n;
+    if (tid < 16) {
+      const int j = tid & 7, off = tid < 8 ? 0 : 8;
+      float a = 0.0f;
+      int i = 0;
+      for (; i + 32 <= c16; i += 32) {
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) v[u] = xs[16 * (i + u) + off + j];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) a = __fmaf_rn(v[u], v[u], a);
+      }
+      for (; i < c16; ++i) {
+        const float v = xs[16 * i + off + j];
+        a = __fmaf_rn(v, v, a);
+      }
+      if (tid < 8 && extra8) {
+        const float v = xs[16 * c16 + j];
+        a = __fmaf_rn(v, v, a);
+      }
+      chains[tid] = a;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float s[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[j] = chains[j] + chains[8 + j];
+      float sum = ((s[0] + s[4]) + (s[1] + s[5])) + ((s[2] + s[6]) + (s[3] + s[7]));
+      for (int i = 16 * c16 + (extra8 ? 8 : 0); i < n; ++i) sum = sum + xs[i] * xs[i];
+      // Correctly rounded sqrt and divide (the reference's sqrtss / divss).
+      inv_sh = 1.0f / __builtin_sqrtf(sum / (float)n + eps);
+    }
+    __syncthreads();
+    const float inv = inv_sh;
     float *nrow = normed + (size_t)t * n;
     for (int i = tid; i < n; i += 256) nrow[i] = (xs[i] * inv) * ws[i];
-    return;
-  } else {
-  const int groups = n / GS;
-  constexpr int NB = GS / 8;
-  float *nrow = normed ? normed + (size_t)t * n : nullptr;
-  int8_t *qs = q_split + (size_t)t * n;
-  int8_t *qn = q_nat ? q_nat + (size_t)t * n : nullptr;
-  // 8 lanes per group; every lane of a wave iterates the same number of times
-  // so the group shuffles always see all 64 lanes.
-  const int per_pass = 256 / 8;
-  const int passes = (groups + per_pass - 1) / per_pass;
-  for (int p = 0; p < passes; ++p) {
-    const int g = p * per_pass + tid / 8;
-    const int j = tid & 7;
-    const bool ok = g < groups;
-    const int col0 = (ok ? g : 0) * GS;
-    float v[NB];
-#pragma unroll
-    for (int c = 0; c < NB; ++c) {
-      const int col = col0 + 8 * c + j;
-      v[c] = ok ? (xs[col] * inv) * ws[col] : 0.0f;
-      if (ok && nrow) nrow[col] = v[c];
-    }
-    quantize_group8<NB>(v, j, col0, ok, qs, qn, scales + (size_t)t * groups + g,
-                        sums + (size_t)t * groups + g);
-  }
   }
 }
 
@@ -588,7 +526,7 @@ template <int GS>
 void launch_norm_quant_t(const float *x, const float *w, float *normed, int m, int n, float eps,
                          int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
                          hipStream_t s) {
-  const size_t smem = 2 * sizeof(float) * (size_t)n;
+  const size_t smem = (GS > 0 ? 1 : 2) * sizeof(float) * (size_t)n;
   static size_t configured = 0;
   if (smem > 48 * 1024 && smem > configured) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_norm_quant<GS>),

@@ -28,6 +28,14 @@ void launch_w4a8(float *out, const float *add, const uint8_t *nib, const uint8_t
                  const float *sums, int rows, int cols, int m, int gs, hipStream_t s,
                  const _Float16 *qa = nullptr);
 
+// One token: rms_norm(x) * norm_w (layers.rs:325-376), its group-32
+// quantization and the W4A8 GEMV in one launch; each block normalises and
+// quantizes the row into its own LDS (no workspace traffic).  Applies when
+// w4a8_norm1_path holds (group 32, at most 128 groups); false otherwise.
+bool w4a8_norm1_path(int rows, int cols, int gs);
+bool launch_w4a8_norm1(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const float *x,
+                       const float *norm_w, float eps, int rows, int cols, int gs, hipStream_t s);
+
 // Matrix-core W4A8 (gemv.hip): group 32, K a multiple of 256, 2..16 tokens.
 constexpr int kMfmaMaxTokens = 16;
 bool w4a8_mfma_path(int rows, int cols, int m, int gs);

@@ -14,6 +14,7 @@
 
 #include "exact_math.h"
 #include "kernels.h"
+#include "quant_dev.h"
 
 namespace rai {
 
@@ -373,7 +374,8 @@ template <int GS, int MT, int R, int PD, bool WHOLE>
 __global__ __launch_bounds__(kThreads) void k_w4a8_small(
     float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
     const int8_t *__restrict__ q_split, const float *__restrict__ scales,
-    const float *__restrict__ sums, int rows, int cols, int m_total, int groups) {
+    const float *__restrict__ sums, int rows, int cols, int m_total, int groups,
+    const float *__restrict__ nx, const float *__restrict__ nw, float eps) {
   using C = SmallCfg<GS, MT, R, PD, WHOLE>;
   constexpr int NL = C::NL, NC = C::NC, NW = C::NW, GT = C::GT, PSTR = C::PSTR, QSTR = C::QSTR;
   constexpr int CPT = C::CPT, QV = C::QV;
@@ -401,23 +403,29 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_small(
   const uint8_t *nrow = nib + (size_t)(row_ok ? row_item : 0) * row_bytes;
   const uint8_t *prow = params + (size_t)(row_ok ? row_item : 0) * groups * 4;
 
-  // Weight ring: tile kt lives in slot kt % PD.
+  // Fused RMSNorm input (one token, whole K staged, group 32, at most 128
+  // groups): its loads go out before the weights'.
+  constexpr bool NORM_OK = MT == 1 && WHOLE && GS == 32;
+  constexpr int NPN = NORM_OK ? 4 : 1;
+  float xr[NPN][GS / 8], wr[NPN][GS / 8];
+  if (NORM_OK && nx) rmsnorm_regs_load<GS, NPN>(nx, nw, cols, xr, wr);
+  // Weight ring: tile kt lives in slot kt % PD.  Every load is issued,
+  // clamped into the row (items past the row are never read back), so the
+  // waits on earlier loads stay exact.
   uint32_t ring_c[PD][NW];
   uint32_t ring_p[PD];
   auto load_tile = [&](int kt, uint32_t (&c)[NW], uint32_t &p) {
-    const int gi = kt * GT + g_item;
-    if (row_ok && gi < groups) {
-      const uint4 *cp = reinterpret_cast<const uint4 *>(nrow + (size_t)gi * (GS / 2));
+    const int gi = min(kt * GT + g_item, groups - 1);
+    const uint4 *cp = reinterpret_cast<const uint4 *>(nrow + (size_t)gi * (GS / 2));
 #pragma unroll
-      for (int v = 0; v < NW / 4; ++v) {
-        const uint4 u = cp[v];
-        c[4 * v + 0] = u.x;
-        c[4 * v + 1] = u.y;
-        c[4 * v + 2] = u.z;
-        c[4 * v + 3] = u.w;
-      }
-      p = *reinterpret_cast<const uint32_t *>(prow + (size_t)gi * 4);
+    for (int v = 0; v < NW / 4; ++v) {
+      const uint4 u = cp[v];
+      c[4 * v + 0] = u.x;
+      c[4 * v + 1] = u.y;
+      c[4 * v + 2] = u.z;
+      c[4 * v + 3] = u.w;
     }
+    p = *reinterpret_cast<const uint32_t *>(prow + (size_t)gi * 4);
   };
   // Stage activations for groups [g0, g0+gn) of tokens t0.. into buffer b.
   auto stage_direct = [&](int b, int g0, int gn) {
@@ -441,9 +449,15 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_small(
   for (int j = 0; j < CPT; ++j) acc[j] = 0.0f;
 
 #pragma unroll
-  for (int j = 0; j < PD; ++j)
-    if (j < ktiles) load_tile(j, ring_c[j], ring_p[j]);
-  stage_direct(0, 0, WHOLE ? groups : min(GT, groups));
+  for (int j = 0; j < PD; ++j) load_tile(j, ring_c[j], ring_p[j]);
+  if constexpr (NORM_OK) {
+    if (nx)
+      rmsnorm_quant_regs<GS, NPN>(xr, wr, cols, eps, psh, qsh, QSTR, ash, ssh);
+    else
+      stage_direct(0, 0, groups);
+  } else {
+    stage_direct(0, 0, WHOLE ? groups : min(GT, groups));
+  }
   __syncthreads();
 
   uint2 qn[QV];
@@ -498,8 +512,8 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_small(
           pt[(size_t)NL * R * PSTR] = wz * ssh[(buf * m + t) * gstage + gq];
         }
       }
-      // Refill this ring slot with tile kt + PD.
-      if (kt + PD < ktiles) load_tile(kt + PD, ring_c[j], ring_p[j]);
+      // Refill this ring slot with tile kt + PD (clamped past the row).
+      load_tile(kt + PD, ring_c[j], ring_p[j]);
       // Publish the next tile's activations into the other buffer.
       if (!WHOLE && gn_next > 0) {
         int8_t *qb = qsh + (size_t)((kt + 1) & 1) * m * gstage * QSTR;
@@ -554,21 +568,23 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_small(
 }
 
 // LDS bytes for a launch whose token tiles hold at most m tokens.
+// With a fused RMSNorm (norm_cols > 0) the products area doubles as the
+// row scratch.
 template <int GS, int MT, int R, int PD, bool WHOLE>
-size_t small_smem(int groups, int m) {
+size_t small_smem(int groups, int m, int norm_cols = 0) {
   using C = SmallCfg<GS, MT, R, PD, WHOLE>;
   const int gstage = WHOLE ? groups : C::GT;
   const int nbuf = WHOLE ? 1 : 2;
   const size_t qbytes = (((size_t)nbuf * m * gstage * C::QSTR) + 15) & ~size_t(15);
   return qbytes + 2 * sizeof(float) * (size_t)nbuf * m * gstage +
-         sizeof(float) * (size_t)m * C::NC * R * C::PSTR;
+         std::max(sizeof(float) * (size_t)m * C::NC * R * C::PSTR, sizeof(float) * (size_t)norm_cols);
 }
 
 template <int GS, int MT, int R, int PD, bool WHOLE>
 void launch_small_t(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                     const float *scales, const float *sums, int rows, int cols, int m, int groups,
-                    hipStream_t s) {
-  const size_t smem = small_smem<GS, MT, R, PD, WHOLE>(groups, std::min(m, MT));
+                    hipStream_t s, const float *nx = nullptr, const float *nw = nullptr, float eps = 0.0f) {
+  const size_t smem = small_smem<GS, MT, R, PD, WHOLE>(groups, std::min(m, MT), nx ? cols : 0);
   static size_t configured = 0;
   if (smem > configured) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_small<GS, MT, R, PD, WHOLE>),
@@ -577,7 +593,7 @@ void launch_small_t(float *out, const float *add, const uint8_t *nib, const uint
   }
   dim3 grid((rows + R - 1) / R, (m + MT - 1) / MT);
   hipLaunchKernelGGL((k_w4a8_small<GS, MT, R, PD, WHOLE>), grid, dim3(kThreads), smem, s, out, add,
-                     nib, params, q_split, scales, sums, rows, cols, m, groups);
+                     nib, params, q_split, scales, sums, rows, cols, m, groups, nx, nw, eps);
 }
 
 // ---------------------------------------------------------- w4a8 M = 1 --
@@ -596,7 +612,8 @@ template <int GS, int R, int IPT>
 __global__ __launch_bounds__(kThreads) void k_w4a8_m1(
     float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
     const int8_t *__restrict__ q_split, const float *__restrict__ scales,
-    const float *__restrict__ sums, int rows, int cols, int groups) {
+    const float *__restrict__ sums, int rows, int cols, int groups, const float *__restrict__ nx,
+    const float *__restrict__ nw, float eps) {
   constexpr int NL = (GS == 32) ? 4 : 8;
   constexpr int NC = NL + 1;
   constexpr int NW = GS / 8;
@@ -606,11 +623,16 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_m1(
   const int row0 = blockIdx.x * R;
   const int pstr = groups + 1;  // padded product stride
   // LDS: q [K] (block-split) | scale, sum [G] | products [NC][R][G+1]
+  // (16-byte aligned)
   int8_t *qsh = reinterpret_cast<int8_t *>(smem);
   float *ash = reinterpret_cast<float *>(smem + ((cols + 15) & ~15));
   float *ssh = ash + groups;
-  float *psh = ssh + groups;
+  float *psh = ash + ((2 * groups + 3) & ~3);  // 16-byte aligned
   const int items = R * groups;
+  // Fused RMSNorm input (group 32, at most 128 groups): loaded first.
+  constexpr int NP = (GS == 32) ? 4 : 1;
+  float xr[NP][GS / 8], wr[NP][GS / 8];
+  if (GS == 32 && nx) rmsnorm_regs_load<GS, NP>(nx, nw, cols, xr, wr);
   uint32_t cw[IPT][NW];
   uint32_t pw[IPT];
   int ir[IPT], ig[IPT];
@@ -619,25 +641,32 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_m1(
     const int i = tid + j * kThreads;
     ir[j] = i / groups;
     ig[j] = i - ir[j] * groups;
-    const int row = row0 + ir[j];
-    if (i < items && row < rows) {
-      const uint4 *cp = reinterpret_cast<const uint4 *>(nib + (size_t)row * (cols / 2) + ig[j] * (GS / 2));
+    // Every load is issued (clamped into the matrix; unused items are never
+    // read back), so the waits on earlier loads stay exact.
+    const int row = min(row0 + ir[j], rows - 1);
+    const int gi = i < items ? ig[j] : 0;
+    const uint4 *cp = reinterpret_cast<const uint4 *>(nib + (size_t)row * (cols / 2) + gi * (GS / 2));
 #pragma unroll
-      for (int v = 0; v < NW / 4; ++v) {
-        const uint4 u = cp[v];
-        cw[j][4 * v + 0] = u.x;
-        cw[j][4 * v + 1] = u.y;
-        cw[j][4 * v + 2] = u.z;
-        cw[j][4 * v + 3] = u.w;
-      }
-      pw[j] = *reinterpret_cast<const uint32_t *>(params + ((size_t)row * groups + ig[j]) * 4);
+    for (int v = 0; v < NW / 4; ++v) {
+      const uint4 u = cp[v];
+      cw[j][4 * v + 0] = u.x;
+      cw[j][4 * v + 1] = u.y;
+      cw[j][4 * v + 2] = u.z;
+      cw[j][4 * v + 3] = u.w;
     }
+    pw[j] = *reinterpret_cast<const uint32_t *>(params + ((size_t)row * groups + gi) * 4);
   }
-  for (int i = tid; i < cols / 16; i += kThreads)
-    reinterpret_cast<uint4 *>(qsh)[i] = reinterpret_cast<const uint4 *>(q_split)[i];
-  for (int i = tid; i < groups; i += kThreads) {
-    ash[i] = scales[i];
-    ssh[i] = sums[i];
+  if (GS == 32 && nx) {
+    // RMSNorm + quantization of the input row into LDS (the products area
+    // serves as the row scratch) while the weight loads are in flight.
+    rmsnorm_quant_regs<GS, NP>(xr, wr, cols, eps, psh, qsh, GS, ash, ssh);
+  } else {
+    for (int i = tid; i < cols / 16; i += kThreads)
+      reinterpret_cast<uint4 *>(qsh)[i] = reinterpret_cast<const uint4 *>(q_split)[i];
+    for (int i = tid; i < groups; i += kThreads) {
+      ash[i] = scales[i];
+      ssh[i] = sums[i];
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -683,11 +712,12 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_m1(
 template <int GS, int R>
 void launch_m1_t(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                  const float *scales, const float *sums, int rows, int cols, int groups,
-                 hipStream_t s) {
+                 hipStream_t s, const float *nx = nullptr, const float *nw = nullptr, float eps = 0.0f) {
   constexpr int NC = (GS == 32) ? 5 : 9;
   constexpr int IPT = m1_items_per_thread(GS);
-  const size_t smem = (size_t)((cols + 15) & ~15) + 8 * (size_t)groups +
-                      4 * (size_t)NC * R * (groups + 1);
+  // With a fused RMSNorm the products area doubles as the row scratch.
+  const size_t prod = std::max(4 * (size_t)NC * R * (groups + 1), nx ? 4 * (size_t)cols : 0);
+  const size_t smem = (size_t)((cols + 15) & ~15) + 4 * (size_t)((2 * groups + 3) & ~3) + prod;
   static size_t configured = 0;
   if (smem > configured) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_m1<GS, R, IPT>),
@@ -695,7 +725,7 @@ void launch_m1_t(float *out, const float *add, const uint8_t *nib, const uint8_t
     configured = smem;
   }
   hipLaunchKernelGGL((k_w4a8_m1<GS, R, IPT>), dim3((rows + R - 1) / R), dim3(kThreads), smem, s,
-                     out, add, nib, params, q_split, scales, sums, rows, cols, groups);
+                     out, add, nib, params, q_split, scales, sums, rows, cols, groups, nx, nw, eps);
 }
 
 // Rows per block: the largest power of two whose R*G items fit IPT per
@@ -730,11 +760,11 @@ bool launch_m1(float *out, const float *add, const uint8_t *nib, const uint8_t *
 // Activation staging of the whole K fits comfortably in LDS.
 constexpr size_t kWholeStageBytes = 24 * 1024;
 
-template <int GS, int MT>
+template <int GS, int MT, int R = 16>
 void launch_small_mt(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                      const float *scales, const float *sums, int rows, int cols, int m, int groups,
                      hipStream_t s) {
-  constexpr int R = 16, PD = 4;
+  constexpr int PD = 4;
   const size_t whole = (size_t)std::min(m, MT) * groups * (GS + 8 + 8);
   if (whole <= kWholeStageBytes)
     launch_small_t<GS, MT, R, PD, true>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
@@ -1183,6 +1213,23 @@ void launch_quantize(const float *x, int m, int k, int gs, int8_t *q_nat, int8_t
                      (k % 8 == 0) ? q_split : nullptr, scales, sums);
 }
 
+bool w4a8_norm1_path(int rows, int cols, int gs) {
+  return gs == 32 && rows > 0 && cols % 32 == 0 && cols / 32 <= 128 && cols >= 256;
+}
+
+bool launch_w4a8_norm1(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const float *x,
+                       const float *norm_w, float eps, int rows, int cols, int gs, hipStream_t s) {
+  if (!w4a8_norm1_path(rows, cols, gs)) return false;
+  const int groups = cols / 32;
+  // Same tiles as the unfused one-token dispatch in launch_w4a8.
+  if (rows >= 16384)
+    launch_small_t<32, 1, 16, 4, true>(out, add, nib, params, nullptr, nullptr, nullptr, rows, cols, 1, groups, s,
+                                       x, norm_w, eps);
+  else
+    launch_m1_t<32, 8>(out, add, nib, params, nullptr, nullptr, nullptr, rows, cols, groups, s, x, norm_w, eps);
+  return true;
+}
+
 bool w4a8_fast_path(int cols, int gs) {
   return (gs == 32 || gs == 64 || gs == 128) && cols % gs == 0;
 }
@@ -1193,6 +1240,23 @@ void launch_w4a8(float *out, const float *add, const uint8_t *nib, const uint8_t
                  const _Float16 *qa) {
   const int groups = (cols + gs - 1) / gs;
   if (launch_w4a8_mfma(out, add, nib, params, qa, scales, sums, rows, cols, m, gs, s)) return;
+  // Decode (one token) at group 32, measured on the 7B shapes (4096..32000
+  // rows, K 4096 / 14336): 16-row tiles for many rows, 8-row tiles for long
+  // rows, 8-row whole-K blocks otherwise.
+  if (gs == 32 && m == 1 && w4a8_fast_path(cols, gs)) {
+    if (rows >= 16384) {
+      launch_small_mt<32, 1, 16>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+      return;
+    }
+    if (cols >= 8192) {
+      launch_small_mt<32, 1, 8>(out, add, nib, params, q_split, scales, sums, rows, cols, m, groups, s);
+      return;
+    }
+    if (8 * groups <= m1_items_per_thread(32) * kThreads) {
+      launch_m1_t<32, 8>(out, add, nib, params, q_split, scales, sums, rows, cols, groups, s);
+      return;
+    }
+  }
   // The whole-K kernel wins where few, long rows leave the streaming kernel
   // with too few blocks (measured on 1024..32000 x 2048..14336, g32).
   if (w4a8_fast_path(cols, gs) && m == 1 && cols >= 4096 && rows <= cols) {

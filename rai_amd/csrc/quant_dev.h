@@ -1,0 +1,204 @@
+// Device helpers shared by the fused quantization kernels (fused.hip) and
+// the GEMV kernels that quantize their own input (kernels.hip): per-group
+// int8 quantization in the reference's order and the block-wide RMSNorm that
+// feeds it.  Same bit-exact contract as the kernels: f32 operations in rai's
+// AVX2 order (rai-infer/src/layers.rs, gemm.rs).
+#ifndef RAI_QUANT_DEV_H
+#define RAI_QUANT_DEV_H
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace rai {
+
+// Column c of a block-split row: 8-column block b holds its even columns at
+// 8b+0..3 and its odd columns at 8b+4..7 (the q_split layout).
+__device__ __forceinline__ int split_col(int c) {
+  const int j = c & 7;
+  return (c & ~7) + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
+}
+
+// Quantize one group held by 8 consecutive lanes (lane j owns the columns
+// 8c + j, c = 0..NB-1, of the group) exactly as quantize_input_split_avx2
+// and compute_input_sums do (gemm.rs:182-212, 280-374):
+//   sum   = ((a0+a4)+(a1+a5))+((a2+a6)+(a3+a7)), a_j = sequential sum of the
+//           lane's values in column order;
+//   scale = absmax/127 (1 when absmax <= 1e-10); q = clamp(rne(v/scale)).
+// qs_grp / qn_grp point at the group's first byte in the block-split and
+// natural layouts (qn_grp may be null; either may be in LDS).
+// All 64 lanes of the wave must call this together.
+// Lanes with ok == false take part in the shuffles and store nothing.
+template <int NB>
+__device__ __forceinline__ void quantize_group8_to(const float (&v)[NB], int j, bool ok, int8_t *qs_grp,
+                                                   int8_t *qn_grp, float *scale_out, float *sum_out) {
+  float a = 0.0f, amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+    a = a + v[c];
+    amax = fmaxf(amax, fabsf(v[c]));
+  }
+  // hsum8 in the reference's order via 8-lane shuffles.
+  const float a4 = __shfl(a, (j + 4) & 7, 8);
+  const float b = a + a4;  // lanes 0..3: a_j + a_{j+4}
+  const float b1 = __shfl(b, (j + 1) & 7, 8);
+  const float c = b + b1;  // lane 0: b0+b1, lane 2: b2+b3
+  const float c2 = __shfl(c, (j + 2) & 7, 8);
+  const float total = c + c2;  // lane 0
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+  const float scale = amax > 1e-10f ? amax / 127.0f : 1.0f;
+  const float inv = 1.0f / scale;
+  if (!ok) return;
+#pragma unroll
+  for (int c8 = 0; c8 < NB; ++c8) {
+    float r = rintf(v[c8] * inv);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    const int8_t q = (int8_t)(int)r;
+    const int col = 8 * c8 + j;
+    qs_grp[split_col(col)] = q;
+    if (qn_grp) qn_grp[col] = q;
+  }
+  if (j == 0) {
+    *scale_out = scale;
+    *sum_out = total;
+  }
+}
+
+// inv = 1 / sqrt(sum(x^2) / n + eps) of rms_norm_avx2 (layers.rs:325-376)
+// for the row staged in LDS at xs (visible to the whole 256-thread block),
+// returned to every thread.  n % 8 == 0.  The sum of squares runs as the
+// reference's 16 FMA chains (lane c: j = c & 7 over the elements
+// 16i + (c < 8 ? 0 : 8) + j, the trailing 8-block into chains 0..7), then
+// lane-wise sq0 + sq1 and hsum8 (no scalar tail when n % 8 == 0).
+__device__ __forceinline__ float rmsnorm_inv_block(const float *xs, int n, float eps) {
+  __shared__ float chains[16];
+  __shared__ float inv_sh;
+  const int tid = threadIdx.x;
+  const int c16 = (n / 8) / 2;
+  const bool extra8 = 16 * c16 + 8 <= n;
+  if (tid < 16) {
+    const int j = tid & 7, off = tid < 8 ? 0 : 8;
+    float a = 0.0f;
+    int i = 0;
+    for (; i + 32 <= c16; i += 32) {
+      float v[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) v[u] = xs[16 * (i + u) + off + j];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) a = __fmaf_rn(v[u], v[u], a);
+    }
+    for (; i < c16; ++i) {
+      const float v = xs[16 * i + off + j];
+      a = __fmaf_rn(v, v, a);
+    }
+    if (tid < 8 && extra8) {
+      const float v = xs[16 * c16 + j];
+      a = __fmaf_rn(v, v, a);
+    }
+    chains[tid] = a;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = chains[j] + chains[8 + j];
+    const float sum = ((s[0] + s[4]) + (s[1] + s[5])) + ((s[2] + s[6]) + (s[3] + s[7]));
+    // Correctly rounded sqrt and divide (the reference's sqrtss / divss).
+    inv_sh = 1.0f / __builtin_sqrtf(sum / (float)n + eps);
+  }
+  __syncthreads();
+  return inv_sh;
+}
+
+// rms_norm_avx2 of one row followed by the per-group quantization of the
+// normalised row (gemm.rs:147-374), by a 256-thread block; out =
+// (x * inv) * w.  xs: LDS scratch of n floats; n % 8 == 0, GS | n.
+// Group g goes to qs + g * qstr (block-split order), qn + g * GS (natural,
+// may be null), scale_out[g], sum_out[g]; nrow (may be null) receives the
+// normalised row.  Ends without a barrier: the caller synchronises before
+// reading the outputs.
+template <int GS>
+__device__ __forceinline__ void rmsnorm_quant_block(const float *__restrict__ row, const float *__restrict__ w,
+                                                    int n, float eps, float *xs, int8_t *qs, int qstr,
+                                                    int8_t *qn, float *scale_out, float *sum_out,
+                                                    float *__restrict__ nrow) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < n / 4; i += 256)
+    reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(row)[i];
+  __syncthreads();
+  const float inv = rmsnorm_inv_block(xs, n, eps);
+  const int groups = n / GS;
+  constexpr int NB = GS / 8;
+  // 8 lanes per group; every lane of a wave iterates the same number of
+  // times so the group shuffles always see all 64 lanes.
+  const int passes = (groups + 31) / 32;
+  for (int p = 0; p < passes; ++p) {
+    const int g = p * 32 + tid / 8;
+    const int j = tid & 7;
+    const bool ok = g < groups;
+    const int col0 = (ok ? g : 0) * GS;
+    float v[NB];
+#pragma unroll
+    for (int c = 0; c < NB; ++c) {
+      const int col = col0 + 8 * c + j;
+      v[c] = ok ? (xs[col] * inv) * w[col] : 0.0f;
+      if (ok && nrow) nrow[col] = v[c];
+    }
+    quantize_group8_to<NB>(v, j, ok, qs + (size_t)(ok ? g : 0) * qstr, qn ? qn + col0 : nullptr,
+                           scale_out + (ok ? g : 0), sum_out + (ok ? g : 0));
+  }
+}
+
+// The same for a row of at most 32 * P groups whose values a kernel loads
+// into registers before anything else (rmsnorm_regs_load), so that waiting
+// for them never waits for the loads issued after them: slot (p, c) of the
+// thread is column 8c + (tid & 7) of group 32p + tid / 8 (clamped to the
+// last group past the row).
+template <int GS, int P>
+__device__ __forceinline__ void rmsnorm_regs_load(const float *__restrict__ row, const float *__restrict__ w,
+                                                  int n, float (&xr)[P][GS / 8], float (&wr)[P][GS / 8]) {
+  const int tid = threadIdx.x, groups = n / GS;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int g = min(p * 32 + tid / 8, groups - 1);
+#pragma unroll
+    for (int c = 0; c < GS / 8; ++c) {
+      const int col = g * GS + 8 * c + (tid & 7);
+      xr[p][c] = row[col];
+      wr[p][c] = w[col];
+    }
+  }
+}
+
+template <int GS, int P>
+__device__ __forceinline__ void rmsnorm_quant_regs(const float (&xr)[P][GS / 8], const float (&wr)[P][GS / 8],
+                                                   int n, float eps, float *xs, int8_t *qs, int qstr,
+                                                   float *scale_out, float *sum_out) {
+  const int tid = threadIdx.x, groups = n / GS, j = tid & 7;
+  constexpr int NB = GS / 8;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int g = p * 32 + tid / 8;
+    if (g < groups) {
+#pragma unroll
+      for (int c = 0; c < NB; ++c) xs[g * GS + 8 * c + j] = xr[p][c];
+    }
+  }
+  __syncthreads();
+  const float inv = rmsnorm_inv_block(xs, n, eps);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int g = p * 32 + tid / 8;
+    const bool ok = g < groups;
+    float v[NB];
+#pragma unroll
+    for (int c = 0; c < NB; ++c) v[c] = ok ? (xr[p][c] * inv) * wr[p][c] : 0.0f;
+    quantize_group8_to<NB>(v, j, ok, qs + (size_t)(ok ? g : 0) * qstr, nullptr, scale_out + (ok ? g : 0),
+                           sum_out + (ok ? g : 0));
+  }
+}
+
+}  // namespace rai
+
+#endif

@@ -480,12 +480,23 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
       quantize(md, normed, m, H, w, s);
     }
   };
+  // One token: the projections behind a norm normalise and quantize the
+  // row inside the GEMV launch.
+  const bool norm1 = m == 1 && c.num_experts == 0;
   for (int li = 0; li < (int)c.num_layers; ++li) {
     const DLayer &L = md.layers[li];
-    norm_then_quant(L.in_norm);
+    const bool qkv1 = norm1 && L.qkv.rows && w4a8_norm1_path(L.qkv.rows, L.qkv.cols, L.qkv.gs);
+    if (!qkv1) norm_then_quant(L.in_norm);
     float *qp, *kp, *vp;
     int q_ld, kv_ld;
-    if (L.qkv.rows) {
+    if (qkv1) {
+      launch_w4a8_norm1(w.qkvb.as<float>(), nullptr, L.qkv.nib, L.qkv.params, hid, L.in_norm, c.norm_eps,
+                        L.qkv.rows, L.qkv.cols, L.qkv.gs, s);
+      qp = w.qkvb.as<float>();
+      kp = qp + qd;
+      vp = kp + nkv * hd;
+      q_ld = kv_ld = L.qkv.rows;
+    } else if (L.qkv.rows) {
       linear(L.qkv, normed, w, w.qkvb.as<float>(), m, s);
       qp = w.qkvb.as<float>();
       kp = qp + qd;
@@ -508,14 +519,22 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
     quantize(md, w.att.as<float>(), m, qd, w, s);
     // o_proj with the first residual add (model.rs:858-863) in its epilogue.
     linear(L.lin[3], w.att.as<float>(), w, hid, m, s, hid);
-    norm_then_quant(L.post_norm);
+    const bool gu1 = norm1 && L.gate_up.rows && fused_quant_ok(F, gs) &&
+                     w4a8_norm1_path(L.gate_up.rows, L.gate_up.cols, L.gate_up.gs);
+    if (!gu1) norm_then_quant(L.post_norm);
     if (c.num_experts > 0) {
       moe_block(md, L, w, m, s);
       launch_vec_add(hid, hid, w.mo.as<float>(), (size_t)m * H, s);
     } else {
       float *gp, *up;
       int gu_ld;
-      if (L.gate_up.rows && fused_quant_ok(F, gs)) {
+      if (gu1) {
+        launch_w4a8_norm1(w.gub.as<float>(), nullptr, L.gate_up.nib, L.gate_up.params, hid, L.post_norm,
+                          c.norm_eps, L.gate_up.rows, L.gate_up.cols, L.gate_up.gs, s);
+        gp = w.gub.as<float>();
+        up = gp + F;
+        gu_ld = 2 * F;
+      } else if (L.gate_up.rows && fused_quant_ok(F, gs)) {
         linear(L.gate_up, normed, w, w.gub.as<float>(), m, s);
         gp = w.gub.as<float>();
         up = gp + F;
@@ -553,7 +572,11 @@ static void logits(rai_model &md, Workspace &w, int m, hipStream_t s) {
   const rai_model_config &c = md.cfg;
   const int H = c.hidden_size, V = c.vocab_size;
   if (m > w.logit_rows) fail(RAI_E_SHAPE, "logit rows exceed the workspace");
-  if (!md.tied) {
+  if (!md.tied && m == 1 &&
+      w4a8_norm1_path(md.lm_head.rows, md.lm_head.cols, md.lm_head.gs)) {
+    launch_w4a8_norm1(w.logits.as<float>(), nullptr, md.lm_head.nib, md.lm_head.params, w.hid.as<float>(),
+                      md.final_norm, c.norm_eps, md.lm_head.rows, md.lm_head.cols, md.lm_head.gs, s);
+  } else if (!md.tied) {
     if (fused_quant_ok(H, c.group_size)) {
       launch_norm_quant(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), m, H, c.norm_eps, c.group_size,
                         w.q_split.as<int8_t>(), nullptr, w.qscale.as<float>(), w.qsum.as<float>(), s);
@@ -989,10 +1012,10 @@ int rai_w4a8_matmul_dev(float *out, const uint8_t *nib, const uint8_t *params, c
 }
 
 int rai_w4a8_time_dev(float *out, const uint8_t *nib, const uint8_t *params, const float *x, size_t rows,
-                      size_t cols, size_t m, size_t gs, int iters, float *avg_ms) {
+                      size_t cols, size_t m, size_t gs, size_t copies, int iters, float *avg_ms) {
   RAI_API_BODY({
     if (!out || !nib || !params || !x || !avg_ms) rai::fail(RAI_E_ARG, "null argument");
-    if (rows == 0 || cols == 0 || cols % 2 || gs == 0 || gs % 2 || m == 0 || iters <= 0)
+    if (rows == 0 || cols == 0 || cols % 2 || gs == 0 || gs % 2 || m == 0 || iters <= 0 || copies == 0)
       rai::fail(RAI_E_SHAPE, "invalid shape");
     const size_t groups = rai::ceil_div(cols, gs);
     rai::DevBuf qn, qs, sc, su;
@@ -1013,13 +1036,15 @@ int rai_w4a8_time_dev(float *out, const uint8_t *nib, const uint8_t *params, con
       qa.alloc(sizeof(_Float16) * rai::qa_pack_halves((int)m, (int)cols));
       rai::launch_qa_pack(qs.as<int8_t>(), (int)m, (int)cols, qa.as<_Float16>(), s);
     }
-    auto run = [&] {
-      rai::launch_w4a8(out, nullptr, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
-                       su.as<float>(), (int)rows, (int)cols, (int)m, (int)gs, s, mfma ? qa.as<_Float16>() : nullptr);
+    const size_t nib_bytes = rows * cols / 2, par_bytes = rows * groups * 4;
+    auto run = [&](size_t c) {
+      rai::launch_w4a8(out, nullptr, nib + c * nib_bytes, params + c * par_bytes, x, qn.as<int8_t>(),
+                       qs.as<int8_t>(), sc.as<float>(), su.as<float>(), (int)rows, (int)cols, (int)m, (int)gs, s,
+                       mfma ? qa.as<_Float16>() : nullptr);
     };
-    run();  // warm-up
+    run(0);  // warm-up
     HIP_CHECK(hipEventRecord(e0, s));
-    for (int i = 0; i < iters; ++i) run();
+    for (int i = 0; i < iters; ++i) run((size_t)(i + 1) % copies);
     HIP_CHECK(hipEventRecord(e1, s));
     HIP_CHECK(hipEventSynchronize(e1));
     float ms = 0.0f;

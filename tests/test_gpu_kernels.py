@@ -69,6 +69,34 @@ def test_w4a8_matrix_core_path_bit_exact(rai, ora, rows, cols, m):
     assert np.array_equal(_bits(got), _bits(want)), (rows, cols, m)
 
 
+@pytest.mark.parametrize("rows,cols", [(8209, 2304), (16389, 4096)])
+@pytest.mark.parametrize("m", [2, 5, 9, 13, 16])
+def test_w4a8_register_streamed_path_bit_exact(rai, ora, rows, cols, m):
+    """Row counts that select the register-streamed matrix-core kernel (two
+    ring depths), a partial last 64-row block, a K whose 18 four-group steps
+    leave a partial staging chunk, and every token-group width."""
+    nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + cols + 5 * m)
+    want = ora.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    got = rai.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    assert np.array_equal(_bits(got), _bits(want)), (rows, cols, m)
+
+
+@pytest.mark.parametrize("rows", [1000, 8209, 16389])
+def test_w4a8_matrix_core_huge_activation_scales(rai, ora, rows):
+    """Activation groups scaled past 2^88 (absmax ~1e29..1e30): the chunks
+    holding them switch to the 1024 + n code form, which stays exact, and the
+    other chunks keep the subnormal form."""
+    cols, m = 2304, 9
+    nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows)
+    x = x.copy()
+    x[3, 64:96] *= np.float32(1e30)
+    x[8, 2016:2048] *= np.float32(3e29)
+    want = ora.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    got = rai.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    assert np.isfinite(want).all()
+    assert np.array_equal(_bits(got), _bits(want)), rows
+
+
 @pytest.mark.parametrize("rows,cols,gs", SHAPES[:6])
 def test_lane_sums_bit_exact(rai, ora, rows, cols, gs):
     nib, _, x = gemv_operands(rows, cols, 3, gs, seed=cols)

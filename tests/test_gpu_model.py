@@ -77,6 +77,33 @@ def test_embed_forward_logits_bit_exact(rai, ora, name):
     assert gkv.filled(0) == 19
 
 
+@pytest.mark.parametrize("kw", [
+    {},
+    # 128 groups per row (the widest fused row), a 16384+-row lm_head (the
+    # tiled kernel) and m1-kernel projections.
+    dict(hidden_size=4096, num_layers=1, num_heads=32, num_kv_heads=8, head_dim=128,
+         intermediate_size=1024, vocab_size=17000, max_context=64, seed=11),
+])
+def test_single_token_fused_norm_bit_exact(rai, ora, kw):
+    """One-token forward and logits, where each projection behind a norm
+    normalises and quantizes its input inside the GEMV launch, equal the
+    oracle bit for bit after a few positions of context."""
+    img = _small_synth(rai, **kw)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    toks = _token_sequence(om.cfg.vocab_size, 6)
+    hs = np.stack([om.embed_token(t) for t in toks])
+    okv, gkv = om.create_kv(64), gm.create_kv_cache(64)
+    om.forward_batch(hs[:4], np.arange(4), okv)
+    gm.forward_batch(hs[:4], np.arange(4), gkv)
+    for p in (4, 5):
+        oh = om.forward_batch(hs[p:p + 1], np.arange(p, p + 1), okv)
+        gh = gm.forward_batch(hs[p:p + 1], np.arange(p, p + 1), gkv)
+        assert np.array_equal(_bits(gh), _bits(oh)), p
+        assert np.array_equal(_bits(gm.hidden_to_logits_batch(gh, 1)),
+                              _bits(om.hidden_to_logits_batch(oh, 1))), p
+
+
 @pytest.mark.parametrize("name", FIXTURES)
 def test_batched_equals_sequential_on_gpu(rai, name):
     """model_invariants.rs:92-134 on the GPU path: batched and sequential
