@@ -35,8 +35,8 @@ template <int NB>
 __device__ __forceinline__ void quantize_group8(const float (&v)[NB], int j, int col0, bool ok,
                                                 int8_t *__restrict__ qs, int8_t *__restrict__ qn,
                                                 float *__restrict__ scale_out,
-                                                float *__restrict__ sum_out) {
-  quantize_group8_to<NB>(v, j, ok, qs + col0, qn ? qn + col0 : nullptr, scale_out, sum_out);
+                                                float *__restrict__ sum_out, _Float16 *qa_slot = nullptr) {
+  quantize_group8_to<NB>(v, j, ok, qs + col0, qn ? qn + col0 : nullptr, scale_out, sum_out, qa_slot);
 }
 
 // ------------------------------------------------------ RMSNorm + quant --
@@ -54,7 +54,8 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
                                                     int8_t *__restrict__ q_split,
                                                     int8_t *__restrict__ q_nat,
                                                     float *__restrict__ scales,
-                                                    float *__restrict__ sums, int n, float eps) {
+                                                    float *__restrict__ sums, int n, float eps,
+                                                    _Float16 *qa) {
   extern __shared__ float xs[];
   const int t = blockIdx.x, tid = threadIdx.x;
   const float *row = x + (size_t)t * n;
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
     const int groups = n / GS;
     rmsnorm_quant_block<GS>(row, w, n, eps, xs, q_split + (size_t)t * n, GS,
                             q_nat ? q_nat + (size_t)t * n : nullptr, scales + (size_t)t * groups,
-                            sums + (size_t)t * groups, normed ? normed + (size_t)t * n : nullptr);
+                            sums + (size_t)t * groups, normed ? normed + (size_t)t * n : nullptr, qa, t);
   } else {
     // RMSNorm only (rms_norm / rms_norm_with_residual): out = (x*inv)*w.
     float *ws = xs + n;  // [n] row, then [n] weights
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(256) void k_silu_quant(float *__restrict__ gate,
                                                     int8_t *__restrict__ q_split,
                                                     int8_t *__restrict__ q_nat,
                                                     float *__restrict__ scales,
-                                                    float *__restrict__ sums) {
+                                                    float *__restrict__ sums, _Float16 *qa) {
   constexpr int NB = GS / 8;
   const int t = blockIdx.y;
   const int groups = n / GS;
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(256) void k_silu_quant(float *__restrict__ gate,
   int8_t *qs = q_split + (size_t)t * n;
   int8_t *qn = q_nat ? q_nat + (size_t)t * n : nullptr;
   quantize_group8<NB>(v, j, col0, ok, qs, qn, scales + (size_t)t * groups + g,
-                      sums + (size_t)t * groups + g);
+                      sums + (size_t)t * groups + g, qa ? qa4_slot(qa, t, ok ? g : 0, groups) : nullptr);
 }
 
 // Per-group quantization of m rows of n (quantize_input_split +
@@ -165,7 +166,7 @@ __global__ __launch_bounds__(256) void k_quant(const float *__restrict__ x, int 
                                                int8_t *__restrict__ q_split,
                                                int8_t *__restrict__ q_nat,
                                                float *__restrict__ scales,
-                                               float *__restrict__ sums) {
+                                               float *__restrict__ sums, _Float16 *qa) {
   constexpr int NB = GS / 8;
   const int t = blockIdx.y;
   const int groups = n / GS;
@@ -180,7 +181,7 @@ __global__ __launch_bounds__(256) void k_quant(const float *__restrict__ x, int 
   int8_t *qs = q_split + (size_t)t * n;
   int8_t *qn = q_nat ? q_nat + (size_t)t * n : nullptr;
   quantize_group8<NB>(v, j, col0, ok, qs, qn, scales + (size_t)t * groups + g,
-                      sums + (size_t)t * groups + g);
+                      sums + (size_t)t * groups + g, qa ? qa4_slot(qa, t, ok ? g : 0, groups) : nullptr);
 }
 
 // -------------------------------------------------------------- attention --
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(64) void k_pv_any(const float *__restrict__ P,
 template <int GS>
 void launch_norm_quant_t(const float *x, const float *w, float *normed, int m, int n, float eps,
                          int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
-                         hipStream_t s) {
+                         hipStream_t s, _Float16 *qa = nullptr) {
   const size_t smem = (GS > 0 ? 1 : 2) * sizeof(float) * (size_t)n;
   static size_t configured = 0;
   if (smem > 48 * 1024 && smem > configured) {
@@ -534,15 +535,15 @@ void launch_norm_quant_t(const float *x, const float *w, float *normed, int m, i
     configured = smem;
   }
   hipLaunchKernelGGL(k_norm_quant<GS>, dim3(m), dim3(256), smem, s, x, w, normed, q_split, q_nat,
-                     scales, sums, n, eps);
+                     scales, sums, n, eps, qa);
 }
 
 template <int GS>
 void launch_silu_quant_t(float *gate, const float *up, int m, int n, int ld, int8_t *q_split,
-                         int8_t *q_nat, float *scales, float *sums, hipStream_t s) {
+                         int8_t *q_nat, float *scales, float *sums, hipStream_t s, _Float16 *qa) {
   const int groups = n / GS;
   hipLaunchKernelGGL(k_silu_quant<GS>, dim3((groups + 31) / 32, m), dim3(256), 0, s, gate, up, n,
-                     ld, q_split, q_nat, scales, sums);
+                     ld, q_split, q_nat, scales, sums, qa);
 }
 
 }  // namespace
@@ -560,9 +561,9 @@ bool fused_quant_ok(int n, int gs) {
 
 void launch_norm_quant(const float *x, const float *w, float *normed, int m, int n, float eps,
                        int gs, int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
-                       hipStream_t s) {
+                       hipStream_t s, _Float16 *qa) {
   if (gs == 32)
-    launch_norm_quant_t<32>(x, w, normed, m, n, eps, q_split, q_nat, scales, sums, s);
+    launch_norm_quant_t<32>(x, w, normed, m, n, eps, q_split, q_nat, scales, sums, s, qa);
   else if (gs == 64)
     launch_norm_quant_t<64>(x, w, normed, m, n, eps, q_split, q_nat, scales, sums, s);
   else
@@ -570,25 +571,25 @@ void launch_norm_quant(const float *x, const float *w, float *normed, int m, int
 }
 
 void launch_quant(const float *x, int m, int n, int gs, int8_t *q_split, int8_t *q_nat,
-                  float *scales, float *sums, hipStream_t s) {
+                  float *scales, float *sums, hipStream_t s, _Float16 *qa) {
   const dim3 grid((n / gs + 31) / 32, m);
   if (gs == 32)
-    hipLaunchKernelGGL(k_quant<32>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums);
+    hipLaunchKernelGGL(k_quant<32>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums, qa);
   else if (gs == 64)
-    hipLaunchKernelGGL(k_quant<64>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums);
+    hipLaunchKernelGGL(k_quant<64>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums, nullptr);
   else
-    hipLaunchKernelGGL(k_quant<128>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums);
+    hipLaunchKernelGGL(k_quant<128>, grid, dim3(256), 0, s, x, n, q_split, q_nat, scales, sums, nullptr);
 }
 
 void launch_silu_quant(float *gate, const float *up, int m, int n, int ld, int gs,
                        int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
-                       hipStream_t s) {
+                       hipStream_t s, _Float16 *qa) {
   if (gs == 32)
-    launch_silu_quant_t<32>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s);
+    launch_silu_quant_t<32>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s, qa);
   else if (gs == 64)
-    launch_silu_quant_t<64>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s);
+    launch_silu_quant_t<64>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s, nullptr);
   else
-    launch_silu_quant_t<128>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s);
+    launch_silu_quant_t<128>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s, nullptr);
 }
 
 size_t attention_scores_floats(int m, int nh, int ctx) {

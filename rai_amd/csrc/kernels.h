@@ -77,17 +77,20 @@ void launch_rmsnorm(const float *x, const float *w, float *out, float *resid, in
 bool fused_quant_ok(int n, int gs);
 // RMSNorm of m rows of n (layers.rs:325-376) + per-group quantization of
 // the result (gemm.rs:147-374); `normed` and `q_nat` may be null.
+// qa (may be null; group 32 only): also write the quantized rows in the
+// matrix-core activation layout (launch_qa_pack's output, padding rows of
+// the last 4-token group left untouched), which saves that pack.
 void launch_norm_quant(const float *x, const float *w, float *normed, int m, int n, float eps,
                        int gs, int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
-                       hipStream_t s);
+                       hipStream_t s, _Float16 *qa = nullptr);
 // Per-group quantization of m rows of n into q_split (q_nat may be null).
 void launch_quant(const float *x, int m, int n, int gs, int8_t *q_split, int8_t *q_nat,
-                  float *scales, float *sums, hipStream_t s);
+                  float *scales, float *sums, hipStream_t s, _Float16 *qa = nullptr);
 // silu_mul (layers.rs:850-883) in place on gate rows of n (row stride ld,
 // up rows likewise) + quantization of the product; requires n % 8 == 0.
 void launch_silu_quant(float *gate, const float *up, int m, int n, int ld, int gs,
                        int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
-                       hipStream_t s);
+                       hipStream_t s, _Float16 *qa = nullptr);
 void launch_vec_add(float *h, const float *r, const float *a, size_t n, hipStream_t s);
 void launch_silu_mul(float *gate, const float *up, int m, int n, hipStream_t s);
 // RoPE on q [m][nh*hd] and k [m][nkv*hd] at positions pos0.., then the

@@ -29,9 +29,17 @@ __device__ __forceinline__ int split_col(int c) {
 // natural layouts (qn_grp may be null; either may be in LDS).
 // All 64 lanes of the wave must call this together.
 // Lanes with ok == false take part in the shuffles and store nothing.
+// Matrix-core activation slot of (token t, group g) for group 32 (see
+// k_qa_pack4 in gemv.hip): qa4[t/4][g/4][b][4(t%4) + g%4][8] f16; block b of
+// the slot is 128 halves further.
+__device__ __forceinline__ _Float16 *qa4_slot(_Float16 *qa, int t, int g, int groups) {
+  return qa + ((((size_t)(t >> 2) * (groups >> 2) + (g >> 2)) * 64) + 4 * (t & 3) + (g & 3)) * 8;
+}
+
 template <int NB>
 __device__ __forceinline__ void quantize_group8_to(const float (&v)[NB], int j, bool ok, int8_t *qs_grp,
-                                                   int8_t *qn_grp, float *scale_out, float *sum_out) {
+                                                   int8_t *qn_grp, float *scale_out, float *sum_out,
+                                                   _Float16 *qa_slot = nullptr) {
   float a = 0.0f, amax = 0.0f;
 #pragma unroll
   for (int c = 0; c < NB; ++c) {
@@ -58,6 +66,8 @@ __device__ __forceinline__ void quantize_group8_to(const float (&v)[NB], int j, 
     const int col = 8 * c8 + j;
     qs_grp[split_col(col)] = q;
     if (qn_grp) qn_grp[col] = q;
+    // f16 element e of a block is its column (0, 4, 1, 5, 2, 6, 3, 7)[e].
+    if (qa_slot) qa_slot[c8 * 128 + 2 * (j & 3) + (j >> 2)] = (_Float16)r;
   }
   if (j == 0) {
     *scale_out = scale;
@@ -122,7 +132,8 @@ template <int GS>
 __device__ __forceinline__ void rmsnorm_quant_block(const float *__restrict__ row, const float *__restrict__ w,
                                                     int n, float eps, float *xs, int8_t *qs, int qstr,
                                                     int8_t *qn, float *scale_out, float *sum_out,
-                                                    float *__restrict__ nrow) {
+                                                    float *__restrict__ nrow, _Float16 *qa = nullptr,
+                                                    int token = 0) {
   const int tid = threadIdx.x;
   for (int i = tid; i < n / 4; i += 256)
     reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(row)[i];
@@ -146,7 +157,8 @@ __device__ __forceinline__ void rmsnorm_quant_block(const float *__restrict__ ro
       if (ok && nrow) nrow[col] = v[c];
     }
     quantize_group8_to<NB>(v, j, ok, qs + (size_t)(ok ? g : 0) * qstr, qn ? qn + col0 : nullptr,
-                           scale_out + (ok ? g : 0), sum_out + (ok ? g : 0));
+                           scale_out + (ok ? g : 0), sum_out + (ok ? g : 0),
+                           qa ? qa4_slot(qa, token, ok ? g : 0, groups) : nullptr);
   }
 }
 

@@ -373,15 +373,22 @@ static void pack_for_mfma(const rai_model &md, int m, int k, const Workspace &w,
     launch_qa_pack(w.q_split.as<int8_t>(), m, k, w.qa.as<_Float16>(), s);
 }
 
+// The matrix-core activation buffer for a fused quantizer to fill directly
+// (null when the matrix-core GEMV does not apply).
+static _Float16 *mfma_acts(const rai_model &md, int m, int k, const Workspace &w) {
+  return w4a8_mfma_path(1, k, m, md.cfg.group_size) ? w.qa.as<_Float16>() : nullptr;
+}
+
 static void quantize(const rai_model &md, const float *x, int m, int k, const Workspace &w,
                      hipStream_t s) {
-  if (fused_quant_ok(k, md.cfg.group_size))
+  if (fused_quant_ok(k, md.cfg.group_size)) {
     launch_quant(x, m, k, md.cfg.group_size, w.q_split.as<int8_t>(), nullptr, w.qscale.as<float>(),
-                 w.qsum.as<float>(), s);
-  else
+                 w.qsum.as<float>(), s, mfma_acts(md, m, k, w));
+  } else {
     launch_quantize(x, m, k, md.cfg.group_size, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
                     w.qscale.as<float>(), w.qsum.as<float>(), s);
-  pack_for_mfma(md, m, k, w, s);
+    pack_for_mfma(md, m, k, w, s);
+  }
 }
 
 // The MLP of a sparse layer: mlp_block's MoE arm (model.rs:208-261) for
@@ -473,8 +480,7 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
   auto norm_then_quant = [&](const float *wn) {
     if (fused_quant_ok(H, gs)) {
       launch_norm_quant(hid, wn, normed, m, H, c.norm_eps, gs, w.q_split.as<int8_t>(), nullptr,
-                        w.qscale.as<float>(), w.qsum.as<float>(), s);
-      pack_for_mfma(md, m, H, w, s);
+                        w.qscale.as<float>(), w.qsum.as<float>(), s, mfma_acts(md, m, H, w));
     } else {
       launch_rmsnorm(hid, wn, normed, nullptr, m, H, c.norm_eps, s);
       quantize(md, normed, m, H, w, s);
@@ -548,8 +554,7 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
       }
       if (fused_quant_ok(F, gs)) {
         launch_silu_quant(gp, up, m, F, gu_ld, gs, w.q_split.as<int8_t>(), nullptr, w.qscale.as<float>(),
-                          w.qsum.as<float>(), s);
-        pack_for_mfma(md, m, F, w, s);
+                          w.qsum.as<float>(), s, mfma_acts(md, m, F, w));
       } else {
         launch_silu_mul(gp, up, m, F, s);
         quantize(md, gp, m, F, w, s);
@@ -579,8 +584,8 @@ static void logits(rai_model &md, Workspace &w, int m, hipStream_t s) {
   } else if (!md.tied) {
     if (fused_quant_ok(H, c.group_size)) {
       launch_norm_quant(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), m, H, c.norm_eps, c.group_size,
-                        w.q_split.as<int8_t>(), nullptr, w.qscale.as<float>(), w.qsum.as<float>(), s);
-      pack_for_mfma(md, m, H, w, s);
+                        w.q_split.as<int8_t>(), nullptr, w.qscale.as<float>(), w.qsum.as<float>(), s,
+                        mfma_acts(md, m, H, w));
     } else {
       launch_rmsnorm(w.hid.as<float>(), md.final_norm, w.normed.as<float>(), nullptr, m, H, c.norm_eps, s);
       quantize(md, w.normed.as<float>(), m, H, w, s);
