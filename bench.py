@@ -60,6 +60,68 @@ def measure_gemv(rai, n, k, m, gs, iters=50):
     return ms, b / (ms * 1e-3) / 1e9, b
 
 
+COPY_BYTES = 256 << 20  # the plain device copy whose counters calibrate the traffic pass
+
+
+def roofline_only(gs: int) -> int:
+    """The roofline GEMV launches (rotating weight copies) and one plain
+    device-to-device copy of COPY_BYTES: the program the counter passes
+    profile."""
+    import rai_amd
+    import torch
+    from rai_amd.workload import MISTRAL_7B
+    n, k = MISTRAL_7B["intermediate_size"], MISTRAL_7B["hidden_size"]
+    measure_gemv(rai_amd, n, k, 9, gs, iters=20)
+    a = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    return 0
+
+
+def _counter_pass(counter: str, gs: int, tmp: str):
+    """Run `bench.py --roofline-only` under one rocprofv3 counter pass; return
+    {kernel name: [per-dispatch values]}."""
+    import csv
+    import subprocess
+    out = os.path.join(tmp, counter)
+    cmd = ["timeout", "-s", "KILL", "150", "rocprofv3", "--pmc", counter, "-f", "csv", "-d", out, "-o", "c",
+           "--", sys.executable, os.path.abspath(__file__), "--roofline-only"]
+    r = subprocess.run(cmd, cwd=tmp, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"rocprofv3 --pmc {counter} exited {r.returncode}: {r.stderr[-400:]}")
+    vals = {}
+    for root, _, files in os.walk(out):
+        for f in files:
+            if f.endswith("counter_collection.csv"):
+                for row in csv.DictReader(open(os.path.join(root, f))):
+                    if row["Counter_Name"] == counter:
+                        vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return vals
+
+
+def measure_traffic(gs: int):
+    """HBM bytes per launch of the roofline GEMV from FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch), each scaled by what the counter reads for the plain
+    copy of COPY_BYTES (read and written once).  None when rocprofv3 is
+    absent."""
+    import shutil
+    import tempfile
+    if not shutil.which("rocprofv3"):
+        return None
+    with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+        res = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            vals = _counter_pass(counter, gs, tmp)
+            gemv = [v for name, vs in vals.items() if "k_gemv" in name for v in vs]
+            copy = [v for name, vs in vals.items() if "copy" in name.lower() or "elementwise" in name for v in vs]
+            if not gemv or not copy:
+                raise RuntimeError(f"{counter}: kernels not found in {list(vals)}")
+            factor = (COPY_BYTES / 1024.0) / max(copy)
+            res[counter] = (float(np.median(gemv)) * 1024.0 * factor, factor)
+    return res
+
+
 def cpu_baseline(img: bytes, cfg: dict, seconds: float, prompt_len: int, threads: int):
     """Oracle (C++ restatement of the reference AVX2 path) on a bounded sample:
     same model, a short copy-heavy prompt, greedy lookup steps for ~`seconds`."""
@@ -112,7 +174,11 @@ def main() -> int:
     ap.add_argument("--prompt", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--roofline-only", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.roofline_only:
+        return roofline_only(32)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
         return 2
@@ -169,6 +235,18 @@ def main() -> int:
     log(f"verify GEMV {n}x{k} M=9: {vms * 1e3:.1f} us, {vgbs:.0f} GB/s; M=1: {dms * 1e3:.1f} us, "
         f"{dgbs:.0f} GB/s")
 
+    traffic = None
+    if not args.no_traffic:
+        try:
+            t = measure_traffic(gs)
+            if t is not None:
+                traffic = round(t["FETCH_SIZE"][0] + t["WRITE_SIZE"][0])
+                log(f"verify GEMV HBM traffic {traffic / 1e6:.2f} MB/launch (fetch {t['FETCH_SIZE'][0] / 1e6:.2f} "
+                    f"MB x{t['FETCH_SIZE'][1]:.3f}, write {t['WRITE_SIZE'][0] / 1e6:.2f} MB "
+                    f"x{t['WRITE_SIZE'][1]:.3f}) vs {vbytes / 1e6:.2f} MB algorithmic")
+        except Exception as e:  # the counter passes are a report, not the run
+            log(f"traffic passes failed: {e}")
+
     cpu = None
     if not args.no_cpu:
         threads = os.cpu_count() or 1
@@ -218,7 +296,7 @@ def main() -> int:
             "decode_gemv_gbs": round(dgbs, 1),
         },
         "roofline": {"bound": "hbm", "achieved": round(vgbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(vgbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(vgbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": f"w4a8 GEMV {n}x{k} g{gs} M=9", "bytes_per_launch": vbytes},
         "cpu_baseline": cpu,
     }

@@ -6,7 +6,7 @@
  * the (k+1)-token verify forward pass, greedy acceptance with KV rollback,
  * and the W4A8 GEMV/GEMM beneath them.  Each entry point below names the
  * reference interface it replaces (rai-infer/src/<file>:<line>).  A Rust
- * `extern "C"` crate can bind these symbols one-to-one (see INTEGRATION.md).
+ * `extern "C"` crate can bind these symbols one-to-one.
  *
  * Conventions
  *   - Every function returns an rai_status (0 = RAI_OK).  On failure the
