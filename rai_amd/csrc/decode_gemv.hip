@@ -1,0 +1,358 @@
+// One-token W4A8 GEMV (decode), group 32, wave-streamed.
+//
+// Same arithmetic as the reference's AVX2 kernel for one input row
+// (gemm.rs:458-537, 1774-1919): per (row, group) the four 8-column block
+// sums S_l (exact int32 via v_dot4), cs = fl(ws * as), the lane products
+// fl(float(S_l) * cs) and the zero term fl(wz * xsum); per row four lane
+// chains and one zero chain accumulated in group order, and at the end
+// hsum8(f0..f3, 0, 0, 0, 0) + zc.
+//
+// Work split.  Every wave owns tiles of R rows and walks them chunk by chunk
+// (32 groups = 1024 columns per chunk).  Lane (h = lane / 32, k = lane % 32)
+// holds group k of the chunk for the R/2 rows 2i + h, so one load
+// instruction reads two 512-byte runs of packed codes and two 128-byte runs
+// of group parameters.  Loads stream through a ring of D chunks in
+// registers: every load is issued (past the last chunk it points beyond the
+// buffer, which a raw buffer load answers with zeros without touching
+// memory), so the compiler's wait counts stay exact and D chunks stay in
+// flight across tile boundaries.  The lane products go through a
+// wave-private LDS area and come back transposed: lane c = l * R + r runs
+// chain l of row r over the chunk's 32 products in group order.  No block
+// barrier is taken after the prologue, which stages the activations
+// (int8 codes in the block-split order, scales and sums; ST = 1, 2, 4
+// sixteen-byte loads of codes per thread) once per block - or, with the
+// fused input RMSNorm (ST = 0), normalises and quantizes the hidden row there (rms_norm_avx2 then quantize_input_split, layers.rs:325-376,
+// gemm.rs:147-374).
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "kernels.h"
+#include "quant_dev.h"
+
+namespace rai {
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kDecWaves = 4;       // waves per block
+constexpr int kDecChunk = 32;      // groups per chunk
+constexpr int kDecRowStride = 36;  // floats per (chain, row) run of 32 products, padded
+constexpr int kDecMaxGroups = 448; // K <= 14336 staged in LDS
+
+__device__ __forceinline__ float dec_f16(uint32_t bits) {
+  return __half2float(__ushort_as_half((uint16_t)bits));
+}
+
+// Integer dot of one 8-column block: low nibbles (even columns) against the
+// 4 even activations, high nibbles against the 4 odd ones (the PMADDUBSW
+// pairing of gemm.rs:470-476).
+__device__ __forceinline__ int dec_block_dot(uint32_t codes, uint32_t q_even, uint32_t q_odd) {
+  const uint32_t lo = codes & 0x0F0F0F0Fu;
+  const uint32_t hi = (codes >> 4) & 0x0F0F0F0Fu;
+  return __builtin_amdgcn_sdot4((int)hi, (int)q_odd, __builtin_amdgcn_sdot4((int)lo, (int)q_even, 0, false),
+                                false);
+}
+
+template <int R>
+struct DecCfg {
+  static_assert(R % 2 == 0 && 5 * R <= 64, "one chain per lane");
+  static constexpr int IPL = R / 2;                    // (row, group) items per lane and chunk
+  static constexpr int LSTR = R * kDecRowStride;       // floats per chain
+  static constexpr int WAVE_FLOATS = 5 * LSTR + 64;    // products + final chain values
+};
+
+// LDS bytes of a block: activations (codes, scales, sums) and the waves'
+// product areas; with the fused RMSNorm the product areas double as the
+// row scratch, which needs cols floats.
+__host__ __device__ inline int dec_act_bytes(int cols) { return (cols + 8 * (cols / 32) + 15) & ~15; }
+
+template <int R>
+size_t dec_smem(int cols, bool fused) {
+  const size_t act = dec_act_bytes(cols);
+  const size_t waves = sizeof(float) * (size_t)kDecWaves * DecCfg<R>::WAVE_FLOATS;
+  return act + std::max(waves, fused ? sizeof(float) * (size_t)cols : size_t(0));
+}
+
+template <int R, int D, int ST>
+__global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, const uint8_t *__restrict__ nib,
+                                                  const uint8_t *__restrict__ params,
+                                                  const int8_t *__restrict__ q_split,
+                                                  const float *__restrict__ scales,
+                                                  const float *__restrict__ sums, int rows, int cols,
+                                                  int tiles_per_wave, const float *__restrict__ nx,
+                                                  const float *__restrict__ nw, float eps) {
+  using C = DecCfg<R>;
+  constexpr int IPL = C::IPL, LSTR = C::LSTR;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int groups = cols / 32;
+  const int nchunks = (groups + kDecChunk - 1) / kDecChunk;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, k = lane & 31;
+  // LDS: q [cols] bytes | scales [groups] | sums [groups] | waves' areas.
+  int8_t *qsh = reinterpret_cast<int8_t *>(smem);
+  float *ash = reinterpret_cast<float *>(smem + cols);
+  float *ssh = ash + groups;
+  float *wbase = reinterpret_cast<float *>(smem + dec_act_bytes(cols));
+  float *pw_lds = wbase + wave * C::WAVE_FLOATS;
+  float *fin = pw_lds + 5 * LSTR;
+
+  // Wave w of W walks tiles w, w + W, ...; every wave runs the same number
+  // of tiles, those past the matrix read zeros and store nothing.
+  const int W = gridDim.x * kDecWaves;
+  const int wg = blockIdx.x * kDecWaves + wave;
+  const int it_total = tiles_per_wave * nchunks;
+  const int rowb = cols / 2;
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(nib), 0, rows * rowb, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rp =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(params), 0, rows * groups * 4, 0x00020000);
+
+  // Activations first (the hidden row and the norm weights, or the
+  // quantized row, its scales and sums), then the weight ring: loads
+  // complete in issue order, so staging the activations never waits for
+  // the ring.
+  constexpr bool FUSED = ST == 0;
+  constexpr int NP = FUSED ? 4 : 1;
+  constexpr int QV = FUSED ? 1 : ST;
+  float xr[NP][4], wr[NP][4];
+  uint4 qv[QV];
+  float av[2], sv[2];
+  if constexpr (FUSED) {
+    rmsnorm_regs_load<32, NP>(nx, nw, cols, xr, wr);
+  } else {
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(q_split), 0, cols, 0x00020000);
+#pragma unroll
+    for (int v = 0; v < QV; ++v) {
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rq, 16 * min(tid + v * 256, cols / 16 - 1), 0, 0);
+      qv[v] = make_uint4(w.x, w.y, w.z, w.w);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      av[u] = scales[min(tid + u * 256, groups - 1)];
+      sv[u] = sums[min(tid + u * 256, groups - 1)];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  u32x4 ring_c[D][IPL];
+  uint32_t ring_p[D][IPL];
+  // Issue the loads of iteration it into ring slot j.
+  auto load = [&](int it, u32x4 (&c)[IPL], uint32_t (&p)[IPL]) {
+    const int t = it / nchunks, ch = it - t * nchunks;
+    const int row = (wg + t * W) * R + h;
+    const int g = ch * kDecChunk + k;
+    uint32_t vc = (uint32_t)row * rowb + g * 16;
+    uint32_t vp = ((uint32_t)row * groups + g) * 4;
+    if (it >= it_total) {
+      vc = 0x80000000u;  // past num_records: zeros, no memory access
+      vp = 0x80000000u;
+    }
+    // The item offsets go into the VGPR offset: the range check covers the
+    // VGPR and instruction offsets, not the SGPR one.
+#pragma unroll
+    for (int i = 0; i < IPL; ++i)
+      c[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)(vc + (uint32_t)(i * 2 * rowb)), 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < IPL; ++i)
+      p[i] = __builtin_amdgcn_raw_buffer_load_b32(rp, (int)(vp + (uint32_t)(i * 8 * groups)), 0, 0);
+  };
+  // Same issue order as the loop's refills (slot by slot), which keeps the
+  // compiler's wait counts exact at the loop head.
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    load(j, ring_c[j], ring_p[j]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Stage the activations in LDS while the ring fills.
+  if constexpr (FUSED) {
+    rmsnorm_quant_regs<32, NP>(xr, wr, cols, eps, wbase, qsh, 32, ash, ssh);
+  } else {
+    // Unconditional stores to the clamped slots (threads past the row
+    // rewrite the last slot with the value already there): a conditional
+    // store would let the compiler sink the loads behind the ring.
+#pragma unroll
+    for (int v = 0; v < QV; ++v) reinterpret_cast<uint4 *>(qsh)[min(tid + v * 256, cols / 16 - 1)] = qv[v];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      ash[min(tid + u * 256, groups - 1)] = av[u];
+      ssh[min(tid + u * 256, groups - 1)] = sv[u];
+    }
+  }
+  __syncthreads();
+
+  float acc = 0.0f;
+  const int crow = lane % R, cl = lane / R;  // chain lane: row, chain
+  const bool chain_lane = lane < 5 * R;
+
+  for (int it0 = 0; it0 < it_total; it0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int it = it0 + j;
+      if (it < it_total) {
+        const int t = it / nchunks, ch = it - t * nchunks;
+        const int gc = min(kDecChunk, groups - ch * kDecChunk);
+        if (ch == 0) acc = 0.0f;
+        // Products of this lane's items (group ch*32 + k; lanes past a
+        // partial last chunk compute on whatever they read and are never
+        // chained).
+        const int gq = min(ch * kDecChunk + k, groups - 1);
+        const uint4 q0 = *reinterpret_cast<const uint4 *>(qsh + gq * 32);
+        const uint4 q1 = *reinterpret_cast<const uint4 *>(qsh + gq * 32 + 16);
+        const float as = ash[gq], xsum = ssh[gq];
+#pragma unroll
+        for (int i = 0; i < IPL; ++i) {
+          const u32x4 cw = ring_c[j][i];
+          const uint32_t pw = ring_p[j][i];
+          const float cs = dec_f16(pw & 0xFFFF) * as;
+          const float z = dec_f16(pw >> 16) * xsum;
+          const int s0 = dec_block_dot(cw.x, q0.x, q0.y);
+          const int s1 = dec_block_dot(cw.y, q0.z, q0.w);
+          const int s2 = dec_block_dot(cw.z, q1.x, q1.y);
+          const int s3 = dec_block_dot(cw.w, q1.z, q1.w);
+          float *pt = pw_lds + (2 * i + h) * kDecRowStride + k;
+          pt[0] = (float)s0 * cs;
+          pt[LSTR] = (float)s1 * cs;
+          pt[2 * LSTR] = (float)s2 * cs;
+          pt[3 * LSTR] = (float)s3 * cs;
+          pt[4 * LSTR] = z;
+        }
+        // LDS operations of one wave complete in order; the fences only
+        // keep the compiler from moving the chain reads above the writes.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (chain_lane) {
+          const float *pc = pw_lds + cl * LSTR + crow * kDecRowStride;
+          if (gc == kDecChunk) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = reinterpret_cast<const float4 *>(pc)[u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              acc = acc + v[u].x;
+              acc = acc + v[u].y;
+              acc = acc + v[u].z;
+              acc = acc + v[u].w;
+            }
+          } else {
+            for (int u = 0; u < gc; ++u) acc = acc + pc[u];
+          }
+        }
+        if (ch == nchunks - 1) {
+          if (chain_lane) fin[lane] = acc;
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          const int row = (wg + t * W) * R + lane;
+          if (lane < R && row < rows) {
+            // hsum8 of (f0, f1, f2, f3, 0, 0, 0, 0) in the _mm256 order.
+            const float f0 = fin[lane], f1 = fin[R + lane], f2 = fin[2 * R + lane], f3 = fin[3 * R + lane];
+            const float zero = 0.0f;
+            const float v = ((f0 + zero) + (f1 + zero)) + ((f2 + zero) + (f3 + zero)) + fin[4 * R + lane];
+            out[row] = add ? add[row] + v : v;
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      load(it + D, ring_c[j], ring_p[j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+template <int R, int D, int ST>
+void launch_dec_t(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                  const float *scales, const float *sums, int rows, int cols, const float *nx, const float *nw,
+                  float eps, int blocks, hipStream_t s) {
+  const size_t smem = dec_smem<R>(cols, ST == 0);
+  static size_t configured = 0;
+  if (smem > configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<R, D, ST>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = smem;
+  }
+  const int tiles = (rows + R - 1) / R;
+  if (blocks <= 0) blocks = (tiles + kDecWaves - 1) / kDecWaves;
+  blocks = std::max(1, std::min(blocks, 1024));
+  const int waves = blocks * kDecWaves;
+  const int per_wave = (tiles + waves - 1) / waves;
+  hipLaunchKernelGGL((k_w4a8_dec<R, D, ST>), dim3(blocks), dim3(256), smem, s, out, add, nib, params, q_split,
+                     scales, sums, rows, cols, per_wave, nx, nw, eps);
+}
+
+template <int R, int D>
+void launch_dec_rd(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                   const float *scales, const float *sums, int rows, int cols, const float *nx, const float *nw,
+                   float eps, int blocks, hipStream_t s) {
+  if (nx)
+    launch_dec_t<R, D, 0>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s);
+  else if (cols <= 16 * 256)
+    launch_dec_t<R, D, 1>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s);
+  else if (cols <= 16 * 512)
+    launch_dec_t<R, D, 2>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s);
+  else
+    launch_dec_t<R, D, 4>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s);
+}
+
+}  // namespace
+
+// Group 32, whole groups, K staged in LDS, byte offsets of every tile the
+// waves address (including the zero-reading ones past the matrix) inside
+// 31 bits.
+bool w4a8_dec_path(int rows, int cols, int gs) {
+  if (gs != 32 || rows <= 0 || cols % 32 != 0 || cols / 32 > kDecMaxGroups || cols < 256) return false;
+  const long long span = ((long long)rows + 4096LL * 12) * (cols / 2);
+  return span < (1LL << 31) - (1LL << 20);
+}
+
+bool w4a8_dec_fused_ok(int cols) { return cols / 32 <= 128; }
+
+// Tile height, ring depth and grid per shape, measured on the 7B decode
+// shapes (4096..32000 rows, K 4096 / 14336) with the weights streamed from
+// HBM: 4-row tiles with a 4-chunk ring, or 8-row tiles with a 3-chunk ring
+// where the fused RMSNorm prologue needs fewer blocks; a 512-block grid for
+// many rows, one tile per wave otherwise.
+static void dec_choice(int rows, bool fused, int &variant, int &blocks) {
+  if (!fused) {
+    variant = 4;
+    blocks = rows >= 16384 ? 512 : 0;
+  } else if (rows >= 16384) {
+    variant = 2;
+    blocks = 512;
+  } else if (rows >= 8192) {
+    variant = 4;
+    blocks = 512;
+  } else {
+    variant = rows > 4096 ? 2 : 4;
+    blocks = 0;
+  }
+}
+
+bool launch_w4a8_dec(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                     const float *scales, const float *sums, int rows, int cols, int gs, const float *nx,
+                     const float *nw, float eps, hipStream_t s, int variant, int blocks) {
+  if (!w4a8_dec_path(rows, cols, gs)) return false;
+  if (nx && !w4a8_dec_fused_ok(cols)) return false;
+  if (variant == 0) dec_choice(rows, nx != nullptr, variant, blocks);
+  switch (variant) {
+    case 1: launch_dec_rd<4, 6>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
+    case 2: launch_dec_rd<8, 3>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
+    case 3: launch_dec_rd<12, 2>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
+    case 4: launch_dec_rd<4, 4>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
+    case 5: launch_dec_rd<8, 4>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
+    case 6: launch_dec_rd<12, 3>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
+    default: launch_dec_rd<8, 3>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
+  }
+  return true;
+}
+
+}  // namespace rai

@@ -36,6 +36,16 @@ bool w4a8_norm1_path(int rows, int cols, int gs);
 bool launch_w4a8_norm1(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const float *x,
                        const float *norm_w, float eps, int rows, int cols, int gs, hipStream_t s);
 
+// One-token W4A8 GEMV, wave-streamed (decode_gemv.hip): group 32, K <= 14336.
+// With nx/nw (K <= 4096) the kernel applies rms_norm(nx) * nw and the
+// group-32 quantization itself (q_split, scales, sums unused).  variant
+// selects the tile height and ring depth, blocks the grid (0: one tile per
+// wave).  False when the shape is not covered.
+bool w4a8_dec_path(int rows, int cols, int gs);
+bool launch_w4a8_dec(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                     const float *scales, const float *sums, int rows, int cols, int gs, const float *nx,
+                     const float *nw, float eps, hipStream_t s, int variant = 0, int blocks = 0);
+
 // Matrix-core W4A8 (gemv.hip): group 32, K a multiple of 256, 2..16 tokens.
 constexpr int kMfmaMaxTokens = 16;
 bool w4a8_mfma_path(int rows, int cols, int m, int gs);

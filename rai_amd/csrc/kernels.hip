@@ -1220,6 +1220,7 @@ bool w4a8_norm1_path(int rows, int cols, int gs) {
 bool launch_w4a8_norm1(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const float *x,
                        const float *norm_w, float eps, int rows, int cols, int gs, hipStream_t s) {
   if (!w4a8_norm1_path(rows, cols, gs)) return false;
+  if (launch_w4a8_dec(out, add, nib, params, nullptr, nullptr, nullptr, rows, cols, gs, x, norm_w, eps, s)) return true;
   const int groups = cols / 32;
   // Same tiles as the unfused one-token dispatch in launch_w4a8.
   if (rows >= 16384)
@@ -1240,6 +1241,9 @@ void launch_w4a8(float *out, const float *add, const uint8_t *nib, const uint8_t
                  const _Float16 *qa) {
   const int groups = (cols + gs - 1) / gs;
   if (launch_w4a8_mfma(out, add, nib, params, qa, scales, sums, rows, cols, m, gs, s)) return;
+  if (m == 1 && q_split &&
+      launch_w4a8_dec(out, add, nib, params, q_split, scales, sums, rows, cols, gs, nullptr, nullptr, 0.0f, s))
+    return;
   // Decode (one token) at group 32, measured on the 7B shapes (4096..32000
   // rows, K 4096 / 14336): 16-row tiles for many rows, 8-row tiles for long
   // rows, 8-row whole-K blocks otherwise.
