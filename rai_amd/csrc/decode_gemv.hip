@@ -20,8 +20,9 @@
 // chain l of row r over the chunk's 32 products in group order.  No block
 // barrier is taken after the prologue, which stages the activations
 // (int8 codes in the block-split order, scales and sums; ST = 1, 2, 4
-// sixteen-byte loads of codes per thread) once per block - or, with the
-// fused input RMSNorm (ST = 0), normalises and quantizes the hidden row there (rms_norm_avx2 then quantize_input_split, layers.rs:325-376,
+// sixteen-byte loads of codes per thread) once per block - or quantizes the
+// f32 input row there (ST = 8, quantize_input_split), or, with the fused
+// input RMSNorm (ST = 0), normalises and quantizes the hidden row (rms_norm_avx2 then quantize_input_split, layers.rs:325-376,
 // gemm.rs:147-374).
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -29,6 +30,7 @@
 #include <algorithm>
 #include <cstdint>
 
+#include "exact_math.h"
 #include "kernels.h"
 #include "quant_dev.h"
 
@@ -77,7 +79,7 @@ size_t dec_smem(int cols, bool fused) {
   return act + std::max(waves, fused ? sizeof(float) * (size_t)cols : size_t(0));
 }
 
-template <int R, int D, int ST>
+template <int R, int D, int ST, bool GLU>
 __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, const uint8_t *__restrict__ nib,
                                                   const uint8_t *__restrict__ params,
                                                   const int8_t *__restrict__ q_split,
@@ -87,6 +89,7 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
                                                   const float *__restrict__ nw, float eps) {
   using C = DecCfg<R>;
   constexpr int IPL = C::IPL, LSTR = C::LSTR;
+  static_assert(!GLU || (R == 8 && ST == 0), "a gate|up block: 4 waves x 8 rows, fused input norm");
   extern __shared__ __align__(16) unsigned char smem[];
   const int groups = cols / 32;
   const int nchunks = (groups + kDecChunk - 1) / kDecChunk;
@@ -106,6 +109,15 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   const int wg = blockIdx.x * kDecWaves + wave;
   const int it_total = tiles_per_wave * nchunks;
   const int rowb = cols / 2;
+  // First row of the wave's tile t.  GLU: block b owns output group b of
+  // silu(gate) * up, i.e. gate rows 32b.. (tile 0) and up rows
+  // rows/2 + 32b.. (tile 1), 8 per wave.
+  auto tile_row0 = [&](int t) {
+    if constexpr (GLU)
+      return (t ? rows / 2 : 0) + 32 * (int)blockIdx.x + R * wave;
+    else
+      return (wg + t * W) * R;
+  };
   const __amdgpu_buffer_rsrc_t rc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(nib), 0, rows * rowb, 0x00020000);
   const __amdgpu_buffer_rsrc_t rp =
@@ -115,14 +127,16 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   // quantized row, its scales and sums), then the weight ring: loads
   // complete in issue order, so staging the activations never waits for
   // the ring.
-  constexpr bool FUSED = ST == 0;
-  constexpr int NP = FUSED ? 4 : 1;
-  constexpr int QV = FUSED ? 1 : ST;
+  constexpr bool FUSED = ST == 0, QONLY = ST == 8;
+  constexpr int NP = (FUSED || QONLY) ? 4 : 1;
+  constexpr int QV = (FUSED || QONLY) ? 1 : ST;
   float xr[NP][4], wr[NP][4];
   uint4 qv[QV];
   float av[2], sv[2];
   if constexpr (FUSED) {
     rmsnorm_regs_load<32, NP>(nx, nw, cols, xr, wr);
+  } else if constexpr (QONLY) {
+    xr_only<32, NP>(nx, cols, xr);
   } else {
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(q_split), 0, cols, 0x00020000);
@@ -144,7 +158,7 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   // Issue the loads of iteration it into ring slot j.
   auto load = [&](int it, u32x4 (&c)[IPL], uint32_t (&p)[IPL]) {
     const int t = it / nchunks, ch = it - t * nchunks;
-    const int row = (wg + t * W) * R + h;
+    const int row = tile_row0(t) + h;
     const int g = ch * kDecChunk + k;
     uint32_t vc = (uint32_t)row * rowb + g * 16;
     uint32_t vp = ((uint32_t)row * groups + g) * 4;
@@ -173,6 +187,8 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   // Stage the activations in LDS while the ring fills.
   if constexpr (FUSED) {
     rmsnorm_quant_regs<32, NP>(xr, wr, cols, eps, wbase, qsh, 32, ash, ssh);
+  } else if constexpr (QONLY) {
+    quant_regs<32, NP>(xr, cols, qsh, 32, ash, ssh);
   } else {
     // Unconditional stores to the clamped slots (threads past the row
     // rewrite the last slot with the value already there): a conditional
@@ -187,7 +203,7 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   }
   __syncthreads();
 
-  float acc = 0.0f;
+  float acc = 0.0f, gate_v = 0.0f, up_v = 0.0f;
   const int crow = lane % R, cl = lane / R;  // chain lane: row, chain
   const bool chain_lane = lane < 5 * R;
 
@@ -250,13 +266,20 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
           __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
           __builtin_amdgcn_wave_barrier();
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-          const int row = (wg + t * W) * R + lane;
+          const int row = tile_row0(t) + lane;
           if (lane < R && row < rows) {
             // hsum8 of (f0, f1, f2, f3, 0, 0, 0, 0) in the _mm256 order.
             const float f0 = fin[lane], f1 = fin[R + lane], f2 = fin[2 * R + lane], f3 = fin[3 * R + lane];
             const float zero = 0.0f;
             const float v = ((f0 + zero) + (f1 + zero)) + ((f2 + zero) + (f3 + zero)) + fin[4 * R + lane];
-            out[row] = add ? add[row] + v : v;
+            if constexpr (GLU) {
+              if (t == 0)
+                gate_v = v;
+              else
+                up_v = v;
+            } else {
+              out[row] = add ? add[row] + v : v;
+            }
           }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -267,16 +290,41 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  if constexpr (GLU) {
+    // silu_mul_inplace (layers.rs:850-883) of the block's 32 outputs and
+    // their quantization (gemm.rs:147-374) as k_silu_quant does; the
+    // quantized group goes to q_split / scales / sums, which are outputs
+    // here.
+    __syncthreads();  // every wave is done with the staged activations
+    float *glu = reinterpret_cast<float *>(smem);
+    if (lane < R) {
+      glu[R * wave + lane] = gate_v;
+      glu[32 + R * wave + lane] = up_v;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int j = lane & 7, b = blockIdx.x;
+      float v[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float xv = glu[8 * c + j];
+        const float e = rai_exact::schraudolph(xv * -1.0f);
+        v[c] = (xv / (1.0f + e)) * glu[32 + 8 * c + j];
+      }
+      quantize_group8_to<4>(v, j, lane < 8, const_cast<int8_t *>(q_split) + 32 * b, nullptr,
+                            const_cast<float *>(scales) + b, const_cast<float *>(sums) + b);
+    }
+  }
 }
 
 template <int R, int D, int ST>
 void launch_dec_t(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                   const float *scales, const float *sums, int rows, int cols, const float *nx, const float *nw,
                   float eps, int blocks, hipStream_t s) {
-  const size_t smem = dec_smem<R>(cols, ST == 0);
+  const size_t smem = dec_smem<R>(cols, ST == 0);  // the norm's row scratch
   static size_t configured = 0;
   if (smem > configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<R, D, ST>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<R, D, ST, false>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     configured = smem;
   }
@@ -285,16 +333,18 @@ void launch_dec_t(float *out, const float *add, const uint8_t *nib, const uint8_
   blocks = std::max(1, std::min(blocks, 1024));
   const int waves = blocks * kDecWaves;
   const int per_wave = (tiles + waves - 1) / waves;
-  hipLaunchKernelGGL((k_w4a8_dec<R, D, ST>), dim3(blocks), dim3(256), smem, s, out, add, nib, params, q_split,
-                     scales, sums, rows, cols, per_wave, nx, nw, eps);
+  hipLaunchKernelGGL((k_w4a8_dec<R, D, ST, false>), dim3(blocks), dim3(256), smem, s, out, add, nib, params,
+                     q_split, scales, sums, rows, cols, per_wave, nx, nw, eps);
 }
 
 template <int R, int D>
 void launch_dec_rd(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                    const float *scales, const float *sums, int rows, int cols, const float *nx, const float *nw,
                    float eps, int blocks, hipStream_t s) {
-  if (nx)
+  if (nx && nw)
     launch_dec_t<R, D, 0>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s);
+  else if (nx)
+    launch_dec_t<R, D, 8>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s);
   else if (cols <= 16 * 256)
     launch_dec_t<R, D, 1>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s);
   else if (cols <= 16 * 512)
@@ -342,7 +392,7 @@ bool launch_w4a8_dec(float *out, const float *add, const uint8_t *nib, const uin
                      const float *nw, float eps, hipStream_t s, int variant, int blocks) {
   if (!w4a8_dec_path(rows, cols, gs)) return false;
   if (nx && !w4a8_dec_fused_ok(cols)) return false;
-  if (variant == 0) dec_choice(rows, nx != nullptr, variant, blocks);
+  if (variant == 0) dec_choice(rows, nw != nullptr, variant, blocks);
   switch (variant) {
     case 1: launch_dec_rd<4, 6>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
     case 2: launch_dec_rd<8, 3>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
@@ -352,6 +402,21 @@ bool launch_w4a8_dec(float *out, const float *add, const uint8_t *nib, const uin
     case 6: launch_dec_rd<12, 3>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
     default: launch_dec_rd<8, 3>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s); break;
   }
+  return true;
+}
+
+bool launch_w4a8_glu1(const uint8_t *nib, const uint8_t *params, const float *x, const float *norm_w, float eps,
+                      int rows, int cols, int gs, int8_t *q_out, float *scale_out, float *sum_out, hipStream_t s) {
+  if (!w4a8_dec_path(rows, cols, gs) || !w4a8_dec_fused_ok(cols) || rows % 64 != 0) return false;
+  const size_t smem = dec_smem<8>(cols, true);
+  static size_t configured = 0;
+  if (smem > configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<8, 3, 0, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = smem;
+  }
+  hipLaunchKernelGGL((k_w4a8_dec<8, 3, 0, true>), dim3(rows / 64), dim3(256), smem, s, nullptr, nullptr, nib,
+                     params, q_out, scale_out, sum_out, rows, cols, 2, x, norm_w, eps);
   return true;
 }
 

@@ -38,13 +38,22 @@ bool launch_w4a8_norm1(float *out, const float *add, const uint8_t *nib, const u
 
 // One-token W4A8 GEMV, wave-streamed (decode_gemv.hip): group 32, K <= 14336.
 // With nx/nw (K <= 4096) the kernel applies rms_norm(nx) * nw and the
-// group-32 quantization itself (q_split, scales, sums unused).  variant
+// group-32 quantization itself (q_split, scales, sums unused); with nx alone
+// it quantizes nx (quantize_input_split of the f32 row).  variant
 // selects the tile height and ring depth, blocks the grid (0: one tile per
 // wave).  False when the shape is not covered.
 bool w4a8_dec_path(int rows, int cols, int gs);
 bool launch_w4a8_dec(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                      const float *scales, const float *sums, int rows, int cols, int gs, const float *nx,
                      const float *nw, float eps, hipStream_t s, int variant = 0, int blocks = 0);
+
+// One token through a stacked gate|up projection (rows = 2F, gate rows
+// first): rms_norm(x) * norm_w, quantization, the GEMV, silu(gate) * up and
+// the group-32 quantization of that product in one launch; writes only the
+// quantized product (q_out [F] block-split, scale_out / sum_out [F / 32]).
+// False when the shape is not covered (F % 32 != 0, K > 4096, ...).
+bool launch_w4a8_glu1(const uint8_t *nib, const uint8_t *params, const float *x, const float *norm_w, float eps,
+                      int rows, int cols, int gs, int8_t *q_out, float *scale_out, float *sum_out, hipStream_t s);
 
 // Matrix-core W4A8 (gemv.hip): group 32, K a multiple of 256, 2..16 tokens.
 constexpr int kMfmaMaxTokens = 16;

@@ -183,6 +183,33 @@ __device__ __forceinline__ void rmsnorm_regs_load(const float *__restrict__ row,
   }
 }
 
+// Per-group quantization (as k_quant) of a row of at most 32 * P groups held
+// in registers in rmsnorm_regs_load's slots; xr_only loads them.
+template <int GS, int P>
+__device__ __forceinline__ void xr_only(const float *__restrict__ row, int n, float (&xr)[P][GS / 8]) {
+  const int tid = threadIdx.x, groups = n / GS;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int g = min(p * 32 + tid / 8, groups - 1);
+#pragma unroll
+    for (int c = 0; c < GS / 8; ++c) xr[p][c] = row[g * GS + 8 * c + (tid & 7)];
+  }
+}
+
+template <int GS, int P>
+__device__ __forceinline__ void quant_regs(const float (&xr)[P][GS / 8], int n, int8_t *qs, int qstr,
+                                           float *scale_out, float *sum_out) {
+  const int tid = threadIdx.x, groups = n / GS, j = tid & 7;
+  constexpr int NB = GS / 8;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int g = p * 32 + tid / 8;
+    const bool ok = g < groups;
+    quantize_group8_to<NB>(xr[p], j, ok, qs + (size_t)(ok ? g : 0) * qstr, nullptr, scale_out + (ok ? g : 0),
+                           sum_out + (ok ? g : 0));
+  }
+}
+
 template <int GS, int P>
 __device__ __forceinline__ void rmsnorm_quant_regs(const float (&xr)[P][GS / 8], const float (&wr)[P][GS / 8],
                                                    int n, float eps, float *xs, int8_t *qs, int qstr,

@@ -522,15 +522,27 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
                       (int)kv.cap, (int)kv.vstride, q_ld, kv_ld, s, st);
     launch_attention(qp, q_ld, kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, (int)pos0, m, nh, nkv, hd,
                      md.attn_scale, w.att.as<float>(), scores, s, st);
-    quantize(md, w.att.as<float>(), m, qd, w, s);
-    // o_proj with the first residual add (model.rs:858-863) in its epilogue.
-    linear(L.lin[3], w.att.as<float>(), w, hid, m, s, hid);
+    // o_proj with the first residual add (model.rs:858-863) in its epilogue;
+    // one token: the GEMV launch quantizes the attention output itself.
+    const DLinear &O = L.lin[3];
+    if (!(norm1 && launch_w4a8_dec(hid, hid, O.nib, O.params, nullptr, nullptr, nullptr, O.rows, O.cols, O.gs,
+                                   w.att.as<float>(), nullptr, 0.0f, s))) {
+      quantize(md, w.att.as<float>(), m, qd, w, s);
+      linear(O, w.att.as<float>(), w, hid, m, s, hid);
+    }
     const bool gu1 = norm1 && L.gate_up.rows && fused_quant_ok(F, gs) &&
                      w4a8_norm1_path(L.gate_up.rows, L.gate_up.cols, L.gate_up.gs);
     if (!gu1) norm_then_quant(L.post_norm);
     if (c.num_experts > 0) {
       moe_block(md, L, w, m, s);
       launch_vec_add(hid, hid, w.mo.as<float>(), (size_t)m * H, s);
+    } else if (gu1 && w4a8_dec_path(L.lin[6].rows, L.lin[6].cols, L.lin[6].gs) &&
+               launch_w4a8_glu1(L.gate_up.nib, L.gate_up.params, hid, L.post_norm, c.norm_eps, L.gate_up.rows,
+                                L.gate_up.cols, L.gate_up.gs, w.q_split.as<int8_t>(), w.qscale.as<float>(),
+                                w.qsum.as<float>(), s)) {
+      // One token: the gate|up launch applied the norm, SiLU-mul and the
+      // quantization; down with the second residual add.
+      linear(L.lin[6], w.gub.as<float>(), w, hid, m, s, hid);
     } else {
       float *gp, *up;
       int gu_ld;
