@@ -69,14 +69,14 @@ struct DecCfg {
 
 // LDS bytes of a block: activations (codes, scales, sums) and the waves'
 // product areas; with the fused RMSNorm the product areas double as the
-// row scratch, which needs cols floats.
+// norm's chain-major row scratch.
 __host__ __device__ inline int dec_act_bytes(int cols) { return (cols + 8 * (cols / 32) + 15) & ~15; }
 
 template <int R>
 size_t dec_smem(int cols, bool fused) {
   const size_t act = dec_act_bytes(cols);
   const size_t waves = sizeof(float) * (size_t)kDecWaves * DecCfg<R>::WAVE_FLOATS;
-  return act + std::max(waves, fused ? sizeof(float) * (size_t)cols : size_t(0));
+  return act + std::max(waves, fused ? sizeof(float) * (size_t)rms_scratch_floats(cols) : size_t(0));
 }
 
 template <int R, int D, int ST, bool GLU>

@@ -394,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void k_w4a8_small(
   int8_t *qsh = reinterpret_cast<int8_t *>(smem);
   float *ash = reinterpret_cast<float *>(smem + ((qbytes + 15) & ~size_t(15)));
   float *ssh = ash + nbuf * m * gstage;
-  float *psh = ssh + nbuf * m * gstage;
+  float *psh = ash + ((2 * nbuf * m * gstage + 3) & ~3);  // 16-byte aligned
 
   const int r_item = tid / GT, g_item = tid % GT;
   const int row_item = row0 + r_item;
@@ -576,8 +576,9 @@ size_t small_smem(int groups, int m, int norm_cols = 0) {
   const int gstage = WHOLE ? groups : C::GT;
   const int nbuf = WHOLE ? 1 : 2;
   const size_t qbytes = (((size_t)nbuf * m * gstage * C::QSTR) + 15) & ~size_t(15);
-  return qbytes + 2 * sizeof(float) * (size_t)nbuf * m * gstage +
-         std::max(sizeof(float) * (size_t)m * C::NC * R * C::PSTR, sizeof(float) * (size_t)norm_cols);
+  return qbytes + sizeof(float) * ((2 * (size_t)nbuf * m * gstage + 3) & ~size_t(3)) +
+         std::max(sizeof(float) * (size_t)m * C::NC * R * C::PSTR,
+                  norm_cols ? sizeof(float) * (size_t)rms_scratch_floats(norm_cols) : size_t(0));
 }
 
 template <int GS, int MT, int R, int PD, bool WHOLE>
@@ -716,7 +717,7 @@ void launch_m1_t(float *out, const float *add, const uint8_t *nib, const uint8_t
   constexpr int NC = (GS == 32) ? 5 : 9;
   constexpr int IPT = m1_items_per_thread(GS);
   // With a fused RMSNorm the products area doubles as the row scratch.
-  const size_t prod = std::max(4 * (size_t)NC * R * (groups + 1), nx ? 4 * (size_t)cols : 0);
+  const size_t prod = std::max(4 * (size_t)NC * R * (groups + 1), nx ? 4 * (size_t)rms_scratch_floats(cols) : 0);
   const size_t smem = (size_t)((cols + 15) & ~15) + 4 * (size_t)((2 * groups + 3) & ~3) + prod;
   static size_t configured = 0;
   if (smem > configured) {

@@ -36,6 +36,16 @@ __device__ __forceinline__ _Float16 *qa4_slot(_Float16 *qa, int t, int g, int gr
   return qa + ((((size_t)(t >> 2) * (groups >> 2) + (g >> 2)) * 64) + 4 * (t & 3) + (g & 3)) * 8;
 }
 
+// Lane moves inside 16-lane rows (DPP, no LDS round trip): lane i reads
+// lane i + n (0 past the row), lane 7 - i of its 8-lane half, and the
+// quad permutations (1,0,3,2) and (2,3,0,1).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppShl1 = 0x101, kDppShl2 = 0x102, kDppShl4 = 0x104, kDppHalfMirror = 0x141, kDppXor1 = 0xB1,
+              kDppXor2 = 0x4E;
+
 template <int NB>
 __device__ __forceinline__ void quantize_group8_to(const float (&v)[NB], int j, bool ok, int8_t *qs_grp,
                                                    int8_t *qn_grp, float *scale_out, float *sum_out,
@@ -46,15 +56,15 @@ __device__ __forceinline__ void quantize_group8_to(const float (&v)[NB], int j, 
     a = a + v[c];
     amax = fmaxf(amax, fabsf(v[c]));
   }
-  // hsum8 in the reference's order via 8-lane shuffles.
-  const float a4 = __shfl(a, (j + 4) & 7, 8);
-  const float b = a + a4;  // lanes 0..3: a_j + a_{j+4}
-  const float b1 = __shfl(b, (j + 1) & 7, 8);
-  const float c = b + b1;  // lane 0: b0+b1, lane 2: b2+b3
-  const float c2 = __shfl(c, (j + 2) & 7, 8);
-  const float total = c + c2;  // lane 0
-#pragma unroll
-  for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+  // hsum8 in the reference's order: lanes 0..3 form a_j + a_{j+4}, lanes 0
+  // and 2 add their right neighbour, lane 0 adds lane 2.
+  const float b = a + dpp_mov<kDppShl4>(a);
+  const float c = b + dpp_mov<kDppShl1>(b);
+  const float total = c + dpp_mov<kDppShl2>(c);
+  // Max over the 8 lanes (order-free), delivered to all of them.
+  amax = fmaxf(amax, dpp_mov<kDppHalfMirror>(amax));
+  amax = fmaxf(amax, dpp_mov<kDppXor1>(amax));
+  amax = fmaxf(amax, dpp_mov<kDppXor2>(amax));
   const float scale = amax > 1e-10f ? amax / 127.0f : 1.0f;
   const float inv = 1.0f / scale;
   if (!ok) return;
@@ -210,22 +220,88 @@ __device__ __forceinline__ void quant_regs(const float (&xr)[P][GS / 8], int n, 
   }
 }
 
+// Chain-major scratch for rms_norm_avx2's sum of squares: chain c (0..15)
+// takes the elements c, c + 16, c + 32, ... (the trailing 8-block of an
+// odd n / 8 goes to chains 0..7 as their last element), so row c of the
+// scratch holds exactly chain c's elements in order.  The row stride is
+// 4 mod 64 floats, so the 16 chain lanes' 16-byte reads hit distinct banks.
+__host__ __device__ constexpr int rms_t_stride(int n) { return 64 * ((n / 16 + 1 - 4 + 63) / 64) + 4; }
+__host__ __device__ constexpr int rms_scratch_floats(int n) { return 16 * rms_t_stride(n); }
+
+// inv of rms_norm_avx2 from the chain-major scratch (all 256 threads call;
+// every thread gets inv).  Each chain lane streams its row with 16-byte
+// reads kept 32 elements ahead of its FMA chain.
+__device__ __forceinline__ float rmsnorm_inv_t(const float *xt, int n, float eps) {
+  __shared__ float chains[16];
+  __shared__ float inv_sh;
+  const int tid = threadIdx.x;
+  const int c16 = (n / 8) / 2;
+  const bool extra8 = 16 * c16 + 8 <= n;
+  const int stride = rms_t_stride(n);
+  if (tid < 16) {
+    const float *row = xt + tid * stride;
+    const int len = c16 + ((tid < 8 && extra8) ? 1 : 0);
+    float a = 0.0f;
+    int i = 0;
+    if (len >= 32) {
+      float4 cur[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cur[u] = reinterpret_cast<const float4 *>(row)[u];
+      for (; i + 32 <= len; i += 32) {
+        float4 nxt[8];
+        const bool more = i + 64 <= len;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) nxt[u] = reinterpret_cast<const float4 *>(row + (more ? i + 32 : i))[u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          a = __fmaf_rn(cur[u].x, cur[u].x, a);
+          a = __fmaf_rn(cur[u].y, cur[u].y, a);
+          a = __fmaf_rn(cur[u].z, cur[u].z, a);
+          a = __fmaf_rn(cur[u].w, cur[u].w, a);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+      }
+    }
+    for (; i < len; ++i) a = __fmaf_rn(row[i], row[i], a);
+    chains[tid] = a;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = chains[j] + chains[8 + j];
+    const float sum = ((s[0] + s[4]) + (s[1] + s[5])) + ((s[2] + s[6]) + (s[3] + s[7]));
+    // Correctly rounded sqrt and divide (the reference's sqrtss / divss).
+    inv_sh = 1.0f / __builtin_sqrtf(sum / (float)n + eps);
+  }
+  __syncthreads();
+  return inv_sh;
+}
+
+// rms_norm_avx2 + quantization of a row held in rmsnorm_regs_load's slots
+// (x and the norm weights) by a 256-thread block; xs: LDS scratch of
+// rms_scratch_floats(n) floats, 16-byte aligned.
 template <int GS, int P>
 __device__ __forceinline__ void rmsnorm_quant_regs(const float (&xr)[P][GS / 8], const float (&wr)[P][GS / 8],
                                                    int n, float eps, float *xs, int8_t *qs, int qstr,
                                                    float *scale_out, float *sum_out) {
   const int tid = threadIdx.x, groups = n / GS, j = tid & 7;
   constexpr int NB = GS / 8;
+  const int stride = rms_t_stride(n);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int g = p * 32 + tid / 8;
     if (g < groups) {
 #pragma unroll
-      for (int c = 0; c < NB; ++c) xs[g * GS + 8 * c + j] = xr[p][c];
+      for (int c = 0; c < NB; ++c) {
+        const int col = g * GS + 8 * c + j;
+        xs[(col & 15) * stride + (col >> 4)] = xr[p][c];
+      }
     }
   }
   __syncthreads();
-  const float inv = rmsnorm_inv_block(xs, n, eps);
+  const float inv = rmsnorm_inv_t(xs, n, eps);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int g = p * 32 + tid / 8;
