@@ -367,6 +367,97 @@ __global__ __launch_bounds__(256) void k_softmax(float *__restrict__ S, int pos0
   for (int s = tid; s < n; s += 256) row[s] = e[s] * inv;
 }
 
+// The same softmax with the row held in registers: thread t of 512 owns
+// the positions p = 512u + t (u < NB, n <= 512 NB), all of them in lane
+// chain t % 8 (512 is a multiple of 8) at chain step 64u + t / 8.  One load
+// burst, the maximum by lane moves, the exponentials written chain-major to
+// LDS (row j = chain j, row stride cstr = 4 mod 64 floats, so the 8 chain
+// lanes' 16-byte reads hit distinct banks) and normalised from the
+// registers.  The tail exponentials (expf) go to LDS for the final sum.
+template <int NB>
+__global__ __launch_bounds__(512) void k_softmax_r(float *__restrict__ S, int pos0, int nh, int sstride,
+                                                   int cstr, const int *__restrict__ st) {
+  extern __shared__ __align__(16) float ech[];  // [8][cstr]
+  __shared__ float red[8];
+  __shared__ float csum[8];
+  __shared__ float tail[8];
+  __shared__ float bc;
+  if (st) pos0 = st[0];
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = pos0 + t + 1, n8 = n / 8;
+  float *row = S + ((size_t)t * nh + h) * sstride;
+  float v[NB];
+#pragma unroll
+  for (int u = 0; u < NB; ++u) v[u] = 512 * u < n ? row[min(512 * u + tid, n - 1)] : -INFINITY;
+  float mx = v[0];
+#pragma unroll
+  for (int u = 1; u < NB; ++u) mx = fmaxf(mx, v[u]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
+  float *erow = ech + (tid & 7) * cstr + (tid >> 3);
+#pragma unroll
+  for (int u = 0; u < NB; ++u) {
+    const int p = 512 * u + tid;
+    if (p < 8 * n8) {
+      v[u] = rai_exact::schraudolph(v[u] - mx);
+      erow[64 * u] = v[u];
+    } else if (p < n) {
+      v[u] = rai_exact::expf_glibc(v[u] - mx);
+      tail[p - 8 * n8] = v[u];
+    }
+  }
+  __syncthreads();
+  if (tid < 8) {
+    // Chain tid: e_{8i + tid} for i = 0..n8-1 in order, 16-byte reads kept
+    // 32 values ahead.
+    const float *cr = ech + tid * cstr;
+    float acc = 0.0f;
+    int i = 0;
+    if (n8 >= 32) {
+      float4 cur[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cur[u] = reinterpret_cast<const float4 *>(cr)[u];
+      for (; i + 32 <= n8; i += 32) {
+        float4 nxt[8];
+        const int nb = i + 64 <= n8 ? i + 32 : i;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) nxt[u] = reinterpret_cast<const float4 *>(cr + nb)[u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          acc = acc + cur[u].x;
+          acc = acc + cur[u].y;
+          acc = acc + cur[u].z;
+          acc = acc + cur[u].w;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+      }
+    }
+    for (; i < n8; ++i) acc = acc + cr[i];
+    csum[tid] = acc;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float sum = ((csum[0] + csum[4]) + (csum[1] + csum[5])) + ((csum[2] + csum[6]) + (csum[3] + csum[7]));
+    for (int r = 0; r < n - 8 * n8; ++r) sum = sum + tail[r];
+    bc = 1.0f / sum;
+  }
+  __syncthreads();
+  const float inv = bc;
+#pragma unroll
+  for (int u = 0; u < NB; ++u) {
+    const int p = 512 * u + tid;
+    if (p < n) row[p] = v[u] * inv;
+  }
+}
+
+// Chain-major row stride for k_softmax_r: at least ceil(nmax / 8) floats,
+// 4 mod 64.
+static int softmax_r_stride(int nmax) { return (((nmax + 7) / 8 + 63) & ~63) + 4; }
+
 // PV with the V stream spread over loader waves.  The V cache is d-major
 // ([kv head][head dim][vstride] floats, vstride a multiple of 64), so the
 // positions of one dim in a chunk are contiguous.  One block per (token, kv
@@ -630,7 +721,21 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
       sm_configured = smem;
     }
-    hipLaunchKernelGGL(k_softmax, dim3(nh, mt), dim3(256), smem, s, scores, p0, nh, sstride, st);
+    if (nmax <= 512 * 32) {
+      const int cstr = softmax_r_stride(nmax);
+      const size_t rsm = sizeof(float) * 8 * (size_t)cstr;
+      const dim3 g(nh, mt);
+      if (nmax <= 512 * 4)
+        hipLaunchKernelGGL(k_softmax_r<4>, g, dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
+      else if (nmax <= 512 * 8)
+        hipLaunchKernelGGL(k_softmax_r<8>, g, dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
+      else if (nmax <= 512 * 16)
+        hipLaunchKernelGGL(k_softmax_r<16>, g, dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
+      else
+        hipLaunchKernelGGL(k_softmax_r<32>, g, dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
+    } else {
+      hipLaunchKernelGGL(k_softmax, dim3(nh, mt), dim3(256), smem, s, scores, p0, nh, sstride, st);
+    }
     const size_t total = (size_t)mt * nh * hd;
     const int G = nh / nkv;
     const int DL = (G == 1) ? 64 : (G == 2) ? 32 : 16;
