@@ -79,17 +79,52 @@ size_t dec_smem(int cols, bool fused) {
   return act + std::max(waves, fused ? sizeof(float) * (size_t)rms_scratch_floats(cols) : size_t(0));
 }
 
-template <int R, int D, int ST, bool GLU>
+constexpr int kEpiPlain = 0, kEpiGlu = 1, kEpiRope = 2;
+
+// rope_store of one rotation pair (x0 at head element i, x1 at i + hd/2)
+// as k_rope_store does it (layers.rs:561-726): q and k rotated in the qkv
+// output, k also into the K cache row of the position, v unrotated into
+// the d-major V cache.  Row index r of the stacked [q; k; v] output.
+__device__ __forceinline__ void rope_store_pair(const DecRope &rp, float *out, int r, int pos, float c, float sn,
+                                                float x0, float x1) {
+  const int hd = rp.hd, half = hd / 2, body = (half / 8) * 8;
+  const int head = r / hd, i = r - head * hd;
+  float r0 = x0, r1 = x1;
+  if (head < rp.nh + rp.nkv) {
+    if (i < body) {
+      r0 = __fmaf_rn(x0, c, -(x1 * sn));
+      r1 = __fmaf_rn(x1, c, x0 * sn);
+    } else {
+      r0 = x0 * c - x1 * sn;
+      r1 = x1 * c + x0 * sn;
+    }
+  }
+  out[r] = r0;
+  out[r + half] = r1;
+  if (head >= rp.nh && head < rp.nh + rp.nkv) {
+    const size_t dst = ((size_t)(head - rp.nh) * rp.cap + pos) * hd;
+    rp.kc[dst + i] = r0;
+    rp.kc[dst + half + i] = r1;
+  } else if (head >= rp.nh + rp.nkv) {
+    float *vd = rp.vc + (size_t)(head - rp.nh - rp.nkv) * hd * rp.vstride + pos;
+    vd[(size_t)i * rp.vstride] = r0;
+    vd[(size_t)(half + i) * rp.vstride] = r1;
+  }
+}
+
+template <int R, int D, int ST, int EPI>
 __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, const uint8_t *__restrict__ nib,
                                                   const uint8_t *__restrict__ params,
                                                   const int8_t *__restrict__ q_split,
                                                   const float *__restrict__ scales,
                                                   const float *__restrict__ sums, int rows, int cols,
                                                   int tiles_per_wave, const float *__restrict__ nx,
-                                                  const float *__restrict__ nw, float eps) {
+                                                  const float *__restrict__ nw, float eps, DecRope rope) {
   using C = DecCfg<R>;
   constexpr int IPL = C::IPL, LSTR = C::LSTR;
+  constexpr bool GLU = EPI == kEpiGlu, ROPE = EPI == kEpiRope;
   static_assert(!GLU || (R == 8 && ST == 0), "a gate|up block: 4 waves x 8 rows, fused input norm");
+  static_assert(!ROPE || R == 8, "a rope tile: 4 rows of each half of a head");
   extern __shared__ __align__(16) unsigned char smem[];
   const int groups = cols / 32;
   const int nchunks = (groups + kDecChunk - 1) / kDecChunk;
@@ -111,13 +146,22 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   const int rowb = cols / 2;
   // First row of the wave's tile t.  GLU: block b owns output group b of
   // silu(gate) * up, i.e. gate rows 32b.. (tile 0) and up rows
-  // rows/2 + 32b.. (tile 1), 8 per wave.
+  // rows/2 + 32b.. (tile 1), 8 per wave.  ROPE: tile u of head u / (hd/8)
+  // holds the rotation pairs (i, i + hd/2), i = 4 (u % (hd/8)) + 0..3: local
+  // rows 0..3 are i, local rows 4..7 are i + hd/2.
+  const int rhalf = ROPE ? rope.hd / 2 : 0;
   auto tile_row0 = [&](int t) {
-    if constexpr (GLU)
+    if constexpr (GLU) {
       return (t ? rows / 2 : 0) + 32 * (int)blockIdx.x + R * wave;
-    else
+    } else if constexpr (ROPE) {
+      const int u = wg + t * W, per = rope.hd / 8;
+      return (u / per) * rope.hd + 4 * (u % per);
+    } else {
       return (wg + t * W) * R;
+    }
   };
+  // Row offset of local row r (0..R-1) from tile_row0.
+  auto lrow = [&](int r) { return (ROPE && r >= 4) ? rhalf - 4 + r : r; };
   const __amdgpu_buffer_rsrc_t rc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(nib), 0, rows * rowb, 0x00020000);
   const __amdgpu_buffer_rsrc_t rp =
@@ -127,6 +171,19 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   // quantized row, its scales and sums), then the weight ring: loads
   // complete in issue order, so staging the activations never waits for
   // the ring.
+  // Rotation entries of the lane's pair (rope tiles: lanes 0..3, one tile
+  // per wave), requested first.
+  int rpos = 0;
+  float rcos = 0.0f, rsin = 0.0f;
+  if constexpr (ROPE) {
+    rpos = rope.st ? rope.st[0] : rope.pos0;
+    const int r = tile_row0(0) + min(lane, 3);
+    const int i = r % rope.hd;
+    const bool rot = r < rows && r / rope.hd < rope.nh + rope.nkv;
+    const size_t ci = (size_t)rpos * rhalf + (rot ? i : 0);
+    rcos = rope.cos_t[ci];
+    rsin = rope.sin_t[ci];
+  }
   constexpr bool FUSED = ST == 0, QONLY = ST == 8;
   constexpr int NP = (FUSED || QONLY) ? 4 : 1;
   constexpr int QV = (FUSED || QONLY) ? 1 : ST;
@@ -158,7 +215,7 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   // Issue the loads of iteration it into ring slot j.
   auto load = [&](int it, u32x4 (&c)[IPL], uint32_t (&p)[IPL]) {
     const int t = it / nchunks, ch = it - t * nchunks;
-    const int row = tile_row0(t) + h;
+    const int row = tile_row0(t) + h;  // local row h; item i adds lrow(2i) rows
     const int g = ch * kDecChunk + k;
     uint32_t vc = (uint32_t)row * rowb + g * 16;
     uint32_t vp = ((uint32_t)row * groups + g) * 4;
@@ -170,11 +227,11 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
     // VGPR and instruction offsets, not the SGPR one.
 #pragma unroll
     for (int i = 0; i < IPL; ++i)
-      c[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)(vc + (uint32_t)(i * 2 * rowb)), 0, 0);
+      c[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)(vc + (uint32_t)(lrow(2 * i) * rowb)), 0, 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < IPL; ++i)
-      p[i] = __builtin_amdgcn_raw_buffer_load_b32(rp, (int)(vp + (uint32_t)(i * 8 * groups)), 0, 0);
+      p[i] = __builtin_amdgcn_raw_buffer_load_b32(rp, (int)(vp + (uint32_t)(lrow(2 * i) * 4 * groups)), 0, 0);
   };
   // Same issue order as the loop's refills (slot by slot), which keeps the
   // compiler's wait counts exact at the loop head.
@@ -266,7 +323,7 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
           __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
           __builtin_amdgcn_wave_barrier();
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-          const int row = tile_row0(t) + lane;
+          const int row = tile_row0(t) + lrow(lane);
           if (lane < R && row < rows) {
             // hsum8 of (f0, f1, f2, f3, 0, 0, 0, 0) in the _mm256 order.
             const float f0 = fin[lane], f1 = fin[R + lane], f2 = fin[2 * R + lane], f3 = fin[3 * R + lane];
@@ -277,9 +334,18 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
                 gate_v = v;
               else
                 up_v = v;
+            } else if constexpr (ROPE) {
+              fin[40 + lane] = v;
             } else {
               out[row] = add ? add[row] + v : v;
             }
+          }
+          if constexpr (ROPE) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (lane < 4 && tile_row0(t) < rows)
+              rope_store_pair(rope, out, tile_row0(t) + lane, rpos, rcos, rsin, fin[40 + lane], fin[44 + lane]);
           }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -324,7 +390,7 @@ void launch_dec_t(float *out, const float *add, const uint8_t *nib, const uint8_
   const size_t smem = dec_smem<R>(cols, ST == 0);  // the norm's row scratch
   static size_t configured = 0;
   if (smem > configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<R, D, ST, false>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<R, D, ST, kEpiPlain>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     configured = smem;
   }
@@ -333,8 +399,8 @@ void launch_dec_t(float *out, const float *add, const uint8_t *nib, const uint8_
   blocks = std::max(1, std::min(blocks, 1024));
   const int waves = blocks * kDecWaves;
   const int per_wave = (tiles + waves - 1) / waves;
-  hipLaunchKernelGGL((k_w4a8_dec<R, D, ST, false>), dim3(blocks), dim3(256), smem, s, out, add, nib, params,
-                     q_split, scales, sums, rows, cols, per_wave, nx, nw, eps);
+  hipLaunchKernelGGL((k_w4a8_dec<R, D, ST, kEpiPlain>), dim3(blocks), dim3(256), smem, s, out, add, nib, params,
+                     q_split, scales, sums, rows, cols, per_wave, nx, nw, eps, DecRope{});
 }
 
 template <int R, int D>
@@ -411,12 +477,30 @@ bool launch_w4a8_glu1(const uint8_t *nib, const uint8_t *params, const float *x,
   const size_t smem = dec_smem<8>(cols, true);
   static size_t configured = 0;
   if (smem > configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<8, 3, 0, true>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<8, 3, 0, kEpiGlu>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     configured = smem;
   }
-  hipLaunchKernelGGL((k_w4a8_dec<8, 3, 0, true>), dim3(rows / 64), dim3(256), smem, s, nullptr, nullptr, nib,
-                     params, q_out, scale_out, sum_out, rows, cols, 2, x, norm_w, eps);
+  hipLaunchKernelGGL((k_w4a8_dec<8, 3, 0, kEpiGlu>), dim3(rows / 64), dim3(256), smem, s, nullptr, nullptr, nib,
+                     params, q_out, scale_out, sum_out, rows, cols, 2, x, norm_w, eps, DecRope{});
+  return true;
+}
+
+bool launch_w4a8_qkv_rope1(float *out, const uint8_t *nib, const uint8_t *params, const float *x,
+                           const float *norm_w, float eps, int rows, int cols, int gs, const DecRope &rope,
+                           hipStream_t s) {
+  if (!w4a8_dec_path(rows, cols, gs) || !w4a8_dec_fused_ok(cols)) return false;
+  if (rope.hd % 8 != 0 || rows != (rope.nh + 2 * rope.nkv) * rope.hd) return false;
+  const size_t smem = dec_smem<8>(cols, true);
+  static size_t configured = 0;
+  if (smem > configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<8, 3, 0, kEpiRope>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = smem;
+  }
+  const int tiles = rows / 8, blocks = (tiles + kDecWaves - 1) / kDecWaves;
+  hipLaunchKernelGGL((k_w4a8_dec<8, 3, 0, kEpiRope>), dim3(blocks), dim3(256), smem, s, out, nullptr, nib, params,
+                     nullptr, nullptr, nullptr, rows, cols, 1, x, norm_w, eps, rope);
   return true;
 }
 

@@ -55,6 +55,21 @@ bool launch_w4a8_dec(float *out, const float *add, const uint8_t *nib, const uin
 bool launch_w4a8_glu1(const uint8_t *nib, const uint8_t *params, const float *x, const float *norm_w, float eps,
                       int rows, int cols, int gs, int8_t *q_out, float *scale_out, float *sum_out, hipStream_t s);
 
+// Rotary embedding and KV store of one token, applied by a GEMV epilogue.
+struct DecRope {
+  const float *cos_t, *sin_t;  // [pos][hd / 2] tables
+  int pos0;                    // token position (read from st[0] when st)
+  const int *st;
+  float *kc, *vc;              // K cache [nkv][cap][hd], V cache d-major [nkv][hd][vstride]
+  int cap, vstride, nh, nkv, hd;
+};
+// One token through the stacked [q; k; v] projection (rows (nh + 2 nkv) hd):
+// rms_norm(x) * norm_w, quantization, the GEMV, then rope_store's rotation of
+// q and k, the K and V cache stores (as launch_rope_store for m = 1).
+bool launch_w4a8_qkv_rope1(float *out, const uint8_t *nib, const uint8_t *params, const float *x,
+                           const float *norm_w, float eps, int rows, int cols, int gs, const DecRope &rope,
+                           hipStream_t s);
+
 // Matrix-core W4A8 (gemv.hip): group 32, K a multiple of 256, 2..16 tokens.
 constexpr int kMfmaMaxTokens = 16;
 bool w4a8_mfma_path(int rows, int cols, int m, int gs);

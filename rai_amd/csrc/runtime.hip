@@ -495,9 +495,17 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
     if (!qkv1) norm_then_quant(L.in_norm);
     float *qp, *kp, *vp;
     int q_ld, kv_ld;
+    // One token: the qkv launch also rotates q and k and stores k and v
+    // into the cache (rope_store in its epilogue).
+    const DecRope rope{md.rope_cos, md.rope_sin, (int)pos0, st, kv.kc(li), kv.vc(li), (int)kv.cap,
+                       (int)kv.vstride, nh, nkv, hd};
+    const bool roped = qkv1 && kv.vstride > 0 &&
+                       launch_w4a8_qkv_rope1(w.qkvb.as<float>(), L.qkv.nib, L.qkv.params, hid, L.in_norm,
+                                             c.norm_eps, L.qkv.rows, L.qkv.cols, L.qkv.gs, rope, s);
     if (qkv1) {
-      launch_w4a8_norm1(w.qkvb.as<float>(), nullptr, L.qkv.nib, L.qkv.params, hid, L.in_norm, c.norm_eps,
-                        L.qkv.rows, L.qkv.cols, L.qkv.gs, s);
+      if (!roped)
+        launch_w4a8_norm1(w.qkvb.as<float>(), nullptr, L.qkv.nib, L.qkv.params, hid, L.in_norm, c.norm_eps,
+                          L.qkv.rows, L.qkv.cols, L.qkv.gs, s);
       qp = w.qkvb.as<float>();
       kp = qp + qd;
       vp = kp + nkv * hd;
@@ -518,8 +526,9 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
       q_ld = qd;
       kv_ld = nkv * hd;
     }
-    launch_rope_store(qp, kp, vp, md.rope_cos, md.rope_sin, (int)pos0, m, nh, nkv, hd, kv.kc(li), kv.vc(li),
-                      (int)kv.cap, (int)kv.vstride, q_ld, kv_ld, s, st);
+    if (!roped)
+      launch_rope_store(qp, kp, vp, md.rope_cos, md.rope_sin, (int)pos0, m, nh, nkv, hd, kv.kc(li), kv.vc(li),
+                        (int)kv.cap, (int)kv.vstride, q_ld, kv_ld, s, st);
     launch_attention(qp, q_ld, kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, (int)pos0, m, nh, nkv, hd,
                      md.attn_scale, w.att.as<float>(), scores, s, st);
     // o_proj with the first residual add (model.rs:858-863) in its epilogue;
