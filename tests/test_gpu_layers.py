@@ -54,6 +54,22 @@ def test_attention_head_bit_exact(rai, ora, hd, pos):
     assert np.array_equal(_bits(got), _bits(want))
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("pos", [2047, 2048, 4100, 8191, 9000, 16383])
+def test_attention_head_long_context_bit_exact(rai, ora, hd, pos):
+    """Contexts that select each register depth of the softmax (up to 2048,
+    4096, 8192 and 16384 positions), with tails of 0..7 positions past the
+    last 8-block and chains long enough for the prefetched LDS reads."""
+    rng = np.random.default_rng(hd * 7 + pos)
+    q = rng.normal(size=hd).astype(np.float32)
+    k = rng.normal(size=(pos + 1, hd)).astype(np.float32)
+    v = rng.normal(size=(pos + 1, hd)).astype(np.float32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    got = rai.attention_head(q, k, v, pos, hd, float(scale))
+    want = ora.attention_head(q, k, v, pos, hd, float(scale))
+    assert np.array_equal(_bits(got), _bits(want)), pos
+
+
 def test_rope_tables_match_oracle(rai, ora):
     """The library builds RoPE tables on the host with the C library's
     powf/cosf/sinf exactly as RoPETable::with_scaling does; position 1 of a
