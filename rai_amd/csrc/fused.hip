@@ -472,7 +472,7 @@ static int softmax_r_stride(int nmax) { return (((nmax + 7) / 8 + 63) & ~63) + 4
 // acc for the finite cached v, and acc is never -0), and the compute waves
 // run the reference's sequential FMA chain over the current chunk, reading
 // 4 positions' V values and (wave-broadcast) probabilities per 16-byte LDS
-// read.  One barrier per chunk.
+// read, 32 positions ahead of the chain.  One barrier per chunk.
 template <int DL, int G, int CP>
 struct PvCfg {
   static constexpr int NCW = G * DL / 64;       // compute waves
@@ -559,14 +559,41 @@ __global__ __launch_bounds__(512) void k_pv_stream(const float *__restrict__ P,
     if (wave < NCW) {
       const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
       const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][g * STR]);
-#pragma unroll 8
-      for (int u = 0; u < Q4; ++u) {
-        const float4 v4 = vr[u];
-        const float4 p4 = pr[u];
-        acc = __fmaf_rn(p4.x, v4.x, acc);
-        acc = __fmaf_rn(p4.y, v4.y, acc);
-        acc = __fmaf_rn(p4.z, v4.z, acc);
-        acc = __fmaf_rn(p4.w, v4.w, acc);
+      // Rolling prefetch: the next 8 float4 pairs (32 positions) are
+      // requested before the 32 FMAs of the current ones, so the LDS
+      // latency is exposed once per chunk instead of once per 32 positions.
+      constexpr int PB = NV + NP <= 24 ? 8 : 4;  // fewer with many loader registers (G = 16)
+      static_assert(Q4 % PB == 0, "whole prefetch blocks per chunk");
+      float4 cv[PB], cp[PB];
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        cv[u] = vr[u];
+        cp[u] = pr[u];
+      }
+#pragma unroll
+      for (int u0 = 0; u0 < Q4; u0 += PB) {
+        float4 nv[PB], np[PB];
+        if (u0 + PB < Q4) {
+#pragma unroll
+          for (int u = 0; u < PB; ++u) {
+            nv[u] = vr[u0 + PB + u];
+            np[u] = pr[u0 + PB + u];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < PB; ++u) {
+          acc = __fmaf_rn(cp[u].x, cv[u].x, acc);
+          acc = __fmaf_rn(cp[u].y, cv[u].y, acc);
+          acc = __fmaf_rn(cp[u].z, cv[u].z, acc);
+          acc = __fmaf_rn(cp[u].w, cv[u].w, acc);
+        }
+        if (u0 + PB < Q4) {
+#pragma unroll
+          for (int u = 0; u < PB; ++u) {
+            cv[u] = nv[u];
+            cp[u] = np[u];
+          }
+        }
       }
     } else if (k + 1 < nchunks && lw == (k + 1) % NL) {
       RAI_PV_PUBLISH(k + 1);
