@@ -23,12 +23,16 @@
 // bounds these kernels at 9 tokens.
 //
 // K order inside a block (8 columns c0..c7): f16 element e of the lane's 8
-// is column (0, 4, 1, 5, 2, 6, 3, 7)[e], which is what the nibble unpack
-// (shifts by 0/4/8/12 of a 0x000F000F mask) produces for the weights.
+// is column (0, 4, 1, 5, 2, 6, 3, 7)[e].  The weight dword of a block holds
+// column c in bits 4c..4c+3; masks 0x000F000F and 0x00F000F0 of the dword
+// and of the dword shifted by 8 give columns (0, 4), (1, 5), (2, 6), (3, 7)
+// as f16 pairs, the odd columns at 16 times their code.  The activation
+// layout holds the odd columns divided by 16 (exact for int8 values), so
+// every product is the exact code x activation.
 //
-// Activations for both kernels are packed once per GEMV input by
-// k_qa_pack4 as qa4[tg][q][b][i = 4t + r][8] f16: token 4*tg + t, group
-// 4*q + r, block b.
+// Activations for all three kernels are packed once per GEMV input
+// (k_qa_pack4, or the quantizing kernels' matrix-core output) as
+// qa4[tg][q][b][i = 4t + r][8] f16: token 4*tg + t, group 4*q + r, block b.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -53,18 +57,15 @@ __device__ __forceinline__ float f16hi(uint32_t w) {
 
 // Eight weight codes of one 8-column block (one dword: byte i = columns
 // 2i (low nibble), 2i+1 (high nibble)) as exact f16 values in the K order
-// (0, 4, 1, 5, 2, 6, 3, 7): 0x6400 | n is the f16 1024 + n, minus 1024.
+// (0, 4, 1, 5, 2, 6, 3, 7), odd columns times 16: 0x6400 | v is the f16
+// 1024 + v (v <= 240), minus 1024.
 __device__ __forceinline__ h8 unpack_codes(uint32_t w) {
-  const uint32_t m = 0x000F000Fu, o = 0x64006400u;
-  const uint32_t d0 = (w & m) | o;
-  const uint32_t d1 = ((w >> 4) & m) | o;
-  const uint32_t d2 = ((w >> 8) & m) | o;
-  const uint32_t d3 = ((w >> 12) & m) | o;
+  const uint32_t lo = 0x000F000Fu, hi = 0x00F000F0u, o = 0x64006400u, t = w >> 8;
   const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
-  const h2 e0 = __builtin_bit_cast(h2, d0) - bias;
-  const h2 e1 = __builtin_bit_cast(h2, d1) - bias;
-  const h2 e2 = __builtin_bit_cast(h2, d2) - bias;
-  const h2 e3 = __builtin_bit_cast(h2, d3) - bias;
+  const h2 e0 = __builtin_bit_cast(h2, (w & lo) | o) - bias;
+  const h2 e1 = __builtin_bit_cast(h2, (w & hi) | o) - bias;
+  const h2 e2 = __builtin_bit_cast(h2, (t & lo) | o) - bias;
+  const h2 e3 = __builtin_bit_cast(h2, (t & hi) | o) - bias;
   h8 r;
   r[0] = e0[0];
   r[1] = e0[1];
@@ -270,10 +271,10 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv_ms(
   }
 }
 
-// Activations in the register-streamed kernel's A layout:
+// Activations in the matrix-core A layout:
 // qa4[tg][q][b][i = 4t + r][8] f16 = token 4*tg + t, group 4*q + r, block b
-// in the K order above (zeros for tokens past m).  One thread per
-// (tg, q, b, i).  Requires groups % 4 == 0.
+// in the K order above, odd columns divided by 16 (zeros for tokens past m).
+// One thread per (tg, q, b, i).  Requires groups % 4 == 0.
 __global__ void k_qa_pack4(const int8_t *__restrict__ q_split, int m, int cols, int ntg,
                            _Float16 *__restrict__ qa) {
   const int groups = cols / 32, nq = groups / 4;
@@ -293,7 +294,8 @@ __global__ void k_qa_pack4(const int8_t *__restrict__ q_split, int m, int cols, 
   for (int e = 0; e < 8; ++e) {
     const int c = col_of_e[e];
     const int sidx = (c & 1) ? 4 + (c >> 1) : (c >> 1);
-    dst[e] = (_Float16)(float)src[sidx];
+    const float v = (float)src[sidx];
+    dst[e] = (_Float16)((c & 1) ? v * 0.0625f : v);
   }
 }
 
@@ -314,9 +316,10 @@ __global__ void k_qa_pack4(const int8_t *__restrict__ q_split, int m, int cols, 
 // registers while chunk c is computed and stored behind it, with one barrier
 // per chunk.
 //
-// Codes enter the MFMA either as f16 subnormals n * 2^-24 (SUB: one mask
-// per pair, D = S * 2^-24 exactly, products and partial sums being
-// multiples of 2^-24 below 2^-10) with the weight scale taken as ws * 2^24,
+// Codes enter the MFMA either as f16 subnormals v * 2^-24 (SUB: one mask
+// per pair, v = n or 16 n; D = S * 2^-24 exactly, products and partial sums
+// being multiples of 2^-24 below 2^-10) with the weight scale taken as
+// ws * 2^24,
 // or as 1024 + n minus 1024 (D = S).  fl(D * fl(ws*2^24 * as)) equals
 // fl(S * fl(ws * as)) whenever |ws * as| < 2^104 (power-of-two scaling
 // commutes with rounding in the normal range, and ws * as is zero or at
@@ -327,8 +330,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ h8 unpack_codes_sub(uint32_t w) {
-  const uint32_t m = 0x000F000Fu;
-  const u32x4 d = {w & m, (w >> 4) & m, (w >> 8) & m, (w >> 12) & m};
+  const uint32_t lo = 0x000F000Fu, hi = 0x00F000F0u, t = w >> 8;
+  const u32x4 d = {w & lo, w & hi, t & lo, t & hi};
   return __builtin_bit_cast(h8, d);
 }
 
@@ -512,6 +515,238 @@ size_t gemv_rs_smem(int tgw, int nq_chunk) {
   return (size_t)2 * tgw * nq_chunk * (68 * 16 + 2 * 4 * 16);
 }
 
+// Register-pipelined version for K <= kRpMaxCols.  The block stages all of
+// its activations in LDS once (no barriers in the main loop).  Each wave
+// streams 16 rows as k_gemv_rs does, through a ring of NQ slots (slot s holds
+// step q = s mod NQ: 16 B of codes of group 4q + h, 16 B of parameters of
+// groups 4q..4q+3), and pipelines by one step: step q unpacks its codes,
+// then per token group runs the epilogue of step q - 1 (its MFMA results
+// and staged scales, issued a step earlier), requests the scales of step q
+// and issues the MFMAs of step q; the A operands of the next token group
+// are requested one group ahead.  The slot of step q - 1 is refilled with
+// step q - 1 + NQ after its parameters are used.
+//
+// fl(ws * x) and fl(wz * xsum) come from v_fma_mix with a -0 addend held in
+// a register the compiler cannot see through: the fused multiply-add of a
+// product and -0 rounds once, like the product, and reads the f16 halves of
+// the parameter dword directly.  With subnormal codes the staged activation
+// scales carry the 2^24 (as * 2^24 is exact below 2^104): fl(ws * (as *
+// 2^24)) = fl((ws * 2^24) * as).
+constexpr int kRpMaxCols = 4096;
+
+template <bool HI>
+__device__ __forceinline__ float mul_h16(uint32_t w, float x, float nz) {
+  const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(HI ? w >> 16 : w & 0xFFFF));
+  return __builtin_fmaf((float)h, x, nz);
+}
+
+// NG token groups; la / lsc / lsu point at the lane's slot of token group
+// 0: A of (group t, step q, block b) at la[((t * nq + q) * 4 + b) * 17],
+// scales / sums of (t, q) at [(t * nq + q) * 4].
+template <int NG, int NQ, bool SUB>
+__device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, const __amdgpu_buffer_rsrc_t rps,
+                                             uint32_t vc0, uint32_t vp0, const u32x4 *__restrict__ la,
+                                             const f32x4 *__restrict__ lsc, const f32x4 *__restrict__ lsu,
+                                             int nq, float nz, u32x4 (&rc)[NQ], u32x4 (&rp)[NQ],
+                                             float (&f)[NG][4], float (&zc)[NG]) {
+  typedef u32x4 u4;
+  typedef f32x4 f4;
+  const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  // Step -1: zero results, scales and parameters (its epilogue adds +0 to
+  // the +0 accumulators).
+  f4 D[NG][4], as4[NG], xs4[NG];
+#pragma unroll
+  for (int t = 0; t < NG; ++t) {
+    as4[t] = zero4;
+    xs4[t] = zero4;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) D[t][b] = zero4;
+  }
+  u4 avc[4], avn[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) avc[b] = la[b * 17];
+  for (int q0 = 0; q0 < nq; q0 += NQ) {
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      const int q = q0 + s;
+      const int sp = (s + NQ - 1) % NQ;
+      // Refill step, clamped to the last one (a repeated read the cache
+      // serves; never used); the uniform part of the offset goes to the
+      // SGPR offset.
+      const int qr = min(q - 1 + NQ, nq - 1);
+      h8 bq[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) bq[b] = SUB ? unpack_codes_sub(rc[s][b]) : unpack_codes(rc[s][b]);
+      rc[sp] = __builtin_amdgcn_raw_buffer_load_b128(rcs, (int)vc0, qr * 64, 0);
+#pragma unroll
+      for (int t = 0; t < NG; ++t) {
+        {
+          const int tn = t + 1 < NG ? t + 1 : 0;
+          const int qn = t + 1 < NG ? q : min(q + 1, nq - 1);
+#pragma unroll
+          for (int b = 0; b < 4; ++b) avn[b] = la[((tn * nq + qn) * 4 + b) * 17];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float cs = mul_h16<false>(rp[sp][r], as4[t][r], nz);
+          f[t][0] = f[t][0] + D[t][0][r] * cs;
+          f[t][1] = f[t][1] + D[t][1][r] * cs;
+          f[t][2] = f[t][2] + D[t][2][r] * cs;
+          f[t][3] = f[t][3] + D[t][3][r] * cs;
+          zc[t] = zc[t] + mul_h16<true>(rp[sp][r], xs4[t][r], nz);
+        }
+        as4[t] = lsc[(t * nq + q) * 4];
+        xs4[t] = lsu[(t * nq + q) * 4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          D[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[b]), bq[b], zero4, 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) avc[b] = avn[b];
+      }
+      rp[sp] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, qr * 16, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // Epilogue of the last step (slot NQ - 1: nq is a multiple of NQ).
+#pragma unroll
+  for (int t = 0; t < NG; ++t) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float cs = mul_h16<false>(rp[NQ - 1][r], as4[t][r], nz);
+      f[t][0] = f[t][0] + D[t][0][r] * cs;
+      f[t][1] = f[t][1] + D[t][1][r] * cs;
+      f[t][2] = f[t][2] + D[t][2][r] * cs;
+      f[t][3] = f[t][3] + D[t][3][r] * cs;
+      zc[t] = zc[t] + mul_h16<true>(rp[NQ - 1][r], xs4[t][r], nz);
+    }
+  }
+}
+
+// Block of WPB waves = 16 * WPB rows and TGW token groups (blockIdx.y picks
+// the token groups); requires K <= kRpMaxCols and (K / 128) % NQ == 0.
+template <int TGW, int NQ, int WPB>
+__global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
+    float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
+    const _Float16 *__restrict__ qa, const float *__restrict__ scales, const float *__restrict__ sums, int rows,
+    int cols, int m, int ntg) {
+  typedef u32x4 u4;
+  typedef f32x4 f4;
+  constexpr int NT = 64 * WPB;
+  constexpr int MAXQ = kRpMaxCols / 128;
+  constexpr int PA = MAXQ * 64 / NT;
+  static_assert(NT >= MAXQ * 4, "one scale f4 per thread and token group");
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int groups = cols / 32, nq = groups / 4;
+  // LDS: A [TGW][nq][4 blocks][17 slots] u4 (slot 16 zero) | scales, sums
+  // [TGW][nq][4 tokens] f4 (groups 4q..4q+3).
+  u4 *la = reinterpret_cast<u4 *>(smem);
+  f4 *lsc = reinterpret_cast<f4 *>(la + TGW * nq * 68);
+  f4 *lsu = lsc + TGW * nq * 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, h = lane >> 4;
+  const int tg0 = blockIdx.y * TGW;
+  const int row = blockIdx.x * (16 * WPB) + 16 * wave + j;
+  const int rowc = min(row, rows - 1);
+  // Every weight load is in range (steps clamped to the last one): the
+  // lane's row offset in the VGPR offset, the step offset in the SGPR one.
+  const __amdgpu_buffer_rsrc_t rcs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(nib), 0, rows * (cols / 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rps =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(params), 0, rows * groups * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rqa =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(qa), 0, ntg * nq * 1024, 0x00020000);
+  const uint32_t vc0 = (uint32_t)rowc * (cols / 2) + h * 16;
+  const uint32_t vp0 = (uint32_t)rowc * groups * 4;
+
+  // Activations, scales and sums first (fixed counts, clamped duplicates
+  // past the end, all issued before any wait), then the ring.
+  u4 sa[TGW][PA];
+  f4 ssc[TGW], ssu[TGW];
+#pragma unroll
+  for (int tg = 0; tg < TGW; ++tg) {
+    const int tgo = min(tg0 + tg, ntg - 1) * nq * 1024;
+#pragma unroll
+    for (int u = 0; u < PA; ++u) {
+      const int ic = min(tid + NT * u, nq * 64 - 1);
+      sa[tg][u] = __builtin_amdgcn_raw_buffer_load_b128(rqa, ic * 16, tgo, 0);
+    }
+    const int i = min(tid, nq * 4 - 1);
+    const int tok = min(4 * (tg0 + tg) + (i & 3), m - 1);
+    ssc[tg] = reinterpret_cast<const f4 *>(scales + (size_t)tok * groups)[i >> 2];
+    ssu[tg] = reinterpret_cast<const f4 *>(sums + (size_t)tok * groups)[i >> 2];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u4 rc[NQ], rp[NQ];
+  rc[NQ - 1] = rp[NQ - 1] = u4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int s = 0; s < NQ - 1; ++s) {
+    rc[s] = __builtin_amdgcn_raw_buffer_load_b128(rcs, (int)vc0, s * 64, 0);
+    rp[s] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, s * 16, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // Unconditional stores (clamped duplicates write the same values); the
+  // codes enter as f16 subnormals unless some activation scale of a real
+  // token is at least 2^88.
+  int big = 0;
+#pragma unroll
+  for (int tg = 0; tg < TGW; ++tg) {
+#pragma unroll
+    for (int u = 0; u < PA; ++u) {
+      const int ic = min(tid + NT * u, nq * 64 - 1);
+      la[tg * nq * 68 + ic + (ic >> 4)] = sa[tg][u];
+    }
+    const int i = min(tid, nq * 4 - 1);
+    lsu[tg * nq * 4 + i] = ssu[tg];
+    const bool real = tid < nq * 4 && 4 * (tg0 + tg) + (i & 3) < m;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v = fabsf(ssc[tg][e]);
+      big |= (real && v >= 0x1p88f && v < INFINITY) ? 1 : 0;
+    }
+  }
+  for (int i = tid; i < TGW * nq * 4; i += NT) la[i * 17 + 16] = u4{0u, 0u, 0u, 0u};
+  const bool huge = __syncthreads_or(big) != 0;
+  const float sk = huge ? 1.0f : 16777216.0f;
+#pragma unroll
+  for (int tg = 0; tg < TGW; ++tg) lsc[tg * nq * 4 + min(tid, nq * 4 - 1)] = ssc[tg] * sk;
+  __syncthreads();
+  float nz;
+  asm volatile("v_mov_b32 %0, 0x80000000" : "=v"(nz));
+  float f[TGW][4], zc[TGW];
+#pragma unroll
+  for (int t = 0; t < TGW; ++t) {
+    f[t][0] = f[t][1] = f[t][2] = f[t][3] = 0.0f;
+    zc[t] = 0.0f;
+  }
+  const int aslot = (h == (j & 3)) ? j : 16;
+  if (huge) {
+    // Rare; this path fills a ring of its own (the prologue's loads go
+    // unused), which keeps the common path's ring in fixed registers.
+    u4 rch[NQ], rph[NQ];
+    rch[NQ - 1] = rph[NQ - 1] = u4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int s = 0; s < NQ - 1; ++s) {
+      rch[s] = __builtin_amdgcn_raw_buffer_load_b128(rcs, (int)vc0, s * 64, 0);
+      rph[s] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, s * 16, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    gemv_rp_main<TGW, NQ, false>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rch, rph, f, zc);
+  } else {
+    gemv_rp_main<TGW, NQ, true>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rc, rp, f, zc);
+  }
+  if (row < rows) {
+#pragma unroll
+    for (int t = 0; t < TGW; ++t) {
+      const int tok = 4 * (tg0 + t) + h;
+      if (tok < m) {
+        const size_t oi = (size_t)tok * rows + row;
+        const float v = ((f[t][0] + f[t][1]) + (f[t][2] + f[t][3])) + zc[t];
+        out[oi] = add ? add[oi] + v : v;
+      }
+    }
+  }
+}
+
 namespace {
 
 template <int TGW, int P>
@@ -558,6 +793,29 @@ void launch_rs(float *out, const float *add, const uint8_t *nib, const uint8_t *
                      scales, sums, rows, cols, m, ntg);
 }
 
+constexpr int kRpRing = 4;
+
+bool gemv_rp_ok(int rows, int cols) {
+  return cols <= kRpMaxCols && (cols / 128) % kRpRing == 0 && (int64_t)rows * (cols / 2) < ((int64_t)1 << 31);
+}
+
+template <int TGW, int WPB>
+void launch_rp(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
+               const float *scales, const float *sums, int rows, int cols, int m, int ntg, hipStream_t s) {
+  constexpr size_t kStepBytes = 68 * 16 + 2 * 4 * 16;  // A blocks, scales, sums of one (group, step)
+  static bool configured = false;
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_rp<TGW, kRpRing, WPB>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)(TGW * (kRpMaxCols / 128) * kStepBytes));
+    configured = true;
+  }
+  const size_t smem = TGW * (size_t)(cols / 128) * kStepBytes;
+  const dim3 grid((rows + 16 * WPB - 1) / (16 * WPB), (ntg + TGW - 1) / TGW);
+  hipLaunchKernelGGL((k_gemv_rp<TGW, kRpRing, WPB>), grid, dim3(64 * WPB), smem, s, out, add, nib, params, qa,
+                     scales, sums, rows, cols, m, ntg);
+}
+
 }  // namespace
 
 bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
@@ -566,8 +824,19 @@ bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const ui
   if (!qa || !w4a8_mfma_path(rows, cols, m, gs)) return false;
   const int ntg = (m + 3) / 4;
   const int groups = cols / 32;
-  // Kernel and tiling per shape, measured on 4096..32000 x 4096..14336 and
-  // M = 2..16: the register-streamed kernel for many rows (one wave keeps up
+  // Kernel and tiling per shape, measured on 4096..32000 x 2048..14336 and
+  // M = 2..16 with the weights streamed from HBM.  K <= 4096: the
+  // register-pipelined kernel, one token group per block below 6144 rows
+  // (more blocks), otherwise up to three per wave (four tokens groups as
+  // two blocks of two), eight waves per block from 16384 rows.
+  if (gemv_rp_ok(rows, cols)) {
+    if (rows < 6144 || ntg == 1) launch_rp<1, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (ntg == 3 && rows >= 16384) launch_rp<3, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (ntg == 3) launch_rp<3, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else launch_rp<2, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    return true;
+  }
+  // Longer K: the register-streamed kernel for many rows (one wave keeps up
   // to four token groups; past 16384 rows a shallower ring lets two blocks
   // share a CU), the block-staged kernel with one token group per wave for
   // fewer rows.

@@ -76,8 +76,9 @@ __device__ __forceinline__ void quantize_group8_to(const float (&v)[NB], int j, 
     const int col = 8 * c8 + j;
     qs_grp[split_col(col)] = q;
     if (qn_grp) qn_grp[col] = q;
-    // f16 element e of a block is its column (0, 4, 1, 5, 2, 6, 3, 7)[e].
-    if (qa_slot) qa_slot[c8 * 128 + 2 * (j & 3) + (j >> 2)] = (_Float16)r;
+    // f16 element e of a block is its column (0, 4, 1, 5, 2, 6, 3, 7)[e];
+    // odd columns are stored divided by 16 (the codes enter at 16 n).
+    if (qa_slot) qa_slot[c8 * 128 + 2 * (j & 3) + (j >> 2)] = (_Float16)((j & 1) ? r * 0.0625f : r);
   }
   if (j == 0) {
     *scale_out = scale;

@@ -97,6 +97,43 @@ def test_w4a8_matrix_core_huge_activation_scales(rai, ora, rows):
     assert np.array_equal(_bits(got), _bits(want)), rows
 
 
+@pytest.mark.parametrize("rows,cols", [(1000, 2048), (6150, 4096), (14336, 4096), (16389, 4096),
+                                       (6144, 2560)])
+@pytest.mark.parametrize("m", [2, 5, 9, 13, 16])
+def test_w4a8_register_pipelined_path_bit_exact(rai, ora, rows, cols, m):
+    """K <= 4096 with K / 128 a multiple of 4 (the register-pipelined
+    matrix-core kernel): one token group per block below 6144 rows, up to
+    three per wave, eight-wave blocks from 16384 rows, partial row blocks,
+    and a K whose steps fill one ring pass (2560)."""
+    nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + 11 * cols + m)
+    want = ora.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    got = rai.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    assert np.array_equal(_bits(got), _bits(want)), (rows, cols, m)
+
+
+@pytest.mark.parametrize("rows,m", [(1000, 9), (6150, 9), (16389, 9), (14336, 16)])
+def test_w4a8_register_pipelined_huge_scales_and_subnormal_params(rai, ora, rows, m):
+    """The register-pipelined kernel with activation groups past 2^88 (its
+    1024 + n code form) and f16 weight scales / zero points that are
+    subnormal or zero (read straight from the parameter halves)."""
+    cols = 4096
+    nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + m)
+    p = params.copy().view(np.float16).reshape(rows, cols // 32, 2)
+    p[::7, ::3, 0] = np.float16(3e-6)
+    p[::5, 1::4, 1] = np.float16(-2e-6)
+    p[3::11, 2::5, :] = np.float16(0.0)
+    params = p.view(np.uint8).reshape(-1)
+    for scaled in (False, True):
+        xs = x.copy()
+        if scaled:
+            xs[3, 64:96] *= np.float32(1e30)
+            xs[m - 1, 2016:2048] *= np.float32(3e29)
+        want = ora.w4a8_matmul(nib, params, xs, rows, cols, m, 32)
+        got = rai.w4a8_matmul(nib, params, xs, rows, cols, m, 32)
+        assert np.isfinite(want).all()
+        assert np.array_equal(_bits(got), _bits(want)), (rows, m, scaled)
+
+
 @pytest.mark.parametrize("rows,cols,gs", SHAPES[:6])
 def test_lane_sums_bit_exact(rai, ora, rows, cols, gs):
     nib, _, x = gemv_operands(rows, cols, 3, gs, seed=cols)
