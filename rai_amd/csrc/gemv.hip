@@ -515,8 +515,9 @@ size_t gemv_rs_smem(int tgw, int nq_chunk) {
   return (size_t)2 * tgw * nq_chunk * (68 * 16 + 2 * 4 * 16);
 }
 
-// Register-pipelined version for K <= kRpMaxCols.  The block stages all of
-// its activations in LDS once (no barriers in the main loop).  Each wave
+// Register-pipelined version for K up to kRpMaxCols (several token groups
+// per block) or kRpMaxColsOne (one).  The block stages all of its
+// activations in LDS once (no barriers in the main loop).  Each wave
 // streams 16 rows as k_gemv_rs does, through a ring of NQ slots (slot s holds
 // step q = s mod NQ: 16 B of codes of group 4q + h, 16 B of parameters of
 // groups 4q..4q+3), and pipelines by one step: step q unpacks its codes,
@@ -532,7 +533,7 @@ size_t gemv_rs_smem(int tgw, int nq_chunk) {
 // the parameter dword directly.  With subnormal codes the staged activation
 // scales carry the 2^24 (as * 2^24 is exact below 2^104): fl(ws * (as *
 // 2^24)) = fl((ws * 2^24) * as).
-constexpr int kRpMaxCols = 4096;
+constexpr int kRpMaxCols = 4096, kRpMaxColsOne = 14336;
 
 template <bool HI>
 __device__ __forceinline__ float mul_h16(uint32_t w, float x, float nz) {
@@ -623,8 +624,8 @@ __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, c
 }
 
 // Block of WPB waves = 16 * WPB rows and TGW token groups (blockIdx.y picks
-// the token groups); requires K <= kRpMaxCols and (K / 128) % NQ == 0.
-template <int TGW, int NQ, int WPB>
+// the token groups); requires K <= 128 * MAXQ and (K / 128) % NQ == 0.
+template <int TGW, int NQ, int WPB, int MAXQ>
 __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
     float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
     const _Float16 *__restrict__ qa, const float *__restrict__ scales, const float *__restrict__ sums, int rows,
@@ -632,9 +633,9 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
   typedef u32x4 u4;
   typedef f32x4 f4;
   constexpr int NT = 64 * WPB;
-  constexpr int MAXQ = kRpMaxCols / 128;
-  constexpr int PA = MAXQ * 64 / NT;
-  static_assert(NT >= MAXQ * 4, "one scale f4 per thread and token group");
+  constexpr int PA = MAXQ * 64 / NT;             // A u4 per thread and token group
+  constexpr int PS = (MAXQ * 4 + NT - 1) / NT;   // scale / sum f4 per thread and token group
+  static_assert(PA * NT == MAXQ * 64, "whole A loads per thread");
   extern __shared__ __align__(16) unsigned char smem[];
   const int groups = cols / 32, nq = groups / 4;
   // LDS: A [TGW][nq][4 blocks][17 slots] u4 (slot 16 zero) | scales, sums
@@ -661,7 +662,7 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
   // Activations, scales and sums first (fixed counts, clamped duplicates
   // past the end, all issued before any wait), then the ring.
   u4 sa[TGW][PA];
-  f4 ssc[TGW], ssu[TGW];
+  f4 ssc[TGW][PS], ssu[TGW][PS];
 #pragma unroll
   for (int tg = 0; tg < TGW; ++tg) {
     const int tgo = min(tg0 + tg, ntg - 1) * nq * 1024;
@@ -670,10 +671,13 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
       const int ic = min(tid + NT * u, nq * 64 - 1);
       sa[tg][u] = __builtin_amdgcn_raw_buffer_load_b128(rqa, ic * 16, tgo, 0);
     }
-    const int i = min(tid, nq * 4 - 1);
-    const int tok = min(4 * (tg0 + tg) + (i & 3), m - 1);
-    ssc[tg] = reinterpret_cast<const f4 *>(scales + (size_t)tok * groups)[i >> 2];
-    ssu[tg] = reinterpret_cast<const f4 *>(sums + (size_t)tok * groups)[i >> 2];
+#pragma unroll
+    for (int u = 0; u < PS; ++u) {
+      const int i = min(tid + NT * u, nq * 4 - 1);
+      const int tok = min(4 * (tg0 + tg) + (i & 3), m - 1);
+      ssc[tg][u] = reinterpret_cast<const f4 *>(scales + (size_t)tok * groups)[i >> 2];
+      ssu[tg][u] = reinterpret_cast<const f4 *>(sums + (size_t)tok * groups)[i >> 2];
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   u4 rc[NQ], rp[NQ];
@@ -695,20 +699,25 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
       const int ic = min(tid + NT * u, nq * 64 - 1);
       la[tg * nq * 68 + ic + (ic >> 4)] = sa[tg][u];
     }
-    const int i = min(tid, nq * 4 - 1);
-    lsu[tg * nq * 4 + i] = ssu[tg];
-    const bool real = tid < nq * 4 && 4 * (tg0 + tg) + (i & 3) < m;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float v = fabsf(ssc[tg][e]);
-      big |= (real && v >= 0x1p88f && v < INFINITY) ? 1 : 0;
+    for (int u = 0; u < PS; ++u) {
+      const int i = min(tid + NT * u, nq * 4 - 1);
+      lsu[tg * nq * 4 + i] = ssu[tg][u];
+      const bool real = tid + NT * u < nq * 4 && 4 * (tg0 + tg) + (i & 3) < m;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = fabsf(ssc[tg][u][e]);
+        big |= (real && v >= 0x1p88f && v < INFINITY) ? 1 : 0;
+      }
     }
   }
   for (int i = tid; i < TGW * nq * 4; i += NT) la[i * 17 + 16] = u4{0u, 0u, 0u, 0u};
   const bool huge = __syncthreads_or(big) != 0;
   const float sk = huge ? 1.0f : 16777216.0f;
 #pragma unroll
-  for (int tg = 0; tg < TGW; ++tg) lsc[tg * nq * 4 + min(tid, nq * 4 - 1)] = ssc[tg] * sk;
+  for (int tg = 0; tg < TGW; ++tg)
+#pragma unroll
+    for (int u = 0; u < PS; ++u) lsc[tg * nq * 4 + min(tid + NT * u, nq * 4 - 1)] = ssc[tg][u] * sk;
   __syncthreads();
   float nz;
   asm volatile("v_mov_b32 %0, 0x80000000" : "=v"(nz));
@@ -795,25 +804,27 @@ void launch_rs(float *out, const float *add, const uint8_t *nib, const uint8_t *
 
 constexpr int kRpRing = 4;
 
+// K the register-pipelined kernel takes with one token group per block
+// (longer K only that way: the block's activations must fit in LDS).
 bool gemv_rp_ok(int rows, int cols) {
-  return cols <= kRpMaxCols && (cols / 128) % kRpRing == 0 && (int64_t)rows * (cols / 2) < ((int64_t)1 << 31);
+  return cols <= kRpMaxColsOne && (cols / 128) % kRpRing == 0 &&
+         (int64_t)rows * (cols / 2) < ((int64_t)1 << 31);
 }
 
-template <int TGW, int WPB>
+template <int TGW, int WPB, int MAXQ>
 void launch_rp(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                const float *scales, const float *sums, int rows, int cols, int m, int ntg, hipStream_t s) {
   constexpr size_t kStepBytes = 68 * 16 + 2 * 4 * 16;  // A blocks, scales, sums of one (group, step)
   static bool configured = false;
   if (!configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_rp<TGW, kRpRing, WPB>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)(TGW * (kRpMaxCols / 128) * kStepBytes));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_rp<TGW, kRpRing, WPB, MAXQ>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)(TGW * MAXQ * kStepBytes));
     configured = true;
   }
   const size_t smem = TGW * (size_t)(cols / 128) * kStepBytes;
   const dim3 grid((rows + 16 * WPB - 1) / (16 * WPB), (ntg + TGW - 1) / TGW);
-  hipLaunchKernelGGL((k_gemv_rp<TGW, kRpRing, WPB>), grid, dim3(64 * WPB), smem, s, out, add, nib, params, qa,
-                     scales, sums, rows, cols, m, ntg);
+  hipLaunchKernelGGL((k_gemv_rp<TGW, kRpRing, WPB, MAXQ>), grid, dim3(64 * WPB), smem, s, out, add, nib, params,
+                     qa, scales, sums, rows, cols, m, ntg);
 }
 
 }  // namespace
@@ -825,15 +836,23 @@ bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const ui
   const int ntg = (m + 3) / 4;
   const int groups = cols / 32;
   // Kernel and tiling per shape, measured on 4096..32000 x 2048..14336 and
-  // M = 2..16 with the weights streamed from HBM.  K <= 4096: the
-  // register-pipelined kernel, one token group per block below 6144 rows
-  // (more blocks), otherwise up to three per wave (four tokens groups as
-  // two blocks of two), eight waves per block from 16384 rows.
+  // M = 2..16 with the weights streamed from HBM.  The register-pipelined
+  // kernel: for K <= 4096 one token group per block below 6144 rows (more
+  // blocks), otherwise up to three per wave (four token groups as two
+  // blocks of two), eight waves per block from 16384 rows; for longer K
+  // (K / 128 a multiple of 4, at most 14336) one token group per block.
+  constexpr int Q = kRpMaxCols / 128, Q1 = kRpMaxColsOne / 128;
   if (gemv_rp_ok(rows, cols)) {
-    if (rows < 6144 || ntg == 1) launch_rp<1, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (ntg == 3 && rows >= 16384) launch_rp<3, 8>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (ntg == 3) launch_rp<3, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else launch_rp<2, 4>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    if (cols > kRpMaxCols)
+      launch_rp<1, 4, Q1>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (rows < 6144 || ntg == 1)
+      launch_rp<1, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (ntg == 3 && rows >= 16384)
+      launch_rp<3, 8, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else if (ntg == 3)
+      launch_rp<3, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    else
+      launch_rp<2, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
     return true;
   }
   // Longer K: the register-streamed kernel for many rows (one wave keeps up

@@ -98,25 +98,27 @@ def test_w4a8_matrix_core_huge_activation_scales(rai, ora, rows):
 
 
 @pytest.mark.parametrize("rows,cols", [(1000, 2048), (6150, 4096), (14336, 4096), (16389, 4096),
-                                       (6144, 2560)])
+                                       (6144, 2560), (4096, 14336), (777, 8704)])
 @pytest.mark.parametrize("m", [2, 5, 9, 13, 16])
 def test_w4a8_register_pipelined_path_bit_exact(rai, ora, rows, cols, m):
-    """K <= 4096 with K / 128 a multiple of 4 (the register-pipelined
+    """K / 128 a multiple of 4, K <= 14336 (the register-pipelined
     matrix-core kernel): one token group per block below 6144 rows, up to
     three per wave, eight-wave blocks from 16384 rows, partial row blocks,
-    and a K whose steps fill one ring pass (2560)."""
+    a K whose steps fill one ring pass (2560), and K past 4096 (one token
+    group per block, activations of up to 14336 columns in LDS)."""
     nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + 11 * cols + m)
     want = ora.w4a8_matmul(nib, params, x, rows, cols, m, 32)
     got = rai.w4a8_matmul(nib, params, x, rows, cols, m, 32)
     assert np.array_equal(_bits(got), _bits(want)), (rows, cols, m)
 
 
-@pytest.mark.parametrize("rows,m", [(1000, 9), (6150, 9), (16389, 9), (14336, 16)])
-def test_w4a8_register_pipelined_huge_scales_and_subnormal_params(rai, ora, rows, m):
+@pytest.mark.parametrize("rows,cols,m", [(1000, 4096, 9), (6150, 4096, 9), (16389, 4096, 9),
+                                         (14336, 4096, 16), (700, 14336, 9)])
+def test_w4a8_register_pipelined_huge_scales_and_subnormal_params(rai, ora, rows, cols, m):
     """The register-pipelined kernel with activation groups past 2^88 (its
     1024 + n code form) and f16 weight scales / zero points that are
-    subnormal or zero (read straight from the parameter halves)."""
-    cols = 4096
+    subnormal or zero (read straight from the parameter halves), at K = 4096
+    and at the longest K (one token group per block)."""
     nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + m)
     p = params.copy().view(np.float16).reshape(rows, cols // 32, 2)
     p[::7, ::3, 0] = np.float16(3e-6)
