@@ -460,50 +460,51 @@ static int softmax_r_stride(int nmax) { return (((nmax + 7) / 8 + 63) & ~63) + 4
 
 // PV with the V stream spread over loader waves.  The V cache is d-major
 // ([kv head][head dim][vstride] floats, vstride a multiple of 64), so the
-// positions of one dim in a chunk are contiguous.  One block per (token, kv
-// head, slice of DL head dims) with NCW compute waves and 8 - NCW loader
-// waves.  Compute lane L = 64w + lane owns the chain of query head
-// kvh*G + L/DL, dim d0 + L%DL, so the G heads of the kv group share every V
-// value.  Loader i fetches chunks i, i + NL, ... (CP positions: the V tile
-// [DL][CP] and the G probability rows) with 16-byte coalesced loads, so NL
-// chunks are in flight while the compute waves work.  Each iteration the
-// owner of the next chunk stores it into the free half of a double-buffered
-// LDS tile (probabilities of positions >= n stored as 0: fma(0, v, acc) ==
-// acc for the finite cached v, and acc is never -0), and the compute waves
-// run the reference's sequential FMA chain over the current chunk, reading
-// 4 positions' V values and (wave-broadcast) probabilities per 16-byte LDS
-// read, 32 positions ahead of the chain.  One barrier per chunk.
-template <int DL, int G, int CP>
+// positions of one dim in a chunk are contiguous.  One block per (kv head,
+// slice of DL head dims, TM tokens) with NCW compute waves and NL loader
+// waves.  Compute lane L = 64w + lane owns the chain of token L / (G*DL),
+// query head kvh*G + (L / DL) % G, dim d0 + L % DL, so the G heads of the kv
+// group and the TM tokens share every V value.  Loader i fetches chunks
+// i, i + NL, ... (CP positions: the V tile [DL][CP] and the TM*G
+// probability rows) with 16-byte coalesced loads, so NL chunks are in flight
+// while the compute waves work.  Each iteration the owner of the next chunk
+// stores it into the free half of a double-buffered LDS tile (probabilities
+// of positions past the row's token, and rows of tokens past m, stored as
+// 0: fma(0, v, acc) == acc for the finite cached v, and acc is never -0),
+// and the compute waves run the reference's sequential FMA chain over the
+// current chunk, reading 4 positions' V values and (wave-broadcast)
+// probabilities per 16-byte LDS read, 32 positions ahead of the chain.  The
+// chunks run to the block's longest token; one barrier per chunk.
+template <int DL, int G, int CP, int TM, int NL>
 struct PvCfg {
-  static constexpr int NCW = G * DL / 64;       // compute waves
-  static constexpr int NL = 8 - NCW;            // loader waves
-  static constexpr int NV = DL * CP / 256;      // V float4 per loader lane per chunk
-  static constexpr int NP = (G * CP / 4 + 63) / 64;  // P float4 per loader lane per chunk
-  static constexpr int STR = CP + 4;            // LDS row stride (floats)
+  static constexpr int NCW = TM * G * DL / 64;       // compute waves
+  static constexpr int NT = 64 * (NCW + NL);         // threads
+  static constexpr int NV = DL * CP / 256;           // V float4 per loader lane per chunk
+  static constexpr int NP = (TM * G * CP / 4 + 63) / 64;  // P float4 per loader lane per chunk
+  static constexpr int STR = CP + 4;                 // LDS row stride (floats)
+  static_assert(TM * G * DL % 64 == 0, "whole compute waves");
 };
 
-template <int DL, int G, int CP>
-__global__ __launch_bounds__(512) void k_pv_stream(const float *__restrict__ P,
-                                                    const float *__restrict__ vt_g, int vstride,
-                                                    int pos0, int nh, int hd, int sstride,
-                                                    float *__restrict__ out,
-                                                    const int *__restrict__ st) {
-  using C = PvCfg<DL, G, CP>;
+template <int DL, int G, int CP, int TM, int NL>
+__global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_stream(
+    const float *__restrict__ P, const float *__restrict__ vt_g, int vstride, int pos0, int m, int nh, int hd,
+    int sstride, float *__restrict__ out, const int *__restrict__ st) {
+  using C = PvCfg<DL, G, CP, TM, NL>;
   if (st) pos0 = st[0];
-  constexpr int NCW = C::NCW, NL = C::NL, NV = C::NV, NP = C::NP, STR = C::STR;
+  constexpr int NCW = C::NCW, NV = C::NV, NP = C::NP, STR = C::STR;
   constexpr int Q4 = CP / 4;  // float4 per tile row
   __shared__ __align__(16) float vt[2][DL * STR];
-  __shared__ __align__(16) float pt[2][G * STR];
+  __shared__ __align__(16) float pt[2][TM * G * STR];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slices = hd / DL;
   const int kvh = blockIdx.x / slices;
   const int d0 = (blockIdx.x - kvh * slices) * DL;
-  const int t = blockIdx.y;
-  const int n = pos0 + t + 1;
-  const int nchunks = (n + CP - 1) / CP;
+  const int t0 = blockIdx.y * TM;
+  const int tn = min(TM, m - t0);              // tokens of this block
+  const int nmax = pos0 + t0 + tn;             // positions of its longest token
+  const int nchunks = (nmax + CP - 1) / CP;
   const float *vbase = vt_g + ((size_t)kvh * hd + d0) * vstride;
-  const float *pbase = P + ((size_t)t * nh + (size_t)kvh * G) * sstride;
 
   typedef float f4 __attribute__((ext_vector_type(4)));
   f4 fv[NV], fp[NP];
@@ -513,13 +514,14 @@ __global__ __launch_bounds__(512) void k_pv_stream(const float *__restrict__ P,
     _Pragma("unroll") for (int u = 0; u < NV; ++u) {                                            \
       const int f = 64 * u + lane; /* float4 index in the [DL][CP] tile */                      \
       const int q0 = min(s0_ + 4 * (f % Q4), vstride - 4);                                      \
-      fv[u] = *reinterpret_cast<const f4 *>(vbase + (size_t)(f / Q4) * vstride + q0);      \
+      fv[u] = *reinterpret_cast<const f4 *>(vbase + (size_t)(f / Q4) * vstride + q0);           \
     }                                                                                           \
     _Pragma("unroll") for (int r = 0; r < NP; ++r) {                                            \
-      const int f = 64 * r + lane; /* float4 index in the [G][CP] tile */                       \
-      const int gg = min(f / Q4, G - 1);                                                        \
+      const int f = 64 * r + lane; /* float4 index in the [TM*G][CP] tile */                    \
+      const int rr = min(f / Q4, TM * G - 1), tl = min(rr / G, tn - 1);                         \
       const int q0 = min(s0_ + 4 * (f % Q4), sstride - 4);                                      \
-      fp[r] = *reinterpret_cast<const f4 *>(pbase + (size_t)gg * sstride + q0);            \
+      fp[r] = *reinterpret_cast<const f4 *>(                                                    \
+          P + ((size_t)(t0 + tl) * nh + (size_t)kvh * G + rr % G) * sstride + q0);              \
     }                                                                                           \
   } while (0)
 #define RAI_PV_PUBLISH(k_)                                                                      \
@@ -527,18 +529,19 @@ __global__ __launch_bounds__(512) void k_pv_stream(const float *__restrict__ P,
     const int s0_ = (k_) * CP, b_ = (k_) & 1;                                                   \
     _Pragma("unroll") for (int u = 0; u < NV; ++u) {                                            \
       const int f = 64 * u + lane;                                                              \
-      *reinterpret_cast<f4 *>(&vt[b_][(f / Q4) * STR + 4 * (f % Q4)]) = fv[u];              \
+      *reinterpret_cast<f4 *>(&vt[b_][(f / Q4) * STR + 4 * (f % Q4)]) = fv[u];                  \
     }                                                                                           \
     _Pragma("unroll") for (int r = 0; r < NP; ++r) {                                            \
       const int f = 64 * r + lane;                                                              \
-      if (f < G * Q4) {                                                                         \
-        const int q = 4 * (f % Q4);                                                             \
-        f4 v = fp[r];                                                                       \
-        if (s0_ + q + 0 >= n) v.x = 0.0f;                                                       \
-        if (s0_ + q + 1 >= n) v.y = 0.0f;                                                       \
-        if (s0_ + q + 2 >= n) v.z = 0.0f;                                                       \
-        if (s0_ + q + 3 >= n) v.w = 0.0f;                                                       \
-        *reinterpret_cast<f4 *>(&pt[b_][(f / Q4) * STR + q]) = v;                           \
+      if (f < TM * G * Q4) {                                                                    \
+        const int q = 4 * (f % Q4), rr = f / Q4, tl = rr / G;                                   \
+        const int n_ = tl < tn ? pos0 + t0 + tl + 1 : 0;                                        \
+        f4 v = fp[r];                                                                           \
+        if (s0_ + q + 0 >= n_) v.x = 0.0f;                                                      \
+        if (s0_ + q + 1 >= n_) v.y = 0.0f;                                                      \
+        if (s0_ + q + 2 >= n_) v.z = 0.0f;                                                      \
+        if (s0_ + q + 3 >= n_) v.w = 0.0f;                                                      \
+        *reinterpret_cast<f4 *>(&pt[b_][rr * STR + q]) = v;                                     \
       }                                                                                         \
     }                                                                                           \
   } while (0)
@@ -553,16 +556,16 @@ __global__ __launch_bounds__(512) void k_pv_stream(const float *__restrict__ P,
   }
   __syncthreads();
   const int L = wave * 64 + lane;
-  const int g = L / DL, dd = L - g * DL;
+  const int tl = L / (G * DL), g = (L / DL) % G, dd = L % DL;
   float acc = 0.0f;
   for (int k = 0; k < nchunks; ++k) {
     if (wave < NCW) {
       const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
-      const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][g * STR]);
+      const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][(tl * G + g) * STR]);
       // Rolling prefetch: the next 8 float4 pairs (32 positions) are
       // requested before the 32 FMAs of the current ones, so the LDS
       // latency is exposed once per chunk instead of once per 32 positions.
-      constexpr int PB = NV + NP <= 24 ? 8 : 4;  // fewer with many loader registers (G = 16)
+      constexpr int PB = NV + NP <= 28 ? 8 : 4;  // fewer with many loader registers
       static_assert(Q4 % PB == 0, "whole prefetch blocks per chunk");
       float4 cv[PB], cp[PB];
 #pragma unroll
@@ -601,9 +604,17 @@ __global__ __launch_bounds__(512) void k_pv_stream(const float *__restrict__ P,
     }
     __syncthreads();
   }
-  if (wave < NCW) out[((size_t)t * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc;
+  if (wave < NCW && tl < tn) out[((size_t)(t0 + tl) * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc;
 #undef RAI_PV_ISSUE
 #undef RAI_PV_PUBLISH
+}
+
+template <int DL, int G, int CP, int TM, int NL>
+void launch_pv_stream(const float *scores, const float *vc, int vstride, int p0, int m, int nh, int nkv, int hd,
+                      int sstride, float *out, const int *st, hipStream_t s) {
+  const dim3 pg(nkv * (hd / DL), (m + TM - 1) / TM);
+  hipLaunchKernelGGL((k_pv_stream<DL, G, CP, TM, NL>), pg, dim3(PvCfg<DL, G, CP, TM, NL>::NT), 0, s, scores, vc,
+                     vstride, p0, m, nh, hd, sstride, out, st);
 }
 
 // PV for any head_dim: thread per output element, same chain order.  V
@@ -769,17 +780,22 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     const bool stream = vstride > 0 && vstride % 64 == 0 &&
                         (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && hd % DL == 0;
     if (stream) {
-      const dim3 pg(nkv * (hd / DL), mt);
-      if (G == 4)
-        hipLaunchKernelGGL((k_pv_stream<16, 4, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
+      // Tokens per block: one for one or two tokens (more blocks), three up
+      // to twelve (the verify batch), four beyond.
+      if (G == 4 && mt > 12)
+        launch_pv_stream<16, 4, 128, 4, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+      else if (G == 4 && mt > 2)
+        launch_pv_stream<16, 4, 256, 3, 5>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+      else if (G == 4)
+        launch_pv_stream<16, 4, 256, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 8)
-        hipLaunchKernelGGL((k_pv_stream<16, 8, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
+        launch_pv_stream<16, 8, 256, 1, 6>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 16)
-        hipLaunchKernelGGL((k_pv_stream<16, 16, 256>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
+        launch_pv_stream<16, 16, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 2)
-        hipLaunchKernelGGL((k_pv_stream<32, 2, 128>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
+        launch_pv_stream<32, 2, 128, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else
-        hipLaunchKernelGGL((k_pv_stream<64, 1, 64>), pg, dim3(512), 0, s, scores, vc, vstride, p0, nh, hd, sstride, ot, st);
+        launch_pv_stream<64, 1, 64, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
     } else if (vstride > 0) {
       hipLaunchKernelGGL(k_pv_any<true>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, scores,
                          vc, cap, vstride, p0, mt, nh, nkv, hd, sstride, ot, st);
