@@ -198,19 +198,25 @@ __global__ __launch_bounds__(256) void k_quant(const float *__restrict__ x, int 
 constexpr int kScoreTile = 64;  // positions per score block (one per lane)
 
 // grid (ceil(nmax / 64), nkv), 256 threads.  The block stages its 64 key
-// rows in LDS (row stride hd + 1: lanes reading the same column of
-// consecutive rows hit distinct banks); each wave takes (token, head) pairs
-// of the kv group, lane = position.  HD > 0: compile-time head_dim.
-template <int HD>
+// rows in LDS; each wave takes (token, head) pairs of the kv group, lane =
+// position.  HD > 0 (compile-time head_dim): key rows HD + 4 floats apart
+// (16-byte reads, conflict-free per 16 lanes), followed by the query rows of
+// the block's pairs (pair pi = (t - tfirst) * G + g at row pi, read by
+// broadcast); a wave runs PB of its pairs at once, head-dim chunk outer, so
+// each key value read serves PB dot products (pairs past the end repeat the
+// last one and store nothing).  HD = 0: rows hd + 1 floats apart, queries
+// from global memory, one pair at a time.  With a step record the token
+// positions start at st[0] + toff.
+template <int HD, int PB>
 __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int q_ld,
                                                 const float *__restrict__ kc, int cap, int pos0,
                                                 int m, int nh, int nkv, int hd_rt, float scale,
                                                 float *__restrict__ S, int sstride,
-                                                const int *__restrict__ st) {
+                                                const int *__restrict__ st, int toff) {
   extern __shared__ float ks[];
-  if (st) pos0 = st[0];
+  if (st) pos0 = st[0] + toff;
   const int hd = HD > 0 ? HD : hd_rt;
-  const int kstride = hd + 1;
+  const int kstride = HD > 0 ? HD + 4 : hd + 1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int s0 = (int)blockIdx.x * kScoreTile;
@@ -220,25 +226,71 @@ __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int
   if (s0 >= nmax) return;  // capacity-sized grids (step record) end early
   const int rows = min(kScoreTile, nmax - s0);
   const float *kb = kc + ((size_t)kvh * cap + s0) * hd;
+  // Token t sees positions <= pos0 + t.
+  const int tfirst = s0 > pos0 ? s0 - pos0 : 0;
+  const int pairs = G * (m - tfirst);
+  typedef float f4 __attribute__((ext_vector_type(4)));
   if constexpr (HD > 0) {
-    // All of the thread's loads are issued before the first LDS store.
+    // All of the thread's key loads are issued before the first LDS store.
     constexpr int NPT = kScoreTile * (HD / 4) / 256;
-    float4 v4[NPT];
+    f4 v4[NPT];
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
       const int i = threadIdx.x + 256 * u;
       const int r = min(i / (HD / 4), rows - 1), c4 = i % (HD / 4);
-      v4[u] = reinterpret_cast<const float4 *>(kb + (size_t)r * HD)[c4];
+      v4[u] = reinterpret_cast<const f4 *>(kb + (size_t)r * HD)[c4];
+    }
+    f4 *lq = reinterpret_cast<f4 *>(ks + kScoreTile * kstride);
+    for (int i = threadIdx.x; i < pairs * (HD / 4); i += 256) {
+      const int pi = i / (HD / 4), c4 = i % (HD / 4);
+      const int t = tfirst + pi / G, h = kvh * G + pi % G;
+      lq[i] = reinterpret_cast<const f4 *>(q + (size_t)t * q_ld + (size_t)h * HD)[c4];
     }
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
       const int i = threadIdx.x + 256 * u;
       const int r = i / (HD / 4), c4 = i % (HD / 4);
-      float *d = ks + r * kstride + 4 * c4;
-      d[0] = v4[u].x;
-      d[1] = v4[u].y;
-      d[2] = v4[u].z;
-      d[3] = v4[u].w;
+      *reinterpret_cast<f4 *>(ks + r * kstride + 4 * c4) = v4[u];
+    }
+    __syncthreads();
+    const int s = s0 + lane;
+    const f4 *kr4 = reinterpret_cast<const f4 *>(ks + lane * kstride);
+    const int npw = (pairs - wave + 3) / 4;  // this wave's pairs: wave, wave + 4, ...
+    for (int b0 = 0; b0 < npw; b0 += PB) {
+      const f4 *ql[PB];
+#pragma unroll
+      for (int p = 0; p < PB; ++p) ql[p] = lq + (wave + 4 * min(b0 + p, npw - 1)) * (HD / 4);
+      float a[PB][8];
+#pragma unroll
+      for (int p = 0; p < PB; ++p)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[p][i] = 0.0f;
+#pragma unroll 4
+      for (int c = 0; c < HD / 8; ++c) {
+        const f4 k0 = kr4[2 * c], k1 = kr4[2 * c + 1];
+#pragma unroll
+        for (int p = 0; p < PB; ++p) {
+          const f4 q0 = ql[p][2 * c];
+          const f4 q1 = ql[p][2 * c + 1];
+          a[p][0] = __fmaf_rn(q0.x, k0.x, a[p][0]);
+          a[p][1] = __fmaf_rn(q0.y, k0.y, a[p][1]);
+          a[p][2] = __fmaf_rn(q0.z, k0.z, a[p][2]);
+          a[p][3] = __fmaf_rn(q0.w, k0.w, a[p][3]);
+          a[p][4] = __fmaf_rn(q1.x, k1.x, a[p][4]);
+          a[p][5] = __fmaf_rn(q1.y, k1.y, a[p][5]);
+          a[p][6] = __fmaf_rn(q1.z, k1.z, a[p][6]);
+          a[p][7] = __fmaf_rn(q1.w, k1.w, a[p][7]);
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < PB; ++p) {
+        const int pi = wave + 4 * (b0 + p);
+        const int t = tfirst + pi / G, h = kvh * G + pi % G;
+        if (b0 + p < npw && lane < rows && s <= pos0 + t) {
+          const float d = ((a[p][0] + a[p][4]) + (a[p][1] + a[p][5])) + ((a[p][2] + a[p][6]) + (a[p][3] + a[p][7]));
+          S[((size_t)t * nh + h) * sstride + s] = d * scale;
+        }
+      }
     }
   } else {
     for (int i = threadIdx.x; i < rows * (hd / 4); i += 256) {
@@ -250,39 +302,101 @@ __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int
       d[2] = v4.z;
       d[3] = v4.w;
     }
-  }
-  __syncthreads();
-  const int s = s0 + lane;
-  const float *kr = ks + lane * kstride;
-  // Token t sees positions <= pos0 + t.
-  const int tfirst = s0 > pos0 ? s0 - pos0 : 0;
-  const int pairs = G * (m - tfirst);
-  for (int pi = wave; pi < pairs; pi += 4) {
-    const int t = tfirst + pi / G;
-    const int h = kvh * G + pi % G;
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    const auto *qh = vector_ptr(reinterpret_cast<const f4 *>(q + (size_t)t * q_ld + (size_t)h * hd));
-    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (lane < rows) {
-      for (int c = 0; c < hd / 8; ++c) {
-        const f4 q0 = qh[2 * c];
-        const f4 q1 = qh[2 * c + 1];
-        const float *k8 = kr + 8 * c;
-        a[0] = __fmaf_rn(q0.x, k8[0], a[0]);
-        a[1] = __fmaf_rn(q0.y, k8[1], a[1]);
-        a[2] = __fmaf_rn(q0.z, k8[2], a[2]);
-        a[3] = __fmaf_rn(q0.w, k8[3], a[3]);
-        a[4] = __fmaf_rn(q1.x, k8[4], a[4]);
-        a[5] = __fmaf_rn(q1.y, k8[5], a[5]);
-        a[6] = __fmaf_rn(q1.z, k8[6], a[6]);
-        a[7] = __fmaf_rn(q1.w, k8[7], a[7]);
+    __syncthreads();
+    const int s = s0 + lane;
+    const float *kr = ks + lane * kstride;
+    for (int pi = wave; pi < pairs; pi += 4) {
+      const int t = tfirst + pi / G;
+      const int h = kvh * G + pi % G;
+      const auto *qh = vector_ptr(reinterpret_cast<const f4 *>(q + (size_t)t * q_ld + (size_t)h * hd));
+      float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (lane < rows) {
+        for (int c = 0; c < hd / 8; ++c) {
+          const f4 q0 = qh[2 * c];
+          const f4 q1 = qh[2 * c + 1];
+          const float *k8 = kr + 8 * c;
+          a[0] = __fmaf_rn(q0.x, k8[0], a[0]);
+          a[1] = __fmaf_rn(q0.y, k8[1], a[1]);
+          a[2] = __fmaf_rn(q0.z, k8[2], a[2]);
+          a[3] = __fmaf_rn(q0.w, k8[3], a[3]);
+          a[4] = __fmaf_rn(q1.x, k8[4], a[4]);
+          a[5] = __fmaf_rn(q1.y, k8[5], a[5]);
+          a[6] = __fmaf_rn(q1.z, k8[6], a[6]);
+          a[7] = __fmaf_rn(q1.w, k8[7], a[7]);
+        }
+      }
+      if (lane < rows && s <= pos0 + t) {
+        const float d = ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]));
+        S[((size_t)t * nh + h) * sstride + s] = d * scale;
       }
     }
-    if (lane < rows && s <= pos0 + t) {
-      const float d = ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]));
-      S[((size_t)t * nh + h) * sstride + s] = d * scale;
-    }
   }
+}
+
+template <int HD, int PB>
+void launch_scores_t(dim3 sg, size_t ksm, hipStream_t s, const float *q, int q_ld, const float *kc, int cap, int p0,
+                     int m, int nh, int nkv, float scale, float *scores, int sstride, const int *st, int toff) {
+  static bool configured = false;
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_scores<HD, PB>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)(sizeof(float) * ((size_t)kScoreTile * (HD + 4) + 16384)));
+    configured = true;
+  }
+  hipLaunchKernelGGL((k_scores<HD, PB>), sg, dim3(256), ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, HD, scale, scores,
+                     sstride, st, toff);
+}
+
+template <int HD>
+void launch_scores_hd(dim3 sg, size_t ksm, int npw, hipStream_t s, const float *q, int q_ld, const float *kc, int cap,
+                      int p0, int m, int nh, int nkv, float scale, float *scores, int sstride, const int *st,
+                      int toff) {
+  // Pairs per wave at once: all of them up to three, nine for the verify
+  // batch, else four at a time.
+  if (npw <= 1)
+    launch_scores_t<HD, 1>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+  else if (npw == 2)
+    launch_scores_t<HD, 2>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+  else if (npw == 3)
+    launch_scores_t<HD, 3>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+  else if (npw <= 4 || npw > 9)
+    launch_scores_t<HD, 4>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+  else
+    launch_scores_t<HD, 9>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+}
+
+// Score launches for tokens [0, m): the compile-time head dims in sub-batches
+// whose query rows fit next to the keys in LDS (at most 64 KB of them).
+void launch_scores(const float *q, int q_ld, const float *kc, int cap, int p0, int m, int nh, int nkv, int hd,
+                   float scale, float *scores, int sstride, int nmax, const int *st, hipStream_t s) {
+  static size_t sc_configured = 0;
+  const int G = nh / nkv;
+  if (hd == 128 || hd == 64) {
+    const int mb = std::max(1, std::min(16, 16384 / (G * hd)));
+    for (int u0 = 0; u0 < m; u0 += mb) {
+      const int mm = std::min(mb, m - u0);
+      const int nmax_u = st ? nmax : p0 + u0 + mm;
+      const dim3 sg((nmax_u + kScoreTile - 1) / kScoreTile, nkv);
+      const size_t ksm = sizeof(float) * ((size_t)kScoreTile * (hd + 4) + (size_t)G * mm * hd);
+      const int npw = (G * mm + 3) / 4;
+      if (hd == 128)
+        launch_scores_hd<128>(sg, ksm, npw, s, q + (size_t)u0 * q_ld, q_ld, kc, cap, p0 + u0, mm, nh, nkv, scale,
+                              scores + (size_t)u0 * nh * sstride, sstride, st, u0);
+      else
+        launch_scores_hd<64>(sg, ksm, npw, s, q + (size_t)u0 * q_ld, q_ld, kc, cap, p0 + u0, mm, nh, nkv, scale,
+                             scores + (size_t)u0 * nh * sstride, sstride, st, u0);
+    }
+    return;
+  }
+  const dim3 sg((nmax + kScoreTile - 1) / kScoreTile, nkv);
+  const size_t ksm = sizeof(float) * (size_t)kScoreTile * (hd + 1);
+  if (ksm > 48 * 1024 && ksm > sc_configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_scores<0, 1>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)ksm);
+    sc_configured = ksm;
+  }
+  hipLaunchKernelGGL((k_scores<0, 1>), sg, dim3(256), ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, hd, scale, scores,
+                     sstride, st, 0);
 }
 
 __device__ __forceinline__ float block_max256(float v, float *red) {
@@ -728,7 +842,7 @@ size_t attention_scores_floats(int m, int nh, int ctx) {
 void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
                       int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
                       float *out, float *scores, hipStream_t s, const int *st) {
-  static size_t sm_configured = 0, sc_configured = 0;
+  static size_t sm_configured = 0;
   for (int t0 = 0; t0 < m; t0 += kAttnTokens) {
     const int mt = std::min(kAttnTokens, m - t0);
     const int p0 = pos0 + t0;
@@ -737,22 +851,7 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     const int sstride = (nmax + 3) & ~3;
     const float *qt = q + (size_t)t0 * q_ld;
     float *ot = out + (size_t)t0 * nh * hd;
-    const dim3 sg((nmax + kScoreTile - 1) / kScoreTile, nkv);
-    const size_t ksm = sizeof(float) * (size_t)kScoreTile * (hd + 1);
-    if (ksm > 48 * 1024 && ksm > sc_configured) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_scores<0>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)ksm);
-      sc_configured = ksm;
-    }
-    if (hd == 128)
-      hipLaunchKernelGGL(k_scores<128>, sg, dim3(256), ksm, s, qt, q_ld, kc, cap, p0, mt, nh, nkv, hd,
-                         scale, scores, sstride, st);
-    else if (hd == 64)
-      hipLaunchKernelGGL(k_scores<64>, sg, dim3(256), ksm, s, qt, q_ld, kc, cap, p0, mt, nh, nkv, hd,
-                         scale, scores, sstride, st);
-    else
-      hipLaunchKernelGGL(k_scores<0>, sg, dim3(256), ksm, s, qt, q_ld, kc, cap, p0, mt, nh, nkv, hd,
-                         scale, scores, sstride, st);
+    launch_scores(qt, q_ld, kc, cap, p0, mt, nh, nkv, hd, scale, scores, sstride, nmax, st, s);
     const size_t smem = sizeof(float) * (size_t)nmax;
     if (smem > 48 * 1024 && smem > sm_configured) {
       (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_softmax),
