@@ -766,10 +766,39 @@ __global__ __launch_bounds__(64) void k_pv_any(const float *__restrict__ P,
   out[(size_t)row * hd + d] = acc;
 }
 
+// Group 32, rows of at most 32 * P groups: the row and the norm weights in
+// registers, the sum of squares over a chain-major LDS copy (one block per
+// token).
+template <int P>
+__global__ __launch_bounds__(256) void k_norm_quant_r(const float *__restrict__ x, const float *__restrict__ w,
+                                                      float *__restrict__ normed, int8_t *__restrict__ q_split,
+                                                      int8_t *__restrict__ q_nat, float *__restrict__ scales,
+                                                      float *__restrict__ sums, int n, float eps, _Float16 *qa) {
+  extern __shared__ __align__(16) float xsr[];
+  const int t = blockIdx.x, groups = n / 32;
+  float xr[P][4], wr[P][4];
+  rmsnorm_regs_load<32, P>(x + (size_t)t * n, w, n, xr, wr);
+  rmsnorm_quant_regs<32, P>(xr, wr, n, eps, xsr, q_split + (size_t)t * n, 32, scales + (size_t)t * groups,
+                            sums + (size_t)t * groups, q_nat ? q_nat + (size_t)t * n : nullptr,
+                            normed ? normed + (size_t)t * n : nullptr, qa, t);
+}
+
 template <int GS>
 void launch_norm_quant_t(const float *x, const float *w, float *normed, int m, int n, float eps,
                          int8_t *q_split, int8_t *q_nat, float *scales, float *sums,
                          hipStream_t s, _Float16 *qa = nullptr) {
+  if (GS == 32 && n <= 32 * 32 * 4) {
+    const size_t smem = sizeof(float) * (size_t)rms_scratch_floats(n);
+    const int groups = n / 32;
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(m), dim3(256), smem, s, x, w, normed, q_split, q_nat, scales, sums, n, eps, qa);
+    };
+    if (groups <= 32) go(k_norm_quant_r<1>);
+    else if (groups <= 64) go(k_norm_quant_r<2>);
+    else if (groups <= 96) go(k_norm_quant_r<3>);
+    else go(k_norm_quant_r<4>);
+    return;
+  }
   const size_t smem = (GS > 0 ? 1 : 2) * sizeof(float) * (size_t)n;
   static size_t configured = 0;
   if (smem > 48 * 1024 && smem > configured) {

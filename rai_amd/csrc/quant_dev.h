@@ -282,11 +282,15 @@ __device__ __forceinline__ float rmsnorm_inv_t(const float *xt, int n, float eps
 
 // rms_norm_avx2 + quantization of a row held in rmsnorm_regs_load's slots
 // (x and the norm weights) by a 256-thread block; xs: LDS scratch of
-// rms_scratch_floats(n) floats, 16-byte aligned.
+// rms_scratch_floats(n) floats, 16-byte aligned.  Optional outputs: the
+// natural-order codes qn, the normalised row nrow and the matrix-core slots
+// of token `token` in qa (group 32).
 template <int GS, int P>
 __device__ __forceinline__ void rmsnorm_quant_regs(const float (&xr)[P][GS / 8], const float (&wr)[P][GS / 8],
                                                    int n, float eps, float *xs, int8_t *qs, int qstr,
-                                                   float *scale_out, float *sum_out) {
+                                                   float *scale_out, float *sum_out, int8_t *qn = nullptr,
+                                                   float *nrow = nullptr, _Float16 *qa = nullptr,
+                                                   int token = 0) {
   const int tid = threadIdx.x, groups = n / GS, j = tid & 7;
   constexpr int NB = GS / 8;
   const int stride = rms_t_stride(n);
@@ -309,9 +313,13 @@ __device__ __forceinline__ void rmsnorm_quant_regs(const float (&xr)[P][GS / 8],
     const bool ok = g < groups;
     float v[NB];
 #pragma unroll
-    for (int c = 0; c < NB; ++c) v[c] = ok ? (xr[p][c] * inv) * wr[p][c] : 0.0f;
-    quantize_group8_to<NB>(v, j, ok, qs + (size_t)(ok ? g : 0) * qstr, nullptr, scale_out + (ok ? g : 0),
-                           sum_out + (ok ? g : 0));
+    for (int c = 0; c < NB; ++c) {
+      v[c] = ok ? (xr[p][c] * inv) * wr[p][c] : 0.0f;
+      if (ok && nrow) nrow[g * GS + 8 * c + j] = v[c];
+    }
+    quantize_group8_to<NB>(v, j, ok, qs + (size_t)(ok ? g : 0) * qstr, qn ? qn + (ok ? g : 0) * GS : nullptr,
+                           scale_out + (ok ? g : 0), sum_out + (ok ? g : 0),
+                           qa ? qa4_slot(qa, token, ok ? g : 0, groups) : nullptr);
   }
 }
 
