@@ -16,8 +16,10 @@
 // buffer, which a raw buffer load answers with zeros without touching
 // memory), so the compiler's wait counts stay exact and D chunks stay in
 // flight across tile boundaries.  The lane products go through a
-// wave-private LDS area and come back transposed: lane c = l * R + r runs
-// chain l of row r over the chunk's 32 products in group order.  No block
+// wave-private LDS area (two buffers) and come back transposed: lane
+// c = l * R + r runs chain l of row r over the chunk's 32 products in group
+// order, one chunk behind the products, so the chain's dependent adds
+// interleave with the next chunk's product instructions.  No block
 // barrier is taken after the prologue, which stages the activations
 // (int8 codes in the block-split order, scales and sums; ST = 1, 2, 4
 // sixteen-byte loads of codes per thread) once per block - or quantizes the
@@ -64,7 +66,7 @@ struct DecCfg {
   static_assert(R % 2 == 0 && 5 * R <= 64, "one chain per lane");
   static constexpr int IPL = R / 2;                    // (row, group) items per lane and chunk
   static constexpr int LSTR = R * kDecRowStride;       // floats per chain
-  static constexpr int WAVE_FLOATS = 5 * LSTR + 64;    // products + final chain values
+  static constexpr int WAVE_FLOATS = 10 * LSTR + 64;   // two product buffers + final chain values
 };
 
 // LDS bytes of a block: activations (codes, scales, sums) and the waves'
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   float *ssh = ash + groups;
   float *wbase = reinterpret_cast<float *>(smem + dec_act_bytes(cols));
   float *pw_lds = wbase + wave * C::WAVE_FLOATS;
-  float *fin = pw_lds + 5 * LSTR;
+  float *fin = pw_lds + 10 * LSTR;
 
   // Wave w of W walks tiles w, w + W, ...; every wave runs the same number
   // of tiles, those past the matrix read zeros and store nothing.
@@ -212,15 +214,21 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
 
   u32x4 ring_c[D][IPL];
   uint32_t ring_p[D][IPL];
-  // Issue the loads of iteration it into ring slot j.
-  auto load = [&](int it, u32x4 (&c)[IPL], uint32_t (&p)[IPL]) {
-    const int t = it / nchunks, ch = it - t * nchunks;
-    const int row = tile_row0(t) + h;  // local row h; item i adds lrow(2i) rows
-    const int g = ch * kDecChunk + k;
+  // Tile and chunk of the next load; loads are issued in iteration order,
+  // one chunk each.
+  int lt = 0, lch = 0;
+  auto load = [&](u32x4 (&c)[IPL], uint32_t (&p)[IPL]) {
+    const int row = tile_row0(lt) + h;  // local row h; item i adds lrow(2i) rows
+    const int g = lch * kDecChunk + k;
     uint32_t vc = (uint32_t)row * rowb + g * 16;
     uint32_t vp = ((uint32_t)row * groups + g) * 4;
-    if (it >= it_total) {
-      vc = 0x80000000u;  // past num_records: zeros, no memory access
+    // Past the last iteration, and on the lanes past the groups of a
+    // partial last chunk: zeros without a memory access.  Zero codes and
+    // parameters give +0 or -0 products, which leave a chain unchanged (a
+    // chain starts at +0 and a sum of floats is -0 only when both terms
+    // are).
+    if (lt >= tiles_per_wave || g >= groups) {
+      vc = 0x80000000u;  // past num_records
       vp = 0x80000000u;
     }
     // The item offsets go into the VGPR offset: the range check covers the
@@ -232,12 +240,16 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
 #pragma unroll
     for (int i = 0; i < IPL; ++i)
       p[i] = __builtin_amdgcn_raw_buffer_load_b32(rp, (int)(vp + (uint32_t)(lrow(2 * i) * 4 * groups)), 0, 0);
+    if (++lch == nchunks) {
+      lch = 0;
+      ++lt;
+    }
   };
   // Same issue order as the loop's refills (slot by slot), which keeps the
   // compiler's wait counts exact at the loop head.
 #pragma unroll
   for (int j = 0; j < D; ++j) {
-    load(j, ring_c[j], ring_p[j]);
+    load(ring_c[j], ring_p[j]);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -261,101 +273,130 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
   __syncthreads();
 
   float acc = 0.0f, gate_v = 0.0f, up_v = 0.0f;
-  const int crow = lane % R, cl = lane / R;  // chain lane: row, chain
+  // Chain lane: row crow, chain cl (lanes past the 5R chains re-read chain
+  // 4 and their sums are never used).
+  const int crow = lane % R, cl = min(lane / R, 4);
   const bool chain_lane = lane < 5 * R;
+  const int cbase = cl * LSTR + crow * kDecRowStride;
+  // Activations of the iteration's chunk (read one iteration ahead).
+  uint4 q0, q1;
+  float as, xsum;
+  auto read_act = [&](int ch) {
+    const int gq = min(ch * kDecChunk + k, groups - 1);
+    q0 = *reinterpret_cast<const uint4 *>(qsh + gq * 32);
+    q1 = *reinterpret_cast<const uint4 *>(qsh + gq * 32 + 16);
+    as = ash[gq];
+    xsum = ssh[gq];
+  };
+  // End of tile t: the row sums from the chain values in acc.
+  auto finish = [&](int t) {
+    if (chain_lane) fin[lane] = acc;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int row = tile_row0(t) + lrow(lane);
+    if (lane < R && row < rows) {
+      // hsum8 of (f0, f1, f2, f3, 0, 0, 0, 0) in the _mm256 order.
+      const float f0 = fin[lane], f1 = fin[R + lane], f2 = fin[2 * R + lane], f3 = fin[3 * R + lane];
+      const float zero = 0.0f;
+      const float v = ((f0 + zero) + (f1 + zero)) + ((f2 + zero) + (f3 + zero)) + fin[4 * R + lane];
+      if constexpr (GLU) {
+        if (t == 0)
+          gate_v = v;
+        else
+          up_v = v;
+      } else if constexpr (ROPE) {
+        fin[40 + lane] = v;
+      } else {
+        out[row] = add ? add[row] + v : v;
+      }
+    }
+    if constexpr (ROPE) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (lane < 4 && tile_row0(t) < rows)
+        rope_store_pair(rope, out, tile_row0(t) + lane, rpos, rcos, rsin, fin[40 + lane], fin[44 + lane]);
+    }
+  };
 
+  // Pipelined by one chunk: iteration it computes chunk it's products into
+  // LDS buffer it & 1 while the chain lanes add chunk it - 1's (read from
+  // LDS at the end of iteration it - 1), so a chain's dependent adds issue
+  // between independent product instructions.
+  float4 cv[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) cv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  int ct = 0, cch = 0;   // tile and chunk of the iteration
+  int pt = 0, pch = -1;  // tile and chunk of the pending chain values (none yet)
+  read_act(0);
   for (int it0 = 0; it0 < it_total; it0 += D) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
       const int it = it0 + j;
       if (it < it_total) {
-        const int t = it / nchunks, ch = it - t * nchunks;
-        const int gc = min(kDecChunk, groups - ch * kDecChunk);
-        if (ch == 0) acc = 0.0f;
-        // Products of this lane's items (group ch*32 + k; lanes past a
-        // partial last chunk compute on whatever they read and are never
-        // chained).
-        const int gq = min(ch * kDecChunk + k, groups - 1);
-        const uint4 q0 = *reinterpret_cast<const uint4 *>(qsh + gq * 32);
-        const uint4 q1 = *reinterpret_cast<const uint4 *>(qsh + gq * 32 + 16);
-        const float as = ash[gq], xsum = ssh[gq];
+        float *pb = pw_lds + (it & 1) * (5 * LSTR);
+        acc = pch == 0 ? 0.0f : acc;  // a tile's chains start at its first chunk
+        // Products of the lane's items, block-major in 8 slots of IPL / 2
+        // block dots each, and in every slot 4 of the pending chain's adds:
+        // a dependent add takes several issue slots to complete, and the
+        // scheduling barriers keep the independent product work between
+        // consecutive adds.
+        float cs[IPL];
 #pragma unroll
         for (int i = 0; i < IPL; ++i) {
-          const u32x4 cw = ring_c[j][i];
           const uint32_t pw = ring_p[j][i];
-          const float cs = dec_f16(pw & 0xFFFF) * as;
-          const float z = dec_f16(pw >> 16) * xsum;
-          const int s0 = dec_block_dot(cw.x, q0.x, q0.y);
-          const int s1 = dec_block_dot(cw.y, q0.z, q0.w);
-          const int s2 = dec_block_dot(cw.z, q1.x, q1.y);
-          const int s3 = dec_block_dot(cw.w, q1.z, q1.w);
-          float *pt = pw_lds + (2 * i + h) * kDecRowStride + k;
-          pt[0] = (float)s0 * cs;
-          pt[LSTR] = (float)s1 * cs;
-          pt[2 * LSTR] = (float)s2 * cs;
-          pt[3 * LSTR] = (float)s3 * cs;
-          pt[4 * LSTR] = z;
+          cs[i] = dec_f16(pw & 0xFFFF) * as;
+          pb[4 * LSTR + (2 * i + h) * kDecRowStride + k] = dec_f16(pw >> 16) * xsum;
         }
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl) {
+#pragma unroll
+          for (int e = sl * IPL / 2; e < (sl + 1) * IPL / 2; ++e) {
+            const int b = e / IPL, i = e % IPL;  // block b of item i
+            const u32x4 cw = ring_c[j][i];
+            const uint32_t code = b == 0 ? cw.x : b == 1 ? cw.y : b == 2 ? cw.z : cw.w;
+            const uint4 qq = b < 2 ? q0 : q1;
+            const int sb = dec_block_dot(code, (b & 1) ? qq.z : qq.x, (b & 1) ? qq.w : qq.y);
+            pb[b * LSTR + (2 * i + h) * kDecRowStride + k] = (float)sb * cs[i];
+          }
+          acc = acc + cv[sl].x;
+          acc = acc + cv[sl].y;
+          acc = acc + cv[sl].z;
+          acc = acc + cv[sl].w;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (pch == nchunks - 1) finish(pt);
         // LDS operations of one wave complete in order; the fences only
         // keep the compiler from moving the chain reads above the writes.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (chain_lane) {
-          const float *pc = pw_lds + cl * LSTR + crow * kDecRowStride;
-          if (gc == kDecChunk) {
-            float4 v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = reinterpret_cast<const float4 *>(pc)[u];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              acc = acc + v[u].x;
-              acc = acc + v[u].y;
-              acc = acc + v[u].z;
-              acc = acc + v[u].w;
-            }
-          } else {
-            for (int u = 0; u < gc; ++u) acc = acc + pc[u];
-          }
+        pt = ct;
+        pch = cch;
+        if (++cch == nchunks) {
+          cch = 0;
+          ++ct;
         }
-        if (ch == nchunks - 1) {
-          if (chain_lane) fin[lane] = acc;
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-          __builtin_amdgcn_wave_barrier();
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-          const int row = tile_row0(t) + lrow(lane);
-          if (lane < R && row < rows) {
-            // hsum8 of (f0, f1, f2, f3, 0, 0, 0, 0) in the _mm256 order.
-            const float f0 = fin[lane], f1 = fin[R + lane], f2 = fin[2 * R + lane], f3 = fin[3 * R + lane];
-            const float zero = 0.0f;
-            const float v = ((f0 + zero) + (f1 + zero)) + ((f2 + zero) + (f3 + zero)) + fin[4 * R + lane];
-            if constexpr (GLU) {
-              if (t == 0)
-                gate_v = v;
-              else
-                up_v = v;
-            } else if constexpr (ROPE) {
-              fin[40 + lane] = v;
-            } else {
-              out[row] = add ? add[row] + v : v;
-            }
-          }
-          if constexpr (ROPE) {
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (lane < 4 && tile_row0(t) < rows)
-              rope_store_pair(rope, out, tile_row0(t) + lane, rpos, rcos, rsin, fin[40 + lane], fin[44 + lane]);
-          }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        read_act(cch);
+        const float4 *pc = reinterpret_cast<const float4 *>(pb + cbase);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cv[u] = pc[u];
       }
-      load(it + D, ring_c[j], ring_p[j]);
+      load(ring_c[j], ring_p[j]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  // The last chunk's chain.
+  acc = pch == 0 ? 0.0f : acc;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    acc = acc + cv[u].x;
+    acc = acc + cv[u].y;
+    acc = acc + cv[u].z;
+    acc = acc + cv[u].w;
+  }
+  if (pch == nchunks - 1) finish(pt);
   if constexpr (GLU) {
     // silu_mul_inplace (layers.rs:850-883) of the block's 32 outputs and
     // their quantization (gemm.rs:147-374) as k_silu_quant does; the

@@ -811,20 +811,20 @@ bool gemv_rp_ok(int rows, int cols) {
          (int64_t)rows * (cols / 2) < ((int64_t)1 << 31);
 }
 
-template <int TGW, int WPB, int MAXQ>
+template <int TGW, int WPB, int MAXQ, int NQ = kRpRing>
 void launch_rp(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                const float *scales, const float *sums, int rows, int cols, int m, int ntg, hipStream_t s) {
   constexpr size_t kStepBytes = 68 * 16 + 2 * 4 * 16;  // A blocks, scales, sums of one (group, step)
   static bool configured = false;
   if (!configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_rp<TGW, kRpRing, WPB, MAXQ>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_rp<TGW, NQ, WPB, MAXQ>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)(TGW * MAXQ * kStepBytes));
     configured = true;
   }
   const size_t smem = TGW * (size_t)(cols / 128) * kStepBytes;
   const dim3 grid((rows + 16 * WPB - 1) / (16 * WPB), (ntg + TGW - 1) / TGW);
-  hipLaunchKernelGGL((k_gemv_rp<TGW, kRpRing, WPB, MAXQ>), grid, dim3(64 * WPB), smem, s, out, add, nib, params,
-                     qa, scales, sums, rows, cols, m, ntg);
+  hipLaunchKernelGGL((k_gemv_rp<TGW, NQ, WPB, MAXQ>), grid, dim3(64 * WPB), smem, s, out, add, nib, params, qa,
+                     scales, sums, rows, cols, m, ntg);
 }
 
 }  // namespace
