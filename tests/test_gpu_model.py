@@ -124,6 +124,42 @@ def test_multi_token_attention_batches_bit_exact(rai, ora):
         p += n
 
 
+def test_single_token_attention_long_context_bit_exact(rai, ora):
+    """One-token steps after 1100 positions with four query heads per kv
+    head and head_dim 128: the softmax's sum chains past their read-ahead,
+    row tails of 5, 6, 7, 0 and 1 exact exponentials, and PV over five
+    256-position V chunks, against the oracle, bit for bit."""
+    img = _small_synth(rai, hidden_size=1024, num_layers=1, num_heads=8, num_kv_heads=2, head_dim=128,
+                       intermediate_size=1024, vocab_size=500, max_context=2048, seed=29)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    toks = _token_sequence(om.cfg.vocab_size, 1105)
+    hs = np.stack([om.embed_token(t) for t in toks])
+    okv, gkv = om.create_kv(2048), gm.create_kv_cache(2048)
+    om.forward_batch(hs[:1100], np.arange(1100), okv)
+    gm.forward_batch(hs[:1100], np.arange(1100), gkv)
+    for p in range(1100, 1105):
+        oh = om.forward_batch(hs[p:p + 1], np.arange(p, p + 1), okv)
+        gh = gm.forward_batch(hs[p:p + 1], np.arange(p, p + 1), gkv)
+        assert np.array_equal(_bits(gh), _bits(oh)), p
+
+
+def test_step_graphs_with_a_long_context_match_eager(rai, monkeypatch):
+    """Replayed steps read the position from the device step record and
+    size the attention for the whole 8192-position cache; past 7168
+    positions their token stream stays that of eager launches, which are
+    sized for the live context."""
+    img = _small_synth(rai, max_context=8192, seed=31)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    prompt = copy_heavy_prompt(7300, 1000, seed=4)
+    cfg = rai.LookupConfig(max_draft=8, min_ngram=3, max_ngram=3)
+    monkeypatch.setenv("RAI_STEP_GRAPHS", "0")
+    eager_toks, _ = rai.LookupDecoder(gm, 8192).generate(prompt, 40, cfg)
+    monkeypatch.setenv("RAI_STEP_GRAPHS", "1")
+    graph_toks, _ = rai.LookupDecoder(gm, 8192).generate(prompt, 40, cfg)
+    assert graph_toks == eager_toks
+
+
 @pytest.mark.parametrize("name", FIXTURES)
 def test_batched_equals_sequential_on_gpu(rai, name):
     """model_invariants.rs:92-134 on the GPU path: batched and sequential
