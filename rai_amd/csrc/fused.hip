@@ -731,6 +731,197 @@ void launch_pv_stream(const float *scores, const float *vc, int vstride, int p0,
                      vstride, p0, m, nh, hd, sstride, out, st);
 }
 
+// k_pv_stream for one token per block without block barriers in the chunk
+// loop: LDS flags hand each tile from its loader to the compute wave.  The
+// loader of chunk c waits until the compute wave has finished chunk c - 2
+// (the same tile half), publishes V and probabilities, then posts
+// ready[c & 1] = c; the compute wave waits for ready[k & 1] >= k, runs the
+// chunk's chain and posts done = k + 1.  Every wait is bounded (kPvSpin
+// polls), so a wait that could not end still lets the block finish.
+constexpr int kPvSpin = 1 << 22;
+
+// Poll an LDS word until it is at least `want` (every lane reads the same
+// word; at most kPvSpin polls).  One asm block, so the compiler keeps the
+// loads that follow inside the block that uses them.
+template <bool SLEEP>
+__device__ __forceinline__ void lds_wait_ge(const int *flag, int want) {
+  typedef const __attribute__((address_space(3))) int lds_int;
+  const unsigned addr = (unsigned)(uintptr_t)((lds_int *)flag);
+  int seen;
+  unsigned polls;
+  if constexpr (SLEEP) {
+    asm volatile(
+        "s_mov_b32 %1, 0\n"
+        "1:\n\t"
+        "ds_read_b32 %0, %2\n\t"
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "v_cmp_lt_i32 vcc, %0, %3\n\t"
+        "s_cbranch_vccz 2f\n\t"
+        "s_sleep 1\n\t"
+        "s_add_u32 %1, %1, 1\n\t"
+        "s_cmp_lt_u32 %1, %4\n\t"
+        "s_cbranch_scc1 1b\n"
+        "2:"
+        : "=&v"(seen), "=&s"(polls)
+        : "v"(addr), "v"(want), "s"(kPvSpin)
+        : "vcc", "scc", "memory");
+  } else {
+    asm volatile(
+        "s_mov_b32 %1, 0\n"
+        "1:\n\t"
+        "ds_read_b32 %0, %2\n\t"
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "v_cmp_lt_i32 vcc, %0, %3\n\t"
+        "s_cbranch_vccz 2f\n\t"
+        "s_add_u32 %1, %1, 1\n\t"
+        "s_cmp_lt_u32 %1, %4\n\t"
+        "s_cbranch_scc1 1b\n"
+        "2:"
+        : "=&v"(seen), "=&s"(polls)
+        : "v"(addr), "v"(want), "s"(kPvSpin)
+        : "vcc", "scc", "memory");
+  }
+}
+
+
+template <int DL, int G, int CP, int NL>
+__global__ __launch_bounds__(G * DL + 64 * NL) void k_pv_flag(const float *__restrict__ P,
+                                                               const float *__restrict__ vt_g, int vstride,
+                                                               int pos0, int nh, int hd, int sstride,
+                                                               float *__restrict__ out, const int *__restrict__ st) {
+  using C = PvCfg<DL, G, CP, 1, NL>;
+  static_assert(C::NCW == 1, "one compute wave");
+  if (st) pos0 = st[0];
+  constexpr int NV = C::NV, NP = C::NP, STR = C::STR;
+  constexpr int Q4 = CP / 4;  // float4 per tile row
+  __shared__ __align__(16) float vt[2][DL * STR];
+  __shared__ __align__(16) float pt[2][G * STR];
+  __shared__ int ready[2];
+  __shared__ int done;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slices = hd / DL;
+  const int kvh = blockIdx.x / slices;
+  const int d0 = (blockIdx.x - kvh * slices) * DL;
+  const int n = pos0 + 1;
+  const int nchunks = (n + CP - 1) / CP;
+  const float *vbase = vt_g + ((size_t)kvh * hd + d0) * vstride;
+  const float *pbase = P + (size_t)kvh * G * sstride;
+
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 fv[NV], fp[NP];
+  auto issue = [&](int k) {
+    const int s0 = k * CP;
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int f = 64 * u + lane;  // float4 index in the [DL][CP] tile
+      const int q0 = min(s0 + 4 * (f % Q4), vstride - 4);
+      fv[u] = *reinterpret_cast<const f4 *>(vbase + (size_t)(f / Q4) * vstride + q0);
+    }
+#pragma unroll
+    for (int r = 0; r < NP; ++r) {
+      const int f = 64 * r + lane;  // float4 index in the [G][CP] tile
+      const int g = min(f / Q4, G - 1);
+      const int q0 = min(s0 + 4 * (f % Q4), sstride - 4);
+      fp[r] = *reinterpret_cast<const f4 *>(pbase + (size_t)g * sstride + q0);
+    }
+  };
+  auto publish = [&](int k) {
+    const int s0 = k * CP, b = k & 1;
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int f = 64 * u + lane;
+      *reinterpret_cast<f4 *>(&vt[b][(f / Q4) * STR + 4 * (f % Q4)]) = fv[u];
+    }
+#pragma unroll
+    for (int r = 0; r < NP; ++r) {
+      const int f = 64 * r + lane;
+      if (f < G * Q4) {
+        const int q = 4 * (f % Q4), g = f / Q4;
+        f4 v = fp[r];
+        if (s0 + q + 0 >= n) v.x = 0.0f;
+        if (s0 + q + 1 >= n) v.y = 0.0f;
+        if (s0 + q + 2 >= n) v.z = 0.0f;
+        if (s0 + q + 3 >= n) v.w = 0.0f;
+        *reinterpret_cast<f4 *>(&pt[b][g * STR + q]) = v;
+      }
+    }
+  };
+
+  if (threadIdx.x == 0) {
+    ready[0] = 0;  // chunk 0 is published before the first barrier
+    ready[1] = -1;
+    done = 0;
+  }
+  const int lw = wave - 1;  // loader index; wave 0 computes
+  if (lw >= 0 && lw < nchunks) issue(lw);
+  if (lw == 0) {
+    publish(0);
+    if (NL < nchunks) issue(NL);
+  }
+  __syncthreads();
+  const int g = lane / DL, dd = lane % DL;
+  float acc = 0.0f;
+  for (int k = 0; k < nchunks; ++k) {
+    if (wave == 0) {
+      lds_wait_ge<false>(&ready[k & 1], k);
+      const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
+      const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][g * STR]);
+      // Rolling prefetch: the next 8 float4 pairs (32 positions) are
+      // requested before the 32 FMAs of the current ones.
+      constexpr int PB = NV + NP <= 28 ? 8 : 4;
+      static_assert(Q4 % PB == 0, "whole prefetch blocks per chunk");
+      float4 cv[PB], cp[PB];
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        cv[u] = vr[u];
+        cp[u] = pr[u];
+      }
+#pragma unroll
+      for (int u0 = 0; u0 < Q4; u0 += PB) {
+        float4 nv[PB], np[PB];
+        if (u0 + PB < Q4) {
+#pragma unroll
+          for (int u = 0; u < PB; ++u) {
+            nv[u] = vr[u0 + PB + u];
+            np[u] = pr[u0 + PB + u];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < PB; ++u) {
+          acc = __fmaf_rn(cp[u].x, cv[u].x, acc);
+          acc = __fmaf_rn(cp[u].y, cv[u].y, acc);
+          acc = __fmaf_rn(cp[u].z, cv[u].z, acc);
+          acc = __fmaf_rn(cp[u].w, cv[u].w, acc);
+        }
+        if (u0 + PB < Q4) {
+#pragma unroll
+          for (int u = 0; u < PB; ++u) {
+            cv[u] = nv[u];
+            cp[u] = np[u];
+          }
+        }
+      }
+      // The release orders this chunk's tile reads before the post.
+      __hip_atomic_store(&done, k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else if (k + 1 < nchunks && lw == (k + 1) % NL) {
+      // Tile half (k + 1) & 1 held chunk k - 1: wait until it is consumed.
+      lds_wait_ge<true>(&done, k);
+      publish(k + 1);
+      __hip_atomic_store(&ready[(k + 1) & 1], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (k + 1 + NL < nchunks) issue(k + 1 + NL);
+    }
+  }
+  if (wave == 0) out[((size_t)kvh * G + g) * hd + d0 + dd] = acc;
+}
+
+template <int DL, int G, int CP, int NL>
+void launch_pv_flag(const float *scores, const float *vc, int vstride, int p0, int nh, int nkv, int hd,
+                    int sstride, float *out, const int *st, hipStream_t s) {
+  hipLaunchKernelGGL((k_pv_flag<DL, G, CP, NL>), dim3(nkv * (hd / DL)), dim3(PvCfg<DL, G, CP, 1, NL>::NT), 0, s,
+                     scores, vc, vstride, p0, nh, hd, sstride, out, st);
+}
+
 // PV for any head_dim: thread per output element, same chain order.  V
 // layout: DMAJOR [kv][hd][vstride], else [kv][cap][hd].
 template <bool DMAJOR>
@@ -914,6 +1105,8 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
         launch_pv_stream<16, 4, 128, 4, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 4 && mt > 2)
         launch_pv_stream<16, 4, 256, 3, 5>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+      else if (G == 4 && mt == 1)
+        launch_pv_flag<16, 4, 256, 7>(scores, vc, vstride, p0, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 4)
         launch_pv_stream<16, 4, 256, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 8)
