@@ -588,7 +588,8 @@ static int softmax_r_stride(int nmax) { return (((nmax + 7) / 8 + 63) & ~63) + 4
 // and the compute waves run the reference's sequential FMA chain over the
 // current chunk, reading 4 positions' V values and (wave-broadcast)
 // probabilities per 16-byte LDS read, 32 positions ahead of the chain.  The
-// chunks run to the block's longest token; one barrier per chunk.
+// chunks run to the block's longest token.  No block barrier in the chunk
+// loop: LDS flags hand each tile over (k_pv_flag).
 template <int DL, int G, int CP, int TM, int NL>
 struct PvCfg {
   static constexpr int NCW = TM * G * DL / 64;       // compute waves
@@ -599,145 +600,13 @@ struct PvCfg {
   static_assert(TM * G * DL % 64 == 0, "whole compute waves");
 };
 
-template <int DL, int G, int CP, int TM, int NL>
-__global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_stream(
-    const float *__restrict__ P, const float *__restrict__ vt_g, int vstride, int pos0, int m, int nh, int hd,
-    int sstride, float *__restrict__ out, const int *__restrict__ st) {
-  using C = PvCfg<DL, G, CP, TM, NL>;
-  if (st) pos0 = st[0];
-  constexpr int NCW = C::NCW, NV = C::NV, NP = C::NP, STR = C::STR;
-  constexpr int Q4 = CP / 4;  // float4 per tile row
-  __shared__ __align__(16) float vt[2][DL * STR];
-  __shared__ __align__(16) float pt[2][TM * G * STR];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int slices = hd / DL;
-  const int kvh = blockIdx.x / slices;
-  const int d0 = (blockIdx.x - kvh * slices) * DL;
-  const int t0 = blockIdx.y * TM;
-  const int tn = min(TM, m - t0);              // tokens of this block
-  const int nmax = pos0 + t0 + tn;             // positions of its longest token
-  const int nchunks = (nmax + CP - 1) / CP;
-  const float *vbase = vt_g + ((size_t)kvh * hd + d0) * vstride;
 
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  f4 fv[NV], fp[NP];
-#define RAI_PV_ISSUE(k_)                                                                        \
-  do {                                                                                          \
-    const int s0_ = (k_) * CP;                                                                  \
-    _Pragma("unroll") for (int u = 0; u < NV; ++u) {                                            \
-      const int f = 64 * u + lane; /* float4 index in the [DL][CP] tile */                      \
-      const int q0 = min(s0_ + 4 * (f % Q4), vstride - 4);                                      \
-      fv[u] = *reinterpret_cast<const f4 *>(vbase + (size_t)(f / Q4) * vstride + q0);           \
-    }                                                                                           \
-    _Pragma("unroll") for (int r = 0; r < NP; ++r) {                                            \
-      const int f = 64 * r + lane; /* float4 index in the [TM*G][CP] tile */                    \
-      const int rr = min(f / Q4, TM * G - 1), tl = min(rr / G, tn - 1);                         \
-      const int q0 = min(s0_ + 4 * (f % Q4), sstride - 4);                                      \
-      fp[r] = *reinterpret_cast<const f4 *>(                                                    \
-          P + ((size_t)(t0 + tl) * nh + (size_t)kvh * G + rr % G) * sstride + q0);              \
-    }                                                                                           \
-  } while (0)
-#define RAI_PV_PUBLISH(k_)                                                                      \
-  do {                                                                                          \
-    const int s0_ = (k_) * CP, b_ = (k_) & 1;                                                   \
-    _Pragma("unroll") for (int u = 0; u < NV; ++u) {                                            \
-      const int f = 64 * u + lane;                                                              \
-      *reinterpret_cast<f4 *>(&vt[b_][(f / Q4) * STR + 4 * (f % Q4)]) = fv[u];                  \
-    }                                                                                           \
-    _Pragma("unroll") for (int r = 0; r < NP; ++r) {                                            \
-      const int f = 64 * r + lane;                                                              \
-      if (f < TM * G * Q4) {                                                                    \
-        const int q = 4 * (f % Q4), rr = f / Q4, tl = rr / G;                                   \
-        const int n_ = tl < tn ? pos0 + t0 + tl + 1 : 0;                                        \
-        f4 v = fp[r];                                                                           \
-        if (s0_ + q + 0 >= n_) v.x = 0.0f;                                                      \
-        if (s0_ + q + 1 >= n_) v.y = 0.0f;                                                      \
-        if (s0_ + q + 2 >= n_) v.z = 0.0f;                                                      \
-        if (s0_ + q + 3 >= n_) v.w = 0.0f;                                                      \
-        *reinterpret_cast<f4 *>(&pt[b_][rr * STR + q]) = v;                                     \
-      }                                                                                         \
-    }                                                                                           \
-  } while (0)
-
-  const int lw = wave - NCW;  // loader index, negative for compute waves
-  if (lw >= 0 && lw < nchunks) {
-    RAI_PV_ISSUE(lw);
-    if (lw == 0) {
-      RAI_PV_PUBLISH(0);
-      if (NL < nchunks) RAI_PV_ISSUE(NL);
-    }
-  }
-  __syncthreads();
-  const int L = wave * 64 + lane;
-  const int tl = L / (G * DL), g = (L / DL) % G, dd = L % DL;
-  float acc = 0.0f;
-  for (int k = 0; k < nchunks; ++k) {
-    if (wave < NCW) {
-      const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
-      const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][(tl * G + g) * STR]);
-      // Rolling prefetch: the next 8 float4 pairs (32 positions) are
-      // requested before the 32 FMAs of the current ones, so the LDS
-      // latency is exposed once per chunk instead of once per 32 positions.
-      constexpr int PB = NV + NP <= 28 ? 8 : 4;  // fewer with many loader registers
-      static_assert(Q4 % PB == 0, "whole prefetch blocks per chunk");
-      float4 cv[PB], cp[PB];
-#pragma unroll
-      for (int u = 0; u < PB; ++u) {
-        cv[u] = vr[u];
-        cp[u] = pr[u];
-      }
-#pragma unroll
-      for (int u0 = 0; u0 < Q4; u0 += PB) {
-        float4 nv[PB], np[PB];
-        if (u0 + PB < Q4) {
-#pragma unroll
-          for (int u = 0; u < PB; ++u) {
-            nv[u] = vr[u0 + PB + u];
-            np[u] = pr[u0 + PB + u];
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < PB; ++u) {
-          acc = __fmaf_rn(cp[u].x, cv[u].x, acc);
-          acc = __fmaf_rn(cp[u].y, cv[u].y, acc);
-          acc = __fmaf_rn(cp[u].z, cv[u].z, acc);
-          acc = __fmaf_rn(cp[u].w, cv[u].w, acc);
-        }
-        if (u0 + PB < Q4) {
-#pragma unroll
-          for (int u = 0; u < PB; ++u) {
-            cv[u] = nv[u];
-            cp[u] = np[u];
-          }
-        }
-      }
-    } else if (k + 1 < nchunks && lw == (k + 1) % NL) {
-      RAI_PV_PUBLISH(k + 1);
-      if (k + 1 + NL < nchunks) RAI_PV_ISSUE(k + 1 + NL);
-    }
-    __syncthreads();
-  }
-  if (wave < NCW && tl < tn) out[((size_t)(t0 + tl) * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc;
-#undef RAI_PV_ISSUE
-#undef RAI_PV_PUBLISH
-}
-
-template <int DL, int G, int CP, int TM, int NL>
-void launch_pv_stream(const float *scores, const float *vc, int vstride, int p0, int m, int nh, int nkv, int hd,
-                      int sstride, float *out, const int *st, hipStream_t s) {
-  const dim3 pg(nkv * (hd / DL), (m + TM - 1) / TM);
-  hipLaunchKernelGGL((k_pv_stream<DL, G, CP, TM, NL>), pg, dim3(PvCfg<DL, G, CP, TM, NL>::NT), 0, s, scores, vc,
-                     vstride, p0, m, nh, hd, sstride, out, st);
-}
-
-// k_pv_stream for one token per block without block barriers in the chunk
-// loop: LDS flags hand each tile from its loader to the compute wave.  The
-// loader of chunk c waits until the compute wave has finished chunk c - 2
-// (the same tile half), publishes V and probabilities, then posts
-// ready[c & 1] = c; the compute wave waits for ready[k & 1] >= k, runs the
-// chunk's chain and posts done = k + 1.  Every wait is bounded (kPvSpin
-// polls), so a wait that could not end still lets the block finish.
+// The tile hand-off without block barriers: the loader of chunk c waits
+// until every compute wave has finished chunk c - 2 (the same tile half),
+// publishes V and probabilities, then posts ready[c & 1] = c; a compute wave
+// waits for ready[k & 1] >= k, runs the chunk's chains and posts its
+// done[w] = k + 1.  Every wait is bounded (kPvSpin polls), so a wait that
+// could not end still lets the block finish.
 constexpr int kPvSpin = 1 << 22;
 
 // Poll an LDS word until it is at least `want` (every lane reads the same
@@ -784,29 +653,28 @@ __device__ __forceinline__ void lds_wait_ge(const int *flag, int want) {
 }
 
 
-template <int DL, int G, int CP, int NL>
-__global__ __launch_bounds__(G * DL + 64 * NL) void k_pv_flag(const float *__restrict__ P,
-                                                               const float *__restrict__ vt_g, int vstride,
-                                                               int pos0, int nh, int hd, int sstride,
-                                                               float *__restrict__ out, const int *__restrict__ st) {
-  using C = PvCfg<DL, G, CP, 1, NL>;
-  static_assert(C::NCW == 1, "one compute wave");
+template <int DL, int G, int CP, int TM, int NL>
+__global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
+    const float *__restrict__ P, const float *__restrict__ vt_g, int vstride, int pos0, int m, int nh, int hd,
+    int sstride, float *__restrict__ out, const int *__restrict__ st) {
+  using C = PvCfg<DL, G, CP, TM, NL>;
   if (st) pos0 = st[0];
-  constexpr int NV = C::NV, NP = C::NP, STR = C::STR;
+  constexpr int NCW = C::NCW, NV = C::NV, NP = C::NP, STR = C::STR;
   constexpr int Q4 = CP / 4;  // float4 per tile row
   __shared__ __align__(16) float vt[2][DL * STR];
-  __shared__ __align__(16) float pt[2][G * STR];
+  __shared__ __align__(16) float pt[2][TM * G * STR];
   __shared__ int ready[2];
-  __shared__ int done;
+  __shared__ int done[NCW];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slices = hd / DL;
   const int kvh = blockIdx.x / slices;
   const int d0 = (blockIdx.x - kvh * slices) * DL;
-  const int n = pos0 + 1;
-  const int nchunks = (n + CP - 1) / CP;
+  const int t0 = blockIdx.y * TM;
+  const int tn = min(TM, m - t0);   // tokens of this block
+  const int nmax = pos0 + t0 + tn;  // positions of its longest token
+  const int nchunks = (nmax + CP - 1) / CP;
   const float *vbase = vt_g + ((size_t)kvh * hd + d0) * vstride;
-  const float *pbase = P + (size_t)kvh * G * sstride;
 
   typedef float f4 __attribute__((ext_vector_type(4)));
   f4 fv[NV], fp[NP];
@@ -820,10 +688,11 @@ __global__ __launch_bounds__(G * DL + 64 * NL) void k_pv_flag(const float *__res
     }
 #pragma unroll
     for (int r = 0; r < NP; ++r) {
-      const int f = 64 * r + lane;  // float4 index in the [G][CP] tile
-      const int g = min(f / Q4, G - 1);
+      const int f = 64 * r + lane;  // float4 index in the [TM*G][CP] tile
+      const int rr = min(f / Q4, TM * G - 1), tl = min(rr / G, tn - 1);
       const int q0 = min(s0 + 4 * (f % Q4), sstride - 4);
-      fp[r] = *reinterpret_cast<const f4 *>(pbase + (size_t)g * sstride + q0);
+      fp[r] = *reinterpret_cast<const f4 *>(P + ((size_t)(t0 + tl) * nh + (size_t)kvh * G + rr % G) * sstride +
+                                            q0);
     }
   };
   auto publish = [&](int k) {
@@ -836,14 +705,15 @@ __global__ __launch_bounds__(G * DL + 64 * NL) void k_pv_flag(const float *__res
 #pragma unroll
     for (int r = 0; r < NP; ++r) {
       const int f = 64 * r + lane;
-      if (f < G * Q4) {
-        const int q = 4 * (f % Q4), g = f / Q4;
+      if (f < TM * G * Q4) {
+        const int q = 4 * (f % Q4), rr = f / Q4, tl = rr / G;
+        const int n_ = tl < tn ? pos0 + t0 + tl + 1 : 0;
         f4 v = fp[r];
-        if (s0 + q + 0 >= n) v.x = 0.0f;
-        if (s0 + q + 1 >= n) v.y = 0.0f;
-        if (s0 + q + 2 >= n) v.z = 0.0f;
-        if (s0 + q + 3 >= n) v.w = 0.0f;
-        *reinterpret_cast<f4 *>(&pt[b][g * STR + q]) = v;
+        if (s0 + q + 0 >= n_) v.x = 0.0f;
+        if (s0 + q + 1 >= n_) v.y = 0.0f;
+        if (s0 + q + 2 >= n_) v.z = 0.0f;
+        if (s0 + q + 3 >= n_) v.w = 0.0f;
+        *reinterpret_cast<f4 *>(&pt[b][rr * STR + q]) = v;
       }
     }
   };
@@ -851,25 +721,27 @@ __global__ __launch_bounds__(G * DL + 64 * NL) void k_pv_flag(const float *__res
   if (threadIdx.x == 0) {
     ready[0] = 0;  // chunk 0 is published before the first barrier
     ready[1] = -1;
-    done = 0;
   }
-  const int lw = wave - 1;  // loader index; wave 0 computes
+  if (threadIdx.x < NCW) done[threadIdx.x] = 0;
+  const int lw = wave - NCW;  // loader index, negative for compute waves
   if (lw >= 0 && lw < nchunks) issue(lw);
   if (lw == 0) {
     publish(0);
     if (NL < nchunks) issue(NL);
   }
   __syncthreads();
-  const int g = lane / DL, dd = lane % DL;
+  const int L = wave * 64 + lane;
+  const int tl = L / (G * DL), g = (L / DL) % G, dd = L % DL;
   float acc = 0.0f;
   for (int k = 0; k < nchunks; ++k) {
-    if (wave == 0) {
+    if (wave < NCW) {
       lds_wait_ge<false>(&ready[k & 1], k);
       const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
-      const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][g * STR]);
+      const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][(tl * G + g) * STR]);
       // Rolling prefetch: the next 8 float4 pairs (32 positions) are
-      // requested before the 32 FMAs of the current ones.
-      constexpr int PB = NV + NP <= 28 ? 8 : 4;
+      // requested before the 32 FMAs of the current ones, so the LDS
+      // latency is exposed once per chunk instead of once per 32 positions.
+      constexpr int PB = NV + NP <= 28 ? 8 : 4;  // fewer with many loader registers
       static_assert(Q4 % PB == 0, "whole prefetch blocks per chunk");
       float4 cv[PB], cp[PB];
 #pragma unroll
@@ -903,23 +775,26 @@ __global__ __launch_bounds__(G * DL + 64 * NL) void k_pv_flag(const float *__res
         }
       }
       // The release orders this chunk's tile reads before the post.
-      __hip_atomic_store(&done, k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_store(&done[wave], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     } else if (k + 1 < nchunks && lw == (k + 1) % NL) {
-      // Tile half (k + 1) & 1 held chunk k - 1: wait until it is consumed.
-      lds_wait_ge<true>(&done, k);
+      // Tile half (k + 1) & 1 held chunk k - 1: wait until every compute
+      // wave has consumed it.
+#pragma unroll
+      for (int w = 0; w < NCW; ++w) lds_wait_ge<true>(&done[w], k);
       publish(k + 1);
       __hip_atomic_store(&ready[(k + 1) & 1], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       if (k + 1 + NL < nchunks) issue(k + 1 + NL);
     }
   }
-  if (wave == 0) out[((size_t)kvh * G + g) * hd + d0 + dd] = acc;
+  if (wave < NCW && tl < tn) out[((size_t)(t0 + tl) * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc;
 }
 
-template <int DL, int G, int CP, int NL>
-void launch_pv_flag(const float *scores, const float *vc, int vstride, int p0, int nh, int nkv, int hd,
+template <int DL, int G, int CP, int TM, int NL>
+void launch_pv_flag(const float *scores, const float *vc, int vstride, int p0, int m, int nh, int nkv, int hd,
                     int sstride, float *out, const int *st, hipStream_t s) {
-  hipLaunchKernelGGL((k_pv_flag<DL, G, CP, NL>), dim3(nkv * (hd / DL)), dim3(PvCfg<DL, G, CP, 1, NL>::NT), 0, s,
-                     scores, vc, vstride, p0, nh, hd, sstride, out, st);
+  const dim3 pg(nkv * (hd / DL), (m + TM - 1) / TM);
+  hipLaunchKernelGGL((k_pv_flag<DL, G, CP, TM, NL>), pg, dim3(PvCfg<DL, G, CP, TM, NL>::NT), 0, s, scores, vc,
+                     vstride, p0, m, nh, hd, sstride, out, st);
 }
 
 // PV for any head_dim: thread per output element, same chain order.  V
@@ -1102,21 +977,19 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
       // Tokens per block: one for one or two tokens (more blocks), three up
       // to twelve (the verify batch), four beyond.
       if (G == 4 && mt > 12)
-        launch_pv_stream<16, 4, 128, 4, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 4, 128, 4, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 4 && mt > 2)
-        launch_pv_stream<16, 4, 256, 3, 5>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
-      else if (G == 4 && mt == 1)
-        launch_pv_flag<16, 4, 256, 7>(scores, vc, vstride, p0, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 4, 256, 3, 5>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 4)
-        launch_pv_stream<16, 4, 256, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 4, 256, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 8)
-        launch_pv_stream<16, 8, 256, 1, 6>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 8, 256, 1, 6>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 16)
-        launch_pv_stream<16, 16, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 16, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 2)
-        launch_pv_stream<32, 2, 128, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<32, 2, 128, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else
-        launch_pv_stream<64, 1, 64, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<64, 1, 64, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
     } else if (vstride > 0) {
       hipLaunchKernelGGL(k_pv_any<true>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, scores,
                          vc, cap, vstride, p0, mt, nh, nkv, hd, sstride, ot, st);
