@@ -975,13 +975,15 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
                         (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && hd % DL == 0;
     if (stream) {
       // Tokens per block: one for one or two tokens (more blocks), three up
-      // to twelve (the verify batch), four beyond.
+      // to twelve (the verify batch), four beyond; loader waves measured on
+      // 4.35K positions with V streamed from HBM (four for one token, three
+      // for three).
       if (G == 4 && mt > 12)
         launch_pv_flag<16, 4, 128, 4, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 4 && mt > 2)
-        launch_pv_flag<16, 4, 256, 3, 5>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 4, 256, 3, 3>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 4)
-        launch_pv_flag<16, 4, 256, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 4, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 8)
         launch_pv_flag<16, 8, 256, 1, 6>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
       else if (G == 16)
