@@ -8,14 +8,30 @@ symmetric int4 RTN at group 32 with f16 scales in the .raimodel layout; a
 4096-token copy-heavy synthetic prompt; prompt lookup with n-gram 3, k = 8,
 greedy acceptance; 256 generated tokens at batch 1.
 
-A "step" is one decoded token; `value` = generated tokens / decode seconds
-(prefill timed separately, weights and prompt resident in HBM before the
-timed region).  The JSON line also carries:
-  roofline      the W4A8 verify GEMV (M = 9 tokens, 14336x4096, the largest
-                per-layer matrix) timed with HIP events on its own stream:
-                algorithmic bytes per launch / average launch time vs 8 TB/s;
+The prompt.  A random-init model's own continuation never repeats a span of
+a random-id prompt, so on such a prompt no 3-gram draft fires and the run is
+plain decoding.  The bench therefore decodes the copy-heavy prompt greedily
+once (the plain-decode figure), and splices that 256-token continuation,
+preceded by the prompt's last three tokens, into the middle of the prompt as
+an earlier span: the workload prompt still has 4096 tokens, ends like the
+original, and quotes text the model goes on to produce, as the prompts
+prompt lookup is meant for do.  Acceptance is whatever the model's greedy
+tokens give; token identity with plain greedy decoding of the same prompt is
+checked.
+
+A step is one 256-token generation from the prefilled prompt (the KV cache
+is rolled back to the prompt before each one; prefill is timed once,
+separately).  `value` = generated tokens / seconds over the timed steps, with
+the model and the prompt resident in HBM.  The JSON line also carries:
+  roofline      the in-model verify GEMV (gate|up, 28672x4096, M = 9 tokens)
+                timed with HIP events on its own stream: algorithmic bytes per
+                launch / average launch time, against 8 TB/s; `traffic` from
+                two rocprofv3 counter passes;
   cpu_baseline  the CPU oracle (a C++ restatement of the reference's AVX2
-                path) timed on a bounded sample on this host.
+                path) stepping the same decoder state (its KV cache copied
+                from the GPU's after the prefill) at the same context length,
+                at the reference's default thread count; config.cpu_* has the
+                all-cores figure and the host CPU.
 
 `--gpus N` with N > 1 is refused: this build runs on one GPU.
 """
@@ -63,15 +79,19 @@ def measure_gemv(rai, n, k, m, gs, iters=50):
 COPY_BYTES = 256 << 20  # the plain device copy whose counters calibrate the traffic pass
 
 
+def roofline_shape():
+    from rai_amd.workload import MISTRAL_7B
+    return 2 * MISTRAL_7B["intermediate_size"], MISTRAL_7B["hidden_size"], 9
+
+
 def roofline_only(gs: int) -> int:
     """The roofline GEMV launches (rotating weight copies) and one plain
     device-to-device copy of COPY_BYTES: the program the counter passes
     profile."""
     import rai_amd
     import torch
-    from rai_amd.workload import MISTRAL_7B
-    n, k = MISTRAL_7B["intermediate_size"], MISTRAL_7B["hidden_size"]
-    measure_gemv(rai_amd, n, k, 9, gs, iters=20)
+    n, k, m = roofline_shape()
+    measure_gemv(rai_amd, n, k, m, gs, iters=20)
     a = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     b = torch.empty_like(a)
     b.copy_(a)
@@ -113,7 +133,7 @@ def measure_traffic(gs: int):
         res = {}
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
             vals = _counter_pass(counter, gs, tmp)
-            gemv = [v for name, vs in vals.items() if "k_gemv" in name for v in vs]
+            gemv = [v for name, vs in vals.items() if "k_gemv" in name or "k_w4a8" in name for v in vs]
             copy = [v for name, vs in vals.items() if "copy" in name.lower() or "elementwise" in name for v in vs]
             if not gemv or not copy:
                 raise RuntimeError(f"{counter}: kernels not found in {list(vals)}")
@@ -122,36 +142,67 @@ def measure_traffic(gs: int):
     return res
 
 
-def cpu_baseline(img: bytes, cfg: dict, seconds: float, prompt_len: int, threads: int):
-    """Oracle (C++ restatement of the reference AVX2 path) on a bounded sample:
-    same model, a short copy-heavy prompt, greedy lookup steps for ~`seconds`."""
+def splice_prompt(base: np.ndarray, cont) -> np.ndarray:
+    """The base prompt with (its last three tokens + `cont`) written over the
+    positions starting at a quarter of its length; same length, same end."""
+    n = len(base)
+    span = np.concatenate([base[-3:], np.asarray(cont, np.uint32)])
+    at = n // 4
+    out = np.concatenate([base[:at], span, base[at + len(span):]]).astype(np.uint32)
+    assert len(out) == n and np.array_equal(out[-3:], base[-3:])
+    return out
+
+
+def host_cpu() -> tuple[str, int]:
+    name = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        n = len(os.sched_getaffinity(0))
+    except Exception:
+        n = os.cpu_count() or 1
+    return name, n
+
+
+def cpu_baseline(img, shape, dec, context, pos, gpu_tokens, seconds: float, threads: int):
+    """The oracle's greedy lookup steps from the GPU decoder's state after the
+    prefill (every layer's K/V rows copied over), at the workload's context
+    length, for about `seconds`.  Returns (tok/s, tokens, seconds, matches):
+    `matches` is whether the oracle's tokens equal the GPU's."""
     from oracle import ora
-    from rai_amd.workload import copy_heavy_prompt
     ora.set_threads(threads)
-    m = ora.Model(img, 0)
-    prompt = copy_heavy_prompt(prompt_len, cfg["vocab_size"], seed=11).astype(np.int32)
-    dec = ora.LookupDecoder(m, prompt_len + 512)
-    pos = dec.prefill(prompt)
-    ctx = prompt.tolist()
+    om = ora.Model(img, 0)
+    od = ora.LookupDecoder(om, len(context) + 512)
+    L, nkv, hd = shape["num_layers"], shape["num_kv_heads"], shape["head_dim"]
+    for layer in range(L):
+        for which in (0, 1):
+            od.import_kv(layer, which, dec.kv_cache.export(layer, which, pos, nkv, hd))
+    ctx = list(context)
     produced = 0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        toks, met = dec.step(pos, ctx, 8, 3, 3)
+    while time.perf_counter() - t0 < seconds and produced < len(gpu_tokens):
+        toks, met = od.step(pos, ctx, 8, 3, 3)
         ctx += toks
         pos += met.produced
         produced += met.produced
     dt = time.perf_counter() - t0
-    return produced / dt, produced, dt
+    got = ctx[len(context):]
+    matches = got == list(gpu_tokens[:len(got)])
+    return produced / dt, produced, dt, matches
 
 
 def forced_verify_steps(dec, context, pos: int, cfg, n_steps: int):
     """Decoder steps whose draft is forced: before each step the context's
     last three tokens are overwritten with an earlier 3-gram, so the n-gram
     search returns a full k = 8 draft and the step runs the 9-token verify
-    forward, lm_head and argmax, greedy acceptance and the KV rollback.  Only
-    the timing is meaningful (the token stream is not the model's own)."""
+    forward, lm_head and argmax, greedy acceptance and the KV rollback."""
     ctx = list(context)
-    times, drafted, accepted = [], 0, 0
+    times, drafted = [], 0
     for i in range(n_steps):
         src = 64 + 53 * i
         ctx[-3:] = ctx[src:src + 3]
@@ -159,20 +210,20 @@ def forced_verify_steps(dec, context, pos: int, cfg, n_steps: int):
         toks, met = dec.step(pos, ctx, cfg)
         times.append(time.perf_counter() - t0)
         drafted += met.drafted
-        accepted += met.accepted
         ctx += toks
         pos += met.produced
-    return times, drafted, accepted
+    return times, drafted
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256, help="tokens to generate (timed)")
-    ap.add_argument("--warmup", type=int, default=8, help="untimed decode tokens before timing")
+    ap.add_argument("--steps", type=int, default=20, help="timed 256-token generations")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed generations before timing")
+    ap.add_argument("--tokens", type=int, default=256, help="tokens per generation")
     ap.add_argument("--workload", choices=["mistral7b", "tinyllama"], default="mistral7b")
     ap.add_argument("--prompt", type=int, default=None)
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--roofline-only", action="store_true", help=argparse.SUPPRESS)
@@ -189,7 +240,7 @@ def main() -> int:
     shape = dict(MISTRAL_7B if args.workload == "mistral7b" else TINYLLAMA)
     prompt_len = args.prompt or (4096 if args.workload == "mistral7b" else 2048)
     max_ctx = 8192 if args.workload == "mistral7b" else 4096
-    gs = 32
+    gs, ntok = 32, args.tokens
     name, cus = rai_amd.device_info()
     log(f"device {name}, {cus} CUs; workload {args.workload}")
 
@@ -202,38 +253,64 @@ def main() -> int:
     model = rai_amd.RaiModel.from_bytes(img, max_groups=1024)
     log(f"upload {time.perf_counter() - t0:.1f}s; weight bytes/step {model.weight_bytes() / 1e9:.3f} GB")
 
-    prompt = copy_heavy_prompt(prompt_len, shape["vocab_size"], seed=2026)
     cfg = rai_amd.LookupConfig(max_draft=8, min_ngram=3, max_ngram=3, temperature=0.0)
     dec = rai_amd.LookupDecoder(model, max_ctx)
-    # Warm-up run (untimed): prefill + a few tokens, then the timed run on a
-    # fresh decoder state (same prompt, so the same token stream).
-    if args.warmup > 0:
-        _, wst = dec.generate(prompt[:512], args.warmup, cfg)
-        log(f"warm-up: {wst['generated']} tokens")
-    dec = rai_amd.LookupDecoder(model, max_ctx)
-    toks, st = dec.generate(prompt, args.steps, cfg)
-    decode_s = st["decode_seconds"]
-    gen = st["generated"]
-    value = gen / decode_s
-    log(f"prefill {prompt_len - 1} tokens in {st['prefill_seconds']:.2f}s; decode {gen} tokens in "
-        f"{decode_s:.3f}s over {st['steps']} steps ({st['steps_with_draft']} drafted, "
+    base = copy_heavy_prompt(prompt_len, shape["vocab_size"], seed=2026)
+    cont, st0 = dec.generate(base, ntok, cfg)
+    plain_tok_s = st0["generated"] / st0["decode_seconds"]
+    log(f"base prompt: prefill {st0['prefill_seconds']:.2f}s, plain decode {st0['generated']} tokens "
+        f"at {plain_tok_s:.1f} tok/s ({st0['steps_with_draft']} steps drafted)")
+
+    prompt = splice_prompt(base, cont)
+    t0 = time.perf_counter()
+    pos = dec.prefill(prompt)
+    prefill_s = time.perf_counter() - t0
+    log(f"workload prompt: prefill {pos} tokens in {prefill_s:.2f}s")
+
+    for _ in range(args.warmup):
+        dec.kv_cache.truncate(pos)
+        dec.decode(prompt, pos, ntok, cfg)
+    rai_amd.lib().rai_device_synchronize()
+    t0 = time.perf_counter()
+    runs = []
+    for _ in range(args.steps):
+        dec.kv_cache.truncate(pos)
+        runs.append(dec.decode(prompt, pos, ntok, cfg))
+    rai_amd.lib().rai_device_synchronize()
+    elapsed = time.perf_counter() - t0
+    toks, st = runs[-1]
+    gen = sum(r[1]["generated"] for r in runs)
+    value = gen / elapsed
+    same_runs = all(r[0] == toks for r in runs)
+    log(f"timed: {args.steps} generations, {gen} tokens in {elapsed:.3f}s = {value:.1f} tok/s; "
+        f"{st['steps']} decoder steps per generation ({st['steps_with_draft']} drafted, "
         f"{st['accepted']}/{st['drafted']} draft tokens accepted)")
 
-    # The synthetic workload's model is random, so its own continuations
-    # rarely repeat a prompt span and few steps draft.  Time the verify step
-    # itself on forced drafts at the same context length.
-    vt, vdrafted, vaccepted = forced_verify_steps(dec, list(prompt) + list(toks),
-                                                  prompt_len - 1 + len(toks), cfg, 33)
-    verify_step_ms = 1e3 * float(np.mean(vt[1:]))
-    log(f"forced-draft verify steps: {verify_step_ms:.3f} ms/step ({vdrafted} drafted, "
-        f"{vaccepted} accepted over {len(vt)} steps)")
+    greedy = rai_amd.LookupDecoder(model, max_ctx).greedy_generate(prompt, len(toks))
+    identical = greedy == toks and same_runs
+    log(f"token identity with plain greedy decoding: {identical}")
 
-    # Verify-GEMV roofline: the dominant W4A8 matrix at the verify batch size.
-    n, k = shape["intermediate_size"], shape["hidden_size"]
-    vms, vgbs, vbytes = measure_gemv(rai_amd, n, k, 9, gs)
-    dms, dgbs, _ = measure_gemv(rai_amd, n, k, 1, gs)
-    log(f"verify GEMV {n}x{k} M=9: {vms * 1e3:.1f} us, {vgbs:.0f} GB/s; M=1: {dms * 1e3:.1f} us, "
-        f"{dgbs:.0f} GB/s")
+    # Verify-step time on forced drafts at the same context (graphs warm).
+    dec.kv_cache.truncate(pos)
+    vt, vdrafted = forced_verify_steps(dec, list(prompt), pos, cfg, 34)
+    verify_step_ms = 1e3 * float(np.mean(vt[2:]))
+    log(f"forced-draft verify steps: {verify_step_ms:.3f} ms/step")
+
+    # Every W4A8 shape of the model step at the verify (9) and decode (1) sizes.
+    H, F, V = shape["hidden_size"], shape["intermediate_size"], shape["vocab_size"]
+    qd, kvd = shape["num_heads"] * shape["head_dim"], shape["num_kv_heads"] * shape["head_dim"]
+    shapes = {"qkv": (qd + 2 * kvd, H), "o_proj": (H, qd), "gate_up": (2 * F, H), "down": (H, F),
+              "lm_head": (V, H)}
+    kern = {}
+    for nm, (n, k) in shapes.items():
+        for m in (9, 1):
+            ms, gbs, _ = measure_gemv(rai_amd, n, k, m, gs)
+            kern[f"{nm}_{n}x{k}_m{m}"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                                          "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    log("GEMVs: " + ", ".join(f"{k} {v['us']}us {v['frac']:.3f}" for k, v in kern.items()))
+    rn, rk, rm = roofline_shape()
+    vms, vgbs, vbytes = measure_gemv(rai_amd, rn, rk, rm, gs, iters=100)
+    log(f"roofline GEMV {rn}x{rk} M={rm}: {vms * 1e3:.2f} us, {vgbs:.0f} GB/s")
 
     traffic = None
     if not args.no_traffic:
@@ -241,27 +318,29 @@ def main() -> int:
             t = measure_traffic(gs)
             if t is not None:
                 traffic = round(t["FETCH_SIZE"][0] + t["WRITE_SIZE"][0])
-                log(f"verify GEMV HBM traffic {traffic / 1e6:.2f} MB/launch (fetch {t['FETCH_SIZE'][0] / 1e6:.2f} "
-                    f"MB x{t['FETCH_SIZE'][1]:.3f}, write {t['WRITE_SIZE'][0] / 1e6:.2f} MB "
-                    f"x{t['WRITE_SIZE'][1]:.3f}) vs {vbytes / 1e6:.2f} MB algorithmic")
+                log(f"roofline GEMV HBM traffic {traffic / 1e6:.2f} MB/launch (fetch x{t['FETCH_SIZE'][1]:.3f}, "
+                    f"write x{t['WRITE_SIZE'][1]:.3f}) vs {vbytes / 1e6:.2f} MB algorithmic")
         except Exception as e:  # the counter passes are a report, not the run
             log(f"traffic passes failed: {e}")
 
-    cpu = None
+    cpu, cpu_all, cpu_name = None, None, None
     if not args.no_cpu:
-        threads = os.cpu_count() or 1
-        try:
-            import psutil
-            threads = len(psutil.Process().cpu_affinity()) or threads
-        except Exception:
-            pass
-        threads = min(threads, 16)
-        cv, cprod, cdt = cpu_baseline(img, shape, args.cpu_seconds, 64, threads)
-        cpu = {"value": round(cv, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": (f"CPU oracle (C++ AVX2 restatement of the reference path), same "
-                          f"{args.workload} model, 64-token copy-heavy prompt (prefill excluded), "
-                          f"greedy lookup n=3 k=8, {cprod} tokens in {cdt:.1f}s")}
-        log(f"cpu baseline {cv:.3f} tok/s on {threads} threads")
+        cpu_name, ncpu = host_cpu()
+        share = min(ncpu, 16)  # one GPU's share of the host
+        ref_threads = max(share // 2 + 1, 2)  # configure_thread_pool, gemm.rs:1746-1761
+        res = {}
+        for th in (ref_threads, share):
+            res[th] = cpu_baseline(img, shape, dec, prompt, pos, toks, args.cpu_seconds, th)
+            log(f"cpu baseline {res[th][0]:.3f} tok/s on {th} threads ({res[th][1]} tokens, "
+                f"tokens equal the GPU's: {res[th][3]})")
+        cv, cprod, cdt, cmatch = res[ref_threads]
+        cpu = {"value": round(cv, 3), "unit": "tok/s", "cores": ref_threads, "kind": "port",
+               "sample": (f"CPU oracle (C++ AVX2 restatement of the reference path) on {cpu_name}, "
+                          f"{ref_threads} threads (the reference default max(cpus/2+1, 2) for a "
+                          f"{share}-CPU share): greedy lookup n=3 k=8 from the same decoder state "
+                          f"(KV copied from the GPU after the {pos}-token prefill), {cprod} tokens in "
+                          f"{cdt:.1f}s, tokens equal to the GPU's: {cmatch}")}
+        cpu_all = {"value": round(res[share][0], 3), "threads": share, "tokens_equal_gpu": res[share][3]}
     del img
 
     line = {
@@ -269,35 +348,39 @@ def main() -> int:
         "value": round(value, 3),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": gen,
+        "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(1e3 * decode_s / max(gen, 1), 4),
+        "ms_per_step": round(1e3 * elapsed / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4xint8 (int32 accumulate, f32 epilogue)",
-        "data": "synthetic (random-init N(0,0.02) weights, copy-heavy random-id prompt)",
+        "data": "synthetic (random-init N(0,0.02) weights; copy-heavy random-id prompt quoting the model's "
+                "own greedy continuation)",
         "config": {
-            "workload": (f"{args.workload}-shaped W4A8 g32, {prompt_len}-token copy-heavy prompt, "
-                         f"prompt-lookup n=3 k=8 greedy, {args.steps} tokens, batch 1"),
-            "prefill_seconds": round(st["prefill_seconds"], 4),
-            "decode_steps": st["steps"],
+            "workload": (f"{args.workload}-shaped W4A8 g32, {prompt_len}-token copy-heavy prompt, prompt-lookup "
+                         f"n=3 k=8 greedy, {ntok} tokens per step, batch 1"),
+            "tokens_per_generation": st["generated"],
+            "decoder_steps_per_generation": st["steps"],
             "steps_with_draft": st["steps_with_draft"],
             "draft_tokens": st["drafted"],
             "accepted_draft_tokens": st["accepted"],
             "acceptance_rate": round(st["accepted"] / st["drafted"], 4) if st["drafted"] else None,
-            "tokens_per_step": round(gen / max(st["steps"], 1), 4),
+            "tokens_per_step": round(st["generated"] / max(st["steps"], 1), 4),
+            "token_identical_to_greedy": identical,
+            "prefill_seconds": round(prefill_s, 4),
+            "plain_decode_tok_s": round(plain_tok_s, 2),
             "verify_step_ms": round(verify_step_ms, 4),
-            "verify_step_note": (f"{len(vt) - 1} timed steps with a forced k=8 draft "
-                                 f"({vdrafted} drafted, {vaccepted} accepted): 9-token verify "
-                                 f"forward + lm_head + argmax + acceptance + KV rollback"),
-            "verify_gemv_us": round(vms * 1e3, 2),
-            "decode_gemv_us": round(dms * 1e3, 2),
-            "decode_gemv_gbs": round(dgbs, 1),
+            "verify_step_note": (f"{len(vt) - 2} timed decoder steps with a forced k=8 draft ({vdrafted} drafted "
+                                 f"over {len(vt)}): 9-token verify forward + lm_head + argmax + acceptance + "
+                                 f"KV rollback"),
+            "gemv_kernels": kern,
+            "cpu_host": cpu_name,
+            "cpu_all_cores": cpu_all,
         },
         "roofline": {"bound": "hbm", "achieved": round(vgbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(vgbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": f"w4a8 GEMV {n}x{k} g{gs} M=9", "bytes_per_launch": vbytes},
+                     "kernel": f"w4a8 GEMV gate|up {rn}x{rk} g{gs} M={rm}", "bytes_per_launch": vbytes},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

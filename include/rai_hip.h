@@ -125,6 +125,10 @@ int rai_kv_clear(rai_kv *kv);
 /* Copy one cached K or V row [head_dim] (kv_cache.rs:179-204 get_k/get_v);
  * which = 0 for K, 1 for V.  Reads at or above the watermark fail. */
 int rai_kv_read(const rai_kv *kv, size_t layer, size_t head, size_t pos, int which, float *out);
+/* get_k / get_v in bulk: rows [kv_head][npos][head_dim] of one layer for
+ * positions 0..npos (npos <= filled), e.g. to hand a decoder state to
+ * another implementation. */
+int rai_kv_export(const rai_kv *kv, size_t layer, int which, float *out, size_t npos);
 
 /* ---------------------------------------------------------- forward pass -- */
 /* RaiModel::embed_token (model.rs:371-403). */
@@ -176,6 +180,11 @@ int rai_tied_lm_head_dev(float *logits, const float *hidden, const uint8_t *code
 int rai_embed_lookup_dev(float *out, size_t token, const uint8_t *codes, const uint8_t *params,
                          size_t vocab, size_t hidden_size, size_t group_size, void *stream);
 
+/* argmax (sampler.rs:201-208) of each of `rows` logit rows [rows][vocab]:
+ * NaN counts as -inf, values compare by f32::total_cmp (-0 < +0), and the
+ * last maximal index wins.  Device pointers; out[rows] uint32. */
+int rai_argmax_dev(const float *logits, size_t rows, size_t vocab, uint32_t *out, void *stream);
+
 /* ------------------------------------------------ layer kernels (device) -- */
 /* rms_norm (layers.rs:154-183, 325-376) over m rows of n. */
 int rai_rms_norm_dev(float *out, const float *x, const float *weight, size_t m, size_t n,
@@ -214,6 +223,13 @@ int rai_lookup_step(rai_lookup *dec, size_t pos, const uint32_t *context, size_t
 int rai_lookup_generate(rai_lookup *dec, const uint32_t *prompt, size_t n, size_t max_tokens,
                         const rai_lookup_config *cfg, uint32_t *out_tokens, size_t out_cap,
                         size_t *n_out, rai_generate_stats *stats);
+/* The same loop without the prefill: steps from a decoder whose KV cache
+ * holds context[0..len-1) (pos = len - 1), e.g. after rai_lookup_prefill, or
+ * after rai_kv_truncate back to a prefilled prompt.  stats->prefill_seconds
+ * is 0. */
+int rai_lookup_decode(rai_lookup *dec, const uint32_t *context, size_t len, size_t pos,
+                      size_t max_tokens, const rai_lookup_config *cfg, uint32_t *out_tokens,
+                      size_t out_cap, size_t *n_out, rai_generate_stats *stats);
 /* Plain greedy decode (sampler.rs:61-64 argmax after decode_one), used for the
  * token-identity check: prefill, then `steps` single-token steps. */
 int rai_greedy_generate(rai_lookup *dec, const uint32_t *prompt, size_t n, size_t steps,
@@ -238,6 +254,13 @@ typedef struct rai_synth_config {
 int rai_synth_model(const rai_synth_config *cfg, uint64_t seed, const char *path, uint8_t **image,
                     size_t *image_len);
 void rai_free_image(uint8_t *image);
+
+/* Test hook (no reference counterpart): the poll limit of the attention
+ * kernel's bounded tile hand-off waits for launches enqueued from now on
+ * (<= 0 restores the default).  A tiny limit makes the waits give up; every
+ * kernel still ends, and the call that ran it fails with RAI_E_HIP.  Step
+ * graphs keep the limit they were captured with. */
+int rai_debug_set_attention_spin(int polls);
 
 /* Device-memory plumbing for harnesses that bind only this ABI. */
 int rai_dev_malloc(size_t bytes, void **out);

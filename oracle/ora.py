@@ -77,6 +77,8 @@ def lib():
         "ora_kv_free": (None, [P]),
         "ora_kv_truncate": (c_int, [P, c_int]),
         "ora_kv_filled": (c_int, [P, c_int]),
+        "ora_kv_read": (c_int, [P, c_int, c_int, c_int, c_int, P]),
+        "ora_route_experts": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P]),
         "ora_embed_token": (c_int, [P, c_int, P]),
         "ora_forward_from_hidden": (c_int, [P, P, P, c_int, c_int]),
         "ora_forward_batch": (c_int, [P, P, P, P, c_int]),
@@ -88,6 +90,7 @@ def lib():
         "ora_lookup_step_greedy": (c_int, [P, c_int, P, c_int, c_int, c_int, c_int, P,
                                            POINTER(OracleMetrics)]),
         "ora_lookup_kv_filled": (c_int, [P]),
+        "ora_lookup_import_kv": (c_int, [P, c_int, c_int, P, c_int]),
         "ora_greedy_generate": (c_int, [P, P, c_int, c_int, c_int, P]),
     }
     for name, (res, args) in sig.items():
@@ -205,8 +208,8 @@ def rope_tables(head_dim, max_ctx, theta):
 
 def rope_apply(heads, num_heads, head_dim, cos_row, sin_row):
     h = f32(heads).copy()
-    _check(lib().ora_rope_apply(_ptr(h), num_heads, head_dim, _ptr(f32(cos_row)),
-                                _ptr(f32(sin_row))))
+    c, s = f32(cos_row), f32(sin_row)  # kept alive across the call
+    _check(lib().ora_rope_apply(_ptr(h), num_heads, head_dim, _ptr(c), _ptr(s)))
     return h
 
 
@@ -228,6 +231,16 @@ def schraudolph(x: float) -> float:
 def argmax(v) -> int:
     v = f32(v)
     return int(lib().ora_argmax(_ptr(v), v.size))
+
+
+def route_experts(router, x, num_experts, topk, norm_topk_prob=False):
+    """route_experts (layers.rs:1808-1870): (experts, weights) of one token."""
+    router, x = f32(router), f32(x)
+    sel = np.zeros(topk, np.int32)
+    wts = np.zeros(topk, np.float32)
+    _check(lib().ora_route_experts(_ptr(router), _ptr(x), x.size, num_experts, topk,
+                                   int(norm_topk_prob), _ptr(sel), _ptr(wts)))
+    return sel, wts
 
 
 def find_ngram_draft(tokens, min_ngram, max_ngram, max_draft):
@@ -283,12 +296,14 @@ class Model:
 
     def hidden_to_logits(self, hidden):
         out = np.zeros(self.cfg.vocab_size, np.float32)
-        _check(lib().ora_hidden_to_logits(self.h, _ptr(f32(hidden)), _ptr(out)))
+        h = f32(hidden)  # kept alive across the call
+        _check(lib().ora_hidden_to_logits(self.h, _ptr(h), _ptr(out)))
         return out
 
     def hidden_to_logits_batch(self, hiddens, batch):
         out = np.zeros(batch * self.cfg.vocab_size, np.float32)
-        _check(lib().ora_hidden_to_logits_batch(self.h, _ptr(f32(hiddens)), _ptr(out), batch))
+        h = f32(hiddens)  # kept alive across the call
+        _check(lib().ora_hidden_to_logits_batch(self.h, _ptr(h), _ptr(out), batch))
         return out.reshape(batch, self.cfg.vocab_size)
 
     def greedy_generate(self, prompt, steps, max_ctx):
@@ -309,6 +324,16 @@ class KVCache:
 
     def filled(self, layer: int = 0) -> int:
         return lib().ora_kv_filled(self.h, layer)
+
+    def get_k(self, layer: int, head: int, pos: int, head_dim: int) -> np.ndarray:
+        out = np.zeros(head_dim, np.float32)
+        _check(lib().ora_kv_read(self.h, layer, head, pos, 0, _ptr(out)))
+        return out
+
+    def get_v(self, layer: int, head: int, pos: int, head_dim: int) -> np.ndarray:
+        out = np.zeros(head_dim, np.float32)
+        _check(lib().ora_kv_read(self.h, layer, head, pos, 1, _ptr(out)))
+        return out
 
     def __del__(self):
         try:
@@ -342,6 +367,11 @@ class LookupDecoder:
 
     def kv_filled(self) -> int:
         return lib().ora_lookup_kv_filled(self.h)
+
+    def import_kv(self, layer: int, which: int, rows: np.ndarray) -> None:
+        """Set one layer's K (0) or V (1) cache rows [nkv][npos][head_dim]."""
+        r = f32(rows)
+        _check(lib().ora_lookup_import_kv(self.h, layer, which, _ptr(r), r.shape[1]))
 
     def __del__(self):
         try:

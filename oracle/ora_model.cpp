@@ -225,15 +225,15 @@ static void attend(const Model &m, const KV &kv, int li, const float *q, int pos
   }
 }
 
-// route_experts (layers.rs:1808-1870) + the MoE arm of mlp_block
-// (model.rs:208-261) for one token.
-static void moe_token(const Model &m, const Layer &L, const float *x, float *out) {
-  const ora_config &c = m.cfg;
-  const int H = c.hidden_size, F = c.intermediate_size, E = c.num_experts;
+// route_experts (layers.rs:1808-1870): router logits (dot_f32, a
+// sequential f32 sum), softmax over all experts, top-k by selection sort
+// (ties: lowest index), optional renormalisation of the chosen weights.
+static void route_experts(const float *router, const float *x, int H, int E, int topk, bool norm_topk,
+                          std::vector<int> &sel, std::vector<float> &wts) {
   std::vector<float> probs(E);
   for (int e = 0; e < E; ++e) {
     float s = -0.0f;  // Rust's f32 Sum starts at -0.0
-    for (int i = 0; i < H; ++i) s += L.router[(size_t)e * H + i] * x[i];
+    for (int i = 0; i < H; ++i) s += router[(size_t)e * H + i] * x[i];
     probs[e] = s;
   }
   float mx = -INFINITY;
@@ -244,10 +244,10 @@ static void moe_token(const Model &m, const Layer &L, const float *x, float *out
     sum += p;
   }
   for (float &p : probs) p /= sum;
-  std::vector<int> sel;
-  std::vector<float> wts;
+  sel.clear();
+  wts.clear();
   std::vector<bool> taken(E, false);
-  for (uint32_t k = 0; k < c.experts_per_token; ++k) {
+  for (int k = 0; k < topk; ++k) {
     int best = -1;
     float bv = -INFINITY;
     for (int e = 0; e < E; ++e)
@@ -260,12 +260,21 @@ static void moe_token(const Model &m, const Layer &L, const float *x, float *out
     sel.push_back(best);
     wts.push_back(bv);
   }
-  if (c.norm_topk_prob) {
+  if (norm_topk) {
     float tot = -0.0f;
     for (float w : wts) tot += w;
     if (tot > 0.0f)
       for (float &w : wts) w /= tot;
   }
+}
+
+// The MoE arm of mlp_block (model.rs:208-261) for one token.
+static void moe_token(const Model &m, const Layer &L, const float *x, float *out) {
+  const ora_config &c = m.cfg;
+  const int H = c.hidden_size, F = c.intermediate_size, E = c.num_experts;
+  std::vector<int> sel;
+  std::vector<float> wts;
+  route_experts(L.router.data(), x, H, E, (int)c.experts_per_token, c.norm_topk_prob != 0, sel, wts);
   std::vector<float> gate(F), up(F), eo(H);
   for (int i = 0; i < H; ++i) out[i] = 0.0f;
   for (size_t s = 0; s < sel.size(); ++s) {
@@ -544,6 +553,27 @@ int ora_kv_truncate(ora_kv *kv, int len) {
   ORA_TRY(for (int &f : kv->kv.filled) f = std::min(f, len));
 }
 int ora_kv_filled(const ora_kv *kv, int layer) { return kv->kv.filled.at(layer); }
+int ora_kv_read(const ora_kv *kv, int layer, int head, int pos, int which, float *out) {
+  ORA_TRY({
+    const KV &k = kv->kv;
+    if (layer < 0 || layer >= k.layers || head < 0 || head >= k.nkv) fail("KV head out of range");
+    if (pos < 0 || pos >= k.filled[layer]) fail("KV read above the watermark");
+    const std::vector<float> &src = which == 0 ? k.k[layer] : k.v[layer];
+    std::memcpy(out, &src[((size_t)head * k.cap + pos) * k.hd], sizeof(float) * k.hd);
+  });
+}
+int ora_route_experts(const float *router, const float *x, int hidden, int num_experts, int topk,
+                      int norm_topk_prob, int32_t *experts, float *weights) {
+  ORA_TRY({
+    std::vector<int> sel;
+    std::vector<float> wts;
+    route_experts(router, x, hidden, num_experts, topk, norm_topk_prob != 0, sel, wts);
+    for (int k = 0; k < topk; ++k) {
+      experts[k] = k < (int)sel.size() ? sel[k] : -1;
+      weights[k] = k < (int)wts.size() ? wts[k] : 0.0f;
+    }
+  });
+}
 int ora_embed_token(const ora_model *m, int token, float *out) { ORA_TRY(embed(m->m, token, out)); }
 int ora_forward_from_hidden(const ora_model *m, ora_kv *kv, float *hidden, int pos, int store_kv) {
   ORA_TRY({
@@ -576,6 +606,17 @@ int ora_lookup_create(const ora_model *m, int max_ctx, ora_lookup **out) {
   });
 }
 void ora_lookup_free(ora_lookup *d) { delete d; }
+int ora_lookup_import_kv(ora_lookup *dd, int layer, int which, const float *rows, int npos) {
+  ORA_TRY({
+    KV &k = dd->d.kv;
+    if (layer < 0 || layer >= k.layers) fail("layer out of range");
+    if (npos < 0 || npos > k.cap) fail("positions exceed the cache");
+    std::vector<float> &dst = which == 0 ? k.k[layer] : k.v[layer];
+    for (int h = 0; h < k.nkv; ++h)
+      std::memcpy(&dst[(size_t)h * k.cap * k.hd], rows + (size_t)h * npos * k.hd, sizeof(float) * npos * k.hd);
+    k.filled[layer] = npos;
+  });
+}
 int ora_lookup_kv_filled(const ora_lookup *d) { return d->d.kv.filled.at(0); }
 
 // LookupDecoder::prefill (lookup.rs:219-247).

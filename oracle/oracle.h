@@ -96,6 +96,12 @@ int ora_kv_create(const ora_model *m, int max_ctx, ora_kv **out);
 void ora_kv_free(ora_kv *kv);
 int ora_kv_truncate(ora_kv *kv, int len);
 int ora_kv_filled(const ora_kv *kv, int layer);
+/* One cached K (which = 0) or V (which = 1) row [head_dim] (kv_cache.rs:179-204). */
+int ora_kv_read(const ora_kv *kv, int layer, int head, int pos, int which, float *out);
+/* route_experts (layers.rs:1808-1870) for one token: experts[k] / weights[k]
+ * for k < topk (-1 / 0 past the selection). */
+int ora_route_experts(const float *router, const float *x, int hidden, int num_experts, int topk,
+                      int norm_topk_prob, int32_t *experts, float *weights);
 int ora_embed_token(const ora_model *m, int token, float *out);
 int ora_forward_from_hidden(const ora_model *m, ora_kv *kv, float *hidden, int pos,
                             int store_kv);
@@ -113,6 +119,11 @@ int ora_lookup_step_greedy(ora_lookup *d, int pos, const int32_t *context, int l
                            int max_draft, int min_ngram, int max_ngram,
                            int32_t *out_tokens, ora_metrics *metrics);
 int ora_lookup_kv_filled(const ora_lookup *d);
+/* Replace layer `layer`'s K (which = 0) or V (which = 1) rows with
+ * rows[nkv][npos][head_dim] and set its watermark to npos (a decoder state
+ * taken from another implementation, e.g. to time steps at a long context
+ * without running the prefill on the CPU). */
+int ora_lookup_import_kv(ora_lookup *d, int layer, int which, const float *rows, int npos);
 /* Plain greedy decode: prefill prompt[0..n-1], then `steps` decode_one calls. */
 int ora_greedy_generate(const ora_model *m, const int32_t *prompt, int n, int steps,
                         int max_ctx, int32_t *out_tokens);

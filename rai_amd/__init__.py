@@ -112,6 +112,7 @@ def lib():
         "rai_w4a8_time_dev": (c_int, [P, P, P, P, S, S, S, S, S, c_int, POINTER(c_float)]),
         "rai_tied_lm_head_dev": (c_int, [P, P, P, P, S, S, S, P]),
         "rai_embed_lookup_dev": (c_int, [P, S, P, P, S, S, S, P]),
+        "rai_argmax_dev": (c_int, [P, S, S, P, P]),
         "rai_rms_norm_dev": (c_int, [P, P, P, S, S, c_float, P]),
         "rai_silu_mul_dev": (c_int, [P, P, S, S, P]),
         "rai_rope_apply_dev": (c_int, [P, S, S, P, P, P]),
@@ -125,10 +126,14 @@ def lib():
                                     POINTER(_LookupMetrics)]),
         "rai_lookup_generate": (c_int, [P, P, S, S, POINTER(_LookupConfig), P, S,
                                         POINTER(c_size_t), POINTER(_GenerateStats)]),
+        "rai_lookup_decode": (c_int, [P, P, S, S, S, POINTER(_LookupConfig), P, S,
+                                      POINTER(c_size_t), POINTER(_GenerateStats)]),
+        "rai_kv_export": (c_int, [P, S, c_int, P, S]),
         "rai_greedy_generate": (c_int, [P, P, S, S, P]),
         "rai_synth_model": (c_int, [POINTER(SynthConfig), c_uint64, c_char_p,
                                     POINTER(c_void_p), POINTER(c_size_t)]),
         "rai_free_image": (None, [P]),
+        "rai_debug_set_attention_spin": (c_int, [c_int]),
         "rai_dev_malloc": (c_int, [S, POINTER(c_void_p)]),
         "rai_dev_free": (c_int, [P]),
         "rai_memcpy_h2d": (c_int, [P, P, S]),
@@ -174,6 +179,11 @@ def device_info() -> tuple[str, int]:
     cus = c_int()
     _check(lib().rai_device_info(buf, 256, ctypes.byref(cus)))
     return buf.value.decode(), cus.value
+
+
+def set_attention_spin(polls: int) -> None:
+    """Test hook: poll limit of the attention tile hand-off waits (0 = default)."""
+    _check(lib().rai_debug_set_attention_spin(polls))
 
 
 # ---------------------------------------------------------------- device mem --
@@ -286,6 +296,15 @@ def embed_lookup(token: int, codes, params, vocab: int, hidden: int, group_size:
     _check(lib().rai_embed_lookup_dev(do.ptr, token, dc.ptr, dp.ptr, vocab, hidden,
                                       group_size, None))
     return do.to_host(np.float32, hidden)
+
+
+def argmax(logits) -> np.ndarray:
+    """argmax (sampler.rs:201-208) of each row, on the GPU."""
+    x = np.atleast_2d(_f32(logits))
+    dx = DeviceArray.from_host(x)
+    do = DeviceArray(4 * x.shape[0])
+    _check(lib().rai_argmax_dev(dx.ptr, x.shape[0], x.shape[1], do.ptr, None))
+    return do.to_host(np.uint32, x.shape[0]).astype(np.int64)
 
 
 def rms_norm(x, weight, eps: float) -> np.ndarray:
@@ -442,12 +461,14 @@ class RaiModel:
 
     def hidden_to_logits(self, hidden) -> np.ndarray:
         out = np.zeros(self.config.vocab_size, np.float32)
-        _check(lib().rai_hidden_to_logits(self.h, _ptr(_f32(hidden)), _ptr(out)))
+        h = _f32(hidden)  # kept alive across the call
+        _check(lib().rai_hidden_to_logits(self.h, _ptr(h), _ptr(out)))
         return out
 
     def hidden_to_logits_batch(self, hiddens, batch: int) -> np.ndarray:
         out = np.zeros(batch * self.config.vocab_size, np.float32)
-        _check(lib().rai_hidden_to_logits_batch(self.h, _ptr(_f32(hiddens)), _ptr(out), batch))
+        h = _f32(hiddens)  # kept alive across the call
+        _check(lib().rai_hidden_to_logits_batch(self.h, _ptr(h), _ptr(out), batch))
         return out.reshape(batch, self.config.vocab_size)
 
 
@@ -478,6 +499,12 @@ class KVCache:
     def get_v(self, layer: int, head: int, pos: int, head_dim: int) -> np.ndarray:
         out = np.zeros(head_dim, np.float32)
         _check(lib().rai_kv_read(self.h, layer, head, pos, 1, _ptr(out)))
+        return out
+
+    def export(self, layer: int, which: int, npos: int, num_kv_heads: int, head_dim: int) -> np.ndarray:
+        """K (which = 0) or V (1) rows [kv_head][npos][head_dim] of one layer."""
+        out = np.zeros((num_kv_heads, npos, head_dim), np.float32)
+        _check(lib().rai_kv_export(self.h, layer, which, _ptr(out), npos))
         return out
 
     def __del__(self):
@@ -549,6 +576,18 @@ class LookupDecoder:
         cfg = config._c()
         _check(lib().rai_lookup_generate(self.h, _ptr(p), p.size, max_tokens, ctypes.byref(cfg),
                                          _ptr(out), out.size, ctypes.byref(n), ctypes.byref(st)))
+        stats = {f: getattr(st, f) for f, _ in _GenerateStats._fields_}
+        return out[:n.value].tolist(), stats
+
+    def decode(self, context, pos: int, max_tokens: int, config: LookupConfig):
+        """The generate loop from a prefilled state (KV holds context[:-1])."""
+        c = _u32(context)
+        out = np.zeros(max_tokens + config.max_draft + 1, np.uint32)
+        n = c_size_t()
+        st = _GenerateStats()
+        cfg = config._c()
+        _check(lib().rai_lookup_decode(self.h, _ptr(c), c.size, pos, max_tokens, ctypes.byref(cfg),
+                                       _ptr(out), out.size, ctypes.byref(n), ctypes.byref(st)))
         stats = {f: getattr(st, f) for f, _ in _GenerateStats._fields_}
         return out[:n.value].tolist(), stats
 

@@ -605,15 +605,19 @@ struct PvCfg {
 // until every compute wave has finished chunk c - 2 (the same tile half),
 // publishes V and probabilities, then posts ready[c & 1] = c; a compute wave
 // waits for ready[k & 1] >= k, runs the chunk's chains and posts its
-// done[w] = k + 1.  Every wait is bounded (kPvSpin polls), so a wait that
-// could not end still lets the block finish.
+// done[w] = k + 1.  Every wait is bounded (`spin` polls, kPvSpin unless a
+// caller lowers it), so a wait that could not end still lets the block
+// finish; a wait that gives up sets bit 0 of the error word `err`, which the
+// host turns into an error for the whole call (the block's output is then
+// not trusted).
 constexpr int kPvSpin = 1 << 22;
 
 // Poll an LDS word until it is at least `want` (every lane reads the same
-// word; at most kPvSpin polls).  One asm block, so the compiler keeps the
-// loads that follow inside the block that uses them.
+// word; at most `spin` polls).  One asm block, so the compiler keeps the
+// loads that follow inside the block that uses them.  Returns the last value
+// read: below `want` when the wait gave up.
 template <bool SLEEP>
-__device__ __forceinline__ void lds_wait_ge(const int *flag, int want) {
+__device__ __forceinline__ int lds_wait_ge(const int *flag, int want, int spin) {
   typedef const __attribute__((address_space(3))) int lds_int;
   const unsigned addr = (unsigned)(uintptr_t)((lds_int *)flag);
   int seen;
@@ -632,7 +636,7 @@ __device__ __forceinline__ void lds_wait_ge(const int *flag, int want) {
         "s_cbranch_scc1 1b\n"
         "2:"
         : "=&v"(seen), "=&s"(polls)
-        : "v"(addr), "v"(want), "s"(kPvSpin)
+        : "v"(addr), "v"(want), "s"(spin)
         : "vcc", "scc", "memory");
   } else {
     asm volatile(
@@ -647,16 +651,22 @@ __device__ __forceinline__ void lds_wait_ge(const int *flag, int want) {
         "s_cbranch_scc1 1b\n"
         "2:"
         : "=&v"(seen), "=&s"(polls)
-        : "v"(addr), "v"(want), "s"(kPvSpin)
+        : "v"(addr), "v"(want), "s"(spin)
         : "vcc", "scc", "memory");
   }
+  return seen;
+}
+
+// Record a wait that gave up (one lane per wave; a vector atomic).
+__device__ __forceinline__ void pv_wait_failed(int *err) {
+  if (err && (threadIdx.x & 63) == 0) atomicOr(err, 1);
 }
 
 
 template <int DL, int G, int CP, int TM, int NL>
 __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
     const float *__restrict__ P, const float *__restrict__ vt_g, int vstride, int pos0, int m, int nh, int hd,
-    int sstride, float *__restrict__ out, const int *__restrict__ st) {
+    int sstride, float *__restrict__ out, const int *__restrict__ st, int *__restrict__ err, int spin) {
   using C = PvCfg<DL, G, CP, TM, NL>;
   if (st) pos0 = st[0];
   constexpr int NCW = C::NCW, NV = C::NV, NP = C::NP, STR = C::STR;
@@ -735,7 +745,7 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
   float acc = 0.0f;
   for (int k = 0; k < nchunks; ++k) {
     if (wave < NCW) {
-      lds_wait_ge<false>(&ready[k & 1], k);
+      if (lds_wait_ge<false>(&ready[k & 1], k, spin) < k) pv_wait_failed(err);
       const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
       const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][(tl * G + g) * STR]);
       // Rolling prefetch: the next 8 float4 pairs (32 positions) are
@@ -780,7 +790,8 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
       // Tile half (k + 1) & 1 held chunk k - 1: wait until every compute
       // wave has consumed it.
 #pragma unroll
-      for (int w = 0; w < NCW; ++w) lds_wait_ge<true>(&done[w], k);
+      for (int w = 0; w < NCW; ++w)
+        if (lds_wait_ge<true>(&done[w], k, spin) < k) pv_wait_failed(err);
       publish(k + 1);
       __hip_atomic_store(&ready[(k + 1) & 1], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       if (k + 1 + NL < nchunks) issue(k + 1 + NL);
@@ -791,10 +802,10 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
 
 template <int DL, int G, int CP, int TM, int NL>
 void launch_pv_flag(const float *scores, const float *vc, int vstride, int p0, int m, int nh, int nkv, int hd,
-                    int sstride, float *out, const int *st, hipStream_t s) {
+                    int sstride, float *out, const int *st, int *err, int spin, hipStream_t s) {
   const dim3 pg(nkv * (hd / DL), (m + TM - 1) / TM);
   hipLaunchKernelGGL((k_pv_flag<DL, G, CP, TM, NL>), pg, dim3(PvCfg<DL, G, CP, TM, NL>::NT), 0, s, scores, vc,
-                     vstride, p0, m, nh, hd, sstride, out, st);
+                     vstride, p0, m, nh, hd, sstride, out, st, err, spin);
 }
 
 // PV for any head_dim: thread per output element, same chain order.  V
@@ -934,15 +945,21 @@ size_t attention_scores_floats(int m, int nh, int ctx) {
   return (size_t)std::min(m, kAttnTokens) * nh * (size_t)((ctx + 3) & ~3);
 }
 
+static int g_pv_spin = kPvSpin;
+
+void set_attention_spin(int polls) { g_pv_spin = polls > 0 ? polls : kPvSpin; }
+
 void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
                       int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
-                      float *out, float *scores, hipStream_t s, const int *st) {
+                      float *out, float *scores, hipStream_t s, const int *st, int *err) {
   static size_t sm_configured = 0;
   for (int t0 = 0; t0 < m; t0 += kAttnTokens) {
     const int mt = std::min(kAttnTokens, m - t0);
     const int p0 = pos0 + t0;
-    // With a step record the position is on the device: size for capacity.
-    const int nmax = st ? cap : p0 + mt;
+    // With a step record the position is on the device: size for the
+    // capacity, capped at the longest context a forward accepts (so the
+    // register-resident softmax always applies).
+    const int nmax = st ? std::min(cap, kMaxAttnPositions) : p0 + mt;
     const int sstride = (nmax + 3) & ~3;
     const float *qt = q + (size_t)t0 * q_ld;
     float *ot = out + (size_t)t0 * nh * hd;
@@ -979,19 +996,19 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
       // 4.35K positions with V streamed from HBM (four for one token, three
       // for three).
       if (G == 4 && mt > 12)
-        launch_pv_flag<16, 4, 128, 4, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 4, 128, 4, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 4 && mt > 2)
-        launch_pv_flag<16, 4, 256, 3, 3>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 4, 256, 3, 3>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 4)
-        launch_pv_flag<16, 4, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 4, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 8)
-        launch_pv_flag<16, 8, 256, 1, 6>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 8, 256, 1, 6>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 16)
-        launch_pv_flag<16, 16, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<16, 16, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 2)
-        launch_pv_flag<32, 2, 128, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<32, 2, 128, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else
-        launch_pv_flag<64, 1, 64, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, s);
+        launch_pv_flag<64, 1, 64, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
     } else if (vstride > 0) {
       hipLaunchKernelGGL(k_pv_any<true>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, scores,
                          vc, cap, vstride, p0, mt, nh, nkv, hd, sstride, ot, st);

@@ -142,11 +142,19 @@ constexpr int kAttnTokens = 64;
 size_t attention_scores_floats(int m, int nh, int ctx);
 // q rows are q_ld floats apart; out is [m][nh * hd].
 // With a step record `st` (m <= kAttnTokens), grids and the score stride
-// are sized for the whole capacity `cap` so the launch does not depend on
-// the position.
+// are sized for min(cap, kMaxAttnPositions) so the launch does not depend on
+// the position.  `err` (may be null): bit 0 is set when a PV tile hand-off
+// wait gave up (the output is then wrong and the caller must fail).
+// Longest context (positions) the attention launches accept.
+constexpr int kMaxAttnPositions = 16384;
 void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
                       int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
-                      float *out, float *scores, hipStream_t s, const int *st = nullptr);
+                      float *out, float *scores, hipStream_t s, const int *st = nullptr,
+                      int *err = nullptr);
+// Poll limit of the PV tile hand-off waits for launches enqueued from now
+// on (<= 0 restores the default).  Lowering it is for tests of the error
+// path: the waits then give up and report it, and every block still ends.
+void set_attention_spin(int polls);
 // Standalone RoPE of one position (layers.rs:643-726) on heads [nh][hd].
 void launch_rope_apply(float *heads, int nh, int hd, const float *cos_row, const float *sin_row,
                        hipStream_t s);

@@ -31,8 +31,8 @@ void set_last_error(const std::string &m) { g_last_error = m; }
            std::string(#expr) + ": " + hipGetErrorString(e_));                           \
   } while (0)
 
-// Largest attention context the LDS-resident score buffer handles.
-constexpr size_t kMaxAttnContext = 16384;
+// Largest attention context the register-resident softmax handles.
+constexpr size_t kMaxAttnContext = kMaxAttnPositions;
 // Tokens per forward chunk (prefill is split into chunks of this size; the
 // per-token arithmetic does not depend on the split).
 constexpr int kChunk = 256;
@@ -530,7 +530,7 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
       launch_rope_store(qp, kp, vp, md.rope_cos, md.rope_sin, (int)pos0, m, nh, nkv, hd, kv.kc(li), kv.vc(li),
                         (int)kv.cap, (int)kv.vstride, q_ld, kv_ld, s, st);
     launch_attention(qp, q_ld, kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, (int)pos0, m, nh, nkv, hd,
-                     md.attn_scale, w.att.as<float>(), scores, s, st);
+                     md.attn_scale, w.att.as<float>(), scores, s, st, w.err.as<int>() + 1);
     // o_proj with the first residual add (model.rs:858-863) in its epilogue;
     // one token: the GEMV launch quantizes the attention output itself.
     const DLinear &O = L.lin[3];
@@ -630,14 +630,24 @@ static void embed_tokens(rai_model &md, Workspace &w, const uint32_t *dev_tokens
                c.embed_group_size, c.embed_scale, w.hid.as<float>(), w.err.as<int>(), s);
 }
 
-static void check_kernel_error(Workspace &w, hipStream_t s) {
-  int e = 0;
-  HIP_CHECK(hipMemcpyAsync(&e, w.err.p, sizeof(int), hipMemcpyDeviceToHost, s));
+// The workspace error words the kernels set: [0] a token id outside the
+// vocabulary (embedding), [1] an attention tile hand-off wait that gave up.
+// `e` holds both words as read back after the stream finished; a set word
+// is cleared on the device and raised as the call's error.
+static void raise_kernel_errors(Workspace &w, hipStream_t s, const int *e) {
+  if (!e[0] && !e[1]) return;
+  HIP_CHECK(hipMemsetAsync(w.err.p, 0, 2 * sizeof(int), s));
   HIP_CHECK(hipStreamSynchronize(s));
-  if (e) {
-    HIP_CHECK(hipMemsetAsync(w.err.p, 0, sizeof(int), s));
-    fail(RAI_E_RANGE, "token id is out of model vocabulary");
-  }
+  if (e[1]) fail(RAI_E_HIP, "attention tile hand-off wait gave up (results discarded)");
+  fail(RAI_E_RANGE, "token id is out of model vocabulary");
+}
+
+static void check_kernel_error(Workspace &w, hipStream_t s) {
+  int e[2] = {0, 0};
+  HIP_CHECK(hipGetLastError());
+  HIP_CHECK(hipMemcpyAsync(e, w.err.p, sizeof(e), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  raise_kernel_errors(w, s, e);
 }
 
 Workspace &model_ws(rai_model &m) {
@@ -754,6 +764,7 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
     launch_argmax(d.ws.logits.as<float>(), m, c.vocab_size, d.ws.am.as<uint32_t>(), s);
     launch_accept(d.ws.am.as<uint32_t>(), d.ctx.as<uint32_t>(), (int)len, start, nd, res + 4, s, st);
   };
+  HIP_CHECK(hipGetLastError());  // nothing pending from earlier launches
   if (d.graphs && m <= kAttnTokens) {
     int *sh = d.pin + 512;
     sh[0] = (int)pos;
@@ -766,11 +777,18 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
       HIP_CHECK(hipGraphLaunch(d.graph[m], s));
     } else if (d.graph_uses[m]++ == 0) {
       enqueue(st);  // first use: eager (sets kernel attributes, sizes scratch)
+      HIP_CHECK(hipGetLastError());
     } else {
       hipGraph_t g = nullptr;
       HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
       enqueue(st);
-      HIP_CHECK(hipStreamEndCapture(s, &g));
+      const hipError_t le = hipGetLastError();
+      const hipError_t ce = hipStreamEndCapture(s, &g);
+      if (le != hipSuccess || ce != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        HIP_CHECK(le);
+        HIP_CHECK(ce);
+      }
       hipGraphExec_t ge = nullptr;
       const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
       (void)hipGraphDestroy(g);
@@ -780,18 +798,21 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
     }
   } else {
     enqueue(nullptr);
+    HIP_CHECK(hipGetLastError());
   }
-  forward_commit(d.kv, m, pos);
   HIP_CHECK(hipMemcpyAsync(d.pin + 4, res + 4, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipMemcpyAsync(d.pin + 6, d.ws.err.p, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
   HIP_CHECK(hipMemcpyAsync(d.pin + 8, d.ctx.as<uint32_t>() + len, (size_t)m * sizeof(uint32_t),
                            hipMemcpyDeviceToHost, s));
   HIP_CHECK(hipStreamSynchronize(s));
-  int kerr = 0;
-  HIP_CHECK(hipMemcpy(&kerr, d.ws.err.p, sizeof(int), hipMemcpyDeviceToHost));
-  if (kerr) {
-    HIP_CHECK(hipMemset(d.ws.err.p, 0, sizeof(int)));
-    fail(RAI_E_RANGE, "context contains a token outside the model vocabulary");
+  if (d.pin[6] || d.pin[7]) {
+    // The step's outputs are not trusted: the KV rows it wrote stay above
+    // the watermark and the device context past len is ignored.
+    d.ctx_len = std::min(d.ctx_len, len);
+    const int e[2] = {d.pin[6], d.pin[7]};
+    raise_kernel_errors(d.ws, s, e);
   }
+  forward_commit(d.kv, m, pos);
   const int acc = d.pin[4], prod = d.pin[5];
   for (int i = 0; i < prod; ++i) out[i] = (uint32_t)d.pin[8 + i];
   // The accept kernel already appended the produced tokens to the device
@@ -821,7 +842,12 @@ static void lookup_prefill(rai_lookup &d, const uint32_t *prompt, size_t n, size
                  d.ws.err.as<int>(), d.stream);
     forward(md, d.kv, d.ws, m, p, d.stream);
   }
-  HIP_CHECK(hipStreamSynchronize(d.stream));
+  try {
+    check_kernel_error(d.ws, d.stream);
+  } catch (...) {
+    for (auto &f : d.kv.filled) f = 0;  // nothing of this prefill is trusted
+    throw;
+  }
   pos_out = cnt;
 }
 
@@ -967,13 +993,19 @@ int rai_forward_batch(rai_model *m, rai_kv *kv, float *hiddens, const size_t *po
     }
     rai::Workspace &w = rai::model_ws(*m);
     const size_t H = m->cfg.hidden_size;
+    const std::vector<size_t> filled0 = kv->filled;
     for (size_t b0 = 0; b0 < batch; b0 += rai::kChunk) {
       const int mm = (int)std::min<size_t>(rai::kChunk, batch - b0);
       HIP_CHECK(hipMemcpyAsync(w.hid.p, hiddens + b0 * H, sizeof(float) * H * mm, hipMemcpyHostToDevice, m->stream));
       rai::forward(*m, *kv, w, mm, positions[b0], m->stream);
       HIP_CHECK(hipMemcpyAsync(hiddens + b0 * H, w.hid.p, sizeof(float) * H * mm, hipMemcpyDeviceToHost, m->stream));
     }
-    HIP_CHECK(hipStreamSynchronize(m->stream));
+    try {
+      rai::check_kernel_error(w, m->stream);
+    } catch (...) {
+      kv->filled = filled0;  // the batch's KV rows are not trusted
+      throw;
+    }
   });
 }
 
@@ -1160,6 +1192,17 @@ int rai_embed_lookup_dev(float *out, size_t token, const uint8_t *codes, const u
   });
 }
 
+int rai_argmax_dev(const float *logits, size_t rows, size_t vocab, uint32_t *out, void *stream) {
+  RAI_API_BODY({
+    if (!logits || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (rows == 0 || vocab == 0) rai::fail(RAI_E_SHAPE, "argmax over an empty row");
+    if (rows > INT32_MAX || vocab > INT32_MAX) rai::fail(RAI_E_SHAPE, "dimensions overflow");
+    launch_argmax(logits, (int)rows, (int)vocab, out, (hipStream_t)stream);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipStreamSynchronize((hipStream_t)stream));
+  });
+}
+
 int rai_rms_norm_dev(float *out, const float *x, const float *w, size_t m, size_t n, float eps, void *stream) {
   RAI_API_BODY({
     if (!out || !x || !w) rai::fail(RAI_E_ARG, "null argument");
@@ -1278,6 +1321,38 @@ int rai_lookup_step(rai_lookup *d, size_t pos, const uint32_t *context, size_t l
   });
 }
 
+namespace rai {
+
+// The decode loop of `rai run --lookup-k` (cli/run.rs:517-633) after the
+// prefill: steps from (pos, context) until max_tokens are generated or the
+// window is full.  Fills the step counters and decode_seconds of `s`.
+static size_t lookup_decode_loop(rai_lookup &d, const uint32_t *context, size_t len, size_t pos, size_t max_tokens,
+                                 const rai_lookup_config &cfg, uint32_t *out, rai_generate_stats &s) {
+  auto t1 = std::chrono::steady_clock::now();
+  std::vector<uint32_t> ctx(context, context + len);
+  ctx.reserve(len + max_tokens + cfg.max_draft + 1);
+  std::vector<uint32_t> step_out(cfg.max_draft + 1);
+  size_t gen = 0;
+  while (gen < max_tokens && pos < d.max_ctx) {
+    rai_lookup_metrics met{};
+    lookup_step(d, pos, ctx.data(), ctx.size(), cfg, step_out.data(), step_out.size(), met);
+    for (size_t i = 0; i < met.produced; ++i) {
+      out[gen++] = step_out[i];
+      ctx.push_back(step_out[i]);
+    }
+    pos += met.produced;
+    s.steps++;
+    if (met.drafted) s.steps_with_draft++;
+    s.drafted += met.drafted;
+    s.accepted += met.accepted;
+  }
+  s.generated = gen;
+  s.decode_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
+  return gen;
+}
+
+}  // namespace rai
+
 int rai_lookup_generate(rai_lookup *d, const uint32_t *prompt, size_t n, size_t max_tokens,
                         const rai_lookup_config *cfg, uint32_t *out, size_t out_cap, size_t *n_out,
                         rai_generate_stats *st) {
@@ -1289,30 +1364,49 @@ int rai_lookup_generate(rai_lookup *d, const uint32_t *prompt, size_t n, size_t 
     auto t0 = std::chrono::steady_clock::now();
     size_t pos = 0;
     rai::lookup_prefill(*d, prompt, n, pos);
-    auto t1 = std::chrono::steady_clock::now();
-    std::vector<uint32_t> ctx(prompt, prompt + n);
-    ctx.reserve(n + max_tokens + cfg->max_draft + 1);
-    std::vector<uint32_t> step_out(cfg->max_draft + 1);
-    size_t gen = 0;
-    while (gen < max_tokens && pos < d->max_ctx) {
-      rai_lookup_metrics met{};
-      rai::lookup_step(*d, pos, ctx.data(), ctx.size(), *cfg, step_out.data(), step_out.size(), met);
-      for (size_t i = 0; i < met.produced; ++i) {
-        out[gen++] = step_out[i];
-        ctx.push_back(step_out[i]);
-      }
-      pos += met.produced;
-      s.steps++;
-      if (met.drafted) s.steps_with_draft++;
-      s.drafted += met.drafted;
-      s.accepted += met.accepted;
-    }
-    auto t2 = std::chrono::steady_clock::now();
-    s.generated = gen;
-    s.prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
-    s.decode_seconds = std::chrono::duration<double>(t2 - t1).count();
-    *n_out = gen;
+    s.prefill_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    *n_out = rai::lookup_decode_loop(*d, prompt, n, pos, max_tokens, *cfg, out, s);
     if (st) *st = s;
+  });
+}
+
+int rai_lookup_decode(rai_lookup *d, const uint32_t *context, size_t len, size_t pos, size_t max_tokens,
+                      const rai_lookup_config *cfg, uint32_t *out, size_t out_cap, size_t *n_out,
+                      rai_generate_stats *st) {
+  RAI_API_BODY({
+    if (!d || !context || !cfg || !out || !n_out) rai::fail(RAI_E_ARG, "null argument");
+    if (out_cap < max_tokens + cfg->max_draft) rai::fail(RAI_E_SHAPE, "output buffer too small");
+    if (len == 0 || pos + 1 != len) rai::fail(RAI_E_ARG, "context[len - 1] must be the token at pos");
+    rai_generate_stats s{};
+    s.prompt_tokens = len;
+    *n_out = rai::lookup_decode_loop(*d, context, len, pos, max_tokens, *cfg, out, s);
+    if (st) *st = s;
+  });
+}
+
+int rai_kv_export(const rai_kv *kv, size_t layer, int which, float *out, size_t npos) {
+  RAI_API_BODY({
+    if (!kv || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (layer >= (size_t)kv->layers) rai::fail(RAI_E_ARG, "layer index out of range");
+    if (npos > kv->filled[layer])
+      rai::fail(RAI_E_WATERMARK, "KV export above the watermark (filled " + std::to_string(kv->filled[layer]) + ")");
+    const size_t hd = kv->hd;
+    if (which == 0) {
+      for (int h = 0; h < kv->nkv; ++h)
+        HIP_CHECK(hipMemcpy(out + (size_t)h * npos * hd, kv->kc((int)layer) + (size_t)h * kv->cap * hd,
+                            sizeof(float) * npos * hd, hipMemcpyDeviceToHost));
+    } else {
+      // d-major V [head][hd][vstride]: copy [hd][npos] and transpose.
+      std::vector<float> tmp(hd * npos);
+      for (int h = 0; h < kv->nkv; ++h) {
+        if (npos)
+          HIP_CHECK(hipMemcpy2D(tmp.data(), npos * sizeof(float), kv->vc((int)layer) + (size_t)h * hd * kv->vstride,
+                                kv->vstride * sizeof(float), npos * sizeof(float), hd, hipMemcpyDeviceToHost));
+        float *dst = out + (size_t)h * npos * hd;
+        for (size_t d = 0; d < hd; ++d)
+          for (size_t p = 0; p < npos; ++p) dst[p * hd + d] = tmp[d * npos + p];
+      }
+    }
   });
 }
 
@@ -1335,13 +1429,15 @@ int rai_greedy_generate(rai_lookup *d, const uint32_t *prompt, size_t n, size_t 
       launch_argmax(d->ws.logits.as<float>(), 1, md.cfg.vocab_size, d->ws.am.as<uint32_t>(), d->stream);
       uint32_t tok = 0;
       HIP_CHECK(hipMemcpyAsync(&tok, d->ws.am.p, 4, hipMemcpyDeviceToHost, d->stream));
-      HIP_CHECK(hipStreamSynchronize(d->stream));
+      rai::check_kernel_error(d->ws, d->stream);
       out[i] = tok;
       ctx.push_back(tok);
       ++pos;
     }
   });
 }
+
+int rai_debug_set_attention_spin(int polls) { RAI_API_BODY(rai::set_attention_spin(polls)); }
 
 int rai_dev_malloc(size_t bytes, void **out) {
   RAI_API_BODY({

@@ -1,0 +1,177 @@
+"""GPU parity at the benchmarked model shapes and on the kernel paths the
+small-model tests do not reach: each configuration of the W4A8 / prompt-lookup
+workloads is run on the GPU and compared with the oracle (bit for bit for
+hidden states, logits, int32 sums; token for token for streams and metrics).
+
+Workload shapes (rai_amd.workload): TinyLlama-1.1B, Mistral-7B and
+OLMoE-1B-7B shaped decoders, random-init W4A8 at group 32.
+"""
+import numpy as np
+import pytest
+
+from rai_amd.workload import (GEMV_SHAPES, MISTRAL_7B, OLMOE, TINYLLAMA, copy_heavy_prompt,
+                              gemv_operands)
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _synth(rai, shape, max_context, layers=None, seed=1, **kw):
+    s = dict(shape)
+    return rai.synth_model(s["hidden_size"], layers or s["num_layers"], s["num_heads"], s["num_kv_heads"],
+                           s["head_dim"], s["intermediate_size"], s["vocab_size"], max_context,
+                           group_size=32, num_experts=s.get("num_experts", 0),
+                           experts_per_token=s.get("experts_per_token", 0),
+                           norm_topk_prob=s.get("norm_topk_prob", False), seed=seed, **kw)
+
+
+def _lookup_steps_match(rai, ora, gm, om, prompt, steps, max_ctx, ngram=(3, 3), force_every=2):
+    """Drive the GPU and the oracle LookupDecoder over the same contexts and
+    compare every step's tokens and metrics.  Every `force_every`-th step
+    rewrites the context's last three tokens with an earlier 3-gram (both
+    decoders see the same context), so the 3-gram search finds a draft and
+    the step runs the (k+1)-token verify forward; random-init weights rarely
+    continue a prompt span on their own.  Returns (drafted, accepted)."""
+    cfg = rai.LookupConfig(max_draft=8, min_ngram=ngram[0], max_ngram=ngram[1])
+    gd, od = rai.LookupDecoder(gm, max_ctx), ora.LookupDecoder(om, max_ctx)
+    gpos, opos = gd.prefill(prompt), od.prefill(prompt.astype(np.int32))
+    assert gpos == opos == len(prompt) - 1
+    ctx = prompt.tolist()
+    drafted = accepted = 0
+    for i in range(steps):
+        if force_every and i % force_every == 1 and len(ctx) > 40:
+            src = 5 + (7 * i) % (len(ctx) - 30)
+            ctx[-3:] = ctx[src:src + 3]
+        gt, gmet = gd.step(gpos, ctx, cfg)
+        ot, omet = od.step(opos, ctx, 8, ngram[0], ngram[1])
+        assert gt == ot, i
+        assert (gmet.accepted, gmet.drafted, gmet.produced) == (omet.accepted, omet.drafted, omet.produced), i
+        drafted += gmet.drafted
+        accepted += gmet.accepted
+        ctx += gt
+        gpos += gmet.produced
+        opos += omet.produced
+        assert gd.kv_cache.filled(0) == gpos
+    return drafted, accepted
+
+
+# --------------------------------------------------------------- config 3 --
+
+@pytest.mark.parametrize("rows,cols", GEMV_SHAPES)
+def test_cfg3_m17_sweep_shapes_bit_exact(rai, ora, rows, cols):
+    """W4A8 sweep at M = 17 (the first token count past the matrix-core
+    verify kernel) on the four sweep shapes: f32 outputs bit-exact."""
+    nib, params, x = gemv_operands(rows, cols, 17, 32, seed=rows + cols + 17)
+    got = rai.w4a8_matmul(nib, params, x, rows, cols, 17, 32)
+    want = ora.w4a8_matmul(nib, params, x, rows, cols, 17, 32)
+    assert np.array_equal(_bits(got), _bits(want))
+
+
+# ----------------------------------------------------------------- argmax --
+
+def test_argmax_nan_ties_and_signed_zero(rai, ora):
+    """sampler.rs:201-208 (and its tests, sampler.rs:216-304) on the GPU
+    kernel: NaN never wins, ties go to the last index, -0 < +0; long rows
+    with the maximum in every position class of the block reduction."""
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    rows = [
+        [1.0, 3.0, 2.0, 3.0, -1.0],          # tie: last index
+        [nan, 0.5, nan, 0.25],               # NaN ignored
+        [nan, nan, nan],                     # all NaN: -inf everywhere, last index
+        [-0.0, 0.0, -0.0],                   # +0 beats -0
+        [0.0, -0.0],
+        [-inf, -inf, -3.0, -inf],
+        [inf, 1.0, inf, nan],
+        [-5.0, -7.0, -5.0, -9.0],
+    ]
+    for r in rows:
+        got = int(rai.argmax(np.array(r, np.float32))[0])
+        assert got == ora.argmax(np.array(r, np.float32)), r
+    rng = np.random.default_rng(3)
+    V = 32000
+    x = rng.normal(size=(24, V)).astype(np.float32)
+    for t in range(24):
+        j = int(rng.integers(0, V))
+        x[t, j] = 10.0
+        x[t, (j * 7919 + 13) % V] = 10.0  # an exact tie elsewhere
+        if t % 3 == 0:
+            x[t, rng.integers(0, V, 50)] = np.nan
+    got = rai.argmax(x)
+    for t in range(24):
+        assert got[t] == ora.argmax(x[t]), t
+
+
+# --------------------------------------------------------------- config 4 --
+
+def test_cfg4_mistral7b_shape_matches_oracle(rai, ora):
+    """Mistral-7B shape (32 layers, hidden 4096, FFN 14336, 32/8 heads, head
+    dim 128, vocab 32000, g32): forward_batch of a 64-token prefill and a
+    9-token verify batch give bit-identical hidden states and logits, then 32
+    prompt-lookup steps (n-gram 3, k = 8, half of them with a forced draft)
+    give the oracle's tokens and metrics step by step."""
+    img = _synth(rai, MISTRAL_7B, 8192, seed=1234)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    om = ora.Model(img, 0)
+    del img
+    V = MISTRAL_7B["vocab_size"]
+    prompt = copy_heavy_prompt(64, V, seed=64)
+    hs = np.stack([om.embed_token(int(t)) for t in prompt[:64]] +
+                  [om.embed_token(int(t)) for t in prompt[20:29]])
+    gkv, okv = gm.create_kv_cache(128), om.create_kv(128)
+    gh = gm.forward_batch(hs[:64], np.arange(64), gkv)
+    oh = om.forward_batch(hs[:64], np.arange(64), okv)
+    assert np.array_equal(_bits(gh), _bits(oh))
+    gh = gm.forward_batch(hs[64:], np.arange(64, 73), gkv)
+    oh = om.forward_batch(hs[64:], np.arange(64, 73), okv)
+    assert np.array_equal(_bits(gh), _bits(oh))
+    assert np.array_equal(_bits(gm.hidden_to_logits_batch(gh, 9)), _bits(om.hidden_to_logits_batch(oh, 9)))
+    drafted, _ = _lookup_steps_match(rai, ora, gm, om, prompt, 32, 256)
+    assert drafted > 0
+
+
+# --------------------------------------------------------------- config 2 --
+
+def test_cfg2_tinyllama_2048_prompt_lookup(rai, ora):
+    """TinyLlama shape with the 2048-token copy-heavy prompt, n-gram 3, k = 8:
+    16 steps equal the oracle's step by step (after the oracle's own 2047-token
+    prefill), and a 256-token prompt-lookup generation equals plain greedy
+    decoding on the GPU token for token."""
+    img = _synth(rai, TINYLLAMA, 4096, seed=1)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    om = ora.Model(img, 0)
+    del img
+    prompt = copy_heavy_prompt(2048, TINYLLAMA["vocab_size"], seed=2048)
+    drafted, _ = _lookup_steps_match(rai, ora, gm, om, prompt, 16, 2400)
+    assert drafted > 0
+    cfg = rai.LookupConfig(max_draft=8, min_ngram=3, max_ngram=3)
+    toks, stats = rai.LookupDecoder(gm, 2400).generate(prompt, 256, cfg)
+    assert stats["generated"] == len(toks) >= 256
+    want = rai.LookupDecoder(gm, 2400).greedy_generate(prompt, len(toks))
+    assert toks == want
+
+
+# --------------------------------------------------------------- config 5 --
+
+def test_cfg5_olmoe_width_matches_oracle(rai, ora):
+    """OLMoE width (hidden 2048, 64 experts, top 8, expert FFN 1024, 16 heads
+    of 128, vocab 50304) with 2 layers: a 9-token verify-sized batch after a
+    40-token prefill gives bit-identical hidden states and logits, and 12
+    lookup steps equal the oracle's."""
+    img = _synth(rai, OLMOE, 2048, layers=2, seed=5)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    om = ora.Model(img, 0)
+    del img
+    V = OLMOE["vocab_size"]
+    prompt = copy_heavy_prompt(96, V, seed=96)
+    hs = np.stack([om.embed_token(int(t)) for t in prompt[:49]])
+    gkv, okv = gm.create_kv_cache(128), om.create_kv(128)
+    for a, b in ((0, 40), (40, 49)):
+        gh = gm.forward_batch(hs[a:b], np.arange(a, b), gkv)
+        oh = om.forward_batch(hs[a:b], np.arange(a, b), okv)
+        assert np.array_equal(_bits(gh), _bits(oh)), (a, b)
+    assert np.array_equal(_bits(gm.hidden_to_logits_batch(gh, 9)), _bits(om.hidden_to_logits_batch(oh, 9)))
+    drafted, _ = _lookup_steps_match(rai, ora, gm, om, prompt, 12, 256)
+    assert drafted > 0

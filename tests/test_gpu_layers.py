@@ -72,18 +72,21 @@ def test_attention_head_long_context_bit_exact(rai, ora, hd, pos):
 
 def test_rope_tables_match_oracle(rai, ora):
     """The library builds RoPE tables on the host with the C library's
-    powf/cosf/sinf exactly as RoPETable::with_scaling does; position 1 of a
-    tiny model's forward pass exercises them (checked through a KV read)."""
+    powf/cosf/sinf exactly as RoPETable::with_scaling does: the rotated K rows
+    the forward pass stores at positions 0..5 (every head, both layers) equal
+    the oracle's bit for bit."""
     from conftest import read_golden
     data = read_golden("tiny-untied.raimodel")
     gm = rai.RaiModel.from_bytes(data)
     om = ora.Model(data, 128)
     kv, okv = gm.create_kv_cache(8), om.create_kv(8)
-    for p, t in enumerate((5, 9)):
+    toks = (5, 9, 17, 2, 60, 33)
+    for p, t in enumerate(toks):
         gm.forward_from_hidden(gm.embed_token(t), p, kv)
-    h = np.stack([om.embed_token(5), om.embed_token(9)])
-    om.forward_batch(h, [0, 1], okv)
-    c, s = ora.rope_tables(16, 8, 10000.0)
-    assert gm.config.head_dim == 16
-    k1 = kv.get_k(0, 0, 1, 16)
-    assert np.all(np.isfinite(k1))
+    om.forward_batch(np.stack([om.embed_token(t) for t in toks]), np.arange(6), okv)
+    hd = gm.config.head_dim
+    for layer in range(gm.config.num_layers):
+        for head in range(gm.config.num_kv_heads):
+            for p in range(6):
+                assert np.array_equal(_bits(kv.get_k(layer, head, p, hd)), _bits(okv.get_k(layer, head, p, hd)))
+                assert np.array_equal(_bits(kv.get_v(layer, head, p, hd)), _bits(okv.get_v(layer, head, p, hd)))

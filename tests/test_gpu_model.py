@@ -144,6 +144,100 @@ def test_single_token_attention_long_context_bit_exact(rai, ora):
         assert np.array_equal(_bits(gh), _bits(oh)), p
 
 
+@pytest.mark.parametrize("nh,nkv,hd", [(16, 16, 128), (16, 1, 64)])
+def test_pv_head_groupings_bit_exact(rai, ora, nh, nkv, hd):
+    """The PV kernel instances for one query head per kv head (head_dim 128,
+    the OLMoE grouping) and sixteen (head_dim 64): one-token and nine-token
+    batches after 600 positions, bit for bit against the oracle."""
+    img = _small_synth(rai, hidden_size=1024, num_layers=1, num_heads=nh, num_kv_heads=nkv, head_dim=hd,
+                       intermediate_size=1024, vocab_size=500, max_context=1024, seed=nh + nkv + hd)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    toks = _token_sequence(om.cfg.vocab_size, 610)
+    hs = np.stack([om.embed_token(t) for t in toks])
+    okv, gkv = om.create_kv(1024), gm.create_kv_cache(1024)
+    for a, b in ((0, 600), (600, 601), (601, 610)):
+        oh = om.forward_batch(hs[a:b], np.arange(a, b), okv)
+        gh = gm.forward_batch(hs[a:b], np.arange(a, b), gkv)
+        assert np.array_equal(_bits(gh), _bits(oh)), (a, b)
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 128), (16, 2, 64)])
+def test_pv_long_context_through_kv_cache_bit_exact(rai, ora, nh, nkv, hd):
+    """The production PV path (d-major V cache, LDS-flag tile hand-off) at
+    4352 and 8192 positions, four and eight query heads per kv head: a
+    one-token and a nine-token batch after each prefill, against the oracle
+    bit for bit."""
+    img = _small_synth(rai, hidden_size=1024, num_layers=1, num_heads=nh, num_kv_heads=nkv, head_dim=hd,
+                       intermediate_size=1024, vocab_size=500, max_context=8256, seed=nh * hd)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    toks = _token_sequence(om.cfg.vocab_size, 8193)
+    hs = np.stack([om.embed_token(t) for t in toks])
+    okv, gkv = om.create_kv(8256), gm.create_kv_cache(8256)
+    p = 0
+    for end in (4342, 8183):
+        om.forward_batch(hs[p:end], np.arange(p, end), okv)
+        gm.forward_batch(hs[p:end], np.arange(p, end), gkv)
+        for n in (1, 9):
+            oh = om.forward_batch(hs[end:end + n], np.arange(end, end + n), okv)
+            gh = gm.forward_batch(hs[end:end + n], np.arange(end, end + n), gkv)
+            assert np.array_equal(_bits(gh), _bits(oh)), (end, n)
+            end += n
+        p = end
+    assert gkv.filled(0) == 8193
+
+
+def test_attention_wait_give_up_is_reported(rai, ora):
+    """A PV tile hand-off wait that gives up (forced from the host with a
+    poll limit of 1; every kernel still ends) fails the call with RAI_E_HIP
+    and leaves the KV watermark where it was; with the default limit the
+    same batch then runs and equals the oracle."""
+    img = _small_synth(rai, hidden_size=1024, num_layers=1, num_heads=8, num_kv_heads=2, head_dim=128,
+                       intermediate_size=1024, vocab_size=500, max_context=4096, seed=41)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    toks = _token_sequence(om.cfg.vocab_size, 2304)
+    hs = np.stack([om.embed_token(t) for t in toks])
+    okv, gkv = om.create_kv(4096), gm.create_kv_cache(4096)
+    om.forward_batch(hs[:2048], np.arange(2048), okv)
+    gm.forward_batch(hs[:2048], np.arange(2048), gkv)
+    rai.set_attention_spin(1)
+    try:
+        with pytest.raises(rai.RaiError) as e:
+            gm.forward_batch(hs[2048:], np.arange(2048, 2304), gkv)
+        assert e.value.status == "RAI_E_HIP"
+    finally:
+        rai.set_attention_spin(0)
+    assert gkv.filled(0) == 2048
+    oh = om.forward_batch(hs[2048:], np.arange(2048, 2304), okv)
+    gh = gm.forward_batch(hs[2048:], np.arange(2048, 2304), gkv)
+    assert np.array_equal(_bits(gh), _bits(oh))
+
+
+@pytest.mark.parametrize("max_context", [20000, 65536])
+def test_step_graphs_with_large_capacity_match_oracle(rai, ora, max_context):
+    """Decoders whose KV capacity exceeds the longest attention context (the
+    step graphs size attention for min(capacity, 16384) positions) keep the
+    oracle's tokens and metrics step by step, graphs on."""
+    img = _small_synth(rai, max_context=max_context, seed=43)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    prompt = copy_heavy_prompt(300, 1000, seed=max_context)
+    cfg = rai.LookupConfig(max_draft=8, min_ngram=1, max_ngram=3)
+    gd, od = rai.LookupDecoder(gm, max_context), ora.LookupDecoder(om, max_context)
+    gpos, opos = gd.prefill(prompt), od.prefill(prompt.astype(np.int32))
+    ctx = prompt.tolist()
+    for i in range(40):
+        gt, gmet = gd.step(gpos, ctx, cfg)
+        ot, omet = od.step(opos, ctx, 8, 1, 3)
+        assert gt == ot, i
+        assert (gmet.accepted, gmet.drafted, gmet.produced) == (omet.accepted, omet.drafted, omet.produced)
+        ctx += gt
+        gpos += gmet.produced
+        opos += omet.produced
+
+
 def test_step_graphs_with_a_long_context_match_eager(rai, monkeypatch):
     """Replayed steps read the position from the device step record and
     size the attention for the whole 8192-position cache; past 7168
@@ -176,7 +270,6 @@ def test_batched_equals_sequential_on_gpu(rai, name):
     lb = gm.hidden_to_logits_batch(hb, 12)
     for i in range(12):
         assert np.array_equal(_bits(lb[i]), _bits(seq[i]))
-        assert int(np.argmax(lb[i])) == int(np.argmax(seq[i])) or True
 
 
 def test_kv_watermark_and_errors(rai):
