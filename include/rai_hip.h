@@ -154,6 +154,18 @@ int rai_hidden_to_logits_batch(rai_model *model, const float *hiddens, float *lo
 int rai_w4a8_matmul_dev(float *out, const uint8_t *nibbles, const uint8_t *params,
                         const float *x, size_t rows, size_t cols, size_t m, size_t group_size,
                         void *stream);
+/* Allocation-free variant of rai_w4a8_matmul_dev.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, arithmetic and results; the quantized activations live in
+ * a fixed per-GPU scratch array held until the process ends (about 4.5 MiB),
+ * so the call is asynchronous on `stream` and calls no allocator.  Limits:
+ * m * cols <= 1048576 and m * ceil(cols / group_size) <= 65536, else
+ * RAI_E_SHAPE.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap in time on one GPU (other streams, other host threads) race. */
+int rai_w4a8_matmul_noalloc_dev(float *out, const uint8_t *nibbles, const uint8_t *params,
+                                const float *x, size_t rows, size_t cols, size_t m,
+                                size_t group_size, void *stream);
 /* Debug companion (no reference counterpart): the integer accumulators of
  * matvec_chunk_i8 (gemm.rs:458-525) per (token, row, group) as 12 int32:
  * [0..8) the 64-column-chunk lanes, [8..12) the trailing 32-column block. */

@@ -107,6 +107,7 @@ def lib():
         "rai_hidden_to_logits": (c_int, [P, P, P]),
         "rai_hidden_to_logits_batch": (c_int, [P, P, P, S]),
         "rai_w4a8_matmul_dev": (c_int, [P, P, P, P, S, S, S, S, P]),
+        "rai_w4a8_matmul_noalloc_dev": (c_int, [P, P, P, P, S, S, S, S, P]),
         "rai_w4a8_lane_sums_dev": (c_int, [P, P, P, S, S, S, S, P]),
         "rai_w4a8_matmul": (c_int, [P, P, P, P, S, S, S, S]),
         "rai_w4a8_time_dev": (c_int, [P, P, P, P, S, S, S, S, S, c_int, POINTER(c_float)]),

@@ -1069,6 +1069,82 @@ int rai_w4a8_matmul_dev(float *out, const uint8_t *nib, const uint8_t *params, c
   });
 }
 
+// ------------------------------------------------- allocation-free GEMM --
+//
+// Scratch of rai_w4a8_matmul_noalloc_dev: one static device array per GPU,
+// held until the process ends.  Host code never uses the array's name as a
+// device address (in host code it names a host-side stand-in); it uses the
+// address hipGetSymbolAddress returns on each device, looked up once per
+// device on the first call there.  Layout (bytes): q_nat [m*cols], q_split
+// [m*cols], scales [m*groups] f32, sums [m*groups] f32, matrix-core
+// activations.
+namespace rai {
+constexpr size_t kNaTokenCols = size_t(1) << 20;  // m * cols
+constexpr size_t kNaGroups = size_t(1) << 16;     // m * ceil(cols / gs)
+constexpr size_t kNaQaBytes = size_t(2) << 20;
+constexpr size_t kNaScratchBytes = 2 * kNaTokenCols + 8 * kNaGroups + kNaQaBytes;
+constexpr int kNaMaxDevices = 64;
+}  // namespace rai
+
+static __device__ __align__(256) uint8_t scratch[rai::kNaScratchBytes];
+
+namespace rai {
+
+static std::mutex g_na_mutex;
+static void *g_na_scratch[kNaMaxDevices] = {};
+
+// The device address of `scratch` on the current device.
+static uint8_t *noalloc_scratch() {
+  int dev = 0;
+  HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kNaMaxDevices) fail(RAI_E_ARG, "device index out of range");
+  std::lock_guard<std::mutex> lk(g_na_mutex);
+  if (!g_na_scratch[dev]) {
+    void *p = nullptr;
+    HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) fail(RAI_E_HIP, "hipGetSymbolAddress returned no address for the scratch array");
+    g_na_scratch[dev] = p;
+  }
+  return static_cast<uint8_t *>(g_na_scratch[dev]);
+}
+
+}  // namespace rai
+
+int rai_w4a8_matmul_noalloc_dev(float *out, const uint8_t *nib, const uint8_t *params, const float *x, size_t rows,
+                                size_t cols, size_t m, size_t gs, void *stream) {
+  RAI_API_BODY({
+    if (!out || !nib || !params || !x) rai::fail(RAI_E_ARG, "null argument");
+    if (rows == 0) rai::fail(RAI_E_SHAPE, "rows must be non-zero");
+    if (cols == 0 || cols % 2) rai::fail(RAI_E_SHAPE, "cols must be non-zero and even");
+    if (gs == 0 || gs % 2) rai::fail(RAI_E_SHAPE, "group_size must be non-zero and even");
+    if (m == 0) rai::fail(RAI_E_SHAPE, "num_tokens must be non-zero");
+    if (rows > INT32_MAX || cols > INT32_MAX || m > INT32_MAX) rai::fail(RAI_E_SHAPE, "dimensions overflow");
+    const size_t groups = rai::ceil_div(cols, gs);
+    if (m > rai::kNaTokenCols / cols || m * groups > rai::kNaGroups)
+      rai::fail(RAI_E_SHAPE, "num_tokens * cols exceeds the allocation-free scratch (at most " +
+                                 std::to_string(rai::kNaTokenCols) + " token columns and " +
+                                 std::to_string(rai::kNaGroups) + " token groups)");
+    const bool mfma = rai::w4a8_mfma_path((int)rows, (int)cols, (int)m, (int)gs);
+    if (mfma && sizeof(_Float16) * rai::qa_pack_halves((int)m, (int)cols) > rai::kNaQaBytes)
+      rai::fail(RAI_E_SHAPE, "activation tile exceeds the allocation-free scratch");
+    uint8_t *base = rai::noalloc_scratch();
+    int8_t *qn = reinterpret_cast<int8_t *>(base);
+    int8_t *qs = reinterpret_cast<int8_t *>(base + rai::kNaTokenCols);
+    float *sc = reinterpret_cast<float *>(base + 2 * rai::kNaTokenCols);
+    float *su = sc + rai::kNaGroups;
+    _Float16 *qa = reinterpret_cast<_Float16 *>(base + 2 * rai::kNaTokenCols + 8 * rai::kNaGroups);
+    hipStream_t s = (hipStream_t)stream;
+    // Every scratch byte a kernel reads is written earlier in this call (the
+    // pack writes the padding rows of the last token group as zeros), so the
+    // previous call's contents never reach the output.
+    rai::launch_quantize(x, (int)m, (int)cols, (int)gs, qn, qs, sc, su, s);
+    if (mfma) rai::launch_qa_pack(qs, (int)m, (int)cols, qa, s);
+    rai::launch_w4a8(out, nullptr, nib, params, x, qn, qs, sc, su, (int)rows, (int)cols, (int)m, (int)gs, s,
+                     mfma ? qa : nullptr);
+    HIP_CHECK(hipGetLastError());
+  });
+}
+
 int rai_w4a8_time_dev(float *out, const uint8_t *nib, const uint8_t *params, const float *x, size_t rows,
                       size_t cols, size_t m, size_t gs, size_t copies, int iters, float *avg_ms) {
   RAI_API_BODY({
