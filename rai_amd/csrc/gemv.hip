@@ -836,12 +836,13 @@ bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const ui
   const int ntg = (m + 3) / 4;
   const int groups = cols / 32;
   // Kernel and tiling per shape, measured on 4096..32000 x 2048..14336 and
-  // M = 2..16 with the weights streamed from HBM.  The register-pipelined
-  // kernel: for K <= 4096 three token groups per wave, or two (an even
-  // number of groups, or three as 2 + 1), when that still gives at least
-  // 192 blocks of four waves (64 rows), else one; eight waves per block
-  // for three groups from 16384 rows.  For longer K (K / 128 a multiple of
-  // 4, at most 14336) one token group per block.
+  // M = 2..64 with the weights streamed from HBM.  The register-pipelined
+  // kernel: for K <= 4096 three token groups per wave, or two, when that
+  // still gives at least 192 blocks of four waves (64 rows), else one (an
+  // odd count of token groups runs in pairs, the last pair's second group
+  // a clamped duplicate whose outputs are not stored); eight waves per
+  // block for three groups from 16384 rows.  For longer K (K / 128 a
+  // multiple of 4, at most 14336) one token group per block.
   constexpr int Q = kRpMaxCols / 128, Q1 = kRpMaxColsOne / 128;
   if (gemv_rp_ok(rows, cols)) {
     const int rb = (rows + 63) / 64;
@@ -852,7 +853,7 @@ bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const ui
       launch_rp<3, 8, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
     else if (ntg == 3 && blocks(3) >= 192)
       launch_rp<3, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if ((ntg % 2 == 0 || ntg == 3) && blocks(2) >= 192)
+    else if (ntg >= 2 && blocks(2) >= 192)
       launch_rp<2, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
     else
       launch_rp<1, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);

@@ -23,10 +23,12 @@ void launch_quantize(const float *x, int m, int k, int gs, int8_t *q_nat, int8_t
 // layers.rs:503-531, fused into the epilogue).
 // `qa` (may be null): the activations packed by launch_qa_pack, which
 // enables the matrix-core kernel for 2..kMfmaMaxTokens tokens at group 32.
+// `mm` (may be null): mm_pack_bytes(m, cols) bytes of scratch, which
+// enables the matrix-core GEMM for more than kMfmaMaxTokens tokens.
 void launch_w4a8(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const float *x,
                  const int8_t *q_nat, const int8_t *q_split, const float *scales,
                  const float *sums, int rows, int cols, int m, int gs, hipStream_t s,
-                 const _Float16 *qa = nullptr);
+                 const _Float16 *qa = nullptr, uint8_t *mm = nullptr);
 
 // One token: rms_norm(x) * norm_w (layers.rs:325-376), its group-32
 // quantization and the W4A8 GEMV in one launch; each block normalises and
@@ -70,8 +72,9 @@ bool launch_w4a8_qkv_rope1(float *out, const uint8_t *nib, const uint8_t *params
                            const float *norm_w, float eps, int rows, int cols, int gs, const DecRope &rope,
                            hipStream_t s);
 
-// Matrix-core W4A8 (gemv.hip): group 32, K a multiple of 256, 2..16 tokens.
-constexpr int kMfmaMaxTokens = 16;
+// Matrix-core W4A8 (gemv.hip): group 32, K a multiple of 256, 2..64 tokens
+// (past 64 the GEMM of gemm_mm.hip is faster on every measured shape).
+constexpr int kMfmaMaxTokens = 64;
 bool w4a8_mfma_path(int rows, int cols, int m, int gs);
 // Halves of the packed activation buffer for m tokens of `cols` columns.
 size_t qa_pack_halves(int m, int cols);
@@ -81,6 +84,14 @@ void launch_qa_pack(const int8_t *q_split, int m, int cols, _Float16 *qa, hipStr
 bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                       const float *scales, const float *sums, int rows, int cols, int m, int gs,
                       hipStream_t s);
+// Matrix-core W4A8 GEMM (gemm_mm.hip): group 32, K a multiple of 512,
+// more than kMfmaMaxTokens tokens.  Packs the block-split activations into
+// `pack` (mm_pack_bytes(m, cols) bytes), then runs the GEMM.
+bool w4a8_mm_path(int rows, int cols, int m, int gs);
+size_t mm_pack_bytes(int m, int cols);
+void launch_w4a8_mm(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
+                    const float *scales, const float *sums, int rows, int cols, int m, uint8_t *pack,
+                    hipStream_t s);
 // True when launch_w4a8 takes the tiled fast path for this shape.
 bool w4a8_fast_path(int cols, int gs);
 

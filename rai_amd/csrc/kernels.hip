@@ -1239,9 +1239,13 @@ bool w4a8_fast_path(int cols, int gs) {
 void launch_w4a8(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const float *x,
                  const int8_t *q_nat, const int8_t *q_split, const float *scales,
                  const float *sums, int rows, int cols, int m, int gs, hipStream_t s,
-                 const _Float16 *qa) {
+                 const _Float16 *qa, uint8_t *mm) {
   const int groups = (cols + gs - 1) / gs;
   if (launch_w4a8_mfma(out, add, nib, params, qa, scales, sums, rows, cols, m, gs, s)) return;
+  if (mm && q_split && w4a8_mm_path(rows, cols, m, gs)) {
+    launch_w4a8_mm(out, add, nib, params, q_split, scales, sums, rows, cols, m, mm, s);
+    return;
+  }
   if (m == 1 && q_split &&
       launch_w4a8_dec(out, add, nib, params, q_split, scales, sums, rows, cols, gs, nullptr, nullptr, 0.0f, s))
     return;

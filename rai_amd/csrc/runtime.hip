@@ -35,7 +35,7 @@ void set_last_error(const std::string &m) { g_last_error = m; }
 constexpr size_t kMaxAttnContext = kMaxAttnPositions;
 // Tokens per forward chunk (prefill is split into chunks of this size; the
 // per-token arithmetic does not depend on the split).
-constexpr int kChunk = 256;
+constexpr int kChunk = 1024;
 
 struct DevBuf {
   void *p = nullptr;
@@ -116,7 +116,8 @@ struct Workspace {
   DevBuf hid, normed, qb, kb, vb, att, ob, gb, ub, mo, logits, am;
   DevBuf qkvb, gub;  // fused q|k|v and gate|up outputs [m][rows]
   DevBuf q_nat, q_split, qscale, qsum, hq;
-  DevBuf qa;  // activations packed for the matrix-core W4A8 kernel (<= 16 tokens)
+  DevBuf qa;   // activations packed for the matrix-core W4A8 kernel (<= 64 tokens)
+  DevBuf qmm;  // activation records of the matrix-core W4A8 GEMM (> 64 tokens)
   DevBuf err;
   // Attention score/probability rows; grown to the largest KV capacity seen.
   DevBuf scores;
@@ -158,6 +159,7 @@ struct Workspace {
     q_nat.alloc(K * maxm);
     q_split.alloc(K * maxm);
     qa.alloc(sizeof(_Float16) * qa_pack_halves(std::min(maxm, kMfmaMaxTokens), (int)K));
+    if (maxm > kMfmaMaxTokens) qmm.alloc(mm_pack_bytes(maxm, (int)K));
     hq.alloc(H * maxm);
     qscale.alloc(sizeof(float) * G * maxm);
     qsum.alloc(sizeof(float) * G * maxm);
@@ -363,7 +365,7 @@ static void linear(const DLinear &L, const float *x, const Workspace &w, float *
                    hipStream_t s, const float *add = nullptr) {
   launch_w4a8(out, add, L.nib, L.params, x, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
               w.qscale.as<float>(), w.qsum.as<float>(), L.rows, L.cols, m, L.gs, s,
-              w.qa.as<_Float16>());
+              w.qa.as<_Float16>(), w.qmm.as<uint8_t>());
 }
 
 // After any quantization of m rows of k columns into the workspace: pack
@@ -1056,14 +1058,16 @@ int rai_w4a8_matmul_dev(float *out, const uint8_t *nib, const uint8_t *params, c
     su.alloc(m * groups * 4);
     rai::launch_quantize(x, (int)m, (int)cols, (int)gs, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
                          su.as<float>(), s);
-    rai::DevBuf qa;
+    rai::DevBuf qa, mm;
     const bool mfma = rai::w4a8_mfma_path((int)rows, (int)cols, (int)m, (int)gs);
     if (mfma) {
       qa.alloc(sizeof(_Float16) * rai::qa_pack_halves((int)m, (int)cols));
       rai::launch_qa_pack(qs.as<int8_t>(), (int)m, (int)cols, qa.as<_Float16>(), s);
     }
+    if (rai::w4a8_mm_path((int)rows, (int)cols, (int)m, (int)gs)) mm.alloc(rai::mm_pack_bytes((int)m, (int)cols));
     rai::launch_w4a8(out, nullptr, nib, params, x, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
-                     su.as<float>(), (int)rows, (int)cols, (int)m, (int)gs, s, mfma ? qa.as<_Float16>() : nullptr);
+                     su.as<float>(), (int)rows, (int)cols, (int)m, (int)gs, s, mfma ? qa.as<_Float16>() : nullptr,
+                     mm.as<uint8_t>());
     HIP_CHECK(hipGetLastError());
     HIP_CHECK(hipStreamSynchronize(s));  // scratch is freed on return
   });
@@ -1164,17 +1168,18 @@ int rai_w4a8_time_dev(float *out, const uint8_t *nib, const uint8_t *params, con
     HIP_CHECK(hipEventCreate(&e1));
     rai::launch_quantize(x, (int)m, (int)cols, (int)gs, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(),
                          su.as<float>(), s);
-    rai::DevBuf qa;
+    rai::DevBuf qa, mm;
     const bool mfma = rai::w4a8_mfma_path((int)rows, (int)cols, (int)m, (int)gs);
     if (mfma) {
       qa.alloc(sizeof(_Float16) * rai::qa_pack_halves((int)m, (int)cols));
       rai::launch_qa_pack(qs.as<int8_t>(), (int)m, (int)cols, qa.as<_Float16>(), s);
     }
+    if (rai::w4a8_mm_path((int)rows, (int)cols, (int)m, (int)gs)) mm.alloc(rai::mm_pack_bytes((int)m, (int)cols));
     const size_t nib_bytes = rows * cols / 2, par_bytes = rows * groups * 4;
     auto run = [&](size_t c) {
       rai::launch_w4a8(out, nullptr, nib + c * nib_bytes, params + c * par_bytes, x, qn.as<int8_t>(),
                        qs.as<int8_t>(), sc.as<float>(), su.as<float>(), (int)rows, (int)cols, (int)m, (int)gs, s,
-                       mfma ? qa.as<_Float16>() : nullptr);
+                       mfma ? qa.as<_Float16>() : nullptr, mm.as<uint8_t>());
     };
     run(0);  // warm-up
     HIP_CHECK(hipEventRecord(e0, s));
