@@ -187,6 +187,18 @@ void launch_moe_accumulate(float *out, const float *eo, const float *w, int m, i
                            hipStream_t s);
 void launch_fill(float *p, float v, size_t n, hipStream_t s);
 
+// Device MoE (moe.hip): group 32/64/128, hidden and FFN multiples of 256,
+// at most 1024 experts.
+bool moe_device_path(int hidden, int ffn, int gs, int experts);
+void launch_moe_plan(const int *sel, int m, int K, int E, int *off, int *ent_of, int *ent_tok, hipStream_t s);
+void launch_moe_gather(const int8_t *q, const float *sc, const float *su, const int *ent_tok, const int *off, int E,
+                       int max_entries, int cols, int groups, int8_t *qg, float *scg, float *sug, hipStream_t s);
+void launch_moe_gemv(float *out, int ld, const uint8_t *const *nibp, const uint8_t *const *parp, int nmat, int rows,
+                     int cols, int gs, int E, const int8_t *q, const float *sc, const float *su, const int *off,
+                     hipStream_t s);
+void launch_moe_combine(float *hid, const float *eo, const float *wts, const int *ent_of, int m, int K, int H,
+                        hipStream_t s);
+
 }  // namespace rai
 
 #endif

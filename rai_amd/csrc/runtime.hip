@@ -92,6 +92,9 @@ struct rai_model {
   uint64_t weight_bytes = 0;
   hipStream_t stream = nullptr;
   std::unique_ptr<Workspace> ws;  // for the model-level host-buffer API
+  // Sparse layers: per layer 6 * num_experts device pointers, the code and
+  // parameter arrays of gate|up (expert-major, gate then up), then of down.
+  DevBuf moe_tab;
   ~rai_model();
 };
 
@@ -132,6 +135,8 @@ struct Workspace {
   }
   // MoE
   DevBuf sel, wts, eo, xg, yg, gg, ug, idx, wcol;
+  // Device MoE path: entry plan, gathered quantized inputs, gate|up outputs.
+  DevBuf moff, ment_of, ment_tok, mq, msc, msu, mgu;
   int logit_rows = 0;
   void init(const rai_model &m, int maxm_, int logit_rows_) {
     const rai_model_config &c = m.cfg;
@@ -174,6 +179,14 @@ struct Workspace {
       gg.alloc(sizeof(float) * maxm * F);
       ug.alloc(sizeof(float) * maxm * F);
       idx.alloc(sizeof(int) * maxm * c.experts_per_token);
+      const size_t ne = (size_t)maxm * c.experts_per_token;
+      moff.alloc(sizeof(int) * (c.num_experts + 1));
+      ment_of.alloc(sizeof(int) * ne);
+      ment_tok.alloc(sizeof(int) * ne);
+      mq.alloc(ne * std::max(H, F));
+      msc.alloc(sizeof(float) * ne * G);
+      msu.alloc(sizeof(float) * ne * G);
+      mgu.alloc(sizeof(float) * ne * 2 * F);
       wcol.alloc(sizeof(float) * maxm);
     }
   }
@@ -356,6 +369,24 @@ static void upload_model(rai_model &m, const uint8_t *img, size_t len, int max_g
     m.lm_head.nib = base + pieces[lmn].dst;
   }
   m.weight_bytes = wbytes;
+  if (c.num_experts > 0) {
+    const size_t E = c.num_experts;
+    std::vector<const uint8_t *> tab(6 * E * c.num_layers);
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+      const DLayer &D = m.layers[l];
+      const uint8_t **t = tab.data() + 6 * E * l;
+      for (size_t e = 0; e < E; ++e) {
+        for (int j = 0; j < 2; ++j) {
+          t[2 * e + j] = D.experts[3 * e + j].nib;
+          t[2 * E + 2 * e + j] = D.experts[3 * e + j].params;
+        }
+        t[4 * E + e] = D.experts[3 * e + 2].nib;
+        t[5 * E + e] = D.experts[3 * e + 2].params;
+      }
+    }
+    m.moe_tab.alloc(sizeof(void *) * tab.size());
+    HIP_CHECK(hipMemcpy(m.moe_tab.p, tab.data(), sizeof(void *) * tab.size(), hipMemcpyHostToDevice));
+  }
   HIP_CHECK(hipStreamCreateWithFlags(&m.stream, hipStreamNonBlocking));
 }
 
@@ -396,6 +427,36 @@ static void quantize(const rai_model &md, const float *x, int m, int k, const Wo
 // The MLP of a sparse layer: mlp_block's MoE arm (model.rs:208-261) for
 // every token, grouping each expert's tokens into one GEMV batch (each
 // token's arithmetic is the M = 1 arithmetic: matmul == matvec).
+static bool moe_on_device(const rai_model &md) {
+  const rai_model_config &c = md.cfg;
+  return md.moe_tab.p && moe_device_path((int)c.hidden_size, (int)c.intermediate_size, (int)c.group_size,
+                                         (int)c.num_experts) &&
+         fused_quant_ok((int)c.intermediate_size, (int)c.group_size);
+}
+
+// The sparse MLP with every step on the device (no host synchronisation);
+// w.q_split / qscale / qsum hold the quantized normalised rows.  Adds the
+// block's output to the hidden states (model.rs:208-261, then the residual).
+static void moe_block_device(const rai_model &md, int li, Workspace &w, int m, hipStream_t s) {
+  const rai_model_config &c = md.cfg;
+  const DLayer &L = md.layers[li];
+  const int H = c.hidden_size, F = c.intermediate_size, E = c.num_experts, K = c.experts_per_token;
+  const int gs = c.group_size, ne = m * K;
+  const uint8_t *const *tab = md.moe_tab.as<const uint8_t *>() + (size_t)6 * E * li;
+  launch_router(w.normed.as<float>(), L.router, m, H, E, K, c.norm_topk_prob, w.sel.as<int>(),
+                w.wts.as<float>(), s);
+  launch_moe_plan(w.sel.as<int>(), m, K, E, w.moff.as<int>(), w.ment_of.as<int>(), w.ment_tok.as<int>(), s);
+  launch_moe_gather(w.q_split.as<int8_t>(), w.qscale.as<float>(), w.qsum.as<float>(), w.ment_tok.as<int>(),
+                    w.moff.as<int>(), E, ne, H, H / gs, w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), s);
+  launch_moe_gemv(w.mgu.as<float>(), 2 * F, tab, tab + 2 * E, 2, F, H, gs, E, w.mq.as<int8_t>(), w.msc.as<float>(),
+                  w.msu.as<float>(), w.moff.as<int>(), s);
+  launch_silu_quant(w.mgu.as<float>(), w.mgu.as<float>() + F, ne, F, 2 * F, gs, w.mq.as<int8_t>(), nullptr,
+                    w.msc.as<float>(), w.msu.as<float>(), s, nullptr);
+  launch_moe_gemv(w.eo.as<float>(), H, tab + 4 * E, tab + 5 * E, 1, H, F, gs, E, w.mq.as<int8_t>(),
+                  w.msc.as<float>(), w.msu.as<float>(), w.moff.as<int>(), s);
+  launch_moe_combine(w.hid.as<float>(), w.eo.as<float>(), w.wts.as<float>(), w.ment_of.as<int>(), m, K, H, s);
+}
+
 static void moe_block(const rai_model &md, const DLayer &L, Workspace &w, int m, hipStream_t s) {
   const rai_model_config &c = md.cfg;
   const int H = c.hidden_size, F = c.intermediate_size, E = c.num_experts, K = c.experts_per_token;
@@ -544,7 +605,9 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
     const bool gu1 = norm1 && L.gate_up.rows && fused_quant_ok(F, gs) &&
                      w4a8_norm1_path(L.gate_up.rows, L.gate_up.cols, L.gate_up.gs);
     if (!gu1) norm_then_quant(L.post_norm);
-    if (c.num_experts > 0) {
+    if (c.num_experts > 0 && moe_on_device(md)) {
+      moe_block_device(md, li, w, m, s);
+    } else if (c.num_experts > 0) {
       moe_block(md, L, w, m, s);
       launch_vec_add(hid, hid, w.mo.as<float>(), (size_t)m * H, s);
     } else if (gu1 && w4a8_dec_path(L.lin[6].rows, L.lin[6].cols, L.lin[6].gs) &&
@@ -1371,7 +1434,7 @@ int rai_lookup_create(rai_model *m, size_t max_ctx, rai_lookup **out) {
     // Step graphs for dense models (the MoE block synchronises with the
     // host to group tokens by expert, which a graph cannot hold).
     const char *env = std::getenv("RAI_STEP_GRAPHS");
-    d->graphs = m->cfg.num_experts == 0 && !(env && env[0] == '0');
+    d->graphs = (m->cfg.num_experts == 0 || rai::moe_on_device(*m)) && !(env && env[0] == '0');
     d->graph.assign(rai::kAttnTokens + 1, nullptr);
     d->graph_uses.assign(rai::kAttnTokens + 1, 0);
     *out = d.release();

@@ -175,3 +175,29 @@ def test_cfg5_olmoe_width_matches_oracle(rai, ora):
     assert np.array_equal(_bits(gm.hidden_to_logits_batch(gh, 9)), _bits(om.hidden_to_logits_batch(oh, 9)))
     drafted, _ = _lookup_steps_match(rai, ora, gm, om, prompt, 12, 256)
     assert drafted > 0
+
+
+@pytest.mark.parametrize("gs,norm_topk", [(32, False), (64, True), (128, False)])
+def test_moe_device_path_bit_exact(rai, ora, gs, norm_topk):
+    """The device MoE block (router, per-expert entry plan, grouped expert
+    GEMVs, slot-order combine; model.rs:208-261, layers.rs:1808-1870) at
+    group sizes 32/64/128 and with top-k renormalisation: hidden states and
+    logits bit-exact for 1, 9 and 120 tokens (more entries per expert than one
+    pass of the grouped kernel holds), and lookup steps (step graphs) equal
+    the oracle's."""
+    img = rai.synth_model(256, 2, 4, 4, 64, 512, 500, 512, group_size=gs, num_experts=16,
+                          experts_per_token=4, norm_topk_prob=norm_topk, seed=gs)
+    gm = rai.RaiModel.from_bytes(img)
+    om = ora.Model(img, 0)
+    rng = np.random.default_rng(gs)
+    toks = rng.integers(0, 500, size=130)
+    hs = np.stack([om.embed_token(int(t)) for t in toks])
+    gkv, okv = gm.create_kv_cache(256), om.create_kv(256)
+    for a, b in ((0, 120), (120, 121), (121, 130)):
+        gh = gm.forward_batch(hs[a:b], np.arange(a, b), gkv)
+        oh = om.forward_batch(hs[a:b], np.arange(a, b), okv)
+        assert np.array_equal(_bits(gh), _bits(oh)), (a, b)
+    assert np.array_equal(_bits(gm.hidden_to_logits_batch(gh, 9)), _bits(om.hidden_to_logits_batch(oh, 9)))
+    prompt = copy_heavy_prompt(80, 500, seed=gs)
+    drafted, _ = _lookup_steps_match(rai, ora, gm, om, prompt, 16, 256)
+    assert drafted > 0
