@@ -71,7 +71,8 @@ typedef struct rai_lookup_config {
   size_t max_draft;   /* K */
   size_t max_ngram;
   size_t min_ngram;   /* >= 1 */
-  float temperature;  /* <= 1e-6: greedy */
+  float temperature;  /* > 1e-6: exact sampling (lookup.rs:359-403) from the
+                         decoder's StdRng; <= 1e-6: greedy acceptance */
 } rai_lookup_config;
 
 /* LookupMatch (lookup.rs:91-109). */
@@ -220,6 +221,16 @@ int rai_find_ngram_draft(const uint32_t *tokens, size_t len, size_t min_ngram, s
 /* LookupDecoder::new (lookup.rs:192-212). */
 int rai_lookup_create(rai_model *model, size_t max_ctx, rai_lookup **out);
 void rai_lookup_free(rai_lookup *dec);
+/* The decoder's generator for exact sampling: rand::rngs::StdRng::
+ * seed_from_u64(seed) (run.rs:345 seeds the `rng` passed to step).  A new
+ * decoder starts from seed 0. */
+int rai_lookup_seed(rai_lookup *dec, uint64_t seed);
+/* n draws from a fresh StdRng::seed_from_u64(seed) on the device generator
+ * (kinds[i]: 0 next_u32, 1 next_u64, 2 gen::<f32>, 3 gen::<f64>; out[i]
+ * holds the value's bits).  No counterpart in the reference: it exposes the
+ * generator the sampled steps use, for checking against other
+ * implementations of rand 0.8's StdRng. */
+int rai_std_rng_draws(uint64_t seed, const int *kinds, size_t n, uint64_t *out);
 /* The decoder's `pub kv_cache` (lookup.rs:176): borrowed, do not free. */
 int rai_lookup_kv(rai_lookup *dec, rai_kv **out);
 /* LookupDecoder::prefill (lookup.rs:219-247): forward over prompt[0..n-1]. */

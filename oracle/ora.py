@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_float, c_int, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, c_double, c_float, c_int, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
 
 import numpy as np
 
@@ -92,6 +92,19 @@ def lib():
         "ora_lookup_kv_filled": (c_int, [P]),
         "ora_lookup_import_kv": (c_int, [P, c_int, c_int, P, c_int]),
         "ora_greedy_generate": (c_int, [P, P, c_int, c_int, c_int, P]),
+        "ora_chacha_block": (c_int, [P, c_uint64, c_uint64, c_int, P]),
+        "ora_rng_create": (c_int, [c_uint64, c_int, P, POINTER(c_void_p)]),
+        "ora_rng_free": (None, [P]),
+        "ora_rng_next_u32": (c_uint32, [P]),
+        "ora_rng_next_u64": (c_uint64, [P]),
+        "ora_rng_gen_f32": (c_float, [P]),
+        "ora_rng_gen_f64": (c_double, [P]),
+        "ora_rng_key": (None, [P, P]),
+        "ora_softmax_probabilities": (c_int, [P, c_int, c_float, P]),
+        "ora_sample_token": (c_int, [P, c_int, c_float, P, POINTER(c_int)]),
+        "ora_sampled_accept": (c_int, [P, c_int, P, c_int, c_float, P, P, POINTER(c_int), POINTER(c_int)]),
+        "ora_lookup_step_sampled": (c_int, [P, c_int, P, c_int, c_int, c_int, c_int, c_float, P, P,
+                                            POINTER(OracleMetrics)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -342,8 +355,75 @@ class KVCache:
             pass
 
 
+def chacha_block(key, counter: int, stream: int, rounds: int) -> np.ndarray:
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.zeros(16, np.uint32)
+    _check(lib().ora_chacha_block(_ptr(k), counter, stream, rounds, _ptr(out)))
+    return out
+
+
+class Rng:
+    """rand 0.8 StdRng (ChaCha12): seed_from_u64(seed), or from_seed(key)
+    with `rounds` rounds when a key is given."""
+
+    def __init__(self, seed: int = 0, rounds: int = 12, key=None):
+        h = c_void_p()
+        k = None if key is None else np.ascontiguousarray(key, np.uint32)
+        _check(lib().ora_rng_create(seed, rounds, None if k is None else _ptr(k), ctypes.byref(h)))
+        self.h, self._k = h, k
+
+    def next_u32(self) -> int:
+        return int(lib().ora_rng_next_u32(self.h))
+
+    def next_u64(self) -> int:
+        return int(lib().ora_rng_next_u64(self.h))
+
+    def gen_f32(self) -> float:
+        return float(lib().ora_rng_gen_f32(self.h))
+
+    def gen_f64(self) -> float:
+        return float(lib().ora_rng_gen_f64(self.h))
+
+    def key(self) -> np.ndarray:
+        k = np.zeros(8, np.uint32)
+        lib().ora_rng_key(self.h, _ptr(k))
+        return k
+
+    def __del__(self):
+        try:
+            lib().ora_rng_free(self.h)
+        except Exception:
+            pass
+
+
+def softmax_probabilities(logits, temperature: float) -> np.ndarray:
+    x = f32(logits)
+    out = np.zeros_like(x)
+    _check(lib().ora_softmax_probabilities(_ptr(x), x.size, temperature, _ptr(out)))
+    return out
+
+
+def sample_token(logits, temperature: float, rng: Rng) -> int:
+    x = f32(logits)
+    t = c_int()
+    _check(lib().ora_sample_token(_ptr(x), x.size, temperature, rng.h, ctypes.byref(t)))
+    return t.value
+
+
+def sampled_accept(logits, draft, temperature: float, rng: Rng):
+    """lookup.rs:359-403 over verify logits [nd + 1][V]: (tokens, accepted)."""
+    lg = f32(logits)
+    d = np.ascontiguousarray(draft, np.int32)
+    out = np.zeros(d.size + 1, np.int32)
+    prod, acc = c_int(), c_int()
+    _check(lib().ora_sampled_accept(_ptr(lg), lg.shape[1], _ptr(d), d.size, temperature, rng.h, _ptr(out),
+                                    ctypes.byref(prod), ctypes.byref(acc)))
+    return out[:prod.value].tolist(), acc.value
+
+
 class LookupDecoder:
-    """Oracle counterpart of LookupDecoder (lookup.rs:174-455), greedy mode."""
+    """Oracle counterpart of LookupDecoder (lookup.rs:174-455): greedy
+    steps, and exact-sampling steps drawing from an Rng."""
 
     def __init__(self, model: Model, max_ctx: int):
         h = c_void_p()
@@ -363,6 +443,14 @@ class LookupDecoder:
         met = OracleMetrics()
         _check(lib().ora_lookup_step_greedy(self.h, pos, _ptr(c), c.size, max_draft, min_ngram,
                                             max_ngram, _ptr(out), ctypes.byref(met)))
+        return out[:met.produced].tolist(), met
+
+    def step_sampled(self, pos, context, max_draft, min_ngram, max_ngram, temperature, rng: Rng):
+        c = np.ascontiguousarray(context, np.int32)
+        out = np.zeros(max_draft + 1, np.int32)
+        met = OracleMetrics()
+        _check(lib().ora_lookup_step_sampled(self.h, pos, _ptr(c), c.size, max_draft, min_ngram, max_ngram,
+                                             temperature, rng.h, _ptr(out), ctypes.byref(met)))
         return out[:met.produced].tolist(), met
 
     def kv_filled(self) -> int:

@@ -55,4 +55,14 @@ void set_error(const std::string &msg);
 
 }  // namespace ora
 
+// C-ABI body: run the statements, map an exception to -1 and the message.
+#define ORA_TRY(...)                    \
+  try {                                 \
+    __VA_ARGS__;                        \
+    return 0;                           \
+  } catch (const std::exception &e) {   \
+    ora::set_error(e.what());           \
+    return -1;                          \
+  }
+
 #endif

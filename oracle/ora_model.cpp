@@ -422,14 +422,6 @@ struct ora_lookup {
   Lookup d;
 };
 
-#define ORA_TRY(...)                    \
-  try {                                 \
-    __VA_ARGS__;                        \
-    return 0;                           \
-  } catch (const std::exception &e) {   \
-    ora::set_error(e.what());           \
-    return -1;                          \
-  }
 
 static KV make_kv(const Model &m, int max_ctx) {
   const ora_config &c = m.cfg;
@@ -688,6 +680,58 @@ int ora_lookup_step_greedy(ora_lookup *dd, int pos, const int32_t *ctx, int len,
       ++acc;
     }
     if (acc == nd) out[prod++] = (int32_t)argmax(&lg[(size_t)nd * V], V);
+    for (int &f : d.kv.filled) f = std::min(f, pos + prod);
+    *met = {acc, nd, prod, (int32_t)mt[0]};
+  });
+}
+
+// LookupDecoder::step (lookup.rs:260-425) with exact sampling at
+// `temperature` (> 1e-6): the verify forward as in the greedy step, then the
+// accept / correct / bonus loop of lookup.rs:359-403 drawing from `rng`;
+// decode_one samples its token (lookup.rs:428-455).
+int ora_lookup_step_sampled(ora_lookup *dd, int pos, const int32_t *ctx, int len, int max_draft,
+                            int min_ngram, int max_ngram, float temperature, ora_rng *rng, int32_t *out,
+                            ora_metrics *met) {
+  ORA_TRY({
+    Lookup &d = dd->d;
+    const Model &m = *d.m;
+    const int H = m.cfg.hidden_size, V = m.cfg.vocab_size;
+    if (max_draft <= 0 || min_ngram < 1 || min_ngram > max_ngram) fail("invalid lookup config");
+    if (!(std::isfinite(temperature) && temperature > 1e-6f)) fail("exact sampling needs temperature > 1e-6");
+    if (len <= 0) fail("prompt-lookup step requires a non-empty context");
+    if (pos >= d.max_ctx) fail("decode position exceeds the context window");
+    const int last = ctx[len - 1];
+    const int budget = std::max(0, d.max_ctx - pos - 1);
+    int64_t mt[3] = {0, 0, 0};
+    const bool hit = budget > 0 && find_ngram(ctx, len, min_ngram, max_ngram,
+                                              std::min(max_draft, budget), mt);
+    if (!hit) {
+      std::vector<float> h(H), lg(V);
+      embed(m, last, h.data());
+      forward(m, d.kv, h.data(), &pos, 1);
+      logits(m, h.data(), lg.data(), 1);
+      int tok = 0;
+      if (ora_sample_token(lg.data(), V, temperature, rng, &tok)) fail("sample_token failed");
+      out[0] = tok;
+      *met = {0, 0, 1, 0};
+      return 0;
+    }
+    const int nd = (int)mt[2];
+    for (int i = 0; i < nd; ++i)
+      if (ctx[mt[1] + i] < 0 || ctx[mt[1] + i] >= V)
+        fail("context contains a token outside the model vocabulary");
+    const int vb = nd + 1;
+    std::vector<float> h((size_t)vb * H), lg((size_t)vb * V);
+    std::vector<int> ps(vb);
+    for (int i = 0; i < vb; ++i) {
+      embed(m, i == 0 ? last : ctx[mt[1] + i - 1], &h[(size_t)i * H]);
+      ps[i] = pos + i;
+    }
+    forward(m, d.kv, h.data(), ps.data(), vb);
+    logits(m, h.data(), lg.data(), vb);
+    int prod = 0, acc = 0;
+    if (ora_sampled_accept(lg.data(), V, ctx + mt[1], nd, temperature, rng, out, &prod, &acc))
+      fail("sampled acceptance failed");
     for (int &f : d.kv.filled) f = std::min(f, pos + prod);
     *met = {acc, nd, prod, (int32_t)mt[0]};
   });

@@ -1,0 +1,280 @@
+// CPU oracle: exact-sampling prompt-lookup (TEST INFRASTRUCTURE ONLY).
+//
+// Restates, for the checker:
+//   - rand 0.8.6 StdRng = rand_chacha 0.3.1 ChaCha12Rng over rand_core 0.6.4
+//     BlockRng (Cargo.lock of the reference): the ChaCha block function
+//     (RFC 8439 quarter rounds; 64-bit block counter in words 12-13, 64-bit
+//     stream in words 14-15, both zero-based), four blocks per refill, words
+//     consumed in order; next_u64 = low word then high word, straddling a
+//     refill as BlockRng does; SeedableRng::seed_from_u64 (PCG32 output
+//     function filling the 32-byte key); Standard f32 = (u32 >> 8) * 2^-24,
+//     f64 = (u64 >> 11) * 2^-53.
+//   - softmax_probabilities and sample_correction (speculative.rs:414-513),
+//     sample_token with top_k = 0, top_p = 1 (sampler.rs:47-182), and the
+//     accept / correct / bonus loop of LookupDecoder::step (lookup.rs:359-403).
+// Pins: the block function and the buffering order are checked against the
+// RFC 7539 A.1 keystream vectors (20 rounds) and the RFC 8439 2.3.2 block;
+// seed_from_u64 and the float conversions have no published vector and are
+// parity-unpinned beyond their published algorithm.
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "ora_internal.h"
+#include "oracle.h"
+
+namespace ora {
+
+static inline uint32_t rotl(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
+
+static inline void quarter(uint32_t *s, int a, int b, int c, int d) {
+  s[a] += s[b]; s[d] = rotl(s[d] ^ s[a], 16);
+  s[c] += s[d]; s[b] = rotl(s[b] ^ s[c], 12);
+  s[a] += s[b]; s[d] = rotl(s[d] ^ s[a], 8);
+  s[c] += s[d]; s[b] = rotl(s[b] ^ s[c], 7);
+}
+
+void chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds, uint32_t out[16]) {
+  uint32_t in[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u};
+  for (int i = 0; i < 8; ++i) in[4 + i] = key[i];
+  in[12] = (uint32_t)counter;
+  in[13] = (uint32_t)(counter >> 32);
+  in[14] = (uint32_t)stream;
+  in[15] = (uint32_t)(stream >> 32);
+  uint32_t s[16];
+  std::memcpy(s, in, sizeof(s));
+  for (int r = 0; r < rounds; r += 2) {
+    quarter(s, 0, 4, 8, 12);
+    quarter(s, 1, 5, 9, 13);
+    quarter(s, 2, 6, 10, 14);
+    quarter(s, 3, 7, 11, 15);
+    quarter(s, 0, 5, 10, 15);
+    quarter(s, 1, 6, 11, 12);
+    quarter(s, 2, 7, 8, 13);
+    quarter(s, 3, 4, 9, 14);
+  }
+  for (int i = 0; i < 16; ++i) out[i] = s[i] + in[i];
+}
+
+struct StdRng {
+  uint32_t key[8];
+  uint64_t counter = 0;
+  int rounds = 12;
+  uint32_t buf[64];
+  int index = 64;
+  void refill() {
+    for (int b = 0; b < 4; ++b) chacha_block(key, counter + b, 0, rounds, buf + 16 * b);
+    counter += 4;
+  }
+  uint32_t next_u32() {
+    if (index >= 64) {
+      refill();
+      index = 0;
+    }
+    return buf[index++];
+  }
+  uint64_t next_u64() {
+    if (index < 63) {
+      const uint64_t v = (uint64_t)buf[index] | ((uint64_t)buf[index + 1] << 32);
+      index += 2;
+      return v;
+    }
+    if (index >= 64) {
+      refill();
+      index = 2;
+      return (uint64_t)buf[0] | ((uint64_t)buf[1] << 32);
+    }
+    const uint64_t lo = buf[63];
+    refill();
+    index = 1;
+    return lo | ((uint64_t)buf[0] << 32);
+  }
+  float gen_f32() { return (float)(next_u32() >> 8) * (1.0f / 16777216.0f); }
+  double gen_f64() { return (double)(next_u64() >> 11) * (1.0 / 9007199254740992.0); }
+};
+
+static void seed_from_u64(StdRng &r, uint64_t state) {
+  const uint64_t mul = 6364136223846793005ull, inc = 11634580027462260723ull;
+  for (int i = 0; i < 8; ++i) {
+    state = state * mul + inc;
+    const uint32_t xs = (uint32_t)(((state >> 18) ^ state) >> 27);
+    const uint32_t rot = (uint32_t)(state >> 59);
+    r.key[i] = (xs >> rot) | (xs << ((32 - rot) & 31));
+  }
+  r.counter = 0;
+  r.index = 64;
+}
+
+// speculative.rs:431-477.
+static std::vector<float> softmax_probabilities(const float *logits, int n, float temperature) {
+  const float temp = (std::isfinite(temperature) && temperature > 1e-6f) ? temperature : 1.0f;
+  std::vector<float> v(n);
+  for (int i = 0; i < n; ++i) {
+    const float x = logits[i] / temp;
+    v[i] = std::isnan(x) ? -INFINITY : x;
+  }
+  int pinf = 0;
+  for (int i = 0; i < n; ++i) pinf += v[i] == INFINITY;
+  if (pinf > 0) {
+    const float p = 1.0f / (float)pinf;
+    for (int i = 0; i < n; ++i) v[i] = v[i] == INFINITY ? p : 0.0f;
+    return v;
+  }
+  float mx = -INFINITY;
+  for (int i = 0; i < n; ++i) mx = std::fmax(mx, v[i]);
+  if (mx == -INFINITY) return std::vector<float>(n, 1.0f / (float)n);
+  float sum = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    v[i] = std::exp(v[i] - mx);
+    sum += v[i];
+  }
+  if (!std::isfinite(sum) || sum <= 0.0f) return std::vector<float>(n, 1.0f / (float)n);
+  for (int i = 0; i < n; ++i) v[i] /= sum;
+  return v;
+}
+
+// sample_token (sampler.rs:47-182) with top_k = 0 and top_p = 1.
+static int sample_token(std::vector<float> v, float temperature, StdRng &rng) {
+  const int n = (int)v.size();
+  if (n == 0) return 0;
+  for (float &x : v)
+    if (std::isnan(x)) x = -INFINITY;
+  if (!std::isfinite(temperature) || temperature <= 1e-6f) return (int)argmax(v.data(), n);
+  const float inv_temp = 1.0f / temperature;
+  for (float &x : v) x *= inv_temp;
+  int pinf = 0;
+  for (float x : v) pinf += x == INFINITY;
+  if (pinf > 0) {
+    const float p = 1.0f / (float)pinf;
+    for (float &x : v) x = x == INFINITY ? p : 0.0f;
+  } else {
+    float mx = -INFINITY;
+    for (float x : v) mx = std::fmax(mx, x);
+    if (mx == -INFINITY) {
+      for (float &x : v) x = 1.0f / (float)n;
+    } else {
+      float sum = 0.0f;
+      for (float &x : v) {
+        x = std::exp(x - mx);
+        sum += x;
+      }
+      if (std::isfinite(sum) && sum > 0.0f) {
+        const float inv = 1.0f / sum;
+        for (float &x : v) x *= inv;
+      } else {
+        for (float &x : v) x = 1.0f / (float)n;
+      }
+    }
+  }
+  const float r = rng.gen_f32();
+  float cum = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    cum += v[i];
+    if (r < cum) return i;
+  }
+  return (int)argmax(v.data(), n);
+}
+
+// sample_correction (speculative.rs:479-513) against a point-mass draft on
+// `draft` (all other draft logits -inf).
+static int sample_correction(const float *target, int n, int draft, float temperature, StdRng &rng) {
+  const std::vector<float> tp = softmax_probabilities(target, n, temperature);
+  double adj_sum = 0.0;
+  std::vector<float> adj(n);
+  for (int i = 0; i < n; ++i) {
+    const float dp = i == draft ? 1.0f : 0.0f;
+    adj[i] = std::fmax(tp[i] - dp, 0.0f);
+    adj_sum += (double)adj[i];
+  }
+  if (!std::isfinite(adj_sum) || adj_sum <= 0.0)
+    return sample_token(std::vector<float>(target, target + n), temperature, rng);
+  const double u = rng.gen_f64() * adj_sum;
+  double cum = 0.0;
+  for (int i = 0; i < n; ++i) {
+    cum += (double)adj[i];
+    if (cum >= u) return i;
+  }
+  return n - 1;
+}
+
+// The accept / correct / bonus loop of lookup.rs:359-403 over verify logits
+// [nd + 1][V]; returns the number of produced tokens.
+int sampled_accept(const float *lg, int V, const int32_t *draft, int nd, float temperature, StdRng &rng,
+                   int32_t *out, int *accepted) {
+  int acc = 0, prod = 0;
+  for (int i = 0; i < nd; ++i) {
+    const float *row = lg + (size_t)i * V;
+    const int d = draft[i];
+    const float pt = softmax_probabilities(row, V, temperature)[d];
+    const float pd = 1.0f;  // point mass: one +inf among -inf
+    const float ap = pd > 0.0f ? std::fmin(pt / pd, 1.0f) : (pt > 0.0f ? 1.0f : 0.0f);
+    const float u = rng.gen_f32();
+    if (u < ap) {
+      out[prod++] = d;
+      ++acc;
+    } else {
+      out[prod++] = sample_correction(row, V, d, temperature, rng);
+      break;
+    }
+  }
+  if (acc == nd) out[prod++] = sample_token(std::vector<float>(lg + (size_t)nd * V, lg + (size_t)(nd + 1) * V),
+                                            temperature, rng);
+  *accepted = acc;
+  return prod;
+}
+
+int sampled_token(const float *lg, int V, float temperature, StdRng &rng) {
+  return sample_token(std::vector<float>(lg, lg + V), temperature, rng);
+}
+
+}  // namespace ora
+
+using namespace ora;
+
+struct ora_rng {
+  StdRng r;
+};
+
+extern "C" {
+
+int ora_chacha_block(const uint32_t *key, uint64_t counter, uint64_t stream, int rounds, uint32_t *out) {
+  ORA_TRY(chacha_block(key, counter, stream, rounds, out));
+}
+
+int ora_rng_create(uint64_t seed, int rounds, const uint32_t *key, ora_rng **out) {
+  ORA_TRY({
+    auto r = new ora_rng();
+    if (key) {
+      std::memcpy(r->r.key, key, 32);
+      r->r.counter = 0;
+      r->r.index = 64;
+    } else {
+      seed_from_u64(r->r, seed);
+    }
+    r->r.rounds = rounds;
+    *out = r;
+  });
+}
+void ora_rng_free(ora_rng *r) { delete r; }
+uint32_t ora_rng_next_u32(ora_rng *r) { return r->r.next_u32(); }
+uint64_t ora_rng_next_u64(ora_rng *r) { return r->r.next_u64(); }
+float ora_rng_gen_f32(ora_rng *r) { return r->r.gen_f32(); }
+double ora_rng_gen_f64(ora_rng *r) { return r->r.gen_f64(); }
+void ora_rng_key(const ora_rng *r, uint32_t *key) { std::memcpy(key, r->r.key, 32); }
+
+int ora_sample_token(const float *logits, int n, float temperature, ora_rng *r, int *token) {
+  ORA_TRY(*token = sample_token(std::vector<float>(logits, logits + n), temperature, r->r));
+}
+int ora_softmax_probabilities(const float *logits, int n, float temperature, float *out) {
+  ORA_TRY({
+    const std::vector<float> p = softmax_probabilities(logits, n, temperature);
+    std::memcpy(out, p.data(), sizeof(float) * n);
+  });
+}
+int ora_sampled_accept(const float *lg, int V, const int32_t *draft, int nd, float temperature, ora_rng *r,
+                       int32_t *out, int *produced, int *accepted) {
+  ORA_TRY(*produced = sampled_accept(lg, V, draft, nd, temperature, r->r, out, accepted));
+}
+
+}  // extern "C"

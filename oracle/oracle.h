@@ -31,6 +31,7 @@ extern "C" {
 typedef struct ora_model ora_model;
 typedef struct ora_kv ora_kv;
 typedef struct ora_lookup ora_lookup;
+typedef struct ora_rng ora_rng;
 
 typedef struct ora_config {
   uint32_t hidden_size, num_layers, num_heads, num_kv_heads, head_dim;
@@ -88,6 +89,24 @@ int64_t ora_argmax(const float *values, int64_t n);
 int ora_find_ngram_draft(const int32_t *tokens, int64_t len, int64_t min_ngram,
                          int64_t max_ngram, int64_t max_draft, int64_t *match3);
 
+/* ---- exact sampling (rand 0.8 StdRng, sampler.rs, speculative.rs) ---- */
+/* One ChaCha block: key[8], 64-bit counter (words 12-13), 64-bit stream
+ * (words 14-15), `rounds` rounds (20 for the RFC vectors, 12 for StdRng). */
+int ora_chacha_block(const uint32_t *key, uint64_t counter, uint64_t stream, int rounds, uint32_t *out16);
+/* StdRng::seed_from_u64(seed) (key == NULL) or from_seed(key) over `rounds`. */
+int ora_rng_create(uint64_t seed, int rounds, const uint32_t *key, ora_rng **out);
+void ora_rng_free(ora_rng *r);
+uint32_t ora_rng_next_u32(ora_rng *r);
+uint64_t ora_rng_next_u64(ora_rng *r);
+float ora_rng_gen_f32(ora_rng *r);
+double ora_rng_gen_f64(ora_rng *r);
+void ora_rng_key(const ora_rng *r, uint32_t *key8);
+int ora_softmax_probabilities(const float *logits, int n, float temperature, float *out);
+int ora_sample_token(const float *logits, int n, float temperature, ora_rng *r, int *token);
+/* lookup.rs:359-403 over verify logits [nd + 1][V] against draft[nd]. */
+int ora_sampled_accept(const float *logits, int vocab, const int32_t *draft, int nd, float temperature,
+                       ora_rng *r, int32_t *out, int *produced, int *accepted);
+
 /* ---- model (format.rs, model.rs, kv_cache.rs) ---- */
 int ora_model_open(const uint8_t *buf, size_t len, int max_groups, ora_model **out);
 void ora_model_free(ora_model *m);
@@ -118,6 +137,9 @@ int ora_lookup_prefill(ora_lookup *d, const int32_t *prompt, int n, int *pos_out
 int ora_lookup_step_greedy(ora_lookup *d, int pos, const int32_t *context, int len,
                            int max_draft, int min_ngram, int max_ngram,
                            int32_t *out_tokens, ora_metrics *metrics);
+int ora_lookup_step_sampled(ora_lookup *d, int pos, const int32_t *context, int len, int max_draft,
+                            int min_ngram, int max_ngram, float temperature, ora_rng *rng,
+                            int32_t *out_tokens, ora_metrics *metrics);
 int ora_lookup_kv_filled(const ora_lookup *d);
 /* Replace layer `layer`'s K (which = 0) or V (which = 1) rows with
  * rows[nkv][npos][head_dim] and set its watermark to npos (a decoder state

@@ -121,6 +121,8 @@ def lib():
         "rai_find_ngram_draft": (c_int, [P, S, S, S, S, POINTER(_LookupMatch), POINTER(c_int)]),
         "rai_lookup_create": (c_int, [P, S, POINTER(c_void_p)]),
         "rai_lookup_free": (None, [P]),
+        "rai_lookup_seed": (c_int, [P, ctypes.c_uint64]),
+        "rai_std_rng_draws": (c_int, [ctypes.c_uint64, P, S, P]),
         "rai_lookup_kv": (c_int, [P, POINTER(c_void_p)]),
         "rai_lookup_prefill": (c_int, [P, P, S, POINTER(c_size_t)]),
         "rai_lookup_step": (c_int, [P, S, P, S, POINTER(_LookupConfig), P, S,
@@ -359,6 +361,15 @@ class LookupMatch:
         return list(tokens[self.start:self.start + self.len])
 
 
+def std_rng_draws(seed: int, kinds) -> np.ndarray:
+    """Draws from the device StdRng::seed_from_u64(seed): kinds 0 u32, 1 u64,
+    2 f32, 3 f64; returns the raw bits as uint64."""
+    k = np.ascontiguousarray(kinds, np.int32)
+    out = np.zeros(max(k.size, 1), np.uint64)
+    _check(lib().rai_std_rng_draws(seed, _ptr(k), k.size, _ptr(out)))
+    return out[:k.size]
+
+
 def find_ngram_draft(tokens, min_ngram: int, max_ngram: int, max_draft: int):
     """find_ngram_draft (lookup.rs:131-171), evaluated by the GPU search kernel."""
     t = _u32(tokens)
@@ -518,7 +529,8 @@ class KVCache:
 
 @dataclass
 class LookupConfig:
-    """LookupConfig (lookup.rs:64-89).  temperature <= 1e-6 is greedy."""
+    """LookupConfig (lookup.rs:64-89).  temperature > 1e-6 samples exactly
+    (lookup.rs:359-403) from the decoder's StdRng; <= 1e-6 is greedy."""
     max_draft: int = 10
     max_ngram: int = 3
     min_ngram: int = 1
@@ -540,7 +552,8 @@ class LookupMetrics:
 
 class LookupDecoder:
     """LookupDecoder (lookup.rs:174-455): drafts by n-gram lookup on the GPU,
-    verifies [last, draft...] in one batched forward, accepts greedily."""
+    verifies [last, draft...] in one batched forward, accepts greedily or by
+    exact sampling from its own StdRng (seed with `seed`)."""
 
     def __init__(self, model: RaiModel, max_ctx: int):
         h = c_void_p()
@@ -550,6 +563,10 @@ class LookupDecoder:
         kv = c_void_p()
         _check(lib().rai_lookup_kv(self.h, ctypes.byref(kv)))
         self.kv_cache = KVCache(kv.value, owner=self, borrowed=True)
+
+    def seed(self, seed: int) -> None:
+        """StdRng::seed_from_u64(seed) for the sampled steps."""
+        _check(lib().rai_lookup_seed(self.h, seed))
 
     def prefill(self, prompt_tokens) -> int:
         p = _u32(prompt_tokens)

@@ -23,7 +23,7 @@ ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall",
           "-I", os.path.join(ROOT, "include"), "-I", CSRC]
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-SOURCES = ["kernels.hip", "fused.hip", "gemv.hip", "gemm_mm.hip", "moe.hip", "decode_gemv.hip", "runtime.hip", "format.cpp", "synth.cpp"]
+SOURCES = ["kernels.hip", "fused.hip", "gemv.hip", "gemm_mm.hip", "moe.hip", "sample.hip", "decode_gemv.hip", "runtime.hip", "format.cpp", "synth.cpp"]
 # Per-source device flags: the matrix-core GEMV keeps MFMA results in
 # architectural VGPRs, which its epilogue reads directly (without it the
 # compiler routes them through AGPRs and one copy per value).

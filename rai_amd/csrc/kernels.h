@@ -187,6 +187,27 @@ void launch_moe_accumulate(float *out, const float *eo, const float *w, int m, i
                            hipStream_t s);
 void launch_fill(float *p, float v, size_t n, hipStream_t s);
 
+// Exact-sampling acceptance (sample.hip).  The decoder's rand 0.8 StdRng
+// (ChaCha12) in device memory: key, 64-bit block counter, the four-block
+// word buffer and the read index (64 = empty).
+struct RngState {
+  uint32_t key[8];
+  uint32_t counter_lo, counter_hi;
+  int index, pad;
+  uint32_t buf[64];
+};
+// SeedableRng::seed_from_u64 (host side).
+void rng_seed_from_u64(RngState &r, uint64_t seed);
+// k_sample_probs over `rows` verify rows (nd + 1), then the accept / correct
+// / bonus loop; appends the produced tokens to ctx[len..] and writes
+// res = {accepted, produced}.  With a step record st the kernels read len,
+// start, nd (st[1..3]) and the temperature bits (st[4]) from it.  probs
+// holds rows * V floats, scratch V floats.
+void launch_sample(const float *logits, float *probs, int V, uint32_t *ctx, int len, int start, int nd, float T,
+                   RngState *rng, float *scratch, int *res, hipStream_t s, const int *st, int rows);
+// n draws (kinds: 0 u32, 1 u64, 2 f32, 3 f64) from the device generator.
+void launch_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *out, hipStream_t s);
+
 // Device MoE (moe.hip): group 32/64/128, hidden and FFN multiples of 256,
 // at most 1024 experts.
 bool moe_device_path(int hidden, int ffn, int gs, int experts);

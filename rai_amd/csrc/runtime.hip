@@ -740,10 +740,14 @@ struct rai_lookup {
   hipStream_t stream = nullptr;
   // Step graphs: one per verify batch size m (embed, forward, logits,
   // argmax, accept), replayed with the position in the device step record.
-  DevBuf step;            // int[4] {pos0, len, start, nd}
+  DevBuf step;            // int[5] {pos0, len, start, nd, temperature bits}
   bool graphs = false;
+  // Indexed by verify size m, plus kAttnTokens + 1 for exact-sampling steps.
   std::vector<hipGraphExec_t> graph;
   std::vector<int> graph_uses;
+  // Exact sampling: the decoder's StdRng (device), per-row probabilities
+  // [64][V] and one row of scratch.
+  DevBuf rng, probs, pscratch;
   ~rai_lookup() {
     for (hipGraphExec_t g : graph)
       if (g) (void)hipGraphExecDestroy(g);
@@ -795,8 +799,10 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
   if (cfg.max_draft == 0) fail(RAI_E_ARG, "prompt-lookup max_draft must be non-zero");
   if (cfg.min_ngram < 1 || cfg.min_ngram > cfg.max_ngram)
     fail(RAI_E_ARG, "prompt-lookup requires 1 <= min_ngram <= max_ngram");
-  if (!(cfg.temperature <= 1e-6f))
-    fail(RAI_E_UNSUPPORTED, "sampled acceptance (temperature > 0) is not implemented; use greedy");
+  // Above 1e-6 the step samples exactly (lookup.rs:359-403) from the
+  // decoder's generator; at or below it, greedy acceptance.
+  if (!std::isfinite(cfg.temperature)) fail(RAI_E_ARG, "temperature must be finite");
+  const bool sampled = cfg.temperature > 1e-6f;
   // The device context keeps 64 slots past max_ctx for the accepted tokens
   // and the workspace holds 64 logit rows: the verify batch is at most 64.
   if (cfg.max_draft > 63) fail(RAI_E_ARG, "max_draft above 63 is not supported");
@@ -826,8 +832,13 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
                  d.ws.err.as<int>(), s, st);
     forward_enqueue(md, d.kv, d.ws, m, pos, s, st);
     logits(md, d.ws, m, s);
-    launch_argmax(d.ws.logits.as<float>(), m, c.vocab_size, d.ws.am.as<uint32_t>(), s);
-    launch_accept(d.ws.am.as<uint32_t>(), d.ctx.as<uint32_t>(), (int)len, start, nd, res + 4, s, st);
+    if (sampled) {
+      launch_sample(d.ws.logits.as<float>(), d.probs.as<float>(), c.vocab_size, d.ctx.as<uint32_t>(), (int)len,
+                    start, nd, cfg.temperature, d.rng.as<RngState>(), d.pscratch.as<float>(), res + 4, s, st, m);
+    } else {
+      launch_argmax(d.ws.logits.as<float>(), m, c.vocab_size, d.ws.am.as<uint32_t>(), s);
+      launch_accept(d.ws.am.as<uint32_t>(), d.ctx.as<uint32_t>(), (int)len, start, nd, res + 4, s, st);
+    }
   };
   HIP_CHECK(hipGetLastError());  // nothing pending from earlier launches
   if (d.graphs && m <= kAttnTokens) {
@@ -836,11 +847,13 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
     sh[1] = (int)len;
     sh[2] = start;
     sh[3] = nd;
-    HIP_CHECK(hipMemcpyAsync(d.step.p, sh, 4 * sizeof(int), hipMemcpyHostToDevice, s));
+    std::memcpy(&sh[4], &cfg.temperature, sizeof(float));
+    HIP_CHECK(hipMemcpyAsync(d.step.p, sh, 5 * sizeof(int), hipMemcpyHostToDevice, s));
     const int *st = d.step.as<int>();
-    if (d.graph[m]) {
-      HIP_CHECK(hipGraphLaunch(d.graph[m], s));
-    } else if (d.graph_uses[m]++ == 0) {
+    const int gi = m + (sampled ? kAttnTokens + 1 : 0);
+    if (d.graph[gi]) {
+      HIP_CHECK(hipGraphLaunch(d.graph[gi], s));
+    } else if (d.graph_uses[gi]++ == 0) {
       enqueue(st);  // first use: eager (sets kernel attributes, sizes scratch)
       HIP_CHECK(hipGetLastError());
     } else {
@@ -858,7 +871,7 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
       const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
       (void)hipGraphDestroy(g);
       HIP_CHECK(ie);
-      d.graph[m] = ge;
+      d.graph[gi] = ge;
       HIP_CHECK(hipGraphLaunch(ge, s));
     }
   } else {
@@ -1435,13 +1448,48 @@ int rai_lookup_create(rai_model *m, size_t max_ctx, rai_lookup **out) {
     // host to group tokens by expert, which a graph cannot hold).
     const char *env = std::getenv("RAI_STEP_GRAPHS");
     d->graphs = (m->cfg.num_experts == 0 || rai::moe_on_device(*m)) && !(env && env[0] == '0');
-    d->graph.assign(rai::kAttnTokens + 1, nullptr);
-    d->graph_uses.assign(rai::kAttnTokens + 1, 0);
+    d->graph.assign(2 * (rai::kAttnTokens + 1), nullptr);
+    d->graph_uses.assign(2 * (rai::kAttnTokens + 1), 0);
+    d->rng.alloc(sizeof(rai::RngState));
+    d->probs.alloc(sizeof(float) * 64 * (size_t)m->cfg.vocab_size);
+    d->pscratch.alloc(sizeof(float) * (size_t)m->cfg.vocab_size);
+    rai::RngState r;
+    rai::rng_seed_from_u64(r, 0);
+    HIP_CHECK(hipMemcpy(d->rng.p, &r, sizeof(r), hipMemcpyHostToDevice));
     *out = d.release();
   });
 }
 
 void rai_lookup_free(rai_lookup *d) { delete d; }
+
+int rai_lookup_seed(rai_lookup *d, uint64_t seed) {
+  RAI_API_BODY({
+    if (!d) rai::fail(RAI_E_ARG, "null argument");
+    rai::RngState r;
+    rai::rng_seed_from_u64(r, seed);
+    HIP_CHECK(hipStreamSynchronize(d->stream));
+    HIP_CHECK(hipMemcpy(d->rng.p, &r, sizeof(r), hipMemcpyHostToDevice));
+  });
+}
+
+int rai_std_rng_draws(uint64_t seed, const int *kinds, size_t n, uint64_t *out) {
+  RAI_API_BODY({
+    if ((!kinds || !out) && n) rai::fail(RAI_E_ARG, "null argument");
+    for (size_t i = 0; i < n; ++i)
+      if (kinds[i] < 0 || kinds[i] > 3) rai::fail(RAI_E_ARG, "draw kind must be 0..3");
+    rai::RngState r;
+    rai::rng_seed_from_u64(r, seed);
+    DevBuf dr, dk, dout;
+    dr.alloc(sizeof(r));
+    dk.alloc(sizeof(int) * (n + 1));
+    dout.alloc(sizeof(uint64_t) * (n + 1));
+    HIP_CHECK(hipMemcpy(dr.p, &r, sizeof(r), hipMemcpyHostToDevice));
+    if (n) HIP_CHECK(hipMemcpy(dk.p, kinds, sizeof(int) * n, hipMemcpyHostToDevice));
+    rai::launch_rng_draws(dr.as<rai::RngState>(), dk.as<int>(), (int)n, dout.as<uint64_t>(), nullptr);
+    HIP_CHECK(hipGetLastError());
+    if (n) HIP_CHECK(hipMemcpy(out, dout.p, sizeof(uint64_t) * n, hipMemcpyDeviceToHost));
+  });
+}
 
 int rai_lookup_kv(rai_lookup *d, rai_kv **out) {
   RAI_API_BODY({

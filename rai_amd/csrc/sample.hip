@@ -1,0 +1,423 @@
+// Exact-sampling acceptance for prompt lookup (lookup.rs:359-403) and the
+// sampled decode_one token (lookup.rs:428-455), on the device, drawing from
+// the decoder's own rand 0.8 StdRng (ChaCha12, rand_chacha 0.3.1 over
+// rand_core 0.6.4) so a step needs no host round trip and replays as part of
+// the step graph.
+//
+// The reference's arithmetic is kept in its order: the softmax sums
+// (f32, sequential over the vocabulary), the residual sum and its cumulative
+// search (f64, sequential), the sample_token cumulative search (f32,
+// sequential).  Those chains run in one wave (lane 0's order, values
+// broadcast with readlane); everything order-free (scaling, maxima, the
+// exponentials, the normalisation) runs on the whole block.  The draft rows'
+// probabilities (softmax_probabilities: x / T, e / sum) are computed by
+// k_sample_probs, one block per row, so their sum chains run in parallel;
+// the bonus row uses sample_token's own variant (x * (1 / T), e * (1 / sum)).
+//
+// Generator: ChaCha block with 12 rounds, key from SeedableRng::seed_from_u64
+// (set on the host), 64-bit block counter in words 12-13, stream 0; four
+// blocks per refill; u32 draws in order; u64 = low word then high word,
+// across a refill as BlockRng::next_u64 does; Standard f32 = (u32 >> 8) *
+// 2^-24, f64 = (u64 >> 11) * 2^-53.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "exact_math.h"
+#include "kernels.h"
+
+namespace rai {
+
+namespace {
+
+__device__ __forceinline__ uint32_t rotl32(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
+
+__device__ void chacha12(const uint32_t *key, uint64_t counter, uint32_t *out) {
+  uint32_t in[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u};
+  for (int i = 0; i < 8; ++i) in[4 + i] = key[i];
+  in[12] = (uint32_t)counter;
+  in[13] = (uint32_t)(counter >> 32);
+  in[14] = 0u;
+  in[15] = 0u;
+  uint32_t s[16];
+  for (int i = 0; i < 16; ++i) s[i] = in[i];
+  auto qr = [&](int a, int b, int c, int d) {
+    s[a] += s[b]; s[d] = rotl32(s[d] ^ s[a], 16);
+    s[c] += s[d]; s[b] = rotl32(s[b] ^ s[c], 12);
+    s[a] += s[b]; s[d] = rotl32(s[d] ^ s[a], 8);
+    s[c] += s[d]; s[b] = rotl32(s[b] ^ s[c], 7);
+  };
+  for (int r = 0; r < 12; r += 2) {
+    qr(0, 4, 8, 12);
+    qr(1, 5, 9, 13);
+    qr(2, 6, 10, 14);
+    qr(3, 7, 11, 15);
+    qr(0, 5, 10, 15);
+    qr(1, 6, 11, 12);
+    qr(2, 7, 8, 13);
+    qr(3, 4, 9, 14);
+  }
+  for (int i = 0; i < 16; ++i) out[i] = s[i] + in[i];
+}
+
+// One thread drives the generator; the state lives in device memory.
+struct Gen {
+  RngState *st;
+  __device__ void refill() {
+    const uint64_t c = (uint64_t)st->counter_lo | ((uint64_t)st->counter_hi << 32);
+    for (int b = 0; b < 4; ++b) chacha12(st->key, c + b, st->buf + 16 * b);
+    const uint64_t n = c + 4;
+    st->counter_lo = (uint32_t)n;
+    st->counter_hi = (uint32_t)(n >> 32);
+  }
+  __device__ uint32_t next_u32() {
+    if (st->index >= 64) {
+      refill();
+      st->index = 0;
+    }
+    return st->buf[st->index++];
+  }
+  __device__ uint64_t next_u64() {
+    const int i = st->index;
+    if (i < 63) {
+      st->index = i + 2;
+      return (uint64_t)st->buf[i] | ((uint64_t)st->buf[i + 1] << 32);
+    }
+    if (i >= 64) {
+      refill();
+      st->index = 2;
+      return (uint64_t)st->buf[0] | ((uint64_t)st->buf[1] << 32);
+    }
+    const uint64_t lo = st->buf[63];
+    refill();
+    st->index = 1;
+    return lo | ((uint64_t)st->buf[0] << 32);
+  }
+  __device__ float gen_f32() { return (float)(next_u32() >> 8) * (1.0f / 16777216.0f); }
+  __device__ double gen_f64() { return (double)(next_u64() >> 11) * (1.0 / 9007199254740992.0); }
+};
+
+constexpr int kSampleThreads = 1024;
+
+__device__ __forceinline__ float bcast(float v, int k) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), k));
+}
+__device__ __forceinline__ double bcast_d(double v, int k) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, k);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), k);
+  return __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+// Sequential f32 sum of p[0..n) from +0, in index order (one wave; every
+// lane returns the sum).  Values are >= +0, so the +0 padding of the last
+// 64-wide read changes nothing.
+__device__ float chain_sum(const float *p, int n, int lane) {
+  float s = 0.0f;
+  for (int base = 0; base < n; base += 64) {
+    const float v = base + lane < n ? p[base + lane] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < 64; ++k) s = s + bcast(v, k);
+  }
+  return s;
+}
+
+// First i with r < (p[0] + ... + p[i]) (f32, sequential); -1 if none.
+__device__ int chain_search(const float *p, int n, float r, int lane) {
+  float c = 0.0f;
+  for (int base = 0; base < n; base += 64) {
+    const float v = base + lane < n ? p[base + lane] : 0.0f;
+    const int lim = min(64, n - base);
+    for (int k = 0; k < lim; ++k) {
+      c = c + bcast(v, k);
+      if (r < c) return base + k;
+    }
+  }
+  return -1;
+}
+
+// Block-wide reductions (every thread returns the result).
+__device__ float block_max(float v, float *red) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+__device__ int block_sum_i(int v, int *red) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int r = 0;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) r += red[w];
+  return r;
+}
+
+// Probabilities of one logit row into `out` (block-wide).  SAMPLE false:
+// softmax_probabilities (speculative.rs:431-477): x / T, e / sum.  SAMPLE
+// true: sample_token's softmax (sampler.rs:55-126, top_k = 0): NaN -> -inf,
+// x * (1 / T), e * (1 / sum).  NaN scaled values are -inf in both.
+template <bool SAMPLE>
+__device__ void row_probs(const float *row, int V, float T, float *out, float *redf, int *redi) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const float inv = 1.0f / T;
+  int pinf = 0;
+  float mx = -INFINITY;
+  for (int i = tid; i < V; i += nt) {
+    float x = row[i];
+    if (SAMPLE) {
+      if (isnan(x)) x = -INFINITY;
+      x = x * inv;
+    } else {
+      x = x / T;
+      if (isnan(x)) x = -INFINITY;
+    }
+    out[i] = x;
+    pinf += x == INFINITY;
+    mx = fmaxf(mx, x);
+  }
+  pinf = block_sum_i(pinf, redi);
+  mx = block_max(mx, redf);
+  if (pinf > 0) {
+    const float p = 1.0f / (float)pinf;
+    for (int i = tid; i < V; i += nt) out[i] = out[i] == INFINITY ? p : 0.0f;
+    __syncthreads();
+    return;
+  }
+  if (mx == -INFINITY) {
+    for (int i = tid; i < V; i += nt) out[i] = 1.0f / (float)V;
+    __syncthreads();
+    return;
+  }
+  for (int i = tid; i < V; i += nt) out[i] = rai_exact::expf_glibc(out[i] - mx);
+  __syncthreads();
+  __shared__ float ssum;
+  if (tid < 64) {
+    const float s = chain_sum(out, V, tid);
+    if (tid == 0) ssum = s;
+  }
+  __syncthreads();
+  const float sum = ssum;
+  if (!(isfinite(sum) && sum > 0.0f)) {
+    for (int i = tid; i < V; i += nt) out[i] = 1.0f / (float)V;
+  } else if (SAMPLE) {
+    const float is = 1.0f / sum;
+    for (int i = tid; i < V; i += nt) out[i] = out[i] * is;
+  } else {
+    for (int i = tid; i < V; i += nt) out[i] = out[i] / sum;
+  }
+  __syncthreads();
+}
+
+// sample_token's draw over the probabilities p (block-wide; thread 0 draws).
+__device__ int draw_token(const float *p, int V, Gen &g, int *ires) {
+  __shared__ float rr;
+  if (threadIdx.x == 0) rr = g.gen_f32();
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int i = chain_search(p, V, rr, threadIdx.x);
+    if (threadIdx.x == 0) *ires = i;
+  }
+  __syncthreads();
+  int tok = *ires;
+  if (tok < 0) {
+    // Fallback: argmax of the probabilities (sampler.rs:201-208, last
+    // maximum wins).
+    __shared__ long long best[16];
+    long long b = LLONG_MIN;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) {
+      const int32_t bits = __float_as_int(p[i]);
+      const int32_t key = bits ^ (int32_t)(((uint32_t)(bits >> 31)) >> 1);
+      const long long k = ((long long)key << 32) | (uint32_t)i;
+      b = k > b ? k : b;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const long long x = __shfl_xor(b, o, 64);
+      b = x > b ? x : b;
+    }
+    if ((threadIdx.x & 63) == 0) best[threadIdx.x >> 6] = b;
+    __syncthreads();
+    long long r = best[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = best[w] > r ? best[w] : r;
+    tok = (int)(r & 0xFFFFFFFFll);
+    __syncthreads();
+  }
+  return tok;
+}
+
+// Block per verify row: rows < nd get softmax_probabilities, row nd (the
+// bonus row, or the decode_one row when nd = 0) sample_token's variant.
+__global__ __launch_bounds__(kSampleThreads) void k_sample_probs(const float *__restrict__ logits, int V, int nd,
+                                                                 float T, float *__restrict__ probs,
+                                                                 const int *__restrict__ st) {
+  __shared__ float redf[16];
+  __shared__ int redi[16];
+  if (st) {
+    nd = st[3];
+    T = __int_as_float(st[4]);
+  }
+  const int r = blockIdx.x;
+  if (r > nd) return;
+  if (r < nd)
+    row_probs<false>(logits + (size_t)r * V, V, T, probs + (size_t)r * V, redf, redi);
+  else
+    row_probs<true>(logits + (size_t)r * V, V, T, probs + (size_t)r * V, redf, redi);
+}
+
+// lookup.rs:359-403 (and decode_one's sample when nd = 0).  Appends the
+// produced tokens to ctx[len..] and writes res = {accepted, produced}.
+// `scratch` holds V floats for the rare sample_token fallback of a
+// correction.
+__global__ __launch_bounds__(kSampleThreads) void k_sample_accept(
+    const float *__restrict__ logits, const float *__restrict__ probs, int V, uint32_t *__restrict__ ctx, int len,
+    int start, int nd, float T, RngState *rng, float *__restrict__ scratch, int *__restrict__ res,
+    const int *__restrict__ st) {
+  if (st) {
+    len = st[1];
+    start = st[2];
+    nd = st[3];
+    T = __int_as_float(st[4]);
+  }
+  Gen g{rng};
+  __shared__ int sh_acc, sh_prod, sh_tok, sh_dec;
+  __shared__ double sh_u;
+  __shared__ float redf[16];
+  __shared__ int redi[16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid == 0) {
+    sh_acc = 0;
+    sh_prod = 0;
+  }
+  __syncthreads();
+  for (int i = 0; i < nd; ++i) {
+    const float *pa = probs + (size_t)i * V;
+    __syncthreads();  // every thread has read the previous decision
+    if (tid == 0) {
+      const int d = (int)ctx[start + i];
+      const float pt = pa[d];
+      const float ap = fminf(pt / 1.0f, 1.0f);  // p_draft = 1 (point mass)
+      const float u = g.gen_f32();
+      sh_dec = u < ap;
+      if (sh_dec) {
+        ctx[len + sh_prod] = (uint32_t)d;
+        sh_prod = sh_prod + 1;
+        sh_acc = sh_acc + 1;
+      }
+    }
+    __syncthreads();
+    if (sh_dec) continue;
+    // sample_correction (speculative.rs:479-513): residual max(0, p - q)
+    // with q the point mass on the draft; sum and search in f64.
+    const int d = (int)ctx[start + i];
+    __shared__ double adj_sum;
+    if (tid < 64) {
+      double s = 0.0;
+      for (int base = 0; base < V; base += 64) {
+        const int j = base + lane;
+        const double v = j < V ? (double)fmaxf(pa[j] - (j == d ? 1.0f : 0.0f), 0.0f) : 0.0;
+#pragma unroll
+        for (int k = 0; k < 64; ++k) s = s + bcast_d(v, k);
+      }
+      if (tid == 0) adj_sum = s;
+    }
+    __syncthreads();
+    const double as = adj_sum;
+    if (!(isfinite(as) && as > 0.0)) {
+      // sample_token over the target row (unreachable when the draft's
+      // probability is below 1; kept for the reference's semantics).
+      row_probs<true>(logits + (size_t)i * V, V, T, scratch, redf, redi);
+      const int tok = draw_token(scratch, V, g, &sh_tok);
+      if (tid == 0) sh_tok = tok;
+    } else {
+      if (tid == 0) sh_u = g.gen_f64() * as;
+      __syncthreads();
+      if (tid < 64) {
+        const double u = sh_u;
+        double c = 0.0;
+        int found = V - 1;
+        bool done = false;
+        for (int base = 0; base < V && !done; base += 64) {
+          const int j = base + lane;
+          const double v = j < V ? (double)fmaxf(pa[j] - (j == d ? 1.0f : 0.0f), 0.0f) : 0.0;
+          const int lim = min(64, V - base);
+          for (int k = 0; k < lim; ++k) {
+            c = c + bcast_d(v, k);
+            if (c >= u) {
+              found = base + k;
+              done = true;
+              break;
+            }
+          }
+        }
+        if (tid == 0) sh_tok = found;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      ctx[len + sh_prod] = (uint32_t)sh_tok;
+      sh_prod = sh_prod + 1;
+    }
+    __syncthreads();
+    break;
+  }
+  __syncthreads();
+  if (sh_acc == nd) {
+    const int tok = draw_token(probs + (size_t)nd * V, V, g, &sh_tok);
+    if (tid == 0) {
+      ctx[len + sh_prod] = (uint32_t)tok;
+      sh_prod = sh_prod + 1;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    res[0] = sh_acc;
+    res[1] = sh_prod;
+  }
+}
+
+// Device draws for a check against the CPU restatement: kinds[i] 0 = u32,
+// 1 = u64, 2 = f32, 3 = f64; out[i] holds the raw bits (64-bit).
+__global__ void k_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  Gen g{rng};
+  for (int i = 0; i < n; ++i) {
+    switch (kinds[i]) {
+      case 0: out[i] = g.next_u32(); break;
+      case 1: out[i] = g.next_u64(); break;
+      case 2: out[i] = (uint64_t)__float_as_uint(g.gen_f32()); break;
+      default: out[i] = __builtin_bit_cast(uint64_t, g.gen_f64()); break;
+    }
+  }
+}
+
+}  // namespace
+
+void rng_seed_from_u64(RngState &r, uint64_t state) {
+  // SeedableRng::seed_from_u64 (rand_core 0.6.4): PCG32 steps fill the key.
+  const uint64_t mul = 6364136223846793005ull, inc = 11634580027462260723ull;
+  for (int i = 0; i < 8; ++i) {
+    state = state * mul + inc;
+    const uint32_t xs = (uint32_t)(((state >> 18) ^ state) >> 27);
+    const uint32_t rot = (uint32_t)(state >> 59);
+    r.key[i] = (xs >> rot) | (xs << ((32 - rot) & 31));
+  }
+  r.counter_lo = r.counter_hi = 0;
+  r.index = 64;
+  for (uint32_t &w : r.buf) w = 0;
+}
+
+void launch_sample(const float *logits, float *probs, int V, uint32_t *ctx, int len, int start, int nd, float T,
+                   RngState *rng, float *scratch, int *res, hipStream_t s, const int *st, int rows) {
+  hipLaunchKernelGGL(k_sample_probs, dim3(rows), dim3(kSampleThreads), 0, s, logits, V, nd, T, probs, st);
+  hipLaunchKernelGGL(k_sample_accept, dim3(1), dim3(kSampleThreads), 0, s, logits, probs, V, ctx, len, start, nd,
+                     T, rng, scratch, res, st);
+}
+
+void launch_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *out, hipStream_t s) {
+  hipLaunchKernelGGL(k_rng_draws, dim3(1), dim3(64), 0, s, rng, kinds, n, out);
+}
+
+}  // namespace rai

@@ -1,0 +1,126 @@
+"""CPU pins of the oracle's exact-sampling restatement (test infrastructure).
+
+- ChaCha block function, counter/stream layout and four-block buffering:
+  RFC 7539 A.1 keystream test vectors 1 and 2 (20 rounds, zero key and
+  nonce; they are also rand_chacha's ChaCha20 zero-seed true values) and
+  the RFC 8439 2.3.2 block-function vector.
+- BlockRng reads: next_u64 = two consecutive words, low first, including
+  across a refill (rand_core 0.6.4 BlockRng::next_u64).
+- softmax_probabilities (speculative.rs:431-477) against a float64 softmax
+  and its special cases (NaN, +inf, all -inf).
+- sample_token's own tests (sampler.rs:228-306), mirrored.
+- The speculative-sampling identity the accept / correct / bonus loop
+  exists for (lookup.rs:359-403): the first emitted token is distributed as
+  the target's softmax whatever the draft; a correction drawn from the
+  target instead of the residual max(0, p - q) fails it.
+StdRng::seed_from_u64 and the f32/f64 conversions have no published vector:
+parity-unpinned beyond their published algorithm (rand_core 0.6.4, rand 0.8.6).
+"""
+import numpy as np
+import pytest
+
+from oracle import ora
+
+RFC7539_TV1 = [0xade0b876, 0x903df1a0, 0xe56a5d40, 0x28bd8653, 0xb819d2bd, 0x1aed8da0, 0xccef36a8, 0xc70d778b,
+               0x7c5941da, 0x8d485751, 0x3fe02477, 0x374ad8b8, 0xf4b8436a, 0x1ca11815, 0x69b687c3, 0x8665eeb2]
+RFC7539_TV2 = [0xbee7079f, 0x7a385155, 0x7c97ba98, 0x0d082d73, 0xa0290fcb, 0x6965e348, 0x3e53c612, 0xed7aee32,
+               0x7621b729, 0x434ee69c, 0xb03371d5, 0xd539d874, 0x281fed31, 0x45fb0a51, 0x1f0ae1ac, 0x6f4d794b]
+RFC8439_232 = [0xe4e7f110, 0x15593bd1, 0x1fdd0f50, 0xc47120a3, 0xc7f4d1c7, 0x0368c033, 0x9aaa2204, 0x4e6cd4c3,
+               0x466482d2, 0x09aa9f07, 0x05d7c214, 0xa2028bd9, 0xd19c12b5, 0xb94e16de, 0xe883d0cb, 0x4e3c50a2]
+
+
+def test_chacha20_zero_key_keystream_through_the_buffer():
+    r = ora.Rng(key=np.zeros(8, np.uint32), rounds=20)
+    assert [r.next_u32() for _ in range(32)] == RFC7539_TV1 + RFC7539_TV2
+
+
+def test_chacha20_block_function_rfc8439():
+    key = np.arange(32, dtype=np.uint8).view(np.uint32)
+    # RFC 8439 nonce 00:00:00:09:00:00:00:4a:00:00:00:00 over the 64-bit
+    # counter (words 12-13) and 64-bit stream (words 14-15) layout.
+    got = ora.chacha_block(key, 1 | (0x09000000 << 32), 0x4a000000, 20)
+    assert got.tolist() == RFC8439_232
+
+
+@pytest.mark.parametrize("skip", [0, 1, 61, 62, 63, 64, 65, 127])
+def test_u64_reads_are_consecutive_words_across_refills(skip):
+    a, b = ora.Rng(seed=77), ora.Rng(seed=77)
+    for _ in range(skip):
+        a.next_u32()
+    words = [b.next_u32() for _ in range(skip + 6)]
+    got = [a.next_u64() for _ in range(3)]
+    want = [words[skip + 2 * i] | (words[skip + 2 * i + 1] << 32) for i in range(3)]
+    assert got == want
+
+
+def test_rounds_parameter_changes_the_stream():
+    assert ora.Rng(seed=1, rounds=12).next_u32() != ora.Rng(seed=1, rounds=20).next_u32()
+
+
+def test_softmax_probabilities_against_float64():
+    rng = np.random.default_rng(3)
+    for t in (0.3, 0.7, 1.0, 2.5):
+        x = (rng.normal(size=513) * 4).astype(np.float32)
+        p = ora.softmax_probabilities(x, t)
+        z = x.astype(np.float64) / t
+        want = np.exp(z - z.max())
+        want /= want.sum()
+        assert np.allclose(p, want, rtol=2e-5, atol=1e-9), t
+
+
+def test_softmax_probabilities_special_cases():
+    p = ora.softmax_probabilities([np.nan, 0.0, 1.0], 1.0)
+    assert p[0] == 0.0 and abs(p.sum() - 1.0) < 1e-6
+    p = ora.softmax_probabilities([np.inf, 2.0, np.inf, -np.inf], 0.5)
+    assert p.tolist() == [0.5, 0.0, 0.5, 0.0]
+    p = ora.softmax_probabilities([-np.inf, np.nan, -np.inf, -np.inf], 1.0)
+    assert p.tolist() == [0.25] * 4
+
+
+def test_sample_token_reference_tests():
+    """sampler.rs:228-306: low temperature concentrates on the top logit;
+    non-finite logits never select NaN; greedy below 1e-6."""
+    rng = ora.Rng(seed=42)
+    counts = np.zeros(3, int)
+    for _ in range(100):
+        counts[ora.sample_token([1.0, 2.0, 3.0], 0.1, rng)] += 1
+    assert counts[2] > 90
+    rng = ora.Rng(seed=7)
+    assert ora.sample_token([np.nan, 1.0, 2.0], 0.0, rng) == 2
+    for _ in range(32):
+        assert ora.sample_token([np.inf, np.inf, 0.0, np.nan], 0.7, rng) < 2
+    assert ora.sample_token([np.nan, -np.inf], 0.7, rng) < 2
+
+
+@pytest.mark.parametrize("draft", [0, 2, 4])
+def test_accept_and_correct_preserve_the_target_distribution(draft):
+    """Speculative sampling's identity: with a point-mass draft on `draft`,
+    the first emitted token is distributed as softmax(target / T)."""
+    logits = np.array([[1.0, 0.2, 2.0, -1.0, 0.5], [0.0, 0.0, 0.0, 0.0, 0.0]], np.float32)
+    t = 0.8
+    p = ora.softmax_probabilities(logits[0], t).astype(np.float64)
+    rng = ora.Rng(seed=100 + draft)
+    n = 20000
+    counts = np.zeros(5)
+    for _ in range(n):
+        toks, acc = ora.sampled_accept(logits, [draft], t, rng)
+        counts[toks[0]] += 1
+        assert (acc == 1) == (toks[0] == draft) and len(toks) == 1 + acc
+    chi2 = ((counts - n * p) ** 2 / (n * p)).sum()
+    assert chi2 < 25.0, (counts / n, p)  # 4 degrees of freedom: p < 1e-4 for a correct rule
+
+
+def test_bonus_token_follows_the_last_row():
+    logits = np.array([[0.0] * 4, [3.0, 0.0, 1.0, 2.0]], np.float32)
+    logits[0, 1] = 30.0  # the draft (1) is accepted with probability ~1
+    t = 1.3
+    p = ora.softmax_probabilities(logits[1], t).astype(np.float64)
+    rng = ora.Rng(seed=5)
+    n = 12000
+    counts = np.zeros(4)
+    for _ in range(n):
+        toks, acc = ora.sampled_accept(logits, [1], t, rng)
+        assert acc == 1 and toks[0] == 1
+        counts[toks[1]] += 1
+    chi2 = ((counts - n * p) ** 2 / (n * p)).sum()
+    assert chi2 < 22.0, (counts / n, p)
