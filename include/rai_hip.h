@@ -50,6 +50,7 @@ typedef enum rai_status {
 typedef struct rai_model rai_model;
 typedef struct rai_kv rai_kv;
 typedef struct rai_lookup rai_lookup;
+typedef struct rai_spec rai_spec;
 
 /* ModelConfig (format.rs:162-265), the fields this build implements. */
 typedef struct rai_model_config {
@@ -74,6 +75,22 @@ typedef struct rai_lookup_config {
   float temperature;  /* > 1e-6: exact sampling (lookup.rs:359-403) from the
                          decoder's StdRng; <= 1e-6: greedy acceptance */
 } rai_lookup_config;
+
+/* SpeculativeConfig (speculative.rs:25-45): draft_k and the sampler's
+ * temperature (top_k 0, top_p 1, no repetition penalty: the exact
+ * configuration).  temperature <= 1e-6 selects the greedy variant (argmax
+ * drafts, accepted while the target's argmax agrees), which the reference
+ * refuses. */
+typedef struct rai_spec_config {
+  size_t draft_k;
+  float temperature;
+} rai_spec_config;
+
+/* SpeculativeMetrics (speculative.rs:47-58). */
+typedef struct rai_spec_metrics {
+  size_t accepted, drafted, produced;
+  float accept_rate;
+} rai_spec_metrics;
 
 /* LookupMatch (lookup.rs:91-109). */
 typedef struct rai_lookup_match {
@@ -212,6 +229,23 @@ int rai_rope_apply_dev(float *heads, size_t num_heads, size_t head_dim, const fl
  * k[t][head_dim], v[t][head_dim], t in 0..=pos (softcap disabled). */
 int rai_attention_head_dev(float *out, const float *q, const float *k, const float *v, size_t pos,
                            size_t head_dim, float scale, void *stream);
+
+/* -------------------------------------------- draft-model speculation -- */
+/* SpeculativeDecoder::new (speculative.rs:79-110): both models must share
+ * the vocabulary; the context is the smaller of both windows and max_ctx. */
+int rai_spec_create(rai_model *draft, rai_model *target, size_t max_ctx, rai_spec **out);
+void rai_spec_free(rai_spec *dec);
+/* The `pub draft_kv` (which = 0) / `pub target_kv` (1) caches: borrowed. */
+int rai_spec_kv(rai_spec *dec, int which, rai_kv **out);
+/* StdRng::seed_from_u64(seed) for the sampled steps (new decoders: 0). */
+int rai_spec_seed(rai_spec *dec, uint64_t seed);
+/* SpeculativeDecoder::prefill (speculative.rs:112-171): both models over
+ * prompt[0..n-1] (batched; bit-identical to the reference's token loop). */
+int rai_spec_prefill(rai_spec *dec, const uint32_t *prompt, size_t n, size_t *pos_out);
+/* SpeculativeDecoder::step (speculative.rs:180-391): writes metrics->produced
+ * tokens (capacity >= draft_k + 1). */
+int rai_spec_step(rai_spec *dec, size_t pos, uint32_t last_token, const rai_spec_config *cfg,
+                  uint32_t *out_tokens, size_t out_cap, rai_spec_metrics *metrics);
 
 /* ----------------------------------------------------- prompt-lookup path -- */
 /* find_ngram_draft (lookup.rs:131-171), evaluated by the GPU search kernel.

@@ -103,6 +103,10 @@ def lib():
         "ora_softmax_probabilities": (c_int, [P, c_int, c_float, P]),
         "ora_sample_token": (c_int, [P, c_int, c_float, P, POINTER(c_int)]),
         "ora_sampled_accept": (c_int, [P, c_int, P, c_int, c_float, P, P, POINTER(c_int), POINTER(c_int)]),
+        "ora_spec_create": (c_int, [P, P, c_int, POINTER(c_void_p)]),
+        "ora_spec_free": (None, [P]),
+        "ora_spec_prefill": (c_int, [P, P, c_int, POINTER(c_int)]),
+        "ora_spec_step": (c_int, [P, c_int, c_int, c_int, c_float, P, P, POINTER(OracleMetrics)]),
         "ora_lookup_step_sampled": (c_int, [P, c_int, P, c_int, c_int, c_int, c_int, c_float, P, P,
                                             POINTER(OracleMetrics)]),
     }
@@ -464,5 +468,35 @@ class LookupDecoder:
     def __del__(self):
         try:
             lib().ora_lookup_free(self.h)
+        except Exception:
+            pass
+
+
+class SpecDecoder:
+    """Oracle SpeculativeDecoder (speculative.rs:61-391); temperature <= 1e-6
+    is the greedy variant."""
+
+    def __init__(self, draft: Model, target: Model, max_ctx: int):
+        h = c_void_p()
+        _check(lib().ora_spec_create(draft.h, target.h, max_ctx, ctypes.byref(h)))
+        self.h = h
+        self.models = (draft, target)
+
+    def prefill(self, prompt) -> int:
+        p = np.ascontiguousarray(prompt, np.int32)
+        pos = c_int()
+        _check(lib().ora_spec_prefill(self.h, _ptr(p), p.size, ctypes.byref(pos)))
+        return pos.value
+
+    def step(self, pos, last, draft_k, temperature, rng):
+        out = np.zeros(draft_k + 1, np.int32)
+        met = OracleMetrics()
+        _check(lib().ora_spec_step(self.h, pos, last, draft_k, temperature, rng.h if rng else None, _ptr(out),
+                                   ctypes.byref(met)))
+        return out[:met.produced].tolist(), met
+
+    def __del__(self):
+        try:
+            lib().ora_spec_free(self.h)
         except Exception:
             pass

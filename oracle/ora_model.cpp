@@ -737,6 +737,119 @@ int ora_lookup_step_sampled(ora_lookup *dd, int pos, const int32_t *ctx, int len
   });
 }
 
+// SpeculativeDecoder (speculative.rs:79-391): a draft model proposes k
+// tokens one decode step at a time, the target verifies [last, drafts] in
+// one batched forward, then exact acceptance (temperature > 1e-6) or, below
+// that, greedy acceptance (draft tokens by argmax, accepted while the
+// target's argmax agrees).
+struct ora_spec {
+  const Model *draft, *target;
+  KV dkv, tkv;
+  int max_ctx;
+};
+
+int ora_spec_create(const ora_model *draft, const ora_model *target, int max_ctx, ora_spec **out) {
+  ORA_TRY({
+    if (draft->m.cfg.vocab_size != target->m.cfg.vocab_size) fail("draft and target vocabularies differ");
+    const int dctx = std::min(max_ctx, (int)draft->m.cfg.max_context);
+    const int tctx = std::min(max_ctx, (int)target->m.cfg.max_context);
+    const int ctx = std::min(dctx, tctx);
+    if (ctx <= 0) fail("speculative decoding context must be non-zero");
+    auto d = new ora_spec{&draft->m, &target->m, make_kv(draft->m, dctx), make_kv(target->m, tctx), ctx};
+    *out = d;
+  });
+}
+void ora_spec_free(ora_spec *d) { delete d; }
+
+int ora_spec_prefill(ora_spec *d, const int32_t *prompt, int n, int *pos_out) {
+  ORA_TRY({
+    if (n <= 0) fail("prompt must contain at least one token");
+    if (n > d->max_ctx) fail("prompt exceeds the speculative context window");
+    const int cnt = n - 1;
+    for (int w = 0; w < 2; ++w) {
+      const Model &m = w ? *d->target : *d->draft;
+      KV &kv = w ? d->tkv : d->dkv;
+      const int H = m.cfg.hidden_size;
+      for (int p = 0; p < cnt; ++p) {
+        std::vector<float> h(H);
+        embed(m, prompt[p], h.data());
+        forward(m, kv, h.data(), &p, 1);
+      }
+    }
+    *pos_out = cnt;
+  });
+}
+
+int ora_spec_step(ora_spec *d, int pos, int last, int draft_k, float temperature, ora_rng *rng, int32_t *out,
+                  ora_metrics *met) {
+  ORA_TRY({
+    const Model &dm = *d->draft, &tm = *d->target;
+    const int V = tm.cfg.vocab_size, DH = dm.cfg.hidden_size, TH = tm.cfg.hidden_size;
+    const bool sampled = std::isfinite(temperature) && temperature > 1e-6f;
+    if (draft_k <= 0) fail("speculative draft_k must be non-zero");
+    if (pos >= d->max_ctx) fail("decode position exceeds the speculative context window");
+    const int k = std::min(draft_k, std::max(0, d->max_ctx - pos - 1));
+    auto pick = [&](std::vector<float> &lg) {
+      int t = 0;
+      if (!sampled) return (int)argmax(lg.data(), V);
+      if (ora_sample_token(lg.data(), V, temperature, rng, &t)) fail("sample_token failed");
+      return t;
+    };
+    if (k == 0) {
+      std::vector<float> h(TH), lg(V);
+      embed(tm, last, h.data());
+      forward(tm, d->tkv, h.data(), &pos, 1);
+      logits(tm, h.data(), lg.data(), 1);
+      out[0] = pick(lg);
+      *met = {0, 0, 1, 0};
+      return 0;
+    }
+    std::vector<int32_t> toks(k + 1);
+    std::vector<float> dl((size_t)k * V);
+    toks[0] = last;
+    for (int i = 0; i < k; ++i) {
+      std::vector<float> h(DH), lg(V);
+      embed(dm, toks[i], h.data());
+      int p = pos + i;
+      forward(dm, d->dkv, h.data(), &p, 1);
+      logits(dm, h.data(), lg.data(), 1);
+      std::copy(lg.begin(), lg.end(), dl.begin() + (size_t)i * V);
+      toks[i + 1] = pick(lg);
+    }
+    std::vector<float> h((size_t)(k + 1) * TH), tl((size_t)(k + 1) * V);
+    std::vector<int> ps(k + 1);
+    for (int i = 0; i <= k; ++i) {
+      embed(tm, toks[i], &h[(size_t)i * TH]);
+      ps[i] = pos + i;
+    }
+    forward(tm, d->tkv, h.data(), ps.data(), k + 1);
+    logits(tm, h.data(), tl.data(), k + 1);
+    int acc = 0, prod = 0;
+    if (sampled) {
+      if (ora_spec_accept(tl.data(), dl.data(), V, toks.data() + 1, k, temperature, rng, out, &prod, &acc))
+        fail("speculative acceptance failed");
+    } else {
+      for (int i = 0; i < k; ++i) {
+        const int a = (int)argmax(&tl[(size_t)i * V], V);
+        out[prod++] = a;
+        if (a != toks[i + 1]) break;
+        ++acc;
+      }
+      if (acc == k) out[prod++] = (int32_t)argmax(&tl[(size_t)k * V], V);
+    }
+    if (acc == k) {
+      // The last draft token has not been through the draft model yet.
+      std::vector<float> hd(DH);
+      embed(dm, toks[k], hd.data());
+      int p = pos + k;
+      forward(dm, d->dkv, hd.data(), &p, 1);
+    }
+    for (int &f : d->dkv.filled) f = std::min(f, pos + prod);
+    for (int &f : d->tkv.filled) f = std::min(f, pos + prod);
+    *met = {acc, k, prod, 0};
+  });
+}
+
 int ora_greedy_generate(const ora_model *mm, const int32_t *prompt, int n, int steps, int max_ctx,
                         int32_t *out) {
   ORA_TRY({

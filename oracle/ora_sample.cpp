@@ -224,6 +224,55 @@ int sampled_accept(const float *lg, int V, const int32_t *draft, int nd, float t
   return prod;
 }
 
+// SpeculativeDecoder::step's phase 3 (speculative.rs:336-390): target rows
+// [k + 1][V], the draft's logit rows [k][V] (as the draft produced them).
+int spec_accept(const float *tl, const float *dl, int V, const int32_t *draft, int k, float temperature,
+                StdRng &rng, int32_t *out, int *accepted) {
+  int acc = 0, prod = 0;
+  for (int i = 0; i < k; ++i) {
+    const float *trow = tl + (size_t)i * V, *drow = dl + (size_t)i * V;
+    const int d = draft[i];
+    const float pt = softmax_probabilities(trow, V, temperature)[d];
+    const float pd = softmax_probabilities(drow, V, temperature)[d];
+    const float ap = pd > 0.0f ? std::fmin(pt / pd, 1.0f) : (pt > 0.0f ? 1.0f : 0.0f);
+    const float u = rng.gen_f32();
+    if (u < ap) {
+      out[prod++] = d;
+      ++acc;
+    } else {
+      // sample_correction with the draft's own distribution.
+      const std::vector<float> tp = softmax_probabilities(trow, V, temperature);
+      const std::vector<float> dp = softmax_probabilities(drow, V, temperature);
+      double adj_sum = 0.0;
+      std::vector<float> adj(V);
+      for (int j = 0; j < V; ++j) {
+        adj[j] = std::fmax(tp[j] - dp[j], 0.0f);
+        adj_sum += (double)adj[j];
+      }
+      int tok = V - 1;
+      if (!std::isfinite(adj_sum) || adj_sum <= 0.0) {
+        tok = sample_token(std::vector<float>(trow, trow + V), temperature, rng);
+      } else {
+        const double uu = rng.gen_f64() * adj_sum;
+        double cum = 0.0;
+        for (int j = 0; j < V; ++j) {
+          cum += (double)adj[j];
+          if (cum >= uu) {
+            tok = j;
+            break;
+          }
+        }
+      }
+      out[prod++] = tok;
+      break;
+    }
+  }
+  if (acc == k) out[prod++] = sample_token(std::vector<float>(tl + (size_t)k * V, tl + (size_t)(k + 1) * V),
+                                           temperature, rng);
+  *accepted = acc;
+  return prod;
+}
+
 int sampled_token(const float *lg, int V, float temperature, StdRng &rng) {
   return sample_token(std::vector<float>(lg, lg + V), temperature, rng);
 }
@@ -275,6 +324,10 @@ int ora_softmax_probabilities(const float *logits, int n, float temperature, flo
 int ora_sampled_accept(const float *lg, int V, const int32_t *draft, int nd, float temperature, ora_rng *r,
                        int32_t *out, int *produced, int *accepted) {
   ORA_TRY(*produced = sampled_accept(lg, V, draft, nd, temperature, r->r, out, accepted));
+}
+int ora_spec_accept(const float *tl, const float *dl, int V, const int32_t *draft, int k, float temperature,
+                    ora_rng *r, int32_t *out, int *produced, int *accepted) {
+  ORA_TRY(*produced = spec_accept(tl, dl, V, draft, k, temperature, r->r, out, accepted));
 }
 
 }  // extern "C"

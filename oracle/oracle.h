@@ -32,6 +32,7 @@ typedef struct ora_model ora_model;
 typedef struct ora_kv ora_kv;
 typedef struct ora_lookup ora_lookup;
 typedef struct ora_rng ora_rng;
+typedef struct ora_spec ora_spec;
 
 typedef struct ora_config {
   uint32_t hidden_size, num_layers, num_heads, num_kv_heads, head_dim;
@@ -141,6 +142,15 @@ int ora_lookup_step_sampled(ora_lookup *d, int pos, const int32_t *context, int 
                             int min_ngram, int max_ngram, float temperature, ora_rng *rng,
                             int32_t *out_tokens, ora_metrics *metrics);
 int ora_lookup_kv_filled(const ora_lookup *d);
+/* SpeculativeDecoder (speculative.rs:79-391); temperature <= 1e-6 is the
+ * greedy variant (argmax drafts, argmax acceptance). */
+int ora_spec_create(const ora_model *draft, const ora_model *target, int max_ctx, ora_spec **out);
+void ora_spec_free(ora_spec *d);
+int ora_spec_prefill(ora_spec *d, const int32_t *prompt, int n, int *pos_out);
+int ora_spec_step(ora_spec *d, int pos, int last_token, int draft_k, float temperature, ora_rng *rng,
+                  int32_t *out_tokens, ora_metrics *metrics);
+int ora_spec_accept(const float *target_logits, const float *draft_logits, int vocab, const int32_t *draft,
+                    int k, float temperature, ora_rng *r, int32_t *out, int *produced, int *accepted);
 /* Replace layer `layer`'s K (which = 0) or V (which = 1) rows with
  * rows[nkv][npos][head_dim] and set its watermark to npos (a decoder state
  * taken from another implementation, e.g. to time steps at a long context

@@ -122,6 +122,12 @@ def lib():
         "rai_lookup_create": (c_int, [P, S, POINTER(c_void_p)]),
         "rai_lookup_free": (None, [P]),
         "rai_lookup_seed": (c_int, [P, ctypes.c_uint64]),
+        "rai_spec_create": (c_int, [P, P, S, POINTER(c_void_p)]),
+        "rai_spec_free": (None, [P]),
+        "rai_spec_kv": (c_int, [P, c_int, POINTER(c_void_p)]),
+        "rai_spec_seed": (c_int, [P, ctypes.c_uint64]),
+        "rai_spec_prefill": (c_int, [P, P, S, POINTER(c_size_t)]),
+        "rai_spec_step": (c_int, [P, S, ctypes.c_uint32, P, P, S, P]),
         "rai_std_rng_draws": (c_int, [ctypes.c_uint64, P, S, P]),
         "rai_lookup_kv": (c_int, [P, POINTER(c_void_p)]),
         "rai_lookup_prefill": (c_int, [P, P, S, POINTER(c_size_t)]),
@@ -619,6 +625,58 @@ class LookupDecoder:
         try:
             if self.h:
                 lib().rai_lookup_free(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+class _SpecConfig(ctypes.Structure):
+    _fields_ = [("draft_k", c_size_t), ("temperature", ctypes.c_float)]
+
+
+class _SpecMetrics(ctypes.Structure):
+    _fields_ = [("accepted", c_size_t), ("drafted", c_size_t), ("produced", c_size_t),
+                ("accept_rate", ctypes.c_float)]
+
+
+class SpeculativeDecoder:
+    """SpeculativeDecoder (speculative.rs:61-391): a draft model proposes
+    draft_k tokens, the target verifies them in one batched forward; exact
+    acceptance at temperature > 1e-6 (the decoder's StdRng), greedy below."""
+
+    def __init__(self, draft: RaiModel, target: RaiModel, max_ctx: int):
+        h = c_void_p()
+        _check(lib().rai_spec_create(draft.h, target.h, max_ctx, ctypes.byref(h)))
+        self.h = h.value
+        self.draft, self.target = draft, target
+        kv0, kv1 = c_void_p(), c_void_p()
+        _check(lib().rai_spec_kv(self.h, 0, ctypes.byref(kv0)))
+        _check(lib().rai_spec_kv(self.h, 1, ctypes.byref(kv1)))
+        self.draft_kv = KVCache(kv0.value, owner=self, borrowed=True)
+        self.target_kv = KVCache(kv1.value, owner=self, borrowed=True)
+
+    def seed(self, seed: int) -> None:
+        _check(lib().rai_spec_seed(self.h, seed))
+
+    def prefill(self, prompt_tokens) -> int:
+        p = _u32(prompt_tokens)
+        pos = c_size_t()
+        _check(lib().rai_spec_prefill(self.h, _ptr(p), p.size, ctypes.byref(pos)))
+        return pos.value
+
+    def step(self, pos: int, last_token: int, draft_k: int, temperature: float = 0.0):
+        out = np.zeros(draft_k + 1, np.uint32)
+        cfg = _SpecConfig(draft_k, temperature)
+        met = _SpecMetrics()
+        _check(lib().rai_spec_step(self.h, pos, last_token, ctypes.byref(cfg), _ptr(out), out.size,
+                                   ctypes.byref(met)))
+        return out[:met.produced].tolist(), {"accepted": met.accepted, "drafted": met.drafted,
+                                            "produced": met.produced, "accept_rate": met.accept_rate}
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().rai_spec_free(self.h)
                 self.h = None
         except Exception:
             pass

@@ -205,6 +205,15 @@ void rng_seed_from_u64(RngState &r, uint64_t seed);
 // holds rows * V floats, scratch V floats.
 void launch_sample(const float *logits, float *probs, int V, uint32_t *ctx, int len, int start, int nd, float T,
                    RngState *rng, float *scratch, int *res, hipStream_t s, const int *st, int rows);
+// SpeculativeDecoder's phase 3 (speculative.rs:336-390): toks = [last,
+// k drafts, outputs...]; target logits [k + 1][V], the drafts' logit rows
+// [k][V]; appends the produced tokens at toks[k + 1..], res = {accepted,
+// produced}.
+void launch_spec_sample(const float *tlogits, float *tprobs, const float *dlogits, float *dprobs, int V,
+                        uint32_t *toks, int k, float T, RngState *rng, float *scratch, int *res, hipStream_t s);
+// One sampled draft token: keeps the row, draws *out with sample_token.
+void launch_draw(const float *row, int V, float T, RngState *rng, float *keep, float *scratch, uint32_t *out,
+                 hipStream_t s);
 // n draws (kinds: 0 u32, 1 u64, 2 f32, 3 f64) from the device generator.
 void launch_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *out, hipStream_t s);
 

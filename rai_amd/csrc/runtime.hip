@@ -1629,6 +1629,213 @@ int rai_greedy_generate(rai_lookup *d, const uint32_t *prompt, size_t n, size_t 
   });
 }
 
+// ------------------------------------------------ speculative decoder --
+
+struct rai_spec {
+  rai_model *draft = nullptr, *target = nullptr;
+  rai_kv dkv, tkv;
+  size_t max_ctx = 0;
+  rai::Workspace dws, tws;
+  DevBuf prompt;  // prompt tokens for the prefill
+  DevBuf toks;    // [last, drafts (<= 63), produced (<= 64)]
+  DevBuf dlog, dprobs, tprobs, scratch, rng, res;
+  int *pin = nullptr;  // pinned: res (2 ints) then the produced tokens
+  hipStream_t stream = nullptr;
+  ~rai_spec() {
+    if (pin) (void)hipHostFree(pin);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+namespace rai {
+
+// One decode step of model `md` at `pos` on the token at dev_tok: embed,
+// forward (watermark checks and commit), logits into w.logits row 0.
+static void decode_on(rai_model &md, rai_kv &kv, Workspace &w, const uint32_t *dev_tok, size_t pos, hipStream_t s) {
+  forward_check(md, kv, w, 1, pos);
+  launch_embed(dev_tok, nullptr, 0, 0, 1, md.emb_codes, md.emb_params, md.cfg.vocab_size, md.cfg.hidden_size,
+               md.cfg.embed_group_size, md.cfg.embed_scale, w.hid.as<float>(), w.err.as<int>(), s);
+  forward_enqueue(md, kv, w, 1, pos, s, nullptr);
+  forward_commit(kv, 1, pos);
+}
+
+// SpeculativeDecoder::step (speculative.rs:180-391): k draft decode steps
+// (each token sampled, or taken by argmax in the greedy variant), one
+// batched target forward over [last, drafts], then acceptance, the draft
+// model's catch-up on its last token when every draft was accepted, and
+// both watermarks truncated to pos + produced.
+static void spec_step(rai_spec &d, size_t pos, uint32_t last, const rai_spec_config &cfg, uint32_t *out,
+                      size_t cap, rai_spec_metrics &met) {
+  rai_model &dm = *d.draft, &tm = *d.target;
+  const int V = tm.cfg.vocab_size;
+  if (cfg.draft_k == 0) fail(RAI_E_ARG, "speculative draft_k must be non-zero");
+  if (cfg.draft_k > 63) fail(RAI_E_ARG, "draft_k above 63 is not supported");
+  if (!std::isfinite(cfg.temperature)) fail(RAI_E_ARG, "temperature must be finite");
+  if (pos >= d.max_ctx) fail(RAI_E_RANGE, "decode position exceeds the speculative context window");
+  if (cap < cfg.draft_k + 1) fail(RAI_E_SHAPE, "output buffer must hold draft_k + 1 tokens");
+  check_tokens(tm, &last, 1);
+  const bool sampled = cfg.temperature > 1e-6f;
+  const float T = cfg.temperature;
+  const int k = (int)std::min<size_t>(cfg.draft_k, d.max_ctx - pos - 1);
+  hipStream_t s = d.stream;
+  uint32_t *toks = d.toks.as<uint32_t>();
+  int *res = d.res.as<int>();
+  HIP_CHECK(hipGetLastError());
+  d.pin[64] = (int)last;
+  HIP_CHECK(hipMemcpyAsync(toks, d.pin + 64, sizeof(uint32_t), hipMemcpyHostToDevice, s));
+  if (k == 0) {
+    decode_on(tm, d.tkv, d.tws, toks, pos, s);
+    logits(tm, d.tws, 1, s);
+    if (sampled) {
+      launch_spec_sample(d.tws.logits.as<float>(), d.tprobs.as<float>(), nullptr, nullptr, V, toks, 0, T,
+                         d.rng.as<RngState>(), d.scratch.as<float>(), res, s);
+    } else {
+      launch_argmax(d.tws.logits.as<float>(), 1, V, d.tws.am.as<uint32_t>(), s);
+      launch_accept(d.tws.am.as<uint32_t>(), toks, 1, 1, 0, res, s, nullptr);
+    }
+  } else {
+    for (int i = 0; i < k; ++i) {
+      decode_on(dm, d.dkv, d.dws, toks + i, pos + i, s);
+      logits(dm, d.dws, 1, s);
+      if (sampled)
+        launch_draw(d.dws.logits.as<float>(), V, T, d.rng.as<RngState>(), d.dlog.as<float>() + (size_t)i * V,
+                    d.scratch.as<float>(), toks + i + 1, s);
+      else
+        launch_argmax(d.dws.logits.as<float>(), 1, V, toks + i + 1, s);
+    }
+    const int m = k + 1;
+    forward_check(tm, d.tkv, d.tws, m, pos);
+    launch_embed(toks, nullptr, 0, 0, m, tm.emb_codes, tm.emb_params, V, tm.cfg.hidden_size, tm.cfg.embed_group_size,
+                 tm.cfg.embed_scale, d.tws.hid.as<float>(), d.tws.err.as<int>(), s);
+    forward_enqueue(tm, d.tkv, d.tws, m, pos, s, nullptr);
+    forward_commit(d.tkv, m, pos);
+    logits(tm, d.tws, m, s);
+    if (sampled) {
+      launch_spec_sample(d.tws.logits.as<float>(), d.tprobs.as<float>(), d.dlog.as<float>(), d.dprobs.as<float>(),
+                         V, toks, k, T, d.rng.as<RngState>(), d.scratch.as<float>(), res, s);
+    } else {
+      launch_argmax(d.tws.logits.as<float>(), m, V, d.tws.am.as<uint32_t>(), s);
+      launch_accept(d.tws.am.as<uint32_t>(), toks, m, 1, k, res, s, nullptr);
+    }
+  }
+  HIP_CHECK(hipGetLastError());
+  HIP_CHECK(hipMemcpyAsync(d.pin, res, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipMemcpyAsync(d.pin + 2, toks + k + 1, (size_t)(k + 1) * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  int e[2] = {0, 0}, f[2] = {0, 0};
+  HIP_CHECK(hipMemcpyAsync(e, d.tws.err.p, sizeof(e), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipMemcpyAsync(f, d.dws.err.p, sizeof(f), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  if (e[0] || e[1] || f[0] || f[1]) {
+    for (auto &x : d.dkv.filled) x = std::min(x, pos);
+    for (auto &x : d.tkv.filled) x = std::min(x, pos);
+    raise_kernel_errors(d.dws, s, f);
+    raise_kernel_errors(d.tws, s, e);
+  }
+  const int acc = d.pin[0], prod = d.pin[1];
+  if (k > 0 && acc == k) decode_on(dm, d.dkv, d.dws, toks + k, pos + k, s);
+  for (auto &x : d.dkv.filled) x = std::min(x, pos + (size_t)prod);
+  for (auto &x : d.tkv.filled) x = std::min(x, pos + (size_t)prod);
+  for (int i = 0; i < prod; ++i) out[i] = (uint32_t)d.pin[2 + i];
+  met.accepted = (size_t)acc;
+  met.drafted = (size_t)k;
+  met.produced = (size_t)prod;
+  met.accept_rate = k ? (float)acc / (float)k : 0.0f;
+}
+
+}  // namespace rai
+
+int rai_spec_create(rai_model *draft, rai_model *target, size_t max_ctx, rai_spec **out) {
+  RAI_API_BODY({
+    if (!draft || !target || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (draft->cfg.vocab_size != target->cfg.vocab_size)
+      rai::fail(RAI_E_ARG, "draft and target vocabularies differ; speculative decoding needs one tokenizer");
+    auto d = std::make_unique<rai_spec>();
+    d->draft = draft;
+    d->target = target;
+    const size_t dctx = std::min<size_t>(max_ctx, draft->cfg.max_context);
+    const size_t tctx = std::min<size_t>(max_ctx, target->cfg.max_context);
+    d->max_ctx = std::min(dctx, tctx);
+    if (d->max_ctx == 0) rai::fail(RAI_E_ARG, "speculative decoding context must be non-zero");
+    rai::kv_init(d->dkv, *draft, dctx);
+    rai::kv_init(d->tkv, *target, tctx);
+    d->dws.init(*draft, rai::kChunk, 64);
+    d->tws.init(*target, rai::kChunk, 64);
+    const size_t V = target->cfg.vocab_size;
+    d->prompt.alloc(d->max_ctx * sizeof(uint32_t));
+    d->toks.alloc(160 * sizeof(uint32_t));
+    d->dlog.alloc(sizeof(float) * 64 * V);
+    d->dprobs.alloc(sizeof(float) * 64 * V);
+    d->tprobs.alloc(sizeof(float) * 65 * V);
+    d->scratch.alloc(sizeof(float) * V);
+    d->res.alloc(64);
+    d->rng.alloc(sizeof(rai::RngState));
+    rai::RngState r;
+    rai::rng_seed_from_u64(r, 0);
+    HIP_CHECK(hipMemcpy(d->rng.p, &r, sizeof(r), hipMemcpyHostToDevice));
+    HIP_CHECK(hipHostMalloc((void **)&d->pin, 4096, hipHostMallocDefault));
+    HIP_CHECK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+    *out = d.release();
+  });
+}
+
+void rai_spec_free(rai_spec *d) { delete d; }
+
+int rai_spec_kv(rai_spec *d, int which, rai_kv **out) {
+  RAI_API_BODY({
+    if (!d || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (which != 0 && which != 1) rai::fail(RAI_E_ARG, "which must be 0 (draft) or 1 (target)");
+    *out = which ? &d->tkv : &d->dkv;
+  });
+}
+
+int rai_spec_seed(rai_spec *d, uint64_t seed) {
+  RAI_API_BODY({
+    if (!d) rai::fail(RAI_E_ARG, "null argument");
+    rai::RngState r;
+    rai::rng_seed_from_u64(r, seed);
+    HIP_CHECK(hipStreamSynchronize(d->stream));
+    HIP_CHECK(hipMemcpy(d->rng.p, &r, sizeof(r), hipMemcpyHostToDevice));
+  });
+}
+
+int rai_spec_prefill(rai_spec *d, const uint32_t *prompt, size_t n, size_t *pos_out) {
+  RAI_API_BODY({
+    if (!d || !prompt || !pos_out) rai::fail(RAI_E_ARG, "null argument");
+    if (n == 0) rai::fail(RAI_E_ARG, "prompt must contain at least one token");
+    if (n > d->max_ctx) rai::fail(RAI_E_RANGE, "prompt exceeds the speculative context window");
+    rai::check_tokens(*d->target, prompt, n);
+    HIP_CHECK(hipMemcpyAsync(d->prompt.p, prompt, n * sizeof(uint32_t), hipMemcpyHostToDevice, d->stream));
+    const size_t cnt = n - 1;
+    for (int which = 0; which < 2; ++which) {
+      rai_model &md = which ? *d->target : *d->draft;
+      rai_kv &kv = which ? d->tkv : d->dkv;
+      rai::Workspace &w = which ? d->tws : d->dws;
+      for (size_t p = 0; p < cnt; p += rai::kChunk) {
+        const int m = (int)std::min<size_t>(rai::kChunk, cnt - p);
+        launch_embed(d->prompt.as<uint32_t>() + p, nullptr, 0, 0, m, md.emb_codes, md.emb_params,
+                     md.cfg.vocab_size, md.cfg.hidden_size, md.cfg.embed_group_size, md.cfg.embed_scale,
+                     w.hid.as<float>(), w.err.as<int>(), d->stream);
+        rai::forward(md, kv, w, m, p, d->stream);
+      }
+      try {
+        rai::check_kernel_error(w, d->stream);
+      } catch (...) {
+        for (auto &f : kv.filled) f = 0;
+        throw;
+      }
+    }
+    *pos_out = cnt;
+  });
+}
+
+int rai_spec_step(rai_spec *d, size_t pos, uint32_t last_token, const rai_spec_config *cfg, uint32_t *out_tokens,
+                  size_t out_cap, rai_spec_metrics *metrics) {
+  RAI_API_BODY({
+    if (!d || !cfg || !out_tokens || !metrics) rai::fail(RAI_E_ARG, "null argument");
+    rai::spec_step(*d, pos, last_token, *cfg, out_tokens, out_cap, *metrics);
+  });
+}
+
 int rai_debug_set_attention_spin(int polls) { RAI_API_BODY(rai::set_attention_spin(polls)); }
 
 int rai_dev_malloc(size_t bytes, void **out) {

@@ -271,10 +271,13 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_probs(const float *__
 // produced tokens to ctx[len..] and writes res = {accepted, produced}.
 // `scratch` holds V floats for the rare sample_token fallback of a
 // correction.
+// `pdraft` (may be null): the draft's own probabilities [nd][V]
+// (SpeculativeDecoder, speculative.rs:336-370); null is prompt lookup's
+// point mass on the drafted token.
 __global__ __launch_bounds__(kSampleThreads) void k_sample_accept(
-    const float *__restrict__ logits, const float *__restrict__ probs, int V, uint32_t *__restrict__ ctx, int len,
-    int start, int nd, float T, RngState *rng, float *__restrict__ scratch, int *__restrict__ res,
-    const int *__restrict__ st) {
+    const float *__restrict__ logits, const float *__restrict__ probs, const float *__restrict__ pdraft, int V,
+    uint32_t *__restrict__ ctx, int len, int start, int nd, float T, RngState *rng, float *__restrict__ scratch,
+    int *__restrict__ res, const int *__restrict__ st) {
   if (st) {
     len = st[1];
     start = st[2];
@@ -298,7 +301,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_accept(
     if (tid == 0) {
       const int d = (int)ctx[start + i];
       const float pt = pa[d];
-      const float ap = fminf(pt / 1.0f, 1.0f);  // p_draft = 1 (point mass)
+      const float pd = pdraft ? pdraft[(size_t)i * V + d] : 1.0f;  // point mass: 1
+      const float ap = pd > 0.0f ? fminf(pt / pd, 1.0f) : (pt > 0.0f ? 1.0f : 0.0f);
       const float u = g.gen_f32();
       sh_dec = u < ap;
       if (sh_dec) {
@@ -310,14 +314,19 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_accept(
     __syncthreads();
     if (sh_dec) continue;
     // sample_correction (speculative.rs:479-513): residual max(0, p - q)
-    // with q the point mass on the draft; sum and search in f64.
+    // with q the draft's distribution; sum and search in f64.
     const int d = (int)ctx[start + i];
+    const float *pq = pdraft ? pdraft + (size_t)i * V : nullptr;
+    auto resid = [&](int j) {
+      const float q = pq ? pq[j] : (j == d ? 1.0f : 0.0f);
+      return (double)fmaxf(pa[j] - q, 0.0f);
+    };
     __shared__ double adj_sum;
     if (tid < 64) {
       double s = 0.0;
       for (int base = 0; base < V; base += 64) {
         const int j = base + lane;
-        const double v = j < V ? (double)fmaxf(pa[j] - (j == d ? 1.0f : 0.0f), 0.0f) : 0.0;
+        const double v = j < V ? resid(j) : 0.0;
 #pragma unroll
         for (int k = 0; k < 64; ++k) s = s + bcast_d(v, k);
       }
@@ -341,7 +350,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_accept(
         bool done = false;
         for (int base = 0; base < V && !done; base += 64) {
           const int j = base + lane;
-          const double v = j < V ? (double)fmaxf(pa[j] - (j == d ? 1.0f : 0.0f), 0.0f) : 0.0;
+          const double v = j < V ? resid(j) : 0.0;
           const int lim = min(64, V - base);
           for (int k = 0; k < lim; ++k) {
             c = c + bcast_d(v, k);
@@ -378,6 +387,21 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_accept(
   }
 }
 
+// One draft token of SpeculativeDecoder::step (speculative.rs:246-271):
+// the row is kept in `keep` (for p_draft), then sample_token draws *out.
+__global__ __launch_bounds__(kSampleThreads) void k_draw(const float *__restrict__ row, int V, float T,
+                                                         RngState *rng, float *__restrict__ keep,
+                                                         float *__restrict__ scratch, uint32_t *out) {
+  __shared__ float redf[16];
+  __shared__ int redi[16];
+  __shared__ int tok;
+  for (int i = threadIdx.x; i < V; i += blockDim.x) keep[i] = row[i];
+  Gen g{rng};
+  row_probs<true>(row, V, T, scratch, redf, redi);
+  const int t = draw_token(scratch, V, g, &tok);
+  if (threadIdx.x == 0) *out = (uint32_t)t;
+}
+
 // Device draws for a check against the CPU restatement: kinds[i] 0 = u32,
 // 1 = u64, 2 = f32, 3 = f64; out[i] holds the raw bits (64-bit).
 __global__ void k_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *out) {
@@ -412,8 +436,24 @@ void rng_seed_from_u64(RngState &r, uint64_t state) {
 void launch_sample(const float *logits, float *probs, int V, uint32_t *ctx, int len, int start, int nd, float T,
                    RngState *rng, float *scratch, int *res, hipStream_t s, const int *st, int rows) {
   hipLaunchKernelGGL(k_sample_probs, dim3(rows), dim3(kSampleThreads), 0, s, logits, V, nd, T, probs, st);
-  hipLaunchKernelGGL(k_sample_accept, dim3(1), dim3(kSampleThreads), 0, s, logits, probs, V, ctx, len, start, nd,
-                     T, rng, scratch, res, st);
+  hipLaunchKernelGGL(k_sample_accept, dim3(1), dim3(kSampleThreads), 0, s, logits, probs, (const float *)nullptr,
+                     V, ctx, len, start, nd, T, rng, scratch, res, st);
+}
+
+void launch_spec_sample(const float *tlogits, float *tprobs, const float *dlogits, float *dprobs, int V,
+                        uint32_t *toks, int k, float T, RngState *rng, float *scratch, int *res, hipStream_t s) {
+  hipLaunchKernelGGL(k_sample_probs, dim3(k + 1), dim3(kSampleThreads), 0, s, tlogits, V, k, T, tprobs,
+                     (const int *)nullptr);
+  if (k > 0)
+    hipLaunchKernelGGL(k_sample_probs, dim3(k), dim3(kSampleThreads), 0, s, dlogits, V, k, T, dprobs,
+                       (const int *)nullptr);
+  hipLaunchKernelGGL(k_sample_accept, dim3(1), dim3(kSampleThreads), 0, s, tlogits, tprobs,
+                     (const float *)dprobs, V, toks, k + 1, 1, k, T, rng, scratch, res, (const int *)nullptr);
+}
+
+void launch_draw(const float *row, int V, float T, RngState *rng, float *keep, float *scratch, uint32_t *out,
+                 hipStream_t s) {
+  hipLaunchKernelGGL(k_draw, dim3(1), dim3(kSampleThreads), 0, s, row, V, T, rng, keep, scratch, out);
 }
 
 void launch_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *out, hipStream_t s) {
