@@ -17,6 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_obj")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "librai_hip.so")
+RUN = os.path.join(LIB_DIR, "rai-run")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -60,8 +61,16 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
+    # rai-run: the generate loop over the C ABI (host code only).
+    run_tmp = RUN + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), os.path.join(CSRC, "rai_run.cpp"),
+           "-L", LIB_DIR, "-lrai_hip", "-Wl,-rpath,$ORIGIN", "-o", run_tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("rai-run build failed:\n" + r.stdout + r.stderr)
+    os.replace(run_tmp, RUN)
     if verbose:
-        print("built", LIB)
+        print("built", LIB, "and", RUN)
     return LIB
 
 
