@@ -380,13 +380,14 @@ def test_step_graph_replay_matches_eager(rai, monkeypatch):
 
 
 def test_lookup_config_errors(rai):
-    """validate_lookup_config (lookup.rs:457-475); sampled mode is not built."""
+    """validate_lookup_config (lookup.rs:457-475); temperatures must be finite
+    (above 1e-6 the step samples exactly, below it accepts greedily)."""
     gm = rai.RaiModel.from_bytes(read_golden("tiny-untied.raimodel"))
     d = rai.LookupDecoder(gm, 64)
     pos = d.prefill([1, 2, 3, 1, 2])
     for bad, status in ((dict(max_draft=0), "RAI_E_ARG"), (dict(min_ngram=0), "RAI_E_ARG"),
                         (dict(min_ngram=4, max_ngram=3), "RAI_E_ARG"),
-                        (dict(temperature=0.7), "RAI_E_UNSUPPORTED")):
+                        (dict(temperature=float("inf")), "RAI_E_ARG")):
         with pytest.raises(rai.RaiError) as e:
             d.step(pos, [1, 2, 3, 1, 2], rai.LookupConfig(**bad))
         assert e.value.status == status
