@@ -181,7 +181,7 @@ void launch_accept(const uint32_t *argmax, uint32_t *ctx, int len, int start, in
 // MoE (layers.rs:1808-1870, model.rs:208-261): router probabilities and
 // top-k selection per token.
 void launch_router(const float *x, const float *router, int m, int hidden, int experts, int topk,
-                   int norm_topk, int *sel, float *wts, hipStream_t s);
+                   int norm_topk, int *sel, float *wts, float *logits, hipStream_t s);
 // out[t] += w * eo[t] for the m tokens (per-token weight array w[t]).
 void launch_moe_accumulate(float *out, const float *eo, const float *w, int m, int n,
                            hipStream_t s);

@@ -1135,57 +1135,139 @@ __global__ void k_accept(const uint32_t *__restrict__ am, uint32_t *__restrict__
 
 // --------------------------------------------------------------- MoE --
 
-// route_experts (layers.rs:1808-1870) for one token per block: router dot
-// products (scalar sequential, sum starting at -0.0), max, glibc expf, sum,
-// divide, top-k by strict > (lowest index on ties), optional renormalise.
-__global__ void k_router(const float *__restrict__ x, const float *__restrict__ router, int hidden,
-                         int experts, int topk, int norm_topk, int *__restrict__ sel,
-                         float *__restrict__ wts) {
+// Router logits: block (token t, experts e0 .. e0 + 7), 256 threads.  The
+// block computes the products fl(router[e][i] * x[i]) of a 256-column tile
+// for its experts into LDS (coalesced row reads, issued a tile ahead; rows
+// padded to 9 floats against bank conflicts); lane e adds its expert's
+// products in column order.  logits[t][e] = the sequential dot from -0.0.
+constexpr int kRouterEpb = 8, kRouterCols = 256, kRouterThreads = 256;
+__global__ __launch_bounds__(kRouterThreads) void k_router_logits(const float *__restrict__ x,
+                                                                  const float *__restrict__ router, int hidden,
+                                                                  int experts, float *__restrict__ logits) {
+  constexpr int EP = kRouterEpb + 1, TC = kRouterCols;
+  constexpr int RI = kRouterEpb * TC / kRouterThreads;  // items per thread and tile
+  __shared__ float tiles[2][TC * EP];
+  const int t = blockIdx.x, e0 = blockIdx.y * kRouterEpb;
+  const int ne = min(kRouterEpb, experts - e0);
+  const float *xr = x + (size_t)t * hidden;
+  const int tid = threadIdx.x;
+  const int ntile = (hidden + TC - 1) / TC;
+  // Item i = u * 256 + tid: expert i / TC, column i % TC (consecutive
+  // threads read consecutive columns of one row).
+  auto load = [&](int tl, float (&r)[RI], float (&xv)[RI]) {
+#pragma unroll
+    for (int u = 0; u < RI; ++u) {
+      const int i = u * kRouterThreads + tid;
+      const int e = i / TC, col = tl * TC + i % TC;
+      const bool ok = e < ne && col < hidden && tl < ntile;
+      r[u] = ok ? router[(size_t)(e0 + e) * hidden + col] : 0.0f;
+      xv[u] = ok ? xr[col] : 0.0f;
+    }
+  };
+  float s = -0.0f;
+  auto step = [&](int tl, float (&r)[RI], float (&xv)[RI]) {
+    float *cur = tiles[tl & 1];
+#pragma unroll
+    for (int u = 0; u < RI; ++u) {
+      const int i = u * kRouterThreads + tid;
+      cur[(i % TC) * EP + i / TC] = r[u] * xv[u];
+    }
+    load(tl + 2, r, xv);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (tid < ne) {
+      const int cn = min(TC, hidden - tl * TC);
+      int c = 0;
+      for (; c + 8 <= cn; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = cur[(c + k) * EP + tid];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s = s + v[k];
+      }
+      for (; c < cn; ++c) s = s + cur[c * EP + tid];
+    }
+  };
+  float ra[RI], rb[RI], xa[RI], xb[RI];
+  load(0, ra, xa);
+  load(1, rb, xb);
+  for (int tl = 0; tl < ntile; tl += 2) {
+    step(tl, ra, xa);
+    if (tl + 1 < ntile) step(tl + 1, rb, xb);
+  }
+  if (tid < ne) logits[(size_t)t * experts + e0 + tid] = s;
+}
+
+// route_experts (layers.rs:1808-1870) after the logits: softmax over all
+// experts (glibc expf, the sum as one chain in expert order), then top-k by
+// selection (strict >, so the lowest index wins a tie), optional
+// renormalisation.  One block per token.
+__global__ __launch_bounds__(1024) void k_router(const float *__restrict__ logits, int experts, int topk,
+                                                 int norm_topk, int *__restrict__ sel, float *__restrict__ wts) {
   extern __shared__ float probs[];
   const int t = blockIdx.x;
-  const float *xr = x + (size_t)t * hidden;
-  for (int e = threadIdx.x; e < experts; e += blockDim.x) {
-    const float *rr = router + (size_t)e * hidden;
-    float s = -0.0f;
-    for (int i = 0; i < hidden; ++i) s = s + rr[i] * xr[i];
-    probs[e] = s;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  for (int e = tid; e < experts; e += nt) probs[e] = logits[(size_t)t * experts + e];
+  __syncthreads();
+  // Softmax over every expert: max and exponentials in parallel, the sum as
+  // one chain in expert order, then the division.
+  __shared__ float smx, ssum;
+  if (tid < 64) {
+    float mx = -INFINITY;
+    for (int e = tid; e < experts; e += 64) mx = fmaxf(mx, probs[e]);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (tid == 0) smx = mx;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float mx = -INFINITY;
-    for (int e = 0; e < experts; ++e) mx = fmaxf(mx, probs[e]);
+  for (int e = tid; e < experts; e += nt) probs[e] = rai_exact::expf_glibc(probs[e] - smx);
+  __syncthreads();
+  if (tid == 0) {
     float sum = 0.0f;
-    for (int e = 0; e < experts; ++e) {
-      const float v = rai_exact::expf_glibc(probs[e] - mx);
-      probs[e] = v;
-      sum = sum + v;
-    }
-    for (int e = 0; e < experts; ++e) probs[e] = __fdiv_exact(probs[e], sum);
+    for (int e = 0; e < experts; ++e) sum = sum + probs[e];
+    ssum = sum;
+  }
+  __syncthreads();
+  for (int e = tid; e < experts; e += nt) probs[e] = __fdiv_exact(probs[e], ssum);
+  __syncthreads();
+  // Top-k by selection (strict >, so the lowest index wins a tie): lane l
+  // scans experts l, l + 64, ...; a wave-wide argmax picks each slot.
+  if (tid < 64) {
+    const int lane = tid;
+    uint32_t mine = 0;  // taken bits of experts lane + 64 j
     float total = -0.0f;
     int cnt = 0;
     for (int k = 0; k < topk; ++k) {
-      int best = -1;
       float bv = -INFINITY;
-      for (int e = 0; e < experts; ++e) {
-        bool taken = false;
-        for (int j = 0; j < cnt; ++j) taken |= sel[t * topk + j] == e;
-        if (!taken && probs[e] > bv) {
+      int best = -1;
+      for (int j = 0, e = lane; e < experts; ++j, e += 64)
+        if (!((mine >> j) & 1u) && probs[e] > bv) {
           bv = probs[e];
           best = e;
         }
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int ob = __shfl_xor(best, o, 64);
+        if (ob >= 0 && (best < 0 || ov > bv || (ov == bv && ob < best))) {
+          bv = ov;
+          best = ob;
+        }
       }
       if (best < 0) break;
-      sel[t * topk + cnt] = best;
-      wts[t * topk + cnt] = bv;
+      if (lane == (best & 63)) mine |= 1u << (best >> 6);
+      if (lane == 0) {
+        sel[t * topk + cnt] = best;
+        wts[t * topk + cnt] = bv;
+      }
       total = total + bv;
       ++cnt;
     }
-    for (int k = cnt; k < topk; ++k) {
-      sel[t * topk + k] = -1;
-      wts[t * topk + k] = 0.0f;
+    if (lane == 0) {
+      for (int k = cnt; k < topk; ++k) {
+        sel[t * topk + k] = -1;
+        wts[t * topk + k] = 0.0f;
+      }
+      if (norm_topk && total > 0.0f)
+        for (int k = 0; k < cnt; ++k) wts[t * topk + k] = __fdiv_exact(wts[t * topk + k], total);
     }
-    if (norm_topk && total > 0.0f)
-      for (int k = 0; k < cnt; ++k) wts[t * topk + k] = __fdiv_exact(wts[t * topk + k], total);
   }
 }
 
@@ -1363,9 +1445,11 @@ void launch_accept(const uint32_t *am, uint32_t *ctx, int len, int start, int nd
 }
 
 void launch_router(const float *x, const float *router, int m, int hidden, int experts, int topk,
-                   int norm_topk, int *sel, float *wts, hipStream_t s) {
-  hipLaunchKernelGGL(k_router, dim3(m), dim3(64), sizeof(float) * experts, s, x, router, hidden,
-                     experts, topk, norm_topk, sel, wts);
+                   int norm_topk, int *sel, float *wts, float *logits, hipStream_t s) {
+  hipLaunchKernelGGL(k_router_logits, dim3(m, (experts + kRouterEpb - 1) / kRouterEpb), dim3(kRouterThreads), 0, s,
+                     x, router, hidden, experts, logits);
+  hipLaunchKernelGGL(k_router, dim3(m), dim3(1024), sizeof(float) * ((experts + 3) & ~3), s, logits, experts, topk,
+                     norm_topk, sel, wts);
 }
 
 void launch_moe_accumulate(float *out, const float *eo, const float *w, int m, int n,

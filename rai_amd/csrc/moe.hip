@@ -22,6 +22,7 @@
 // matvec, gemm.rs:1774-1919), so the grouping changes no bit.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "kernels.h"
@@ -98,7 +99,9 @@ __global__ void k_moe_gather(const int8_t *__restrict__ q, const float *__restri
 }
 
 // Grid: x = row blocks of 64 over nmat * rows, y = expert.  Thread = one row
-// of matrix `mat` of expert e, against the expert's entries MT at a time.
+// of matrix `mat` of expert e, against the expert's entries MT at a time;
+// the block stages those entries' quantized rows, scales and sums in LDS
+// (dynamic, MT * (cols + 8 * groups) bytes) and reads them as broadcasts.
 // Lane sums as the reference's accumulators: group 32 uses 4 lanes (the
 // 16-byte block32 path, gemm.rs:616-637), groups 64 and 128 use 8 lanes
 // (the 32-byte chunk path, blocks b and b + 8 share lane b % 8).  Codes and
@@ -114,17 +117,39 @@ __global__ __launch_bounds__(64) void k_moe_gemv(float *__restrict__ out, int ld
   constexpr int NL = GS == 32 ? 4 : 8;
   constexpr int NW = GS / 8;          // code dwords per group
   constexpr int CH = 128 / (GS / 2);  // groups per 128-byte chunk
+  extern __shared__ __align__(16) unsigned char lact[];
   const int e = blockIdx.y;
   const int b0 = off[e], cnt = off[e + 1] - b0;
   if (cnt == 0) return;
-  const int rr = blockIdx.x * 64 + threadIdx.x;
-  if (rr >= nmat * rows) return;
-  const int mat = rr / rows, r = rr - mat * rows;
   const int groups = cols / GS, nch = groups / CH;
-  const uint4 *crow = reinterpret_cast<const uint4 *>(nibp[e * nmat + mat] + (size_t)r * (cols / 2));
-  const uint32_t *prow = reinterpret_cast<const uint32_t *>(parp[e * nmat + mat] + (size_t)r * groups * 4);
+  int8_t *lq = reinterpret_cast<int8_t *>(lact);
+  float *lsc = reinterpret_cast<float *>(lact + (size_t)MT * cols);
+  float *lsu = lsc + MT * groups;
+  const int rr = min(blockIdx.x * 64 + (int)threadIdx.x, nmat * rows - 1);
+  const bool live = blockIdx.x * 64 + (int)threadIdx.x < nmat * rows;
+  const int mat = rr / rows, r = rr - mat * rows;
+  // Buffer reads (the table's pointers would otherwise become flat reads,
+  // whose completion the LDS reads of the staged entries would wait for).
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const __amdgpu_buffer_rsrc_t rcs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(nibp[e * nmat + mat]), 0, rows * (cols / 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rps = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(parp[e * nmat + mat]), 0, rows * groups * 4, 0x00020000);
+  const int vc = r * (cols / 2), vp = r * groups * 4;
   for (int t0 = 0; t0 < cnt; t0 += MT) {
     const int mt = min(MT, cnt - t0);
+    __syncthreads();  // the previous chunk's entries are no longer read
+    for (int i = threadIdx.x; i < mt * (cols / 16); i += blockDim.x) {
+      const int t = i / (cols / 16), c = i % (cols / 16);
+      reinterpret_cast<uint4 *>(lq + (size_t)t * cols)[c] =
+          reinterpret_cast<const uint4 *>(q + (size_t)(b0 + t0 + t) * cols)[c];
+    }
+    for (int i = threadIdx.x; i < mt * groups; i += blockDim.x) {
+      const int t = i / groups, g = i % groups;
+      lsc[i] = sc[(size_t)(b0 + t0 + t) * groups + g];
+      lsu[i] = su[(size_t)(b0 + t0 + t) * groups + g];
+    }
+    __syncthreads();
     float f[MT][NL], zc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
@@ -132,14 +157,14 @@ __global__ __launch_bounds__(64) void k_moe_gemv(float *__restrict__ out, int ld
 #pragma unroll
       for (int l = 0; l < NL; ++l) f[t][l] = 0.0f;
     }
-    uint4 cn[8];
+    u4 cn[8];
     uint32_t pn[CH];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) cn[v] = crow[v];
+    for (int v = 0; v < 8; ++v) cn[v] = __builtin_amdgcn_raw_buffer_load_b128(rcs, vc, 16 * v, 0);
 #pragma unroll
-    for (int g = 0; g < CH; ++g) pn[g] = prow[g];
+    for (int g = 0; g < CH; ++g) pn[g] = __builtin_amdgcn_raw_buffer_load_b32(rps, vp, 4 * g, 0);
     for (int c = 0; c < nch; ++c) {
-      uint4 cc[8];
+      u4 cc[8];
       uint32_t pc[CH];
 #pragma unroll
       for (int v = 0; v < 8; ++v) cc[v] = cn[v];
@@ -147,9 +172,9 @@ __global__ __launch_bounds__(64) void k_moe_gemv(float *__restrict__ out, int ld
       for (int g = 0; g < CH; ++g) pc[g] = pn[g];
       const int cnx = min(c + 1, nch - 1);
 #pragma unroll
-      for (int v = 0; v < 8; ++v) cn[v] = crow[cnx * 8 + v];
+      for (int v = 0; v < 8; ++v) cn[v] = __builtin_amdgcn_raw_buffer_load_b128(rcs, vc, (cnx * 8 + v) * 16, 0);
 #pragma unroll
-      for (int g = 0; g < CH; ++g) pn[g] = prow[cnx * CH + g];
+      for (int g = 0; g < CH; ++g) pn[g] = __builtin_amdgcn_raw_buffer_load_b32(rps, vp, (cnx * CH + g) * 4, 0);
       const uint32_t *cw = reinterpret_cast<const uint32_t *>(cc);
 #pragma unroll
       for (int gi = 0; gi < CH; ++gi) {
@@ -158,8 +183,7 @@ __global__ __launch_bounds__(64) void k_moe_gemv(float *__restrict__ out, int ld
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           if (t < mt) {
-            const size_t er = (size_t)(b0 + t0 + t);
-            const uint2 *qv = reinterpret_cast<const uint2 *>(q + er * cols + (size_t)g * GS);
+            const uint2 *qv = reinterpret_cast<const uint2 *>(lq + (size_t)t * cols + (size_t)g * GS);
             int sl[NL];
 #pragma unroll
             for (int l = 0; l < NL; ++l) sl[l] = 0;
@@ -168,17 +192,17 @@ __global__ __launch_bounds__(64) void k_moe_gemv(float *__restrict__ out, int ld
               const uint2 a = qv[b];
               sl[b % NL] = blk_dot(cw[gi * NW + b], a.x, a.y, sl[b % NL]);
             }
-            const float cs = ws * sc[er * groups + g];
+            const float cs = ws * lsc[t * groups + g];
 #pragma unroll
             for (int l = 0; l < NL; ++l) f[t][l] = f[t][l] + (float)sl[l] * cs;
-            zc[t] = zc[t] + wz * su[er * groups + g];
+            zc[t] = zc[t] + wz * lsu[t * groups + g];
           }
         }
       }
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      if (t < mt) {
+      if (t < mt && live) {
         float d;
         if (NL == 4)
           d = (f[t][0] + f[t][1]) + (f[t][2] + f[t][3]);
@@ -208,8 +232,10 @@ __global__ void k_moe_combine(float *__restrict__ hid, const float *__restrict__
 }  // namespace
 
 bool moe_device_path(int hidden, int ffn, int gs, int experts) {
+  // The staged entries (8 rows of int8 plus scales and sums) must fit the
+  // 64 KB of LDS a block may use without an opt-in.
   return (gs == 32 || gs == 64 || gs == 128) && experts >= 1 && experts <= 1024 && hidden % 256 == 0 &&
-         ffn % 256 == 0;
+         ffn % 256 == 0 && (size_t)8 * (std::max(hidden, ffn) + 8 * (std::max(hidden, ffn) / gs)) <= 65536;
 }
 
 void launch_moe_plan(const int *sel, int m, int K, int E, int *off, int *ent_of, int *ent_tok, hipStream_t s) {
@@ -228,14 +254,15 @@ void launch_moe_gemv(float *out, int ld, const uint8_t *const *nibp, const uint8
                      int cols, int gs, int E, const int8_t *q, const float *sc, const float *su, const int *off,
                      hipStream_t s) {
   const dim3 grid((nmat * rows + 63) / 64, E);
+  const size_t lds = (size_t)8 * (cols + 8 * (cols / gs));
   if (gs == 32)
-    hipLaunchKernelGGL((k_moe_gemv<32, 8>), grid, dim3(64), 0, s, out, ld, nibp, parp, nmat, rows, cols, q, sc, su,
+    hipLaunchKernelGGL((k_moe_gemv<32, 8>), grid, dim3(64), lds, s, out, ld, nibp, parp, nmat, rows, cols, q, sc, su,
                        off);
   else if (gs == 64)
-    hipLaunchKernelGGL((k_moe_gemv<64, 8>), grid, dim3(64), 0, s, out, ld, nibp, parp, nmat, rows, cols, q, sc, su,
+    hipLaunchKernelGGL((k_moe_gemv<64, 8>), grid, dim3(64), lds, s, out, ld, nibp, parp, nmat, rows, cols, q, sc, su,
                        off);
   else
-    hipLaunchKernelGGL((k_moe_gemv<128, 8>), grid, dim3(64), 0, s, out, ld, nibp, parp, nmat, rows, cols, q, sc, su,
+    hipLaunchKernelGGL((k_moe_gemv<128, 8>), grid, dim3(64), lds, s, out, ld, nibp, parp, nmat, rows, cols, q, sc, su,
                        off);
 }
 

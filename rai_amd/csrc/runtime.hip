@@ -136,7 +136,7 @@ struct Workspace {
   // MoE
   DevBuf sel, wts, eo, xg, yg, gg, ug, idx, wcol;
   // Device MoE path: entry plan, gathered quantized inputs, gate|up outputs.
-  DevBuf moff, ment_of, ment_tok, mq, msc, msu, mgu;
+  DevBuf moff, ment_of, ment_tok, mq, msc, msu, mgu, mlogit;
   int logit_rows = 0;
   void init(const rai_model &m, int maxm_, int logit_rows_) {
     const rai_model_config &c = m.cfg;
@@ -187,6 +187,7 @@ struct Workspace {
       msc.alloc(sizeof(float) * ne * G);
       msu.alloc(sizeof(float) * ne * G);
       mgu.alloc(sizeof(float) * ne * 2 * F);
+      mlogit.alloc(sizeof(float) * maxm * c.num_experts);
       wcol.alloc(sizeof(float) * maxm);
     }
   }
@@ -444,7 +445,7 @@ static void moe_block_device(const rai_model &md, int li, Workspace &w, int m, h
   const int gs = c.group_size, ne = m * K;
   const uint8_t *const *tab = md.moe_tab.as<const uint8_t *>() + (size_t)6 * E * li;
   launch_router(w.normed.as<float>(), L.router, m, H, E, K, c.norm_topk_prob, w.sel.as<int>(),
-                w.wts.as<float>(), s);
+                w.wts.as<float>(), w.mlogit.as<float>(), s);
   launch_moe_plan(w.sel.as<int>(), m, K, E, w.moff.as<int>(), w.ment_of.as<int>(), w.ment_tok.as<int>(), s);
   launch_moe_gather(w.q_split.as<int8_t>(), w.qscale.as<float>(), w.qsum.as<float>(), w.ment_tok.as<int>(),
                     w.moff.as<int>(), E, ne, H, H / gs, w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), s);
@@ -457,11 +458,60 @@ static void moe_block_device(const rai_model &md, int li, Workspace &w, int m, h
   launch_moe_combine(w.hid.as<float>(), w.eo.as<float>(), w.wts.as<float>(), w.ment_of.as<int>(), m, K, H, s);
 }
 
+// Prefill-sized batches (more than kMfmaMaxTokens tokens): the same plan
+// and gather, then the per-expert offsets on the host (one synchronisation
+// per layer) and each expert's rows through the regular W4A8 kernels, which
+// are far faster than the grouped one once an expert holds many rows.
+static void moe_block_device_large(const rai_model &md, int li, Workspace &w, int m, hipStream_t s) {
+  const rai_model_config &c = md.cfg;
+  const DLayer &L = md.layers[li];
+  const int H = c.hidden_size, F = c.intermediate_size, E = c.num_experts, K = c.experts_per_token;
+  const int gs = c.group_size, ne = m * K, G = H / gs, GF = F / gs;
+  launch_router(w.normed.as<float>(), L.router, m, H, E, K, c.norm_topk_prob, w.sel.as<int>(),
+                w.wts.as<float>(), w.mlogit.as<float>(), s);
+  launch_moe_plan(w.sel.as<int>(), m, K, E, w.moff.as<int>(), w.ment_of.as<int>(), w.ment_tok.as<int>(), s);
+  launch_moe_gather(w.q_split.as<int8_t>(), w.qscale.as<float>(), w.qsum.as<float>(), w.ment_tok.as<int>(),
+                    w.moff.as<int>(), E, ne, H, G, w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), s);
+  std::vector<int> off(E + 1);
+  HIP_CHECK(hipMemcpyAsync(off.data(), w.moff.p, sizeof(int) * (E + 1), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  float *gate = w.mgu.as<float>(), *up = gate + (size_t)ne * F;
+  auto run = [&](const DLinear &lin, const int8_t *q, const float *sc, const float *su, int groups, int o, int cnt,
+                 float *out) {
+    const _Float16 *qa = nullptr;
+    if (w4a8_mfma_path(lin.rows, lin.cols, cnt, lin.gs)) {
+      launch_qa_pack(q + (size_t)o * lin.cols, cnt, lin.cols, w.qa.as<_Float16>(), s);
+      qa = w.qa.as<_Float16>();
+    }
+    launch_w4a8(out, nullptr, lin.nib, lin.params, nullptr, nullptr, q + (size_t)o * lin.cols,
+                sc + (size_t)o * groups, su + (size_t)o * groups, lin.rows, lin.cols, cnt, lin.gs, s, qa,
+                w.qmm.as<uint8_t>());
+  };
+  for (int e = 0; e < E; ++e) {
+    const int o = off[e], cnt = off[e + 1] - off[e];
+    if (cnt == 0) continue;
+    const DLinear *ex = &L.experts[(size_t)e * 3];
+    run(ex[0], w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), G, o, cnt, gate + (size_t)o * F);
+    run(ex[1], w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), G, o, cnt, up + (size_t)o * F);
+  }
+  const int total = off[E];
+  if (total > 0)
+    launch_silu_quant(gate, up, total, F, F, gs, w.mq.as<int8_t>(), nullptr, w.msc.as<float>(), w.msu.as<float>(),
+                      s, nullptr);
+  for (int e = 0; e < E; ++e) {
+    const int o = off[e], cnt = off[e + 1] - off[e];
+    if (cnt == 0) continue;
+    run(L.experts[(size_t)e * 3 + 2], w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), GF, o, cnt,
+        w.eo.as<float>() + (size_t)o * H);
+  }
+  launch_moe_combine(w.hid.as<float>(), w.eo.as<float>(), w.wts.as<float>(), w.ment_of.as<int>(), m, K, H, s);
+}
+
 static void moe_block(const rai_model &md, const DLayer &L, Workspace &w, int m, hipStream_t s) {
   const rai_model_config &c = md.cfg;
   const int H = c.hidden_size, F = c.intermediate_size, E = c.num_experts, K = c.experts_per_token;
   launch_router(w.normed.as<float>(), L.router, m, H, E, K, c.norm_topk_prob, w.sel.as<int>(),
-                w.wts.as<float>(), s);
+                w.wts.as<float>(), w.mlogit.as<float>(), s);
   std::vector<int> sel((size_t)m * K);
   HIP_CHECK(hipMemcpyAsync(sel.data(), w.sel.p, sel.size() * sizeof(int), hipMemcpyDeviceToHost, s));
   HIP_CHECK(hipStreamSynchronize(s));
@@ -605,7 +655,9 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
     const bool gu1 = norm1 && L.gate_up.rows && fused_quant_ok(F, gs) &&
                      w4a8_norm1_path(L.gate_up.rows, L.gate_up.cols, L.gate_up.gs);
     if (!gu1) norm_then_quant(L.post_norm);
-    if (c.num_experts > 0 && moe_on_device(md)) {
+    if (c.num_experts > 0 && moe_on_device(md) && m > kMfmaMaxTokens && !st) {
+      moe_block_device_large(md, li, w, m, s);
+    } else if (c.num_experts > 0 && moe_on_device(md)) {
       moe_block_device(md, li, w, m, s);
     } else if (c.num_experts > 0) {
       moe_block(md, L, w, m, s);

@@ -98,42 +98,151 @@ struct Gen {
 };
 
 constexpr int kSampleThreads = 1024;
+typedef float f4v __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float bcast(float v, int k) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), k));
-}
-__device__ __forceinline__ double bcast_d(double v, int k) {
-  const uint64_t u = __builtin_bit_cast(uint64_t, v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, k);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), k);
-  return __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
-}
+// Sequential chains, block-wide calls.  The values pass through LDS in
+// chunks of kStage; wave 0 walks a chunk with broadcast 16-byte reads (every
+// lane computes the same chain, so the next reads issue while the adds
+// wait on each other), which leaves one dependent add per element.
+constexpr int kStage = 4096;
 
-// Sequential f32 sum of p[0..n) from +0, in index order (one wave; every
-// lane returns the sum).  Values are >= +0, so the +0 padding of the last
-// 64-wide read changes nothing.
-__device__ float chain_sum(const float *p, int n, int lane) {
-  float s = 0.0f;
-  for (int base = 0; base < n; base += 64) {
-    const float v = base + lane < n ? p[base + lane] : 0.0f;
-#pragma unroll
-    for (int k = 0; k < 64; ++k) s = s + bcast(v, k);
-  }
-  return s;
-}
-
-// First i with r < (p[0] + ... + p[i]) (f32, sequential); -1 if none.
-__device__ int chain_search(const float *p, int n, float r, int lane) {
+// f32 sum of p[0..n) from +0 in index order (every thread returns it).
+// The values are >= +0, so padding with +0 changes nothing.
+__device__ float seq_sum(const float *p, int n) {
+  __shared__ __align__(16) float buf[kStage];
+  __shared__ float res;
   float c = 0.0f;
-  for (int base = 0; base < n; base += 64) {
-    const float v = base + lane < n ? p[base + lane] : 0.0f;
-    const int lim = min(64, n - base);
-    for (int k = 0; k < lim; ++k) {
-      c = c + bcast(v, k);
-      if (r < c) return base + k;
+  for (int c0 = 0; c0 < n; c0 += kStage) {
+    const int cn = min(kStage, n - c0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kStage; i += blockDim.x) buf[i] = i < cn ? p[c0 + i] : 0.0f;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      for (int i = 0; i < cn; i += 32) {
+        f4v v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f4v *>(&buf[i + 4 * u]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          c = c + v[u][0];
+          c = c + v[u][1];
+          c = c + v[u][2];
+          c = c + v[u][3];
+        }
+      }
     }
   }
-  return -1;
+  if (threadIdx.x == 0) res = c;
+  __syncthreads();
+  return res;
+}
+
+// First i with r < p[0] + ... + p[i] (f32, index order); -1 if none.  Each
+// 64-element block's running sums land in lane k (off the chain), one
+// ballot finds the first hit.
+__device__ int seq_search(const float *p, int n, float r) {
+  __shared__ __align__(16) float buf[kStage];
+  __shared__ int res;
+  const int lane = threadIdx.x & 63;
+  float c = 0.0f;
+  int found = -1;
+  for (int c0 = 0; c0 < n && found < 0; c0 += kStage) {
+    const int cn = min(kStage, n - c0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kStage; i += blockDim.x) buf[i] = i < cn ? p[c0 + i] : 0.0f;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      for (int i = 0; i < cn && found < 0; i += 64) {
+        f4v v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = *reinterpret_cast<const f4v *>(&buf[i + 4 * u]);
+        float pref = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            c = c + v[u][w];
+            pref = lane == 4 * u + w ? c : pref;
+          }
+        }
+        const uint64_t hit = __ballot(r < pref && i + lane < cn);
+        if (hit) found = c0 + i + __ffsll((unsigned long long)hit) - 1;
+      }
+    }
+    if (threadIdx.x == 0) res = found;
+    __syncthreads();
+    found = res;
+  }
+  return found;
+}
+
+// The residual max(0, p - q) of sample_correction as f64, q the draft's
+// probabilities (pq) or the point mass on d.
+__device__ __forceinline__ double residual(const float *pa, const float *pq, int d, int j) {
+  const float q = pq ? pq[j] : (j == d ? 1.0f : 0.0f);
+  return (double)fmaxf(pa[j] - q, 0.0f);
+}
+
+// f64 sum of the residuals over [0, n) from +0 in index order.
+__device__ double seq_sum_resid(const float *pa, const float *pq, int d, int n) {
+  __shared__ __align__(16) double buf[kStage];
+  __shared__ double res;
+  double c = 0.0;
+  for (int c0 = 0; c0 < n; c0 += kStage) {
+    const int cn = min(kStage, n - c0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kStage; i += blockDim.x) buf[i] = i < cn ? residual(pa, pq, d, c0 + i) : 0.0;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      for (int i = 0; i < cn; i += 16) {
+        double v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = buf[i + u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) c = c + v[u];
+      }
+    }
+  }
+  if (threadIdx.x == 0) res = c;
+  __syncthreads();
+  return res;
+}
+
+// First i with (residual[0] + ... + residual[i]) >= u (f64); n - 1 if none.
+__device__ int seq_search_resid(const float *pa, const float *pq, int d, int n, double u) {
+  __shared__ __align__(16) double buf[kStage];
+  __shared__ int res;
+  const int lane = threadIdx.x & 63;
+  double c = 0.0;
+  int found = -1;
+  for (int c0 = 0; c0 < n && found < 0; c0 += kStage) {
+    const int cn = min(kStage, n - c0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kStage; i += blockDim.x) buf[i] = i < cn ? residual(pa, pq, d, c0 + i) : 0.0;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      for (int i = 0; i < cn && found < 0; i += 64) {
+        double pref = 0.0;
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          double v[16];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) v[k] = buf[i + 16 * sb + k];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            c = c + v[k];
+            pref = lane == 16 * sb + k ? c : pref;
+          }
+        }
+        const uint64_t hit = __ballot(pref >= u && i + lane < cn);
+        if (hit) found = c0 + i + __ffsll((unsigned long long)hit) - 1;
+      }
+    }
+    if (threadIdx.x == 0) res = found;
+    __syncthreads();
+    found = res;
+  }
+  return found < 0 ? n - 1 : found;
 }
 
 // Block-wide reductions (every thread returns the result).
@@ -194,13 +303,7 @@ __device__ void row_probs(const float *row, int V, float T, float *out, float *r
   }
   for (int i = tid; i < V; i += nt) out[i] = rai_exact::expf_glibc(out[i] - mx);
   __syncthreads();
-  __shared__ float ssum;
-  if (tid < 64) {
-    const float s = chain_sum(out, V, tid);
-    if (tid == 0) ssum = s;
-  }
-  __syncthreads();
-  const float sum = ssum;
+  const float sum = seq_sum(out, V);
   if (!(isfinite(sum) && sum > 0.0f)) {
     for (int i = tid; i < V; i += nt) out[i] = 1.0f / (float)V;
   } else if (SAMPLE) {
@@ -217,12 +320,8 @@ __device__ int draw_token(const float *p, int V, Gen &g, int *ires) {
   __shared__ float rr;
   if (threadIdx.x == 0) rr = g.gen_f32();
   __syncthreads();
-  if (threadIdx.x < 64) {
-    const int i = chain_search(p, V, rr, threadIdx.x);
-    if (threadIdx.x == 0) *ires = i;
-  }
-  __syncthreads();
-  int tok = *ires;
+  int tok = seq_search(p, V, rr);
+  (void)ires;
   if (tok < 0) {
     // Fallback: argmax of the probabilities (sampler.rs:201-208, last
     // maximum wins).
@@ -289,7 +388,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_accept(
   __shared__ double sh_u;
   __shared__ float redf[16];
   __shared__ int redi[16];
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x;
   if (tid == 0) {
     sh_acc = 0;
     sh_prod = 0;
@@ -317,23 +416,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_accept(
     // with q the draft's distribution; sum and search in f64.
     const int d = (int)ctx[start + i];
     const float *pq = pdraft ? pdraft + (size_t)i * V : nullptr;
-    auto resid = [&](int j) {
-      const float q = pq ? pq[j] : (j == d ? 1.0f : 0.0f);
-      return (double)fmaxf(pa[j] - q, 0.0f);
-    };
-    __shared__ double adj_sum;
-    if (tid < 64) {
-      double s = 0.0;
-      for (int base = 0; base < V; base += 64) {
-        const int j = base + lane;
-        const double v = j < V ? resid(j) : 0.0;
-#pragma unroll
-        for (int k = 0; k < 64; ++k) s = s + bcast_d(v, k);
-      }
-      if (tid == 0) adj_sum = s;
-    }
-    __syncthreads();
-    const double as = adj_sum;
+    const double as = seq_sum_resid(pa, pq, d, V);
     if (!(isfinite(as) && as > 0.0)) {
       // sample_token over the target row (unreachable when the draft's
       // probability is below 1; kept for the reference's semantics).
@@ -343,26 +426,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_accept(
     } else {
       if (tid == 0) sh_u = g.gen_f64() * as;
       __syncthreads();
-      if (tid < 64) {
-        const double u = sh_u;
-        double c = 0.0;
-        int found = V - 1;
-        bool done = false;
-        for (int base = 0; base < V && !done; base += 64) {
-          const int j = base + lane;
-          const double v = j < V ? resid(j) : 0.0;
-          const int lim = min(64, V - base);
-          for (int k = 0; k < lim; ++k) {
-            c = c + bcast_d(v, k);
-            if (c >= u) {
-              found = base + k;
-              done = true;
-              break;
-            }
-          }
-        }
-        if (tid == 0) sh_tok = found;
-      }
+      const int tok = seq_search_resid(pa, pq, d, V, sh_u);
+      if (tid == 0) sh_tok = tok;
     }
     __syncthreads();
     if (tid == 0) {
