@@ -111,6 +111,54 @@ def roofline_only(gs: int) -> int:
     return 0
 
 
+def profile_workload(which: str) -> int:
+    """One workload on its own, for a kernel trace or a counter pass:
+    prefill   - Mistral-7B shape, a 4096-token copy-heavy prompt prefilled twice;
+    greedy    - Mistral-7B, 2 x 64 greedy lookup tokens (n=3, k=8) after a
+                4096-token prefill, then 12 verify steps with 8 forced drafts;
+    sampled   - the same at temperature 0.7 (seed 42);
+    olmoe     - OLMoE-1B-7B shape, 2048-token prompt, as greedy;
+    gemm512   - the prefill GEMM alone: 28672 x 4096 W4A8 g32 at M = 512.
+    Step graphs are off so the trace shows every kernel launch."""
+    import rai_amd
+    from rai_amd.workload import MISTRAL_7B, OLMOE, copy_heavy_prompt
+    if which == "gemm512":
+        n, k, _ = roofline_shape()
+        ms, _, _ = measure_gemv(rai_amd, n, k, 512, 32, iters=20)
+        log(f"{n}x{k} M=512: {ms * 1e3:.1f} us")
+        return 0
+    os.environ["RAI_STEP_GRAPHS"] = "0"
+    s = OLMOE if which == "olmoe" else MISTRAL_7B
+    ctx, plen = (4096, 2048) if which == "olmoe" else (8192, 4096)
+    img = rai_amd.synth_model(s["hidden_size"], s["num_layers"], s["num_heads"], s["num_kv_heads"], s["head_dim"],
+                              s["intermediate_size"], s["vocab_size"], ctx, group_size=32,
+                              num_experts=s.get("num_experts", 0), experts_per_token=s.get("experts_per_token", 0),
+                              seed=77 if which == "olmoe" else 1234)
+    model = rai_amd.RaiModel.from_bytes(img, max_groups=1024)
+    del img
+    dec = rai_amd.LookupDecoder(model, ctx)
+    prompt = copy_heavy_prompt(plen, s["vocab_size"], seed=55)
+    for _ in range(2 if which == "prefill" else 1):
+        dec.kv_cache.truncate(0)
+        t0 = time.perf_counter()
+        pos = dec.prefill(prompt)
+        rai_amd.lib().rai_device_synchronize()
+        log(f"prefill {pos} tokens: {time.perf_counter() - t0:.3f}s")
+    if which == "prefill":
+        return 0
+    t = 0.7 if which == "sampled" else 0.0
+    cfg = rai_amd.LookupConfig(max_draft=8, min_ngram=3, max_ngram=3, temperature=t)
+    dec.seed(42)
+    for _ in range(2):
+        dec.kv_cache.truncate(pos)
+        _, st = dec.decode(prompt, pos, 64, cfg)
+    log(f"{which} decode: {st}")
+    dec.kv_cache.truncate(pos)
+    vt, _ = forced_verify_steps(dec, list(prompt), pos, cfg, 12)
+    log(f"verify ms {[round(x * 1e3, 2) for x in vt]}")
+    return 0
+
+
 def _counter_pass(counter: str, gs: int, tmp: str):
     """Run `bench.py --roofline-only` under one rocprofv3 counter pass; return
     {kernel name: [per-dispatch values]}."""
@@ -290,9 +338,13 @@ def main() -> int:
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-olmoe", action="store_true", help="skip the config-5 (OLMoE) measurement")
     ap.add_argument("--roofline-only", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--profile", choices=["prefill", "greedy", "sampled", "olmoe", "gemm512"],
+                    help="run one workload alone (for rocprofv3) and print no JSON line")
     args = ap.parse_args()
     if args.roofline_only:
         return roofline_only(32)
+    if args.profile:
+        return profile_workload(args.profile)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
         return 2

@@ -544,12 +544,21 @@ __device__ __forceinline__ float mul_h16(uint32_t w, float x, float nz) {
 // NG token groups; la / lsc / lsu point at the lane's slot of token group
 // 0: A of (group t, step q, block b) at la[((t * nq + q) * 4 + b) * 17],
 // scales / sums of (t, q) at [(t * nq + q) * 4].
-template <int NG, int NQ, bool SUB>
+//
+// L1: the last token group holds a single token, whose four block chains
+// then go to the four lane rows instead of four tokens: its MFMA for block b
+// takes A row 4b + r = the token's block b of group 4q + r (nonzero on K
+// block r only), the four accumulate into one D, and lane (j, h) holds
+// S[row j][group 4q + r][block h] for r = 0..3 (every other term an exact
+// zero).  The lane runs that token's block-h chain, its cs and its zc chain
+// (5 operations per group instead of 11); l1off[b] moves the lane's A slot
+// to the one block b needs, hs moves its scale slot to the token's.
+template <int NG, int NQ, bool SUB, bool L1>
 __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, const __amdgpu_buffer_rsrc_t rps,
                                              uint32_t vc0, uint32_t vp0, const u32x4 *__restrict__ la,
                                              const f32x4 *__restrict__ lsc, const f32x4 *__restrict__ lsu,
                                              int nq, float nz, u32x4 (&rc)[NQ], u32x4 (&rp)[NQ],
-                                             float (&f)[NG][4], float (&zc)[NG]) {
+                                             float (&f)[NG][4], float (&zc)[NG], const int (&l1off)[4], int hs) {
   typedef u32x4 u4;
   typedef f32x4 f4;
   const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -563,9 +572,12 @@ __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, c
 #pragma unroll
     for (int b = 0; b < 4; ++b) D[t][b] = zero4;
   }
+  // Lane offsets of the single-token group's A slots and scale slot.
+  auto aoff = [&](int t, int b) { return L1 && t == NG - 1 ? l1off[b] : 0; };
+  auto soff = [&](int t) { return L1 && t == NG - 1 ? -hs : 0; };
   u4 avc[4], avn[4];
 #pragma unroll
-  for (int b = 0; b < 4; ++b) avc[b] = la[b * 17];
+  for (int b = 0; b < 4; ++b) avc[b] = la[b * 17 + aoff(0, b)];
   for (int q0 = 0; q0 < nq; q0 += NQ) {
 #pragma unroll
     for (int s = 0; s < NQ; ++s) {
@@ -585,22 +597,32 @@ __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, c
           const int tn = t + 1 < NG ? t + 1 : 0;
           const int qn = t + 1 < NG ? q : min(q + 1, nq - 1);
 #pragma unroll
-          for (int b = 0; b < 4; ++b) avn[b] = la[((tn * nq + qn) * 4 + b) * 17];
+          for (int b = 0; b < 4; ++b) avn[b] = la[((tn * nq + qn) * 4 + b) * 17 + aoff(tn, b)];
         }
+        const bool one = L1 && t == NG - 1;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float cs = mul_h16<false>(rp[sp][r], as4[t][r], nz);
           f[t][0] = f[t][0] + D[t][0][r] * cs;
-          f[t][1] = f[t][1] + D[t][1][r] * cs;
-          f[t][2] = f[t][2] + D[t][2][r] * cs;
-          f[t][3] = f[t][3] + D[t][3][r] * cs;
+          if (!one) {
+            f[t][1] = f[t][1] + D[t][1][r] * cs;
+            f[t][2] = f[t][2] + D[t][2][r] * cs;
+            f[t][3] = f[t][3] + D[t][3][r] * cs;
+          }
           zc[t] = zc[t] + mul_h16<true>(rp[sp][r], xs4[t][r], nz);
         }
-        as4[t] = lsc[(t * nq + q) * 4];
-        xs4[t] = lsu[(t * nq + q) * 4];
+        as4[t] = lsc[(t * nq + q) * 4 + soff(t)];
+        xs4[t] = lsu[(t * nq + q) * 4 + soff(t)];
+        if (one) {
+          D[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[0]), bq[0], zero4, 0, 0, 0);
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
-          D[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[b]), bq[b], zero4, 0, 0, 0);
+          for (int b = 1; b < 4; ++b)
+            D[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[b]), bq[b], D[t][0], 0, 0, 0);
+        } else {
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            D[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[b]), bq[b], zero4, 0, 0, 0);
+        }
 #pragma unroll
         for (int b = 0; b < 4; ++b) avc[b] = avn[b];
       }
@@ -611,13 +633,16 @@ __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, c
   // Epilogue of the last step (slot NQ - 1: nq is a multiple of NQ).
 #pragma unroll
   for (int t = 0; t < NG; ++t) {
+    const bool one = L1 && t == NG - 1;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float cs = mul_h16<false>(rp[NQ - 1][r], as4[t][r], nz);
       f[t][0] = f[t][0] + D[t][0][r] * cs;
-      f[t][1] = f[t][1] + D[t][1][r] * cs;
-      f[t][2] = f[t][2] + D[t][2][r] * cs;
-      f[t][3] = f[t][3] + D[t][3][r] * cs;
+      if (!one) {
+        f[t][1] = f[t][1] + D[t][1][r] * cs;
+        f[t][2] = f[t][2] + D[t][2][r] * cs;
+        f[t][3] = f[t][3] + D[t][3][r] * cs;
+      }
       zc[t] = zc[t] + mul_h16<true>(rp[NQ - 1][r], xs4[t][r], nz);
     }
   }
@@ -728,6 +753,11 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
     zc[t] = 0.0f;
   }
   const int aslot = (h == (j & 3)) ? j : 16;
+  // The block's last token group is the single token of m = 4k + 1.
+  const bool l1 = (m & 3) == 1 && tg0 + TGW == ntg;
+  int l1off[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) l1off[b] = ((h == (j & 3) && (j >> 2) == b) ? (j & 3) : 16) - aslot;
   if (huge) {
     // Rare; this path fills a ring of its own (the prologue's loads go
     // unused), which keeps the common path's ring in fixed registers.
@@ -739,17 +769,32 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
       rph[s] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, s * 16, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    gemv_rp_main<TGW, NQ, false>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rch, rph, f, zc);
+    gemv_rp_main<TGW, NQ, false, false>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rch, rph, f, zc,
+                                        l1off, h);
+  } else if (l1) {
+    gemv_rp_main<TGW, NQ, true, true>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rc, rp, f, zc,
+                                      l1off, h);
   } else {
-    gemv_rp_main<TGW, NQ, true>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rc, rp, f, zc);
+    gemv_rp_main<TGW, NQ, true, false>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rc, rp, f, zc,
+                                       l1off, h);
+  }
+  // Single-token group: lane (j, h) holds block chain h; lane (j, 0) sums
+  // the four in the reference order.
+  float g1 = 0.0f, g2 = 0.0f, g3 = 0.0f;
+  if (l1 && !huge) {
+    g1 = __shfl(f[TGW - 1][0], j + 16);
+    g2 = __shfl(f[TGW - 1][0], j + 32);
+    g3 = __shfl(f[TGW - 1][0], j + 48);
   }
   if (row < rows) {
 #pragma unroll
     for (int t = 0; t < TGW; ++t) {
-      const int tok = 4 * (tg0 + t) + h;
-      if (tok < m) {
+      const bool one = l1 && !huge && t == TGW - 1;
+      const int tok = 4 * (tg0 + t) + (one ? 0 : h);
+      if (tok < m && (!one || h == 0)) {
         const size_t oi = (size_t)tok * rows + row;
-        const float v = ((f[t][0] + f[t][1]) + (f[t][2] + f[t][3])) + zc[t];
+        const float v = one ? ((f[t][0] + g1) + (g2 + g3)) + zc[t]
+                            : ((f[t][0] + f[t][1]) + (f[t][2] + f[t][3])) + zc[t];
         out[oi] = add ? add[oi] + v : v;
       }
     }
