@@ -118,7 +118,8 @@ def profile_workload(which: str) -> int:
                 4096-token prefill, then 12 verify steps with 8 forced drafts;
     sampled   - the same at temperature 0.7 (seed 42);
     olmoe     - OLMoE-1B-7B shape, 2048-token prompt, as greedy;
-    gemm512   - the prefill GEMM alone: 28672 x 4096 W4A8 g32 at M = 512.
+    gemm512   - the prefill GEMM alone: 28672 x 4096 W4A8 g32 at M = 512;
+    gemv9     - the five verify-step GEMV shapes alone at M = 9.
     Step graphs are off so the trace shows every kernel launch."""
     import rai_amd
     from rai_amd.workload import MISTRAL_7B, OLMOE, copy_heavy_prompt
@@ -126,6 +127,13 @@ def profile_workload(which: str) -> int:
         n, k, _ = roofline_shape()
         ms, _, _ = measure_gemv(rai_amd, n, k, 512, 32, iters=20)
         log(f"{n}x{k} M=512: {ms * 1e3:.1f} us")
+        return 0
+    if which == "gemv9":
+        h, f, v = MISTRAL_7B["hidden_size"], MISTRAL_7B["intermediate_size"], MISTRAL_7B["vocab_size"]
+        qkv = (MISTRAL_7B["num_heads"] + 2 * MISTRAL_7B["num_kv_heads"]) * MISTRAL_7B["head_dim"]
+        for n, k in ((qkv, h), (h, h), (2 * f, h), (h, f), (v, h)):
+            ms, gbs, _ = measure_gemv(rai_amd, n, k, 9, 32, iters=20)
+            log(f"{n}x{k} M=9: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
         return 0
     os.environ["RAI_STEP_GRAPHS"] = "0"
     s = OLMOE if which == "olmoe" else MISTRAL_7B
@@ -338,7 +346,7 @@ def main() -> int:
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-olmoe", action="store_true", help="skip the config-5 (OLMoE) measurement")
     ap.add_argument("--roofline-only", action="store_true", help=argparse.SUPPRESS)
-    ap.add_argument("--profile", choices=["prefill", "greedy", "sampled", "olmoe", "gemm512"],
+    ap.add_argument("--profile", choices=["prefill", "greedy", "sampled", "olmoe", "gemm512", "gemv9"],
                     help="run one workload alone (for rocprofv3) and print no JSON line")
     args = ap.parse_args()
     if args.roofline_only:
