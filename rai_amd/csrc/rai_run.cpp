@@ -82,7 +82,7 @@ Args parse(int argc, char **argv) {
     else if (!k.empty() && k[0] != '-' && a.model.empty()) a.model = k;
     else die("unknown argument " + k);
   }
-  // validate_args (run.rs:446-510), for the options this driver takes.
+  // validate_args (run.rs:134-215), for the options this driver takes.
   if (a.model.empty()) die("a MODEL path is required");
   if (a.prompt.empty()) die("--prompt-ids must not be empty");
   if (a.max_tokens == 0) die("--max-tokens must be greater than zero");

@@ -61,12 +61,14 @@ def _lookup_steps_match(rai, ora, gm, om, prompt, steps, max_ctx, ngram=(3, 3), 
 # --------------------------------------------------------------- config 3 --
 
 @pytest.mark.parametrize("rows,cols", GEMV_SHAPES)
-def test_cfg3_m17_sweep_shapes_bit_exact(rai, ora, rows, cols):
-    """W4A8 sweep at M = 17 (the first token count past the matrix-core
-    verify kernel) on the four sweep shapes: f32 outputs bit-exact."""
-    nib, params, x = gemv_operands(rows, cols, 17, 32, seed=rows + cols + 17)
-    got = rai.w4a8_matmul(nib, params, x, rows, cols, 17, 32)
-    want = ora.w4a8_matmul(nib, params, x, rows, cols, 17, 32)
+@pytest.mark.parametrize("m", [5, 9, 17])
+def test_cfg3_sweep_shapes_bit_exact(rai, ora, rows, cols, m):
+    """W4A8 sweep at M = 5 and 9 (a single-token last group, whose block
+    chains run across lanes) and 17 on the four sweep shapes: f32 outputs
+    bit-exact."""
+    nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + cols + m)
+    got = rai.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    want = ora.w4a8_matmul(nib, params, x, rows, cols, m, 32)
     assert np.array_equal(_bits(got), _bits(want))
 
 
