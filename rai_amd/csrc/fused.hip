@@ -663,6 +663,67 @@ __device__ __forceinline__ void pv_wait_failed(int *err) {
 }
 
 
+// s_waitcnt lgkmcnt(N) (vmcnt and expcnt not waited for).
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt field");
+  __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));
+}
+
+// The sequential PV chain over one CP-position tile for the lane's output
+// (acc = fma(p_t, v_t, acc), t in order; layers.rs:1354-1379).  A wave
+// issues one dependent FMA per ~8 cycles and each other instruction costs
+// about 3.5 cycles more, so the loop keeps the others few: 16 positions (4
+// V and 4 probability reads of 16 bytes) per group, the reads of group
+// g + 2 issued together ahead of the 16 FMAs of group g, and one LDS wait
+// per group (the 16 reads after group g's are the two groups ahead, so
+// lgkmcnt(15) has group g landed).  64-position quarters at or past
+// `nvalid` (the block's last position, in the tile's last chunk) are not
+// run: their probabilities are 0, and fma(0, v, acc) == acc.
+template <int CP>
+__device__ __forceinline__ float pv_chunk(const float4 *__restrict__ vr, const float4 *__restrict__ pr, int nvalid,
+                                          float acc) {
+  constexpr int NG = CP / 16;
+  static_assert(CP % 64 == 0, "whole 64-position quarters");
+  float4 rv[3][4], rq[3][4];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      rv[b][u] = vr[4 * b + u];
+      rq[b][u] = pr[4 * b + u];
+    }
+#pragma unroll
+  for (int q = 0; q < NG / 4; ++q) {
+    if (64 * q >= nvalid) break;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      const int b = 4 * q + bb;
+      if (b + 2 < NG) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          rv[(b + 2) % 3][u] = vr[4 * (b + 2) + u];
+          rq[(b + 2) % 3][u] = pr[4 * (b + 2) + u];
+        }
+        wait_lgkm<15>();
+      } else {
+        wait_lgkm<0>();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4 v4 = rv[b % 3][u], p4 = rq[b % 3][u];
+        acc = __fmaf_rn(p4.x, v4.x, acc);
+        acc = __fmaf_rn(p4.y, v4.y, acc);
+        acc = __fmaf_rn(p4.z, v4.z, acc);
+        acc = __fmaf_rn(p4.w, v4.w, acc);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  return acc;
+}
+
 template <int DL, int G, int CP, int TM, int NL>
 __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
     const float *__restrict__ P, const float *__restrict__ vt_g, int vstride, int pos0, int m, int nh, int hd,
@@ -748,42 +809,7 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
       if (lds_wait_ge<false>(&ready[k & 1], k, spin) < k) pv_wait_failed(err);
       const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
       const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][(tl * G + g) * STR]);
-      // Rolling prefetch: the next 8 float4 pairs (32 positions) are
-      // requested before the 32 FMAs of the current ones, so the LDS
-      // latency is exposed once per chunk instead of once per 32 positions.
-      constexpr int PB = NV + NP <= 28 ? 8 : 4;  // fewer with many loader registers
-      static_assert(Q4 % PB == 0, "whole prefetch blocks per chunk");
-      float4 cv[PB], cp[PB];
-#pragma unroll
-      for (int u = 0; u < PB; ++u) {
-        cv[u] = vr[u];
-        cp[u] = pr[u];
-      }
-#pragma unroll
-      for (int u0 = 0; u0 < Q4; u0 += PB) {
-        float4 nv[PB], np[PB];
-        if (u0 + PB < Q4) {
-#pragma unroll
-          for (int u = 0; u < PB; ++u) {
-            nv[u] = vr[u0 + PB + u];
-            np[u] = pr[u0 + PB + u];
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < PB; ++u) {
-          acc = __fmaf_rn(cp[u].x, cv[u].x, acc);
-          acc = __fmaf_rn(cp[u].y, cv[u].y, acc);
-          acc = __fmaf_rn(cp[u].z, cv[u].z, acc);
-          acc = __fmaf_rn(cp[u].w, cv[u].w, acc);
-        }
-        if (u0 + PB < Q4) {
-#pragma unroll
-          for (int u = 0; u < PB; ++u) {
-            cv[u] = nv[u];
-            cp[u] = np[u];
-          }
-        }
-      }
+      acc = pv_chunk<CP>(vr, pr, nmax - k * CP, acc);
       // The release orders this chunk's tile reads before the post.
       __hip_atomic_store(&done[wave], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     } else if (k + 1 < nchunks && lw == (k + 1) % NL) {
