@@ -173,6 +173,13 @@ void launch_argmax(const float *logits, int m, int vocab, uint32_t *out, hipStre
 // find_ngram_draft over ctx[0..len): res = {ngram, start, len}; ngram 0 = none.
 void launch_ngram(const uint32_t *ctx, int len, int min_n, int max_n, int max_draft, int *res,
                   hipStream_t s);
+// The next decoder step's search at the end of a step whose acceptance
+// wrote {accepted, produced} to res_acc: over ctx[0..len + produced) for
+// position pos + produced (draft capped by max_ctx).  With a step record
+// `st`, pos, len and min_n / max_n / max_draft are read from st[0], st[1],
+// st[5..7].
+void launch_ngram_next(const uint32_t *ctx, int len, int pos, int min_n, int max_n, int max_draft, int max_ctx,
+                       const int *res_acc, int *res, hipStream_t s, const int *st = nullptr);
 // Greedy acceptance: argmax[0..nd] vs ctx[start..start+nd); writes the
 // produced tokens to ctx[len..] and res2 = {accepted, produced}.
 void launch_accept(const uint32_t *argmax, uint32_t *ctx, int len, int start, int nd, int *res2,

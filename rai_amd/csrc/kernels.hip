@@ -1073,8 +1073,8 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logit
 // find_ngram_draft (lookup.rs:131-171): for n = hi..lo, the largest start
 // <= len-n-1 whose n tokens equal the suffix; draft = min(max_draft,
 // len-start-n) tokens after it.  One 1024-thread block.
-__global__ void k_ngram(const uint32_t *__restrict__ ctx, int len, int min_n, int max_n,
-                        int max_draft, int *__restrict__ res) {
+__device__ __forceinline__ void ngram_search(const uint32_t *__restrict__ ctx, int len, int min_n, int max_n,
+                                             int max_draft, int *__restrict__ res) {
   __shared__ int best;
   __shared__ int done;
   if (threadIdx.x == 0) {
@@ -1110,6 +1110,32 @@ __global__ void k_ngram(const uint32_t *__restrict__ ctx, int len, int min_n, in
     __syncthreads();
     if (done) return;
   }
+}
+
+__global__ void k_ngram(const uint32_t *__restrict__ ctx, int len, int min_n, int max_n,
+                        int max_draft, int *__restrict__ res) {
+  ngram_search(ctx, len, min_n, max_n, max_draft, res);
+}
+
+// The next decoder step's search, run at the end of a step: the context
+// then holds this step's `produced` = res_acc[1] tokens past len, and the
+// next step's position is pos + produced, so its draft is capped at
+// max_ctx - (pos + produced) - 1 tokens (none when that is not positive).
+// With a step record, pos, len and the search parameters come from it
+// (st[0], st[1], st[5..7]).
+__global__ void k_ngram_next(const uint32_t *__restrict__ ctx, int len, int pos, int min_n, int max_n,
+                             int max_draft, int max_ctx, const int *__restrict__ res_acc, int *__restrict__ res,
+                             const int *__restrict__ st) {
+  if (st) {
+    pos = st[0];
+    len = st[1];
+    min_n = st[5];
+    max_n = st[6];
+    max_draft = st[7];
+  }
+  const int produced = res_acc[1];
+  const int budget = max_ctx - (pos + produced) - 1;
+  ngram_search(ctx, len + produced, min_n, max_n, budget > 0 ? min(max_draft, budget) : 0, res);
 }
 
 // Greedy acceptance (the T -> 0 limit of lookup.rs:359-403).
@@ -1437,6 +1463,12 @@ void launch_argmax(const float *logits, int m, int vocab, uint32_t *out, hipStre
 void launch_ngram(const uint32_t *ctx, int len, int min_n, int max_n, int max_draft, int *res,
                   hipStream_t s) {
   hipLaunchKernelGGL(k_ngram, dim3(1), dim3(1024), 0, s, ctx, len, min_n, max_n, max_draft, res);
+}
+
+void launch_ngram_next(const uint32_t *ctx, int len, int pos, int min_n, int max_n, int max_draft, int max_ctx,
+                       const int *res_acc, int *res, hipStream_t s, const int *st) {
+  hipLaunchKernelGGL(k_ngram_next, dim3(1), dim3(1024), 0, s, ctx, len, pos, min_n, max_n, max_draft, max_ctx,
+                     res_acc, res, st);
 }
 
 void launch_accept(const uint32_t *am, uint32_t *ctx, int len, int start, int nd, int *res2,

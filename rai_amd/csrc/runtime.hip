@@ -788,6 +788,12 @@ struct rai_lookup {
   std::vector<uint32_t> ctx_host;  // mirror of ctx[0..ctx_len)
   size_t ctx_len = 0;
   DevBuf res;             // int[8]: ngram result + accept result
+  // The n-gram result for the next step, searched at the end of the last
+  // one (pin[0..2]): valid for that step's position, context length and
+  // search parameters while the caller's context still matches.
+  bool pf_valid = false;
+  size_t pf_pos = 0, pf_len = 0;
+  size_t pf_min = 0, pf_max = 0, pf_draft = 0;
   int *pin = nullptr;     // pinned host mirror of res + tokens (+ the step record at pin[512])
   hipStream_t stream = nullptr;
   // Step graphs: one per verify batch size m (embed, forward, logits,
@@ -827,8 +833,9 @@ static void kv_init(rai_kv &kv, rai_model &m, size_t max_ctx) {
 }
 
 // Bring the device context in line with the caller's host context: only the
-// suffix that differs from the device copy is uploaded.
-static void sync_context(rai_lookup &d, const uint32_t *ctx, size_t len) {
+// suffix that differs from the device copy is uploaded.  Returns whether
+// nothing was uploaded.
+static bool sync_context(rai_lookup &d, const uint32_t *ctx, size_t len) {
   if (len > d.max_ctx) fail(RAI_E_RANGE, "context exceeds the prompt-lookup window");
   size_t same = 0;
   const size_t lim = std::min(len, d.ctx_len);
@@ -840,6 +847,7 @@ static void sync_context(rai_lookup &d, const uint32_t *ctx, size_t len) {
     std::copy(ctx + same, ctx + len, d.ctx_host.begin() + same);
   }
   d.ctx_len = len;
+  return same == len;
 }
 
 // One decode step: LookupDecoder::step (lookup.rs:260-425) in greedy mode.
@@ -862,16 +870,23 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
   if (pos >= d.max_ctx) fail(RAI_E_RANGE, "decode position exceeds the context window");
   if (cap < cfg.max_draft + 1) fail(RAI_E_SHAPE, "output buffer must hold max_draft + 1 tokens");
   if (len > d.max_ctx) fail(RAI_E_RANGE, "context exceeds the prompt-lookup window");
-  sync_context(d, context, len);
+  const bool unchanged = sync_context(d, context, len);
+  // The previous step searched this step's draft already (pin[0..2]) when
+  // the context, position and search parameters are the ones it assumed.
+  const bool prefetched = d.pf_valid && unchanged && len == d.pf_len && pos == d.pf_pos &&
+                          cfg.min_ngram == d.pf_min && cfg.max_ngram == d.pf_max && cfg.max_draft == d.pf_draft;
+  d.pf_valid = false;
   hipStream_t s = d.stream;
   const size_t budget = d.max_ctx > pos + 1 ? d.max_ctx - pos - 1 : 0;
   int *res = d.res.as<int>();
   int nd = 0, start = 0, ngram = 0;
   if (budget > 0) {
-    launch_ngram(d.ctx.as<uint32_t>(), (int)len, (int)cfg.min_ngram, (int)cfg.max_ngram,
-                 (int)std::min(cfg.max_draft, budget), res, s);
-    HIP_CHECK(hipMemcpyAsync(d.pin, res, 3 * sizeof(int), hipMemcpyDeviceToHost, s));
-    HIP_CHECK(hipStreamSynchronize(s));
+    if (!prefetched) {
+      launch_ngram(d.ctx.as<uint32_t>(), (int)len, (int)cfg.min_ngram, (int)cfg.max_ngram,
+                   (int)std::min(cfg.max_draft, budget), res, s);
+      HIP_CHECK(hipMemcpyAsync(d.pin, res, 3 * sizeof(int), hipMemcpyDeviceToHost, s));
+      HIP_CHECK(hipStreamSynchronize(s));
+    }
     ngram = d.pin[0];
     start = d.pin[1];
     nd = ngram ? d.pin[2] : 0;
@@ -891,6 +906,11 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
       launch_argmax(d.ws.logits.as<float>(), m, c.vocab_size, d.ws.am.as<uint32_t>(), s);
       launch_accept(d.ws.am.as<uint32_t>(), d.ctx.as<uint32_t>(), (int)len, start, nd, res + 4, s, st);
     }
+    // The next step's n-gram search over the extended context, so that a
+    // caller continuing from this step's tokens needs one host round trip
+    // per step.
+    launch_ngram_next(d.ctx.as<uint32_t>(), (int)len, (int)pos, (int)cfg.min_ngram, (int)cfg.max_ngram,
+                      (int)cfg.max_draft, (int)d.max_ctx, res + 4, res, s, st);
   };
   HIP_CHECK(hipGetLastError());  // nothing pending from earlier launches
   if (d.graphs && m <= kAttnTokens) {
@@ -900,7 +920,10 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
     sh[2] = start;
     sh[3] = nd;
     std::memcpy(&sh[4], &cfg.temperature, sizeof(float));
-    HIP_CHECK(hipMemcpyAsync(d.step.p, sh, 5 * sizeof(int), hipMemcpyHostToDevice, s));
+    sh[5] = (int)cfg.min_ngram;
+    sh[6] = (int)cfg.max_ngram;
+    sh[7] = (int)cfg.max_draft;
+    HIP_CHECK(hipMemcpyAsync(d.step.p, sh, 8 * sizeof(int), hipMemcpyHostToDevice, s));
     const int *st = d.step.as<int>();
     const int gi = m + (sampled ? kAttnTokens + 1 : 0);
     if (d.graph[gi]) {
@@ -930,6 +953,7 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
     enqueue(nullptr);
     HIP_CHECK(hipGetLastError());
   }
+  HIP_CHECK(hipMemcpyAsync(d.pin, res, 3 * sizeof(int), hipMemcpyDeviceToHost, s));
   HIP_CHECK(hipMemcpyAsync(d.pin + 4, res + 4, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
   HIP_CHECK(hipMemcpyAsync(d.pin + 6, d.ws.err.p, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
   HIP_CHECK(hipMemcpyAsync(d.pin + 8, d.ctx.as<uint32_t>() + len, (size_t)m * sizeof(uint32_t),
@@ -951,6 +975,12 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
   d.ctx_len = len + prod;
   // kv_cache.truncate(pos + produced) (lookup.rs:411).
   for (auto &f : d.kv.filled) f = std::min(f, pos + (size_t)prod);
+  d.pf_valid = true;
+  d.pf_pos = pos + (size_t)prod;
+  d.pf_len = len + (size_t)prod;
+  d.pf_min = cfg.min_ngram;
+  d.pf_max = cfg.max_ngram;
+  d.pf_draft = cfg.max_draft;
   met.accepted = nd ? acc : 0;
   met.drafted = nd;
   met.produced = prod;
@@ -963,6 +993,7 @@ static void lookup_prefill(rai_lookup &d, const uint32_t *prompt, size_t n, size
   if (n == 0) fail(RAI_E_ARG, "prompt must contain at least one token");
   if (n > d.max_ctx) fail(RAI_E_RANGE, "prompt exceeds the prompt-lookup context window");
   check_tokens(md, prompt, n);
+  d.pf_valid = false;
   sync_context(d, prompt, n);
   const size_t cnt = n - 1;
   for (size_t p = 0; p < cnt; p += kChunk) {

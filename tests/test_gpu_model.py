@@ -346,6 +346,48 @@ def test_lookup_greedy_token_identity(rai, ora, name, prompt_len, steps, ngram):
     assert drafted > 0
 
 
+def test_lookup_step_next_search_follows_the_caller(rai, ora):
+    """Each step also searches the next step's draft over its own extended
+    context; a caller that continues differently (rewritten context tail,
+    other search parameters, a rolled-back position) must get the search of
+    what it passed.  Every step's tokens and metrics equal the oracle's on
+    the same inputs."""
+    img = MODELS["synth-g32"](rai)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    prompt = copy_heavy_prompt(200, om.cfg.vocab_size, seed=17)
+    gd, od = rai.LookupDecoder(gm, 512), ora.LookupDecoder(om, 512)
+    gpos, opos = gd.prefill(prompt), od.prefill(prompt.astype(np.int32))
+    ctx = prompt.tolist()
+    rng = np.random.default_rng(5)
+    drafted = 0
+    for i in range(40):
+        kind = i % 4
+        lo, hi = (1, 3) if kind == 2 else (3, 3)
+        k = 4 if kind == 2 else 8
+        if kind == 1:
+            # Rewrite the tail with an earlier 3-gram (a forced draft).
+            src = int(rng.integers(0, len(ctx) - 8))
+            ctx[-3:] = ctx[src:src + 3]
+        if kind == 3 and i > 4:
+            # Roll back one token: position and context shrink together.
+            ctx = ctx[:-1]
+            gpos -= 1
+            opos -= 1
+            gd.kv_cache.truncate(gpos)
+        cfg = rai.LookupConfig(max_draft=k, min_ngram=lo, max_ngram=hi, temperature=0.0)
+        gt, gmet = gd.step(gpos, ctx, cfg)
+        ot, omet = od.step(opos, ctx, k, lo, hi)
+        assert gt == ot, i
+        assert (gmet.accepted, gmet.drafted, gmet.produced) == (omet.accepted, omet.drafted, omet.produced), i
+        assert (gmet.matched_ngram or 0) == omet.matched_ngram, i
+        drafted += gmet.drafted
+        ctx += gt
+        gpos += gmet.produced
+        opos += omet.produced
+    assert drafted > 0
+
+
 def test_lookup_generate_loop_matches_greedy(rai):
     """The native generate loop (cli/run.rs:517-633 without the tokenizer)
     produces the same stream as plain greedy decoding on the GPU."""
