@@ -260,6 +260,39 @@ def olmoe_line(args) -> dict:
             "decode_weight_gbs": round(wb * st["generated"] / (el / runs) / 1e9, 1)}
 
 
+def attention_kernels(rai, shape, pos: int, cap: int) -> dict:
+    """The step's attention launches (scores, softmax, PV) for one decode
+    token and a nine-token verify batch at position `pos`, each timed over
+    back-to-back launches between two HIP events, rotating over enough K/V
+    caches that K and V stream from HBM.  Algorithmic bytes: scores read K (n x hd x 4 per kv
+    head) and q and write the score rows; the softmax reads and writes the
+    score rows; PV reads V (n x hd x 4 per kv head) and the probability rows
+    and writes the head outputs."""
+    nh, nkv, hd = shape["num_heads"], shape["num_kv_heads"], shape["head_dim"]
+    kv_bytes = 2 * nkv * cap * hd * 4
+    copies = max(2, int(ROTATE_BYTES // kv_bytes) + 1)
+    out = {"positions": pos + 1, "kv_cache_positions": cap}
+    for m in (1, 9):
+        sc, sm, pv = attention_time_median(rai, nh, nkv, hd, cap, pos, m, copies)
+        n = pos + m
+        rows = sum(pos + t + 1 for t in range(m)) * nh * 4  # score / probability row bytes
+        b_sc = nkv * n * hd * 4 + m * nh * hd * 4 + rows
+        b_sm = 2 * rows
+        b_pv = nkv * n * hd * 4 + rows + m * nh * hd * 4
+        ent = {}
+        for nm, ms, b in (("scores", sc, b_sc), ("softmax", sm, b_sm), ("pv", pv, b_pv)):
+            gbs = b / (ms * 1e-3) / 1e9
+            ent[nm] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                       "bytes": b}
+        out[f"m{m}"] = ent
+    return out
+
+
+def attention_time_median(rai, nh, nkv, hd, cap, pos, m, copies, reps: int = 3):
+    runs = [rai.attention_time(nh, nkv, hd, cap, pos, m, copies=copies, iters=20) for _ in range(reps)]
+    return tuple(float(np.median([r[k] for r in runs])) for k in range(3))
+
+
 def splice_prompt(base: np.ndarray, cont) -> np.ndarray:
     """The base prompt with (its last three tokens + `cont`) written over the
     positions starting at a quarter of its length; same length, same end."""
@@ -446,6 +479,8 @@ def main() -> int:
             kern[f"{nm}_{n}x{k}_m{m}"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
                                           "frac": round(gbs / HBM_PEAK_GBS, 4)}
     log("GEMVs: " + ", ".join(f"{k} {v['us']}us {v['frac']:.3f}" for k, v in kern.items()))
+    attn = attention_kernels(rai_amd, shape, len(prompt) - 1, max_ctx)
+    log("attention: " + ", ".join(f"{k} {v}" for k, v in attn.items() if isinstance(v, dict)))
     # The prefill GEMM (matrix cores) at M = 512 on gate|up.
     pn, pk, pm = 2 * F, H, 512
     pms, _, _ = measure_gemv(rai_amd, pn, pk, pm, gs, iters=20)
@@ -541,6 +576,7 @@ def main() -> int:
                                  f"over {len(vt)}): 9-token verify forward + lm_head + argmax + acceptance + "
                                  f"KV rollback"),
             "gemv_kernels": kern,
+            "attention_kernels": attn,
             "cpu_host": cpu_name,
             "cpu_all_cores": cpu_all,
         },

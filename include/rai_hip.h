@@ -199,6 +199,17 @@ int rai_w4a8_lane_sums_dev(int32_t *out, const uint8_t *nibbles, const float *x,
 int rai_w4a8_time_dev(float *out, const uint8_t *nibbles, const uint8_t *params, const float *x,
                       size_t rows, size_t cols, size_t m, size_t group_size, size_t copies,
                       int iters, float *avg_ms);
+/* Attention timer (no reference counterpart; the attention-side companion
+ * of rai_w4a8_time_dev): the production attention of `m` tokens at
+ * positions pos..pos+m-1 (m <= 64) over a K cache [nkv][cap][hd] and a
+ * d-major V cache [nkv][hd][vstride] (vstride = cap rounded up to 64): one
+ * full pass, then the score, softmax and PV launches each `iters` times back
+ * to back between two HIP events; ms3 = the average milliseconds of each of
+ * the three.  q is [m][nh*hd]; kc / vc hold `copies` back-to-back caches and
+ * launch i reads copy i % copies (enough copies make every launch stream K
+ * and V from HBM, as in a model step).  Device pointers. */
+int rai_attention_time_dev(const float *q, const float *kc, const float *vc, size_t cap, size_t pos, size_t m,
+                           size_t nh, size_t nkv, size_t hd, size_t copies, int iters, float *ms3);
 /* Host-pointer convenience wrapper of rai_w4a8_matmul_dev (copies in/out). */
 int rai_w4a8_matmul(float *out, const uint8_t *nibbles, const uint8_t *params, const float *x,
                     size_t rows, size_t cols, size_t m, size_t group_size);

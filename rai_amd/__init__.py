@@ -111,6 +111,7 @@ def lib():
         "rai_w4a8_lane_sums_dev": (c_int, [P, P, P, S, S, S, S, P]),
         "rai_w4a8_matmul": (c_int, [P, P, P, P, S, S, S, S]),
         "rai_w4a8_time_dev": (c_int, [P, P, P, P, S, S, S, S, S, c_int, POINTER(c_float)]),
+        "rai_attention_time_dev": (c_int, [P, P, P, S, S, S, S, S, S, S, c_int, POINTER(c_float)]),
         "rai_tied_lm_head_dev": (c_int, [P, P, P, P, S, S, S, P]),
         "rai_embed_lookup_dev": (c_int, [P, S, P, P, S, S, S, P]),
         "rai_argmax_dev": (c_int, [P, S, S, P, P]),
@@ -249,6 +250,28 @@ def w4a8_matmul(nibbles, params, x, rows: int, cols: int, num_tokens: int,
 def w4a8_matvec(nibbles, params, x, rows: int, cols: int, group_size: int) -> np.ndarray:
     """w4a8_matvec (gemm.rs:1336-1384)."""
     return w4a8_matmul(nibbles, params, x, rows, cols, 1, group_size)[0]
+
+
+def attention_time(nh: int, nkv: int, hd: int, cap: int, pos: int, m: int, copies: int = 1,
+                   iters: int = 20, seed: int = 0) -> tuple[float, float, float]:
+    """Average device time (ms) of the attention's score, softmax and PV
+    launches for m tokens at positions pos.. over random N(0, 1) K and V
+    caches of `cap` positions (HIP events between the launches).  With
+    copies > 1 the iterations rotate over that many caches, so that every
+    launch streams K and V from HBM."""
+    rng = np.random.default_rng(seed)
+    vstride = (cap + 63) // 64 * 64
+    kn, vn = nkv * cap * hd, nkv * hd * vstride
+    q = rng.standard_normal((m, nh * hd), dtype=np.float32)
+    kv = rng.standard_normal(max(kn, vn), dtype=np.float32)
+    dq, dk, dv = DeviceArray(q.nbytes), DeviceArray(kn * 4 * copies), DeviceArray(vn * 4 * copies)
+    _check(lib().rai_memcpy_h2d(c_void_p(dq.ptr), _ptr(q), q.nbytes))
+    for c in range(copies):
+        _check(lib().rai_memcpy_h2d(c_void_p(dk.ptr + c * kn * 4), _ptr(kv), kn * 4))
+        _check(lib().rai_memcpy_h2d(c_void_p(dv.ptr + c * vn * 4), _ptr(kv), vn * 4))
+    ms = (c_float * 3)()
+    _check(lib().rai_attention_time_dev(dq.ptr, dk.ptr, dv.ptr, cap, pos, m, nh, nkv, hd, copies, iters, ms))
+    return ms[0], ms[1], ms[2]
 
 
 def w4a8_time(nibbles, params, x, rows: int, cols: int, num_tokens: int, group_size: int,

@@ -977,7 +977,7 @@ void set_attention_spin(int polls) { g_pv_spin = polls > 0 ? polls : kPvSpin; }
 
 void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
                       int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
-                      float *out, float *scores, hipStream_t s, const int *st, int *err) {
+                      float *out, float *scores, hipStream_t s, const int *st, int *err, int stages) {
   static size_t sm_configured = 0;
   for (int t0 = 0; t0 < m; t0 += kAttnTokens) {
     const int mt = std::min(kAttnTokens, m - t0);
@@ -989,14 +989,15 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     const int sstride = (nmax + 3) & ~3;
     const float *qt = q + (size_t)t0 * q_ld;
     float *ot = out + (size_t)t0 * nh * hd;
-    launch_scores(qt, q_ld, kc, cap, p0, mt, nh, nkv, hd, scale, scores, sstride, nmax, st, s);
+    if (stages & 1) launch_scores(qt, q_ld, kc, cap, p0, mt, nh, nkv, hd, scale, scores, sstride, nmax, st, s);
     const size_t smem = sizeof(float) * (size_t)nmax;
     if (smem > 48 * 1024 && smem > sm_configured) {
       (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_softmax),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
       sm_configured = smem;
     }
-    if (nmax <= 512 * 32) {
+    if (!(stages & 2)) {
+    } else if (nmax <= 512 * 32) {
       const int cstr = softmax_r_stride(nmax);
       const size_t rsm = sizeof(float) * 8 * (size_t)cstr;
       const dim3 g(nh, mt);
@@ -1016,7 +1017,8 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     const int DL = (G == 1) ? 64 : (G == 2) ? 32 : 16;
     const bool stream = vstride > 0 && vstride % 64 == 0 &&
                         (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && hd % DL == 0;
-    if (stream) {
+    if (!(stages & 4)) {
+    } else if (stream) {
       // Tokens per block: one for one or two tokens (more blocks), three up
       // to twelve (the verify batch), four beyond; loader waves measured on
       // 4.35K positions with V streamed from HBM (four for one token, three

@@ -158,10 +158,12 @@ size_t attention_scores_floats(int m, int nh, int ctx);
 // wait gave up (the output is then wrong and the caller must fail).
 // Longest context (positions) the attention launches accept.
 constexpr int kMaxAttnPositions = 16384;
+// `stages` (timing only): bit 0 the score launch, bit 1 the softmax, bit 2
+// PV; a stage left out uses what the buffers already hold.
 void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
                       int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
                       float *out, float *scores, hipStream_t s, const int *st = nullptr,
-                      int *err = nullptr);
+                      int *err = nullptr, int stages = 7);
 // Poll limit of the PV tile hand-off waits for launches enqueued from now
 // on (<= 0 restores the default).  Lowering it is for tests of the error
 // path: the waits then give up and report it, and every block still ends.

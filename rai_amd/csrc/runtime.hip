@@ -1354,6 +1354,54 @@ int rai_w4a8_time_dev(float *out, const uint8_t *nib, const uint8_t *params, con
   });
 }
 
+int rai_attention_time_dev(const float *q, const float *kc, const float *vc, size_t cap, size_t pos, size_t m,
+                           size_t nh, size_t nkv, size_t hd, size_t copies, int iters, float *ms3) {
+  RAI_API_BODY({
+    if (!q || !kc || !vc || !ms3) rai::fail(RAI_E_ARG, "null argument");
+    if (m == 0 || m > (size_t)rai::kAttnTokens || nkv == 0 || nh % nkv || hd == 0 || hd % 8 || copies == 0 ||
+        iters <= 0)
+      rai::fail(RAI_E_SHAPE, "invalid attention shape");
+    if (pos + m > cap || cap > (size_t)rai::kMaxAttnPositions) rai::fail(RAI_E_RANGE, "positions exceed the cache");
+    const size_t vstride = (cap + 63) & ~size_t(63);
+    const size_t kbytes = nkv * cap * hd, vbytes = nkv * hd * vstride;  // floats per copy
+    rai::DevBuf out, scores, err;
+    out.alloc(sizeof(float) * m * nh * hd);
+    scores.alloc(sizeof(float) * rai::attention_scores_floats((int)m, (int)nh, (int)(pos + m)));
+    err.alloc(sizeof(int));
+    hipStream_t s;
+    HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    HIP_CHECK(hipMemsetAsync(err.p, 0, sizeof(int), s));
+    // A full warm-up pass, then each stage on its own, `iters` launches back
+    // to back between two events (stage inputs are what the previous pass
+    // left in the buffers), rotating the K / V copies.
+    hipEvent_t ev[2];
+    for (auto &e : ev) HIP_CHECK(hipEventCreate(&e));
+    const float scale = 1.0f / std::sqrt((float)hd);
+    auto run = [&](size_t c, int stages) {
+      rai::launch_attention(q, (int)(nh * hd), kc + c * kbytes, vc + c * vbytes, (int)cap, (int)vstride, (int)pos,
+                            (int)m, (int)nh, (int)nkv, (int)hd, scale, out.as<float>(), scores.as<float>(), s,
+                            nullptr, err.as<int>(), stages);
+    };
+    run(0, 7);
+    HIP_CHECK(hipGetLastError());
+    for (int k = 0; k < 3; ++k) {
+      HIP_CHECK(hipEventRecord(ev[0], s));
+      for (int i = 0; i < iters; ++i) run((size_t)(i + 1) % copies, 1 << k);
+      HIP_CHECK(hipEventRecord(ev[1], s));
+      HIP_CHECK(hipGetLastError());
+      HIP_CHECK(hipEventSynchronize(ev[1]));
+      float ms = 0.0f;
+      HIP_CHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+      ms3[k] = ms / iters;
+    }
+    int e = 0;
+    HIP_CHECK(hipMemcpy(&e, err.p, sizeof(int), hipMemcpyDeviceToHost));
+    for (auto &x : ev) (void)hipEventDestroy(x);
+    (void)hipStreamDestroy(s);
+    if (e) rai::fail(RAI_E_HIP, "attention tile hand-off wait gave up (results discarded)");
+  });
+}
+
 int rai_w4a8_lane_sums_dev(int32_t *out, const uint8_t *nib, const float *x, size_t rows, size_t cols, size_t m,
                            size_t gs, void *stream) {
   RAI_API_BODY({

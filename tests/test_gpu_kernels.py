@@ -210,3 +210,18 @@ def test_shape_errors(rai):
     with pytest.raises(rai.RaiError) as e:
         rai.w4a8_matmul(np.zeros(2, np.uint8), np.zeros(4, np.uint8), np.ones(3), 1, 3, 1, 3)
     assert e.value.status == "RAI_E_SHAPE"
+
+
+@pytest.mark.gpu
+def test_attention_timer_runs_the_production_launches(rai):
+    """rai_attention_time_dev times the decode and verify attention launches
+    (scores, softmax, PV) and refuses shapes the attention does not take."""
+    for m in (1, 9):
+        sc, sm, pv = rai.attention_time(8, 2, 64, 1024, 700, m, copies=2, iters=3)
+        assert all(np.isfinite(x) and x > 0 for x in (sc, sm, pv))
+    with pytest.raises(rai.RaiError) as e:
+        rai.attention_time(8, 3, 64, 1024, 700, 1, iters=1)
+    assert e.value.status == "RAI_E_SHAPE"
+    with pytest.raises(rai.RaiError) as e:
+        rai.attention_time(8, 2, 64, 1024, 1020, 9, iters=1)
+    assert e.value.status == "RAI_E_RANGE"
