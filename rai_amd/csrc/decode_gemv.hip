@@ -81,7 +81,7 @@ size_t dec_smem(int cols, bool fused) {
   return act + std::max(waves, fused ? sizeof(float) * (size_t)rms_scratch_floats(cols) : size_t(0));
 }
 
-constexpr int kEpiPlain = 0, kEpiGlu = 1, kEpiRope = 2;
+constexpr int kEpiPlain = 0, kEpiGlu = 1, kEpiRope = 2, kEpiMoe = 3;
 
 // rope_store of one rotation pair (x0 at head element i, x1 at i + hd/2)
 // as k_rope_store does it (layers.rs:561-726): q and k rotated in the qkv
@@ -121,14 +121,30 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
                                                   const float *__restrict__ scales,
                                                   const float *__restrict__ sums, int rows, int cols,
                                                   int tiles_per_wave, const float *__restrict__ nx,
-                                                  const float *__restrict__ nw, float eps, DecRope rope) {
+                                                  const float *__restrict__ nw, float eps, DecRope rope,
+                                                  DecMoe moe) {
   using C = DecCfg<R>;
   constexpr int IPL = C::IPL, LSTR = C::LSTR;
-  constexpr bool GLU = EPI == kEpiGlu, ROPE = EPI == kEpiRope;
+  constexpr bool GLU = EPI == kEpiGlu, ROPE = EPI == kEpiRope, MOE = EPI == kEpiMoe;
   static_assert(!GLU || (R == 8 && ST == 0), "a gate|up block: 4 waves x 8 rows, fused input norm");
   static_assert(!ROPE || R == 8, "a rope tile: 4 rows of each half of a head");
+  static_assert(!MOE || (ST >= 1 && ST <= 4), "an entry row: quantized activations staged from memory");
   extern __shared__ __align__(16) unsigned char smem[];
   const int groups = cols / 32;
+  if constexpr (MOE) {
+    // Grid row = MoE entry: its expert's matrix, its activation row and its
+    // output row (the whole block leaves together past the last entry).
+    const int ent = blockIdx.y;
+    if (ent >= moe.off[moe.E]) return;
+    const int x = moe.ent_exp[ent];
+    nib = moe.nib_tab[(size_t)x * moe.tstride];
+    params = moe.par_tab[(size_t)x * moe.tstride];
+    const int ar = moe.act_row ? moe.act_row[ent] : ent;
+    q_split += (size_t)ar * cols;
+    scales += (size_t)ar * groups;
+    sums += (size_t)ar * groups;
+    out += (size_t)ent * moe.ld;
+  }
   const int nchunks = (groups + kDecChunk - 1) / kDecChunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, k = lane & 31;
@@ -441,7 +457,7 @@ void launch_dec_t(float *out, const float *add, const uint8_t *nib, const uint8_
   const int waves = blocks * kDecWaves;
   const int per_wave = (tiles + waves - 1) / waves;
   hipLaunchKernelGGL((k_w4a8_dec<R, D, ST, kEpiPlain>), dim3(blocks), dim3(256), smem, s, out, add, nib, params,
-                     q_split, scales, sums, rows, cols, per_wave, nx, nw, eps, DecRope{});
+                     q_split, scales, sums, rows, cols, per_wave, nx, nw, eps, DecRope{}, DecMoe{});
 }
 
 template <int R, int D>
@@ -458,6 +474,23 @@ void launch_dec_rd(float *out, const float *add, const uint8_t *nib, const uint8
     launch_dec_t<R, D, 2>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s);
   else
     launch_dec_t<R, D, 4>(out, add, nib, params, q_split, scales, sums, rows, cols, nx, nw, eps, blocks, s);
+}
+
+template <int R, int D, int ST>
+void launch_dec_moe_t(float *out, const DecMoe &moe, const int8_t *q_split, const float *scales, const float *sums,
+                      int rows, int cols, int blocks, int entries, hipStream_t s) {
+  const size_t smem = dec_smem<R>(cols, false);
+  static size_t configured = 0;
+  if (smem > configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<R, D, ST, kEpiMoe>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    configured = smem;
+  }
+  const int tiles = (rows + R - 1) / R, waves = blocks * kDecWaves;
+  const int per_wave = (tiles + waves - 1) / waves;
+  hipLaunchKernelGGL((k_w4a8_dec<R, D, ST, kEpiMoe>), dim3(blocks, entries), dim3(256), smem, s, out, nullptr,
+                     nullptr, nullptr, q_split, scales, sums, rows, cols, per_wave, nullptr, nullptr, 0.0f,
+                     DecRope{}, moe);
 }
 
 }  // namespace
@@ -512,6 +545,25 @@ bool launch_w4a8_dec(float *out, const float *add, const uint8_t *nib, const uin
   return true;
 }
 
+// 4-row tiles, 4-chunk ring; per entry about 1024 / entries blocks (at
+// least 8, at most one tile per wave), a multiple of 8 so that the blocks of
+// consecutive entries - the entries of one expert are consecutive - fall on
+// the same XCD and share its L2.
+bool launch_w4a8_dec_moe(float *out, const DecMoe &moe, const int8_t *q_split, const float *scales,
+                         const float *sums, int rows, int cols, int gs, int max_entries, hipStream_t s) {
+  if (!w4a8_dec_path(rows, cols, gs) || max_entries <= 0 || max_entries > 65535 || cols > 16 * 1024) return false;
+  const int tiles = (rows + 3) / 4, full = (tiles + kDecWaves - 1) / kDecWaves;
+  int blocks = std::max(8, (1024 / max_entries) & ~7);
+  blocks = std::min(blocks, full);
+  if (cols <= 16 * 256)
+    launch_dec_moe_t<4, 4, 1>(out, moe, q_split, scales, sums, rows, cols, blocks, max_entries, s);
+  else if (cols <= 16 * 512)
+    launch_dec_moe_t<4, 4, 2>(out, moe, q_split, scales, sums, rows, cols, blocks, max_entries, s);
+  else
+    launch_dec_moe_t<4, 4, 4>(out, moe, q_split, scales, sums, rows, cols, blocks, max_entries, s);
+  return true;
+}
+
 bool launch_w4a8_glu1(const uint8_t *nib, const uint8_t *params, const float *x, const float *norm_w, float eps,
                       int rows, int cols, int gs, int8_t *q_out, float *scale_out, float *sum_out, hipStream_t s) {
   if (!w4a8_dec_path(rows, cols, gs) || !w4a8_dec_fused_ok(cols) || rows % 64 != 0) return false;
@@ -523,7 +575,7 @@ bool launch_w4a8_glu1(const uint8_t *nib, const uint8_t *params, const float *x,
     configured = smem;
   }
   hipLaunchKernelGGL((k_w4a8_dec<8, 3, 0, kEpiGlu>), dim3(rows / 64), dim3(256), smem, s, nullptr, nullptr, nib,
-                     params, q_out, scale_out, sum_out, rows, cols, 2, x, norm_w, eps, DecRope{});
+                     params, q_out, scale_out, sum_out, rows, cols, 2, x, norm_w, eps, DecRope{}, DecMoe{});
   return true;
 }
 
@@ -541,7 +593,7 @@ bool launch_w4a8_qkv_rope1(float *out, const uint8_t *nib, const uint8_t *params
   }
   const int tiles = rows / 8, blocks = (tiles + kDecWaves - 1) / kDecWaves;
   hipLaunchKernelGGL((k_w4a8_dec<8, 3, 0, kEpiRope>), dim3(blocks), dim3(256), smem, s, out, nullptr, nib, params,
-                     nullptr, nullptr, nullptr, rows, cols, 1, x, norm_w, eps, rope);
+                     nullptr, nullptr, nullptr, rows, cols, 1, x, norm_w, eps, rope, DecMoe{});
   return true;
 }
 

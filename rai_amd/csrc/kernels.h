@@ -72,6 +72,20 @@ bool launch_w4a8_qkv_rope1(float *out, const uint8_t *nib, const uint8_t *params
                            const float *norm_w, float eps, int rows, int cols, int gs, const DecRope &rope,
                            hipStream_t s);
 
+// Grouped expert GEMV (one-token kernel, one grid row per MoE entry): entry
+// e < off[E] of expert x = ent_exp[e] runs matrix (nib_tab[x * tstride],
+// par_tab[x * tstride]) against activation row act_row[e] (row e when
+// act_row is null) of q_split / scales / sums and writes out + e * ld.
+// Entry rows up to max_entries; those past off[E] are left as they are.
+struct DecMoe {
+  const uint8_t *const *nib_tab, *const *par_tab;
+  int tstride;
+  const int *off, *ent_exp, *act_row;
+  int E, ld;
+};
+bool launch_w4a8_dec_moe(float *out, const DecMoe &moe, const int8_t *q_split, const float *scales,
+                         const float *sums, int rows, int cols, int gs, int max_entries, hipStream_t s);
+
 // Matrix-core W4A8 (gemv.hip): group 32, K a multiple of 256, 2..64 tokens
 // (past 64 the GEMM of gemm_mm.hip is faster on every measured shape).
 constexpr int kMfmaMaxTokens = 64;
@@ -229,7 +243,9 @@ void launch_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *out, hip
 // Device MoE (moe.hip): group 32/64/128, hidden and FFN multiples of 256,
 // at most 1024 experts.
 bool moe_device_path(int hidden, int ffn, int gs, int experts);
-void launch_moe_plan(const int *sel, int m, int K, int E, int *off, int *ent_of, int *ent_tok, hipStream_t s);
+// ent_exp (may be null) receives each entry row's expert.
+void launch_moe_plan(const int *sel, int m, int K, int E, int *off, int *ent_of, int *ent_tok, int *ent_exp,
+                     hipStream_t s);
 void launch_moe_gather(const int8_t *q, const float *sc, const float *su, const int *ent_tok, const int *off, int E,
                        int max_entries, int cols, int groups, int8_t *qg, float *scg, float *sug, hipStream_t s);
 void launch_moe_gemv(float *out, int ld, const uint8_t *const *nibp, const uint8_t *const *parp, int nmat, int rows,

@@ -48,7 +48,7 @@ __device__ __forceinline__ int blk_dot(uint32_t codes, uint32_t q_even, uint32_t
 // (t, k) (-1 when the slot is empty); ent_tok[row] its token.
 __global__ __launch_bounds__(1024) void k_moe_plan(const int *__restrict__ sel, int n, int K, int E,
                                                    int *__restrict__ off, int *__restrict__ ent_of,
-                                                   int *__restrict__ ent_tok) {
+                                                   int *__restrict__ ent_tok, int *__restrict__ ent_exp) {
   extern __shared__ int cnt[];  // E + 1
   for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
@@ -74,6 +74,7 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int *__restrict__ sel, 
       const int row = cnt[e] + ent_of[i];
       ent_of[i] = row;
       ent_tok[row] = i / K;
+      if (ent_exp) ent_exp[row] = e;
     }
   }
 }
@@ -238,9 +239,10 @@ bool moe_device_path(int hidden, int ffn, int gs, int experts) {
          ffn % 256 == 0 && (size_t)8 * (std::max(hidden, ffn) + 8 * (std::max(hidden, ffn) / gs)) <= 65536;
 }
 
-void launch_moe_plan(const int *sel, int m, int K, int E, int *off, int *ent_of, int *ent_tok, hipStream_t s) {
+void launch_moe_plan(const int *sel, int m, int K, int E, int *off, int *ent_of, int *ent_tok, int *ent_exp,
+                     hipStream_t s) {
   hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(1024), sizeof(int) * (E + 1), s, sel, m * K, K, E, off, ent_of,
-                     ent_tok);
+                     ent_tok, ent_exp);
 }
 
 void launch_moe_gather(const int8_t *q, const float *sc, const float *su, const int *ent_tok, const int *off, int E,

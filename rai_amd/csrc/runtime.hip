@@ -68,6 +68,7 @@ struct DLayer {
   // rows == 0 when the pieces could not be placed contiguously.
   DLinear qkv, gate_up;
   std::vector<DLinear> experts;  // all experts, 3 linears each (expert 0 = lin[4..6])
+  bool experts_gu = false;       // every expert's gate and up placed back to back
   const float *router = nullptr;
   const float *in_norm = nullptr, *post_norm = nullptr;
 };
@@ -136,7 +137,7 @@ struct Workspace {
   // MoE
   DevBuf sel, wts, eo, xg, yg, gg, ug, idx, wcol;
   // Device MoE path: entry plan, gathered quantized inputs, gate|up outputs.
-  DevBuf moff, ment_of, ment_tok, mq, msc, msu, mgu, mlogit;
+  DevBuf moff, ment_of, ment_tok, ment_exp, mq, msc, msu, mgu, mlogit;
   int logit_rows = 0;
   void init(const rai_model &m, int maxm_, int logit_rows_) {
     const rai_model_config &c = m.cfg;
@@ -183,6 +184,7 @@ struct Workspace {
       moff.alloc(sizeof(int) * (c.num_experts + 1));
       ment_of.alloc(sizeof(int) * ne);
       ment_tok.alloc(sizeof(int) * ne);
+      ment_exp.alloc(sizeof(int) * ne);
       mq.alloc(ne * std::max(H, F));
       msc.alloc(sizeof(float) * ne * G);
       msu.alloc(sizeof(float) * ne * G);
@@ -251,7 +253,18 @@ static void upload_model(rai_model &m, const uint8_t *img, size_t len, int max_g
       lidx[l].push_back({pi[p], ni[p]});
       wbytes += L.lin[p].params_len + L.lin[p].nib_len;
     }
-    for (const LinearView &e : L.experts) lidx[l].push_back({add(e.params_off, e.params_len), add(e.nib_off, e.nib_len)});
+    // Experts past the first (whose gate|up are lin[4], lin[5] above): gate
+    // and up codes back to back, then their params back to back, then down,
+    // so each expert's gate|up runs as one matrix of 2F rows.
+    for (size_t e = 0; e + 2 < L.experts.size(); e += 3) {
+      const LinearView &g = L.experts[e], &u = L.experts[e + 1], &d = L.experts[e + 2];
+      const size_t gn = add(g.nib_off, g.nib_len), un = add(u.nib_off, u.nib_len);
+      const size_t gp = add(g.params_off, g.params_len), up = add(u.params_off, u.params_len);
+      const size_t dp = add(d.params_off, d.params_len), dn = add(d.nib_off, d.nib_len);
+      lidx[l].push_back({gp, gn});
+      lidx[l].push_back({up, un});
+      lidx[l].push_back({dp, dn});
+    }
     if (c.num_experts > 0) router_idx[l] = add(L.router_off, (size_t)c.num_experts * H * 4);
     n1_idx[l] = add(L.in_norm_off, H * 4);
     n2_idx[l] = add(L.post_norm_off, H * 4);
@@ -351,6 +364,11 @@ static void upload_model(rai_model &m, const uint8_t *img, size_t len, int max_g
       D.experts.push_back(D.lin[5]);
       D.experts.push_back(D.lin[6]);
       for (size_t k = 7; k < lidx[l].size(); ++k) D.experts.push_back(mk(k, 4 + (int)((k - 7) % 3)));
+      // Every expert's gate and up back to back (codes and params): one
+      // gate|up matrix per expert for the entry GEMV.
+      bool gu = contiguous({4, 5});
+      for (int e = 1; e < (int)c.num_experts && gu; ++e) gu = contiguous({4 + 3 * e, 5 + 3 * e});
+      D.experts_gu = gu;
       D.router = reinterpret_cast<const float *>(base + pieces[router_idx[l]].dst);
       // Expert bytes a decode step streams: experts_per_token of them.
       wbytes += (uint64_t)(c.experts_per_token - 1) *
@@ -446,7 +464,24 @@ static void moe_block_device(const rai_model &md, int li, Workspace &w, int m, h
   const uint8_t *const *tab = md.moe_tab.as<const uint8_t *>() + (size_t)6 * E * li;
   launch_router(w.normed.as<float>(), L.router, m, H, E, K, c.norm_topk_prob, w.sel.as<int>(),
                 w.wts.as<float>(), w.mlogit.as<float>(), s);
-  launch_moe_plan(w.sel.as<int>(), m, K, E, w.moff.as<int>(), w.ment_of.as<int>(), w.ment_tok.as<int>(), s);
+  launch_moe_plan(w.sel.as<int>(), m, K, E, w.moff.as<int>(), w.ment_of.as<int>(), w.ment_tok.as<int>(),
+                  w.ment_exp.as<int>(), s);
+  // Entry GEMVs: every expert's gate|up one matrix, each entry's rows through
+  // the one-token kernel, the token's quantized row read in place.
+  if (L.experts_gu && w4a8_dec_path(2 * F, H, gs) && w4a8_dec_path(H, F, gs)) {
+    const DecMoe gu{tab, tab + 2 * E, 2, w.moff.as<int>(), w.ment_exp.as<int>(), w.ment_tok.as<int>(), E, 2 * F};
+    const DecMoe dn{tab + 4 * E, tab + 5 * E, 1, w.moff.as<int>(), w.ment_exp.as<int>(), nullptr, E, H};
+    if (launch_w4a8_dec_moe(w.mgu.as<float>(), gu, w.q_split.as<int8_t>(), w.qscale.as<float>(),
+                            w.qsum.as<float>(), 2 * F, H, gs, ne, s)) {
+      launch_silu_quant(w.mgu.as<float>(), w.mgu.as<float>() + F, ne, F, 2 * F, gs, w.mq.as<int8_t>(), nullptr,
+                        w.msc.as<float>(), w.msu.as<float>(), s, nullptr);
+      if (!launch_w4a8_dec_moe(w.eo.as<float>(), dn, w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), H,
+                               F, gs, ne, s))
+        fail(RAI_E_UNSUPPORTED, "expert down projection shape");
+      launch_moe_combine(w.hid.as<float>(), w.eo.as<float>(), w.wts.as<float>(), w.ment_of.as<int>(), m, K, H, s);
+      return;
+    }
+  }
   launch_moe_gather(w.q_split.as<int8_t>(), w.qscale.as<float>(), w.qsum.as<float>(), w.ment_tok.as<int>(),
                     w.moff.as<int>(), E, ne, H, H / gs, w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), s);
   launch_moe_gemv(w.mgu.as<float>(), 2 * F, tab, tab + 2 * E, 2, F, H, gs, E, w.mq.as<int8_t>(), w.msc.as<float>(),
@@ -469,7 +504,8 @@ static void moe_block_device_large(const rai_model &md, int li, Workspace &w, in
   const int gs = c.group_size, ne = m * K, G = H / gs, GF = F / gs;
   launch_router(w.normed.as<float>(), L.router, m, H, E, K, c.norm_topk_prob, w.sel.as<int>(),
                 w.wts.as<float>(), w.mlogit.as<float>(), s);
-  launch_moe_plan(w.sel.as<int>(), m, K, E, w.moff.as<int>(), w.ment_of.as<int>(), w.ment_tok.as<int>(), s);
+  launch_moe_plan(w.sel.as<int>(), m, K, E, w.moff.as<int>(), w.ment_of.as<int>(), w.ment_tok.as<int>(), nullptr,
+                  s);
   launch_moe_gather(w.q_split.as<int8_t>(), w.qscale.as<float>(), w.qsum.as<float>(), w.ment_tok.as<int>(),
                     w.moff.as<int>(), E, ne, H, G, w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), s);
   std::vector<int> off(E + 1);
