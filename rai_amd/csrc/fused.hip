@@ -409,12 +409,14 @@ __device__ __forceinline__ float block_max256(float v, float *red) {
   return v;
 }
 
-// grid (nh, m), 256 threads; dynamic LDS holds the n exponentials.
+// grid (nh, m), 256 threads; dynamic LDS holds the n exponentials.  Every
+// softmax kernel leaves the row's exponentials e_s in S[s] and 1/sum in
+// S[sstride - 1]; the PV kernels form p_s = e_s * (1/sum) (one rounding, as
+// the reference's normalising multiply) when they read the row.
 __global__ __launch_bounds__(256) void k_softmax(float *__restrict__ S, int pos0, int nh,
                                                  int sstride, const int *__restrict__ st) {
   extern __shared__ float e[];
   __shared__ float red[8];
-  __shared__ float bc;
   if (st) pos0 = st[0];
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const int n = pos0 + t + 1;
@@ -470,15 +472,13 @@ __global__ __launch_bounds__(256) void k_softmax(float *__restrict__ S, int pos0
     for (; i < n8; ++i) acc = acc + e[i * 8 + tid];
     red[tid] = acc;
   }
+  for (int s = tid; s < n; s += 256) row[s] = e[s];
   __syncthreads();
   if (tid == 0) {
     float sum = ((red[0] + red[4]) + (red[1] + red[5])) + ((red[2] + red[6]) + (red[3] + red[7]));
     for (int s = n8 * 8; s < n; ++s) sum = sum + e[s];
-    bc = 1.0f / sum;
+    row[sstride - 1] = 1.0f / sum;
   }
-  __syncthreads();
-  const float inv = bc;
-  for (int s = tid; s < n; s += 256) row[s] = e[s] * inv;
 }
 
 // The same softmax with the row held in registers: thread t of 512 owns
@@ -486,8 +486,8 @@ __global__ __launch_bounds__(256) void k_softmax(float *__restrict__ S, int pos0
 // chain t % 8 (512 is a multiple of 8) at chain step 64u + t / 8.  One load
 // burst, the maximum by lane moves, the exponentials written chain-major to
 // LDS (row j = chain j, row stride cstr = 4 mod 64 floats, so the 8 chain
-// lanes' 16-byte reads hit distinct banks) and normalised from the
-// registers.  The tail exponentials (expf) go to LDS for the final sum.
+// lanes' 16-byte reads hit distinct banks) and stored to the row.  The tail
+// exponentials (expf) go to LDS for the final sum.
 template <int NB>
 __global__ __launch_bounds__(512) void k_softmax_r(float *__restrict__ S, int pos0, int nh, int sstride,
                                                    int cstr, const int *__restrict__ st) {
@@ -495,7 +495,6 @@ __global__ __launch_bounds__(512) void k_softmax_r(float *__restrict__ S, int po
   __shared__ float red[8];
   __shared__ float csum[8];
   __shared__ float tail[8];
-  __shared__ float bc;
   if (st) pos0 = st[0];
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = pos0 + t + 1, n8 = n / 8;
@@ -522,8 +521,10 @@ __global__ __launch_bounds__(512) void k_softmax_r(float *__restrict__ S, int po
       v[u] = rai_exact::expf_glibc(v[u] - mx);
       tail[p - 8 * n8] = v[u];
     }
+    if (p < n) row[p] = v[u];
   }
   __syncthreads();
+  if (wave != 0) return;
   if (tid < 8) {
     // Chain tid: e_{8i + tid} for i = 0..n8-1 in order, 16-byte reads kept
     // 32 values ahead.
@@ -557,20 +558,132 @@ __global__ __launch_bounds__(512) void k_softmax_r(float *__restrict__ S, int po
   if (tid == 0) {
     float sum = ((csum[0] + csum[4]) + (csum[1] + csum[5])) + ((csum[2] + csum[6]) + (csum[3] + csum[7]));
     for (int r = 0; r < n - 8 * n8; ++r) sum = sum + tail[r];
-    bc = 1.0f / sum;
-  }
-  __syncthreads();
-  const float inv = bc;
-#pragma unroll
-  for (int u = 0; u < NB; ++u) {
-    const int p = 512 * u + tid;
-    if (p < n) row[p] = v[u] * inv;
+    row[sstride - 1] = 1.0f / sum;
   }
 }
 
 // Chain-major row stride for k_softmax_r: at least ceil(nmax / 8) floats,
 // 4 mod 64.
 static int softmax_r_stride(int nmax) { return (((nmax + 7) / 8 + 63) & ~63) + 4; }
+
+// Maximum of a wave: DPP moves within rows of 16 lanes (xor 1, xor 2, half
+// mirror, mirror), then the four row maxima by lane reads.
+template <int CTRL>
+__device__ __forceinline__ float max_dpp(float x) {
+  const int xi = __float_as_int(x);
+  return fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(xi, xi, CTRL, 0xF, 0xF, false)));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  x = max_dpp<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+  x = max_dpp<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+  x = max_dpp<0x141>(x);  // row_half_mirror
+  x = max_dpp<0x140>(x);  // row_mirror
+  const int xi = __float_as_int(x);
+  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(xi, 0)), __int_as_float(__builtin_amdgcn_readlane(xi, 16))),
+               fmaxf(__int_as_float(__builtin_amdgcn_readlane(xi, 32)), __int_as_float(__builtin_amdgcn_readlane(xi, 48))));
+}
+
+// The softmax of k_softmax_r with the eight sum chains run from registers.
+// Load, maximum and exponentials as there: every position's Schraudolph
+// exponential (positions past the chains give 0), stored to the row and
+// chain-major to LDS; the (at most 7) tail positions take expf on lanes
+// 0..6, from values loaded at the start.  Then one wave runs the chains
+// over segments of 64 steps: segment q = 8s + u of chain j is read, slot s
+// at a time, into the registers of lane u + 8j.  Phase q adds every lane's
+// values in order (only the segment-q lanes carry a live chain; a padding
+// step adds +0, which leaves a chain unchanged: it starts at +0 and adds
+// non-negative values), then moves each chain to the next segment's lane
+// (DPP row_shr:1, or row_shl:7 from u = 7 to u = 0 of the next slot), so a
+// chain is one sequence of dependent adds with no LDS read between them.
+// The last segment's lanes hold the chains; hsum8 and the tail as the
+// reference, then 1/sum into S[sstride - 1].
+constexpr int kSoftSeg = 64;  // chain steps per segment
+
+__host__ __device__ constexpr int softmax_c_slots(int nb) { return nb > 8 ? nb / 8 : 1; }
+__host__ __device__ constexpr int softmax_c_cstr(int nb) { return 8 * kSoftSeg * softmax_c_slots(nb) + 4; }
+
+template <int NB>
+__global__ __launch_bounds__(512) void k_softmax_c(float *__restrict__ S, int pos0, int nh, int sstride,
+                                                   const int *__restrict__ st) {
+  constexpr int SL = softmax_c_slots(NB), CSTR = softmax_c_cstr(NB);
+  static_assert(8 * kSoftSeg * SL >= 64 * NB, "slots cover every chain step");
+  __shared__ __align__(16) float ech[8 * CSTR];  // [8][CSTR], chain-major
+  __shared__ float red[8];
+  __shared__ float tail[8];
+  if (st) pos0 = st[0];
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = pos0 + t + 1, n8 = n / 8, ntail = n - 8 * n8;
+  float *row = S + ((size_t)t * nh + h) * sstride;
+  float v[NB];
+#pragma unroll
+  for (int u = 0; u < NB; ++u) v[u] = 512 * u < n ? row[min(512 * u + tid, n - 1)] : -INFINITY;
+  const float xt = row[min(8 * n8 + (tid & 7), n - 1)];  // tail value (lanes < ntail)
+  float mx = v[0];
+#pragma unroll
+  for (int u = 1; u < NB; ++u) mx = fmaxf(mx, v[u]);
+  mx = wave_max_dpp(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
+  float *erow = ech + (tid & 7) * CSTR + (tid >> 3);
+#pragma unroll
+  for (int u = 0; u < NB; ++u) {
+    const int p = 512 * u + tid;
+    const float e = p < 8 * n8 ? rai_exact::schraudolph(v[u] - mx) : 0.0f;
+    erow[64 * u] = e;
+    if (p < 8 * n8) row[p] = e;
+  }
+  // Chain steps past 64 NB (slots no row reaches when NB < 8) are never
+  // added by a live lane; zero them anyway.
+  for (int i = 64 * NB + (tid >> 3); i < 8 * kSoftSeg * SL; i += 64) ech[(tid & 7) * CSTR + i] = 0.0f;
+  if (tid < ntail) {
+    const float e = rai_exact::expf_glibc(xt - mx);
+    tail[tid] = e;
+    row[8 * n8 + tid] = e;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const int u8 = lane & 7, j = lane >> 3;
+  const int nseg = (n8 + kSoftSeg - 1) / kSoftSeg;
+  float4 r[kSoftSeg / 4];
+  float acc = 0.0f;
+  int q = 0;
+#pragma unroll
+  for (int sl = 0; sl < SL; ++sl) {
+    if (q >= nseg) break;
+    const float4 *cr = reinterpret_cast<const float4 *>(ech + j * CSTR + kSoftSeg * (8 * sl + u8));
+#pragma unroll
+    for (int g = 0; g < kSoftSeg / 4; ++g) r[g] = cr[g];
+#pragma unroll 1
+    for (int uu = 0; uu < 8 && q < nseg; ++uu, ++q) {
+#pragma unroll
+      for (int g = 0; g < kSoftSeg / 4; ++g) {
+        acc = acc + r[g].x;
+        acc = acc + r[g].y;
+        acc = acc + r[g].z;
+        acc = acc + r[g].w;
+      }
+      // Within each row of 16 lanes: lane l takes lane l - 1 (row_shr:1)
+      // or lane l + 7 (row_shl:7); the 8 lanes of a chain share a row.
+      const int ai = __float_as_int(acc);
+      const float moved = __int_as_float(uu < 7 ? __builtin_amdgcn_update_dpp(ai, ai, 0x111, 0xF, 0xF, false)
+                                                : __builtin_amdgcn_update_dpp(ai, ai, 0x107, 0xF, 0xF, false));
+      acc = u8 == ((uu + 1) & 7) ? moved : acc;
+    }
+  }
+  // The chains ended in the lanes of segment nseg - 1 (with n8 = 0 every
+  // lane still holds +0).
+  const int last = (nseg > 0 ? nseg - 1 : 0) & 7;
+  float c[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) c[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), last + 8 * k));
+  if (lane == 0) {
+    float sum = ((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7]));
+    for (int k = 0; k < ntail; ++k) sum = sum + tail[k];
+    row[sstride - 1] = 1.0f / sum;
+  }
+}
 
 // PV with the V stream spread over loader waves.  The V cache is d-major
 // ([kv head][head dim][vstride] floats, vstride a multiple of 64), so the
@@ -736,6 +849,9 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
   __shared__ __align__(16) float pt[2][TM * G * STR];
   __shared__ int ready[2];
   __shared__ int done[NCW];
+  // 1/sum of each probability row (the softmax leaves it in the row's last
+  // slot): the loaders publish p = e * (1/sum).
+  __shared__ float pinv[TM * G];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slices = hd / DL;
@@ -749,6 +865,10 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
 
   typedef float f4 __attribute__((ext_vector_type(4)));
   f4 fv[NV], fp[NP];
+  auto prow = [&](int r) {
+    const int rr = min((64 * r + lane) / Q4, TM * G - 1), tl = min(rr / G, tn - 1);
+    return ((size_t)(t0 + tl) * nh + (size_t)kvh * G + rr % G) * sstride;
+  };
   auto issue = [&](int k) {
     const int s0 = k * CP;
 #pragma unroll
@@ -760,10 +880,8 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
 #pragma unroll
     for (int r = 0; r < NP; ++r) {
       const int f = 64 * r + lane;  // float4 index in the [TM*G][CP] tile
-      const int rr = min(f / Q4, TM * G - 1), tl = min(rr / G, tn - 1);
       const int q0 = min(s0 + 4 * (f % Q4), sstride - 4);
-      fp[r] = *reinterpret_cast<const f4 *>(P + ((size_t)(t0 + tl) * nh + (size_t)kvh * G + rr % G) * sstride +
-                                            q0);
+      fp[r] = *reinterpret_cast<const f4 *>(P + prow(r) + q0);
     }
   };
   auto publish = [&](int k) {
@@ -779,7 +897,7 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
       if (f < TM * G * Q4) {
         const int q = 4 * (f % Q4), rr = f / Q4, tl = rr / G;
         const int n_ = tl < tn ? pos0 + t0 + tl + 1 : 0;
-        f4 v = fp[r];
+        f4 v = fp[r] * pinv[rr];
         if (s0 + q + 0 >= n_) v.x = 0.0f;
         if (s0 + q + 1 >= n_) v.y = 0.0f;
         if (s0 + q + 2 >= n_) v.z = 0.0f;
@@ -795,7 +913,12 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
   }
   if (threadIdx.x < NCW) done[threadIdx.x] = 0;
   const int lw = wave - NCW;  // loader index, negative for compute waves
+  if (threadIdx.x < TM * G) {
+    const int i = threadIdx.x, tl = min(i / G, tn - 1);
+    pinv[i] = P[((size_t)(t0 + tl) * nh + (size_t)kvh * G + i % G) * sstride + sstride - 1];
+  }
   if (lw >= 0 && lw < nchunks) issue(lw);
+  __syncthreads();  // pinv
   if (lw == 0) {
     publish(0);
     if (NL < nchunks) issue(NL);
@@ -850,6 +973,7 @@ __global__ __launch_bounds__(64) void k_pv_any(const float *__restrict__ P,
   const int t = row / nh, h = row - t * nh;
   const int n = pos0 + t + 1;
   const float *p = P + (size_t)row * sstride;
+  const float inv = p[sstride - 1];  // the softmax's 1/sum: p_s = e_s * inv
   const size_t step = DMAJOR ? 1 : (size_t)hd;
   const float *vb = DMAJOR ? vc + ((size_t)(h / G) * hd + d) * vstride
                            : vc + (size_t)(h / G) * cap * hd + d;
@@ -859,13 +983,13 @@ __global__ __launch_bounds__(64) void k_pv_any(const float *__restrict__ P,
     float pv[8], vv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      pv[u] = p[s + u];
+      pv[u] = p[s + u] * inv;
       vv[u] = vb[(size_t)(s + u) * step];
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc = __fmaf_rn(pv[u], vv[u], acc);
   }
-  for (; s < n; ++s) acc = __fmaf_rn(p[s], vb[(size_t)s * step], acc);
+  for (; s < n; ++s) acc = __fmaf_rn(p[s] * inv, vb[(size_t)s * step], acc);
   out[(size_t)row * hd + d] = acc;
 }
 
@@ -967,8 +1091,12 @@ void launch_silu_quant(float *gate, const float *up, int m, int n, int ld, int g
     launch_silu_quant_t<128>(gate, up, m, n, ld, q_split, q_nat, scales, sums, s, nullptr);
 }
 
+// Floats per score row: the positions, then a slot for the softmax's
+// 1/sum, rounded up to a multiple of 4 (16-byte rows).
+static int score_stride(int nmax) { return (nmax + 4) & ~3; }
+
 size_t attention_scores_floats(int m, int nh, int ctx) {
-  return (size_t)std::min(m, kAttnTokens) * nh * (size_t)((ctx + 3) & ~3);
+  return (size_t)std::min(m, kAttnTokens) * nh * (size_t)score_stride(ctx);
 }
 
 static int g_pv_spin = kPvSpin;
@@ -986,7 +1114,7 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     // capacity, capped at the longest context a forward accepts (so the
     // register-resident softmax always applies).
     const int nmax = st ? std::min(cap, kMaxAttnPositions) : p0 + mt;
-    const int sstride = (nmax + 3) & ~3;
+    const int sstride = score_stride(nmax);
     const float *qt = q + (size_t)t0 * q_ld;
     float *ot = out + (size_t)t0 * nh * hd;
     if (stages & 1) launch_scores(qt, q_ld, kc, cap, p0, mt, nh, nkv, hd, scale, scores, sstride, nmax, st, s);
@@ -997,18 +1125,25 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
       sm_configured = smem;
     }
     if (!(stages & 2)) {
+    } else if (nmax <= 512 * 16) {
+      // Chains from registers (k_softmax_c): the chain-major rows hold
+      // 64 NB steps each.
+      const dim3 g(nh, mt);
+      auto go = [&](auto kern, int) {
+        hipLaunchKernelGGL(kern, g, dim3(512), 0, s, scores, p0, nh, sstride, st);
+      };
+      if (nmax <= 512 * 2)
+        go(k_softmax_c<2>, 2);
+      else if (nmax <= 512 * 4)
+        go(k_softmax_c<4>, 4);
+      else if (nmax <= 512 * 8)
+        go(k_softmax_c<8>, 8);
+      else
+        go(k_softmax_c<16>, 16);
     } else if (nmax <= 512 * 32) {
       const int cstr = softmax_r_stride(nmax);
       const size_t rsm = sizeof(float) * 8 * (size_t)cstr;
-      const dim3 g(nh, mt);
-      if (nmax <= 512 * 4)
-        hipLaunchKernelGGL(k_softmax_r<4>, g, dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
-      else if (nmax <= 512 * 8)
-        hipLaunchKernelGGL(k_softmax_r<8>, g, dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
-      else if (nmax <= 512 * 16)
-        hipLaunchKernelGGL(k_softmax_r<16>, g, dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
-      else
-        hipLaunchKernelGGL(k_softmax_r<32>, g, dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
+      hipLaunchKernelGGL(k_softmax_r<32>, dim3(nh, mt), dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
     } else {
       hipLaunchKernelGGL(k_softmax, dim3(nh, mt), dim3(256), smem, s, scores, p0, nh, sstride, st);
     }
