@@ -182,15 +182,18 @@ template <int GS, int P>
 __device__ __forceinline__ void rmsnorm_regs_load(const float *__restrict__ row, const float *__restrict__ w,
                                                   int n, float (&xr)[P][GS / 8], float (&wr)[P][GS / 8]) {
   const int tid = threadIdx.x, groups = n / GS;
+  // The row first: the sum of squares waits only for it.
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int g = min(p * 32 + tid / 8, groups - 1);
 #pragma unroll
-    for (int c = 0; c < GS / 8; ++c) {
-      const int col = g * GS + 8 * c + (tid & 7);
-      xr[p][c] = row[col];
-      wr[p][c] = w[col];
-    }
+    for (int c = 0; c < GS / 8; ++c) xr[p][c] = row[g * GS + 8 * c + (tid & 7)];
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int g = min(p * 32 + tid / 8, groups - 1);
+#pragma unroll
+    for (int c = 0; c < GS / 8; ++c) wr[p][c] = w[g * GS + 8 * c + (tid & 7)];
   }
 }
 
@@ -229,9 +232,51 @@ __device__ __forceinline__ void quant_regs(const float (&xr)[P][GS / 8], int n, 
 __host__ __device__ constexpr int rms_t_stride(int n) { return 64 * ((n / 16 + 1 - 4 + 63) / 64) + 4; }
 __host__ __device__ constexpr int rms_scratch_floats(int n) { return 16 * rms_t_stride(n); }
 
+// The 16 sum-of-squares chains of a row of n = 1024 K elements (chains of
+// 64 K, no trailing 8-block) from registers, in the first wave: lane 4c + q
+// holds segment q (16 K elements) of chain c; phase q runs every lane's
+// segment as one FMA chain (only the segment-q lanes carry a live chain),
+// then DPP row_shr:1 moves each chain to its next segment's lane, so no LDS
+// read sits between the dependent FMAs.  Returns hsum8(sq0 + sq1) on every
+// lane of the wave.
+template <int K>
+__device__ __forceinline__ float rms_sumsq_regs(const float *xt, int stride) {
+  constexpr int SEG = 16 * K;
+  const int tid = threadIdx.x, c = tid >> 2, q = tid & 3;
+  const float4 *src = reinterpret_cast<const float4 *>(xt + c * stride + SEG * q);
+  float4 r[SEG / 4];
+#pragma unroll
+  for (int g = 0; g < SEG / 4; ++g) r[g] = src[g];
+  float a = 0.0f;
+#pragma unroll
+  for (int ph = 0; ph < 4; ++ph) {
+#pragma unroll
+    for (int g = 0; g < SEG / 4; ++g) {
+      a = __fmaf_rn(r[g].x, r[g].x, a);
+      a = __fmaf_rn(r[g].y, r[g].y, a);
+      a = __fmaf_rn(r[g].z, r[g].z, a);
+      a = __fmaf_rn(r[g].w, r[g].w, a);
+    }
+    if (ph < 3) {
+      const int ai = __float_as_int(a);
+      const float moved = __int_as_float(__builtin_amdgcn_update_dpp(ai, ai, 0x111, 0xF, 0xF, false));
+      a = q == ph + 1 ? moved : a;
+    }
+  }
+  float ch[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) ch[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 4 * k + 3));
+  float s[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s[j] = ch[j] + ch[8 + j];
+  return ((s[0] + s[4]) + (s[1] + s[5])) + ((s[2] + s[6]) + (s[3] + s[7]));
+}
+
 // inv of rms_norm_avx2 from the chain-major scratch (all 256 threads call;
-// every thread gets inv).  Each chain lane streams its row with 16-byte
+// every thread gets inv).  Rows of 1024 K elements (K <= P) take
+// rms_sumsq_regs; otherwise each chain lane streams its row with 16-byte
 // reads kept 32 elements ahead of its FMA chain.
+template <int P>
 __device__ __forceinline__ float rmsnorm_inv_t(const float *xt, int n, float eps) {
   __shared__ float chains[16];
   __shared__ float inv_sh;
@@ -239,6 +284,19 @@ __device__ __forceinline__ float rmsnorm_inv_t(const float *xt, int n, float eps
   const int c16 = (n / 8) / 2;
   const bool extra8 = 16 * c16 + 8 <= n;
   const int stride = rms_t_stride(n);
+  if (n % 1024 == 0 && n <= 1024 * P && n <= 4096) {
+    if (tid < 64) {
+      const int k = n / 1024;
+      const float sum = k == 1 ? rms_sumsq_regs<1>(xt, stride)
+                      : k == 2 ? rms_sumsq_regs<2>(xt, stride)
+                      : k == 3 ? rms_sumsq_regs<3>(xt, stride)
+                               : rms_sumsq_regs<4>(xt, stride);
+      // Correctly rounded sqrt and divide (the reference's sqrtss / divss).
+      if (tid == 0) inv_sh = 1.0f / __builtin_sqrtf(sum / (float)n + eps);
+    }
+    __syncthreads();
+    return inv_sh;
+  }
   if (tid < 16) {
     const float *row = xt + tid * stride;
     const int len = c16 + ((tid < 8 && extra8) ? 1 : 0);
@@ -306,7 +364,7 @@ __device__ __forceinline__ void rmsnorm_quant_regs(const float (&xr)[P][GS / 8],
     }
   }
   __syncthreads();
-  const float inv = rmsnorm_inv_t(xs, n, eps);
+  const float inv = rmsnorm_inv_t<P>(xs, n, eps);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int g = p * 32 + tid / 8;
