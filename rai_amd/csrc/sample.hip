@@ -138,8 +138,11 @@ __device__ float seq_sum(const float *p, int n) {
 }
 
 // First i with r < p[0] + ... + p[i] (f32, index order); -1 if none.  Each
-// 64-element block's running sums land in lane k (off the chain), one
-// ballot finds the first hit.
+// 64-element block runs the chain alone; the values are >= +0, so the sums
+// never decrease and a block holds the first hit only if its last sum is
+// not <= r (a NaN sum also replays).  That block is replayed from its start
+// with the running sums landing in lane k (off the chain), and one ballot
+// finds the first hit.
 __device__ int seq_search(const float *p, int n, float r) {
   __shared__ __align__(16) float buf[kStage];
   __shared__ int res;
@@ -156,17 +159,25 @@ __device__ int seq_search(const float *p, int n, float r) {
         f4v v[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) v[u] = *reinterpret_cast<const f4v *>(&buf[i + 4 * u]);
-        float pref = 0.0f;
+        const float cstart = c;
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
 #pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            c = c + v[u][w];
-            pref = lane == 4 * u + w ? c : pref;
-          }
+          for (int w = 0; w < 4; ++w) c = c + v[u][w];
         }
-        const uint64_t hit = __ballot(r < pref && i + lane < cn);
-        if (hit) found = c0 + i + __ffsll((unsigned long long)hit) - 1;
+        if (!(c <= r)) {
+          float cc = cstart, pref = 0.0f;
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              cc = cc + v[u][w];
+              pref = lane == 4 * u + w ? cc : pref;
+            }
+          }
+          const uint64_t hit = __ballot(r < pref && i + lane < cn);
+          if (hit) found = c0 + i + __ffsll((unsigned long long)hit) - 1;
+        }
       }
     }
     if (threadIdx.x == 0) res = found;
@@ -209,6 +220,8 @@ __device__ double seq_sum_resid(const float *pa, const float *pq, int d, int n) 
 }
 
 // First i with (residual[0] + ... + residual[i]) >= u (f64); n - 1 if none.
+// As seq_search: the chain alone per 64-element block, the block whose last
+// sum is not < u replayed for the first hit.
 __device__ int seq_search_resid(const float *pa, const float *pq, int d, int n, double u) {
   __shared__ __align__(16) double buf[kStage];
   __shared__ int res;
@@ -222,20 +235,31 @@ __device__ int seq_search_resid(const float *pa, const float *pq, int d, int n, 
     __syncthreads();
     if (threadIdx.x < 64) {
       for (int i = 0; i < cn && found < 0; i += 64) {
-        double pref = 0.0;
+        const double cstart = c;
 #pragma unroll
         for (int sb = 0; sb < 4; ++sb) {
           double v[16];
 #pragma unroll
           for (int k = 0; k < 16; ++k) v[k] = buf[i + 16 * sb + k];
 #pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            c = c + v[k];
-            pref = lane == 16 * sb + k ? c : pref;
-          }
+          for (int k = 0; k < 16; ++k) c = c + v[k];
         }
-        const uint64_t hit = __ballot(pref >= u && i + lane < cn);
-        if (hit) found = c0 + i + __ffsll((unsigned long long)hit) - 1;
+        if (!(c < u)) {
+          double cc = cstart, pref = 0.0;
+#pragma unroll
+          for (int sb = 0; sb < 4; ++sb) {
+            double v[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = buf[i + 16 * sb + k];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+              cc = cc + v[k];
+              pref = lane == 16 * sb + k ? cc : pref;
+            }
+          }
+          const uint64_t hit = __ballot(pref >= u && i + lane < cn);
+          if (hit) found = c0 + i + __ffsll((unsigned long long)hit) - 1;
+        }
       }
     }
     if (threadIdx.x == 0) res = found;
