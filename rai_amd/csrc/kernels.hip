@@ -1223,6 +1223,54 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_logits(const float *_
   if (tid < ne) logits[(size_t)t * experts + e0 + tid] = s;
 }
 
+// Router logits with the chains in registers, for hidden = 16 S: one wave
+// per (token, 4 experts); the 16 lanes of DPP row c hold expert e0 + c's
+// chain, lane q of the row the products fl(router[e][i] * x[i]) of columns
+// [S q, S q + S) in registers.  Phase q adds every lane's S products in
+// column order (only lane q of each row carries the live chain), then DPP
+// row_shr:1 moves each chain to lane q + 1 of its row, so the dot from -0.0
+// is one sequence of dependent adds with no memory access between them;
+// lane 15 of each row ends with its expert's logit.
+template <int S>
+__global__ __launch_bounds__(64) void k_router_logits_r(const float *__restrict__ x,
+                                                        const float *__restrict__ router, int experts,
+                                                        float *__restrict__ logits) {
+  constexpr int hidden = 16 * S;
+  const int t = blockIdx.x, lane = threadIdx.x, c = lane >> 4, q = lane & 15;
+  const int e = min((int)blockIdx.y * 4 + c, experts - 1);
+  const float4 *rr = reinterpret_cast<const float4 *>(router + (size_t)e * hidden + S * q);
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)t * hidden + S * q);
+  float p[S];
+#pragma unroll
+  for (int k = 0; k < S / 32; ++k) {
+    float4 rv[8], xv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      rv[u] = rr[8 * k + u];
+      xv[u] = xr[8 * k + u];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      p[32 * k + 4 * u] = rv[u].x * xv[u].x;
+      p[32 * k + 4 * u + 1] = rv[u].y * xv[u].y;
+      p[32 * k + 4 * u + 2] = rv[u].z * xv[u].z;
+      p[32 * k + 4 * u + 3] = rv[u].w * xv[u].w;
+    }
+  }
+  float acc = -0.0f;
+#pragma unroll 1
+  for (int ph = 0; ph < 16; ++ph) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) acc = acc + p[i];
+    if (ph < 15) {
+      const int ai = __float_as_int(acc);
+      const float moved = __int_as_float(__builtin_amdgcn_update_dpp(ai, ai, 0x111, 0xF, 0xF, false));
+      acc = q == ph + 1 ? moved : acc;
+    }
+  }
+  if (q == 15 && (int)blockIdx.y * 4 + c < experts) logits[(size_t)t * experts + blockIdx.y * 4 + c] = acc;
+}
+
 // route_experts (layers.rs:1808-1870) after the logits: softmax over all
 // experts (glibc expf, the sum as one chain in expert order), then top-k by
 // selection (strict >, so the lowest index wins a tie), optional
@@ -1478,8 +1526,16 @@ void launch_accept(const uint32_t *am, uint32_t *ctx, int len, int start, int nd
 
 void launch_router(const float *x, const float *router, int m, int hidden, int experts, int topk,
                    int norm_topk, int *sel, float *wts, float *logits, hipStream_t s) {
-  hipLaunchKernelGGL(k_router_logits, dim3(m, (experts + kRouterEpb - 1) / kRouterEpb), dim3(kRouterThreads), 0, s,
-                     x, router, hidden, experts, logits);
+  const dim3 g4(m, (experts + 3) / 4);
+  if (hidden == 16 * 128)
+    hipLaunchKernelGGL(k_router_logits_r<128>, g4, dim3(64), 0, s, x, router, experts, logits);
+  else if (hidden == 16 * 64)
+    hipLaunchKernelGGL(k_router_logits_r<64>, g4, dim3(64), 0, s, x, router, experts, logits);
+  else if (hidden == 16 * 32)
+    hipLaunchKernelGGL(k_router_logits_r<32>, g4, dim3(64), 0, s, x, router, experts, logits);
+  else
+    hipLaunchKernelGGL(k_router_logits, dim3(m, (experts + kRouterEpb - 1) / kRouterEpb), dim3(kRouterThreads), 0,
+                       s, x, router, hidden, experts, logits);
   hipLaunchKernelGGL(k_router, dim3(m), dim3(1024), sizeof(float) * ((experts + 3) & ~3), s, logits, experts, topk,
                      norm_topk, sel, wts);
 }
