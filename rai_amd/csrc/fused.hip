@@ -1170,6 +1170,10 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
         launch_pv_flag<16, 16, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 2)
         launch_pv_flag<32, 2, 128, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
+      else if (mt > 2)
+        // One query head per kv head: three tokens per block share each V
+        // tile (one token per block streams V once per token).
+        launch_pv_flag<64, 1, 64, 3, 5>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else
         launch_pv_flag<64, 1, 64, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
     } else if (vstride > 0) {
