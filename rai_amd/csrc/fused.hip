@@ -566,24 +566,6 @@ __global__ __launch_bounds__(512) void k_softmax_r(float *__restrict__ S, int po
 // 4 mod 64.
 static int softmax_r_stride(int nmax) { return (((nmax + 7) / 8 + 63) & ~63) + 4; }
 
-// Maximum of a wave: DPP moves within rows of 16 lanes (xor 1, xor 2, half
-// mirror, mirror), then the four row maxima by lane reads.
-template <int CTRL>
-__device__ __forceinline__ float max_dpp(float x) {
-  const int xi = __float_as_int(x);
-  return fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(xi, xi, CTRL, 0xF, 0xF, false)));
-}
-
-__device__ __forceinline__ float wave_max_dpp(float x) {
-  x = max_dpp<0xB1>(x);   // quad_perm [1, 0, 3, 2]
-  x = max_dpp<0x4E>(x);   // quad_perm [2, 3, 0, 1]
-  x = max_dpp<0x141>(x);  // row_half_mirror
-  x = max_dpp<0x140>(x);  // row_mirror
-  const int xi = __float_as_int(x);
-  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(xi, 0)), __int_as_float(__builtin_amdgcn_readlane(xi, 16))),
-               fmaxf(__int_as_float(__builtin_amdgcn_readlane(xi, 32)), __int_as_float(__builtin_amdgcn_readlane(xi, 48))));
-}
-
 // The softmax of k_softmax_r with the eight sum chains run from registers.
 // Load, maximum and exponentials as there: every position's Schraudolph
 // exponential (positions past the chains give 0), stored to the row and

@@ -1271,6 +1271,50 @@ __global__ __launch_bounds__(64) void k_router_logits_r(const float *__restrict_
   if (q == 15 && (int)blockIdx.y * 4 + c < experts) logits[(size_t)t * experts + blockIdx.y * 4 + c] = acc;
 }
 
+// route_experts for at most 64 experts, one wave per token, expert e on
+// lane e: the maximum by DPP moves, glibc expf, the sum as one chain in
+// expert order (lane reads), the division; then each top-k pick is the
+// wave maximum over the untaken finite probabilities and the lowest lane
+// holding it (a ballot), which is k_router's strict-> scan with the lowest
+// index winning a tie; NaN probabilities are never picked.
+__global__ __launch_bounds__(64) void k_router64(const float *__restrict__ logits, int experts, int topk,
+                                                 int norm_topk, int *__restrict__ sel, float *__restrict__ wts) {
+  const int t = blockIdx.x, lane = threadIdx.x;
+  const bool live = lane < experts;
+  const float lg = live ? logits[(size_t)t * experts + lane] : -INFINITY;
+  const float mx = wave_max_dpp(lg);
+  const float ex = live ? rai_exact::expf_glibc(lg - mx) : 0.0f;
+  const int exi = __float_as_int(ex);
+  float sum = 0.0f;
+  for (int e = 0; e < experts; ++e) sum = sum + __int_as_float(__builtin_amdgcn_readlane(exi, e));
+  const float pr = __fdiv_exact(ex, sum);
+  bool taken = false;
+  float total = -0.0f;
+  int cnt = 0;
+  for (int k = 0; k < topk; ++k) {
+    const float v = (live && !taken && pr > -INFINITY) ? pr : -INFINITY;
+    const float bv = wave_max_dpp(v);
+    if (!(bv > -INFINITY)) break;
+    const uint64_t hit = __ballot(v == bv && v > -INFINITY);
+    const int best = __ffsll((unsigned long long)hit) - 1;
+    if (lane == best) taken = true;
+    if (lane == 0) {
+      sel[t * topk + cnt] = best;
+      wts[t * topk + cnt] = bv;
+    }
+    total = total + bv;
+    ++cnt;
+  }
+  if (lane == 0) {
+    for (int k = cnt; k < topk; ++k) {
+      sel[t * topk + k] = -1;
+      wts[t * topk + k] = 0.0f;
+    }
+    if (norm_topk && total > 0.0f)
+      for (int k = 0; k < cnt; ++k) wts[t * topk + k] = __fdiv_exact(wts[t * topk + k], total);
+  }
+}
+
 // route_experts (layers.rs:1808-1870) after the logits: softmax over all
 // experts (glibc expf, the sum as one chain in expert order), then top-k by
 // selection (strict >, so the lowest index wins a tie), optional
@@ -1536,8 +1580,11 @@ void launch_router(const float *x, const float *router, int m, int hidden, int e
   else
     hipLaunchKernelGGL(k_router_logits, dim3(m, (experts + kRouterEpb - 1) / kRouterEpb), dim3(kRouterThreads), 0,
                        s, x, router, hidden, experts, logits);
-  hipLaunchKernelGGL(k_router, dim3(m), dim3(1024), sizeof(float) * ((experts + 3) & ~3), s, logits, experts, topk,
-                     norm_topk, sel, wts);
+  if (experts <= 64)
+    hipLaunchKernelGGL(k_router64, dim3(m), dim3(64), 0, s, logits, experts, topk, norm_topk, sel, wts);
+  else
+    hipLaunchKernelGGL(k_router, dim3(m), dim3(1024), sizeof(float) * ((experts + 3) & ~3), s, logits, experts,
+                       topk, norm_topk, sel, wts);
 }
 
 void launch_moe_accumulate(float *out, const float *eo, const float *w, int m, int n,

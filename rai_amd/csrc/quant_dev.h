@@ -224,6 +224,24 @@ __device__ __forceinline__ void quant_regs(const float (&xr)[P][GS / 8], int n, 
   }
 }
 
+// Maximum of a wave: DPP moves within rows of 16 lanes (xor 1, xor 2, half
+// mirror, mirror), then the four row maxima by lane reads.
+template <int CTRL>
+__device__ __forceinline__ float max_dpp(float x) {
+  const int xi = __float_as_int(x);
+  return fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(xi, xi, CTRL, 0xF, 0xF, false)));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  x = max_dpp<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+  x = max_dpp<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+  x = max_dpp<0x141>(x);  // row_half_mirror
+  x = max_dpp<0x140>(x);  // row_mirror
+  const int xi = __float_as_int(x);
+  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(xi, 0)), __int_as_float(__builtin_amdgcn_readlane(xi, 16))),
+               fmaxf(__int_as_float(__builtin_amdgcn_readlane(xi, 32)), __int_as_float(__builtin_amdgcn_readlane(xi, 48))));
+}
+
 // Chain-major scratch for rms_norm_avx2's sum of squares: chain c (0..15)
 // takes the elements c, c + 16, c + 32, ... (the trailing 8-block of an
 // odd n / 8 goes to chains 0..7 as their last element), so row c of the
