@@ -197,13 +197,63 @@ __global__ __launch_bounds__(256) void k_quant(const float *__restrict__ x, int 
 
 constexpr int kScoreTile = 64;  // positions per score block (one per lane)
 
+// acc = fma(q, k, acc) with q taken from lane n of the lane's row of 16
+// (DPP row_newbcast): a wave-uniform operand held once per 16 values.
+template <int N>
+__device__ __forceinline__ float fma_bcast(float q, float k, float acc) {
+  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(q), "v"(k), "n"(N));
+  return acc;
+}
+
+__device__ __forceinline__ float fma_bcast_n(int n, float q, float k, float acc) {
+  switch (n) {
+    case 0: return fma_bcast<0>(q, k, acc);
+    case 1: return fma_bcast<1>(q, k, acc);
+    case 2: return fma_bcast<2>(q, k, acc);
+    case 3: return fma_bcast<3>(q, k, acc);
+    case 4: return fma_bcast<4>(q, k, acc);
+    case 5: return fma_bcast<5>(q, k, acc);
+    case 6: return fma_bcast<6>(q, k, acc);
+    case 7: return fma_bcast<7>(q, k, acc);
+    case 8: return fma_bcast<8>(q, k, acc);
+    case 9: return fma_bcast<9>(q, k, acc);
+    case 10: return fma_bcast<10>(q, k, acc);
+    case 11: return fma_bcast<11>(q, k, acc);
+    case 12: return fma_bcast<12>(q, k, acc);
+    case 13: return fma_bcast<13>(q, k, acc);
+    case 14: return fma_bcast<14>(q, k, acc);
+    default: return fma_bcast<15>(q, k, acc);
+  }
+}
+
+typedef float sf4 __attribute__((ext_vector_type(4)));
+
+// One 8-column chunk C of the score chains of PB pairs (fully expanded so
+// that the query register and the broadcast lane are compile-time).
+template <int HD, int PB, int C>
+__device__ __forceinline__ void score_chunk(const sf4 *kr4, const float (&qb)[PB][HD / 16], float (&a)[PB][8]) {
+  const sf4 k0 = kr4[2 * C], k1 = kr4[2 * C + 1];
+  const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+  for (int p = 0; p < PB; ++p)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[p][i] = fma_bcast_n((8 * C + i) & 15, qb[p][C >> 1], kv[i], a[p][i]);
+}
+
+template <int HD, int PB, int... Cs>
+__device__ __forceinline__ void score_chunks(std::integer_sequence<int, Cs...>, const sf4 *kr4,
+                                             const float (&qb)[PB][HD / 16], float (&a)[PB][8]) {
+  (score_chunk<HD, PB, Cs>(kr4, qb, a), ...);
+}
+
 // grid (ceil(nmax / 64), nkv), 256 threads.  The block stages its 64 key
 // rows in LDS; each wave takes (token, head) pairs of the kv group, lane =
 // position.  HD > 0 (compile-time head_dim): key rows HD + 4 floats apart
 // (16-byte reads, conflict-free per 16 lanes), followed by the query rows of
-// the block's pairs (pair pi = (t - tfirst) * G + g at row pi, read by
-// broadcast); a wave runs PB of its pairs at once, head-dim chunk outer, so
-// each key value read serves PB dot products (pairs past the end repeat the
+// the block's pairs (pair pi = (t - tfirst) * G + g at row pi, each wave's
+// pairs read into registers 16 values per register and taken by the FMAs
+// through DPP row_newbcast); a wave runs PB of its pairs at once, head-dim
+// chunk outer, so each key value read serves PB dot products (pairs past the end repeat the
 // last one and store nothing).  HD = 0: rows hd + 1 floats apart, queries
 // from global memory, one pair at a time.  With a step record the token
 // positions start at st[0] + toff.
@@ -257,31 +307,23 @@ __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int
     const f4 *kr4 = reinterpret_cast<const f4 *>(ks + lane * kstride);
     const int npw = (pairs - wave + 3) / 4;  // this wave's pairs: wave, wave + 4, ...
     for (int b0 = 0; b0 < npw; b0 += PB) {
-      const f4 *ql[PB];
+      // The pairs' query rows, 16 values per register: lane l holds
+      // q[16 m + l % 16] in qb[p][m]; the FMAs take q[e] from lane e % 16
+      // of their row (one 4-byte LDS read per 16 values instead of a
+      // broadcast 16-byte read per 4).
+      float qb[PB][HD / 16];
 #pragma unroll
-      for (int p = 0; p < PB; ++p) ql[p] = lq + (wave + 4 * min(b0 + p, npw - 1)) * (HD / 4);
+      for (int p = 0; p < PB; ++p) {
+        const float *qrow = reinterpret_cast<const float *>(lq + (wave + 4 * min(b0 + p, npw - 1)) * (HD / 4));
+#pragma unroll
+        for (int mm = 0; mm < HD / 16; ++mm) qb[p][mm] = qrow[16 * mm + (lane & 15)];
+      }
       float a[PB][8];
 #pragma unroll
       for (int p = 0; p < PB; ++p)
 #pragma unroll
         for (int i = 0; i < 8; ++i) a[p][i] = 0.0f;
-#pragma unroll 4
-      for (int c = 0; c < HD / 8; ++c) {
-        const f4 k0 = kr4[2 * c], k1 = kr4[2 * c + 1];
-#pragma unroll
-        for (int p = 0; p < PB; ++p) {
-          const f4 q0 = ql[p][2 * c];
-          const f4 q1 = ql[p][2 * c + 1];
-          a[p][0] = __fmaf_rn(q0.x, k0.x, a[p][0]);
-          a[p][1] = __fmaf_rn(q0.y, k0.y, a[p][1]);
-          a[p][2] = __fmaf_rn(q0.z, k0.z, a[p][2]);
-          a[p][3] = __fmaf_rn(q0.w, k0.w, a[p][3]);
-          a[p][4] = __fmaf_rn(q1.x, k1.x, a[p][4]);
-          a[p][5] = __fmaf_rn(q1.y, k1.y, a[p][5]);
-          a[p][6] = __fmaf_rn(q1.z, k1.z, a[p][6]);
-          a[p][7] = __fmaf_rn(q1.w, k1.w, a[p][7]);
-        }
-      }
+      score_chunks<HD, PB>(std::make_integer_sequence<int, HD / 8>{}, reinterpret_cast<const sf4 *>(kr4), qb, a);
 #pragma unroll
       for (int p = 0; p < PB; ++p) {
         const int pi = wave + 4 * (b0 + p);
