@@ -203,3 +203,36 @@ def test_moe_device_path_bit_exact(rai, ora, gs, norm_topk):
     prompt = copy_heavy_prompt(80, 500, seed=gs)
     drafted, _ = _lookup_steps_match(rai, ora, gm, om, prompt, 16, 256)
     assert drafted > 0
+
+
+@pytest.mark.parametrize("norm_topk", [False, True])
+def test_router_exact_ties_pick_the_lowest_index(rai, ora, norm_topk):
+    """route_experts' tie rule (layers.rs:1808-1870: strict >, the lowest
+    index wins) on the device router: every odd router row is a copy of the
+    even row before it, so every logit and probability comes in exact pairs,
+    and with top-3 the third pick splits a pair.  Hidden 512 takes the
+    register-chain logits kernel.  Hidden states and logits bit-exact for 1
+    and 9 tokens (the combine sums the picks in slot order, so a pick in the
+    wrong order changes the bits)."""
+    from textbook_model import TextbookModel
+
+    img = bytearray(rai.synth_model(512, 1, 4, 4, 64, 512, 500, 256, group_size=32, num_experts=16,
+                                    experts_per_token=3, norm_topk_prob=norm_topk, seed=11))
+    router = TextbookModel(bytes(img)).layers[0]["router"].astype(np.float32)
+    off = bytes(img).find(router.tobytes())
+    assert off > 0
+    tied = router.copy()
+    tied[1::2] = tied[0::2]
+    img[off:off + tied.nbytes] = tied.tobytes()
+    img = bytes(img)
+    gm = rai.RaiModel.from_bytes(img)
+    om = ora.Model(img, 0)
+    rng = np.random.default_rng(3)
+    toks = rng.integers(0, 500, size=10)
+    hs = np.stack([om.embed_token(int(t)) for t in toks])
+    gkv, okv = gm.create_kv_cache(64), om.create_kv(64)
+    for a, b in ((0, 1), (1, 10)):
+        gh = gm.forward_batch(hs[a:b], np.arange(a, b), gkv)
+        oh = om.forward_batch(hs[a:b], np.arange(a, b), okv)
+        assert np.array_equal(_bits(gh), _bits(oh)), (a, b)
+    assert np.array_equal(_bits(gm.hidden_to_logits_batch(gh, 9)), _bits(om.hidden_to_logits_batch(oh, 9)))
