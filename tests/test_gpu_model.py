@@ -124,6 +124,29 @@ def test_multi_token_attention_batches_bit_exact(rai, ora):
         p += n
 
 
+def test_hidden_3072_norm_chains_bit_exact(rai, ora):
+    """Hidden 3072: the RMSNorm sum of squares runs its 16 chains as three
+    register segments of 48 elements per lane (rows of 1024, 2048 and 4096
+    take one, two and four), in the one-token GEMV prologue and the
+    several-token norm+quantize kernel; forwards of 5, 1 and 9 tokens and
+    their logits against the oracle, bit for bit."""
+    img = _small_synth(rai, hidden_size=3072, num_layers=1, num_heads=24, num_kv_heads=8, head_dim=128,
+                       intermediate_size=1024, vocab_size=500, max_context=64, seed=31)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    toks = _token_sequence(om.cfg.vocab_size, 15)
+    hs = np.stack([om.embed_token(t) for t in toks])
+    okv, gkv = om.create_kv(64), gm.create_kv_cache(64)
+    p = 0
+    for n in (5, 1, 9):
+        oh = om.forward_batch(hs[p:p + n], np.arange(p, p + n), okv)
+        gh = gm.forward_batch(hs[p:p + n], np.arange(p, p + n), gkv)
+        assert np.array_equal(_bits(gh), _bits(oh)), (p, n)
+        assert np.array_equal(_bits(gm.hidden_to_logits_batch(gh, n)),
+                              _bits(om.hidden_to_logits_batch(oh, n))), (p, n)
+        p += n
+
+
 def test_single_token_attention_long_context_bit_exact(rai, ora):
     """One-token steps after 1100 positions with four query heads per kv
     head and head_dim 128: the softmax's sum chains past their read-ahead,
