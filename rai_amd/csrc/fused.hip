@@ -1173,7 +1173,7 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     }
     const size_t total = (size_t)mt * nh * hd;
     const int G = nh / nkv;
-    const int DL = (G == 1) ? 64 : (G == 2) ? 32 : 16;
+    const int DL = (G == 2) ? 32 : 16;
     const bool stream = vstride > 0 && vstride % 64 == 0 &&
                         (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && hd % DL == 0;
     if (!(stages & 4)) {
@@ -1194,12 +1194,15 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
         launch_pv_flag<16, 16, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 2)
         launch_pv_flag<32, 2, 128, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
-      else if (mt > 2)
-        // One query head per kv head: three tokens per block share each V
-        // tile (one token per block streams V once per token).
-        launch_pv_flag<64, 1, 64, 3, 5>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
+      else if (mt > 4)
+        // One query head per kv head: 16-d slices, so a wave's four lane
+        // rows take four tokens of one head (eight tokens in two compute
+        // waves here) and a 256-position tile fits the loaders' registers
+        // (64-d slices needed 64-position tiles: 22.5 -> 15.1 us at nine
+        // tokens and 2100 positions, 19.1 -> 13.4 us at one).
+        launch_pv_flag<16, 1, 256, 8, 3>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else
-        launch_pv_flag<64, 1, 64, 1, 7>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
+        launch_pv_flag<16, 1, 256, 4, 2>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
     } else if (vstride > 0) {
       hipLaunchKernelGGL(k_pv_any<true>, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, scores,
                          vc, cap, vstride, p0, mt, nh, nkv, hd, sstride, ot, st);

@@ -185,10 +185,10 @@ def test_pv_head_groupings_bit_exact(rai, ora, nh, nkv, hd):
         assert np.array_equal(_bits(gh), _bits(oh)), (a, b)
 
 
-@pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 128), (16, 2, 64)])
+@pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 128), (16, 2, 64), (8, 8, 128)])
 def test_pv_long_context_through_kv_cache_bit_exact(rai, ora, nh, nkv, hd):
     """The production PV path (d-major V cache, LDS-flag tile hand-off) at
-    4352 and 8192 positions, four and eight query heads per kv head: a
+    4352 and 8192 positions, four, eight and one query heads per kv head: a
     one-token and a nine-token batch after each prefill, against the oracle
     bit for bit."""
     img = _small_synth(rai, hidden_size=1024, num_layers=1, num_heads=nh, num_kv_heads=nkv, head_dim=hd,
