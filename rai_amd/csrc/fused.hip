@@ -1179,15 +1179,17 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     if (!(stages & 4)) {
     } else if (stream) {
       // Tokens per block: one for one or two tokens (more blocks), three up
-      // to twelve (the verify batch), four beyond; loader waves measured on
-      // 4.35K positions with V streamed from HBM (four for one token, three
-      // for three).
+      // to twelve (the verify batch), four beyond; tile length and loader
+      // waves measured on 4.1K-4.35K positions with V streamed from HBM (one
+      // token: 512-position tiles and two loaders, 21.0 -> 20.0 us against
+      // 256 and four; the loaders' registers spill from 640 positions or four
+      // loaders at 512; three tokens: 256 and three).
       if (G == 4 && mt > 12)
         launch_pv_flag<16, 4, 128, 4, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 4 && mt > 2)
         launch_pv_flag<16, 4, 256, 3, 3>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 4)
-        launch_pv_flag<16, 4, 256, 1, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
+        launch_pv_flag<16, 4, 512, 1, 2>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 8)
         launch_pv_flag<16, 8, 256, 1, 6>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 16)
