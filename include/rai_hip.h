@@ -66,8 +66,8 @@ typedef struct rai_model_config {
 } rai_model_config;
 
 /* LookupConfig (lookup.rs:64-89).  temperature <= 1e-6 selects greedy
- * acceptance (argmax == draft), the T->0 limit of lookup.rs:359-403; the
- * sampled mode (T > 0) is not implemented in this build (RAI_E_UNSUPPORTED). */
+ * acceptance (argmax == draft), the T->0 limit of lookup.rs:359-403; above
+ * it the step samples exactly as the reference does. */
 typedef struct rai_lookup_config {
   size_t max_draft;   /* K */
   size_t max_ngram;
@@ -147,6 +147,12 @@ int rai_kv_read(const rai_kv *kv, size_t layer, size_t head, size_t pos, int whi
  * positions 0..npos (npos <= filled), e.g. to hand a decoder state to
  * another implementation. */
 int rai_kv_export(const rai_kv *kv, size_t layer, int which, float *out, size_t npos);
+/* KVCache::store (kv_cache.rs:143-173, 257-265) in bulk, the inverse of
+ * rai_kv_export: rows [kv_head][npos][head_dim] of one layer's K (which = 0)
+ * or V (1) become positions 0..npos, and the layer's watermark becomes npos
+ * (a state handed over from another implementation).  npos above the
+ * cache's positions fails with RAI_E_RANGE. */
+int rai_kv_import(rai_kv *kv, size_t layer, int which, const float *rows, size_t npos);
 
 /* ---------------------------------------------------------- forward pass -- */
 /* RaiModel::embed_token (model.rs:371-403). */
@@ -172,6 +178,25 @@ int rai_hidden_to_logits_batch(rai_model *model, const float *hiddens, float *lo
 int rai_w4a8_matmul_dev(float *out, const uint8_t *nibbles, const uint8_t *params,
                         const float *x, size_t rows, size_t cols, size_t m, size_t group_size,
                         void *stream);
+/* One quantized linear on the device: QuantizedLinear (format.rs:361-367)
+ * with device pointers to its nibbles [rows][cols/2] and params
+ * [rows][ceil(cols/group_size)] x (f16 scale, f16 zero). */
+typedef struct rai_qlinear {
+  const uint8_t *nibbles;
+  const uint8_t *params;
+  size_t rows, cols, group_size;
+} rai_qlinear;
+/* w4a8_fused_qkv (gemm.rs:1386-1557): one input row x [cols] quantized once
+ * and shared by the three projections; q_out [q.rows], k_out [k.rows],
+ * v_out [v.rows], each equal to w4a8_matvec of its projection.  Each
+ * projection is validated as w4a8_matvec's (RAI_E_SHAPE), and the three
+ * must agree on cols and group_size ("Q/K column mismatch" etc.,
+ * RAI_E_SHAPE).  Device pointers; synchronous on `stream`. */
+int rai_w4a8_fused_qkv_dev(float *q_out, float *k_out, float *v_out, const rai_qlinear *q,
+                           const rai_qlinear *k, const rai_qlinear *v, const float *x, void *stream);
+/* w4a8_fused_gate_up (gemm.rs:1559-1703): the same for gate and up. */
+int rai_w4a8_fused_gate_up_dev(float *gate_out, float *up_out, const rai_qlinear *gate,
+                               const rai_qlinear *up, const float *x, void *stream);
 /* Allocation-free variant of rai_w4a8_matmul_dev.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -78,6 +78,7 @@ def lib():
         "ora_kv_truncate": (c_int, [P, c_int]),
         "ora_kv_filled": (c_int, [P, c_int]),
         "ora_kv_read": (c_int, [P, c_int, c_int, c_int, c_int, P]),
+        "ora_kv_import": (c_int, [P, c_int, c_int, P, c_int]),
         "ora_route_experts": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P]),
         "ora_embed_token": (c_int, [P, c_int, P]),
         "ora_forward_from_hidden": (c_int, [P, P, P, c_int, c_int]),
@@ -351,6 +352,11 @@ class KVCache:
         out = np.zeros(head_dim, np.float32)
         _check(lib().ora_kv_read(self.h, layer, head, pos, 1, _ptr(out)))
         return out
+
+    def import_rows(self, layer: int, which: int, rows: np.ndarray) -> None:
+        """Set one layer's K (0) or V (1) rows [nkv][npos][head_dim]."""
+        r = f32(rows)
+        _check(lib().ora_kv_import(self.h, layer, which, _ptr(r), r.shape[1]))
 
     def __del__(self):
         try:

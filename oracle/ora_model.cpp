@@ -598,16 +598,22 @@ int ora_lookup_create(const ora_model *m, int max_ctx, ora_lookup **out) {
   });
 }
 void ora_lookup_free(ora_lookup *d) { delete d; }
+// KVCache::store (kv_cache.rs:143-173) for positions 0..npos of one layer at
+// once: rows [kv_head][npos][head_dim] of K (which = 0) or V (1); the
+// layer's watermark becomes npos.
+static void import_rows(KV &k, int layer, int which, const float *rows, int npos) {
+  if (layer < 0 || layer >= k.layers) fail("layer out of range");
+  if (npos < 0 || npos > k.cap) fail("positions exceed the cache");
+  std::vector<float> &dst = which == 0 ? k.k[layer] : k.v[layer];
+  for (int h = 0; h < k.nkv; ++h)
+    std::memcpy(&dst[(size_t)h * k.cap * k.hd], rows + (size_t)h * npos * k.hd, sizeof(float) * npos * k.hd);
+  k.filled[layer] = npos;
+}
+int ora_kv_import(ora_kv *kv, int layer, int which, const float *rows, int npos) {
+  ORA_TRY(import_rows(kv->kv, layer, which, rows, npos));
+}
 int ora_lookup_import_kv(ora_lookup *dd, int layer, int which, const float *rows, int npos) {
-  ORA_TRY({
-    KV &k = dd->d.kv;
-    if (layer < 0 || layer >= k.layers) fail("layer out of range");
-    if (npos < 0 || npos > k.cap) fail("positions exceed the cache");
-    std::vector<float> &dst = which == 0 ? k.k[layer] : k.v[layer];
-    for (int h = 0; h < k.nkv; ++h)
-      std::memcpy(&dst[(size_t)h * k.cap * k.hd], rows + (size_t)h * npos * k.hd, sizeof(float) * npos * k.hd);
-    k.filled[layer] = npos;
-  });
+  ORA_TRY(import_rows(dd->d.kv, layer, which, rows, npos));
 }
 int ora_lookup_kv_filled(const ora_lookup *d) { return d->d.kv.filled.at(0); }
 

@@ -118,6 +118,9 @@ int ora_kv_truncate(ora_kv *kv, int len);
 int ora_kv_filled(const ora_kv *kv, int layer);
 /* One cached K (which = 0) or V (which = 1) row [head_dim] (kv_cache.rs:179-204). */
 int ora_kv_read(const ora_kv *kv, int layer, int head, int pos, int which, float *out);
+/* Positions 0..npos of one layer's K (which = 0) or V (1) from rows
+ * [kv_head][npos][head_dim] (kv_cache.rs:143-173 in bulk); filled = npos. */
+int ora_kv_import(ora_kv *kv, int layer, int which, const float *rows, int npos);
 /* route_experts (layers.rs:1808-1870) for one token: experts[k] / weights[k]
  * for k < topk (-1 / 0 past the selection). */
 int ora_route_experts(const float *router, const float *x, int hidden, int num_experts, int topk,

@@ -33,6 +33,12 @@ class RaiError(RuntimeError):
         self.status = _STATUS.get(status, str(status))
 
 
+class QLinear(ctypes.Structure):
+    """rai_qlinear: QuantizedLinear (format.rs:361-367) with device pointers."""
+    _fields_ = [("nibbles", c_void_p), ("params", c_void_p), ("rows", c_size_t), ("cols", c_size_t),
+                ("group_size", c_size_t)]
+
+
 class ModelConfig(ctypes.Structure):
     _fields_ = [(n, c_uint32) for n in (
         "hidden_size", "num_layers", "num_heads", "num_kv_heads", "head_dim",
@@ -107,6 +113,8 @@ def lib():
         "rai_hidden_to_logits": (c_int, [P, P, P]),
         "rai_hidden_to_logits_batch": (c_int, [P, P, P, S]),
         "rai_w4a8_matmul_dev": (c_int, [P, P, P, P, S, S, S, S, P]),
+        "rai_w4a8_fused_qkv_dev": (c_int, [P, P, P, POINTER(QLinear), POINTER(QLinear), POINTER(QLinear), P, P]),
+        "rai_w4a8_fused_gate_up_dev": (c_int, [P, P, POINTER(QLinear), POINTER(QLinear), P, P]),
         "rai_w4a8_matmul_noalloc_dev": (c_int, [P, P, P, P, S, S, S, S, P]),
         "rai_w4a8_lane_sums_dev": (c_int, [P, P, P, S, S, S, S, P]),
         "rai_w4a8_matmul": (c_int, [P, P, P, P, S, S, S, S]),
@@ -139,6 +147,7 @@ def lib():
         "rai_lookup_decode": (c_int, [P, P, S, S, S, POINTER(_LookupConfig), P, S,
                                       POINTER(c_size_t), POINTER(_GenerateStats)]),
         "rai_kv_export": (c_int, [P, S, c_int, P, S]),
+        "rai_kv_import": (c_int, [P, S, c_int, P, S]),
         "rai_greedy_generate": (c_int, [P, P, S, S, P]),
         "rai_synth_model": (c_int, [POINTER(SynthConfig), c_uint64, c_char_p,
                                     POINTER(c_void_p), POINTER(c_size_t)]),
@@ -250,6 +259,33 @@ def w4a8_matmul(nibbles, params, x, rows: int, cols: int, num_tokens: int,
 def w4a8_matvec(nibbles, params, x, rows: int, cols: int, group_size: int) -> np.ndarray:
     """w4a8_matvec (gemm.rs:1336-1384)."""
     return w4a8_matmul(nibbles, params, x, rows, cols, 1, group_size)[0]
+
+
+def _fused(fn: str, projections, x) -> list[np.ndarray]:
+    """Upload each projection (nibbles, params, rows, cols, group_size) and
+    the input row, run the fused device entry point, return the outputs."""
+    keep, lins, outs = [], [], []
+    for nib, par, rows, cols, gs in projections:
+        dn = DeviceArray.from_host(np.ascontiguousarray(nib, np.uint8))
+        dp = DeviceArray.from_host(np.ascontiguousarray(par, np.uint8))
+        keep += [dn, dp]
+        lins.append(QLinear(dn.ptr, dp.ptr, rows, cols, gs))
+        outs.append(DeviceArray(4 * rows))
+    dx = DeviceArray.from_host(_f32(x))
+    args = [o.ptr for o in outs] + [ctypes.byref(q) for q in lins] + [dx.ptr, None]
+    _check(getattr(lib(), fn)(*args))
+    return [o.to_host(np.float32, p[2]) for o, p in zip(outs, projections)]
+
+
+def w4a8_fused_qkv(q, k, v, x) -> list[np.ndarray]:
+    """w4a8_fused_qkv (gemm.rs:1386-1557): q, k, v = (nibbles, params, rows,
+    cols, group_size) each; returns [q_out, k_out, v_out]."""
+    return _fused("rai_w4a8_fused_qkv_dev", [q, k, v], x)
+
+
+def w4a8_fused_gate_up(gate, up, x) -> list[np.ndarray]:
+    """w4a8_fused_gate_up (gemm.rs:1559-1703); returns [gate_out, up_out]."""
+    return _fused("rai_w4a8_fused_gate_up_dev", [gate, up], x)
 
 
 def attention_time(nh: int, nkv: int, hd: int, cap: int, pos: int, m: int, copies: int = 1,
@@ -547,6 +583,12 @@ class KVCache:
         out = np.zeros((num_kv_heads, npos, head_dim), np.float32)
         _check(lib().rai_kv_export(self.h, layer, which, _ptr(out), npos))
         return out
+
+    def import_rows(self, layer: int, which: int, rows: np.ndarray) -> None:
+        """Set one layer's K (which = 0) or V (1) rows [kv_head][npos][head_dim]
+        as positions 0..npos; the layer's watermark becomes npos."""
+        r = np.ascontiguousarray(rows, np.float32)
+        _check(lib().rai_kv_import(self.h, layer, which, _ptr(r), r.shape[1]))
 
     def __del__(self):
         try:

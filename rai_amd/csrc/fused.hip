@@ -441,84 +441,113 @@ void launch_scores(const float *q, int q_ld, const float *kc, int cap, int p0, i
                      sstride, st, 0);
 }
 
-__device__ __forceinline__ float block_max256(float v, float *red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  return v;
-}
+// The softmax of rows of any length (used past the register-resident
+// kernels' 16384 positions).  grid (nh, m), 512 threads.  The row stays in
+// global memory: one pass for the maximum, then chunks of kSoftLChunk
+// positions.  Waves 1..7 (448 threads, 8 positions each) turn a chunk's
+// scores into exponentials (Schraudolph on the 8-aligned body, expf on the
+// <= 7 tail positions), store them to the row and chain-major to LDS
+// (position p of the chunk at chain p % 8, step p / 8: 448 is a multiple of
+// 8, so a thread's positions all belong to chain tid % 8), while lanes 0..7
+// of wave 0 add the previous chunk's values into the eight chains in order
+// (acc_j = sum of e[8i + j], i ascending, from +0).  Two chunk buffers, one
+// block barrier per chunk.  Then hsum8 of the chains, the tail in order and
+// 1/sum into S[sstride - 1], as the other softmax kernels.
+constexpr int kSoftLFill = 448;                // filling threads (waves 1..7)
+constexpr int kSoftLChunk = kSoftLFill * 8;    // positions per chunk
+constexpr int kSoftLSteps = kSoftLChunk / 8;   // chain steps per chunk
+constexpr int kSoftLStr = kSoftLSteps + 4;     // LDS row stride (floats)
 
-// grid (nh, m), 256 threads; dynamic LDS holds the n exponentials.  Every
-// softmax kernel leaves the row's exponentials e_s in S[s] and 1/sum in
-// S[sstride - 1]; the PV kernels form p_s = e_s * (1/sum) (one rounding, as
-// the reference's normalising multiply) when they read the row.
-__global__ __launch_bounds__(256) void k_softmax(float *__restrict__ S, int pos0, int nh,
-                                                 int sstride, const int *__restrict__ st) {
-  extern __shared__ float e[];
+__global__ __launch_bounds__(512) void k_softmax_l(float *__restrict__ S, int pos0, int nh, int sstride,
+                                                   const int *__restrict__ st) {
+  __shared__ __align__(16) float ech[2][8 * kSoftLStr];
   __shared__ float red[8];
+  __shared__ float csum[8];
+  __shared__ float tail[8];
   if (st) pos0 = st[0];
-  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-  const int n = pos0 + t + 1;
-  const int n8 = n / 8;
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = pos0 + t + 1, n8 = n / 8, body = 8 * n8;
   float *row = S + ((size_t)t * nh + h) * sstride;
   float mx = -INFINITY;
-  for (int base = 0; base < n; base += 256 * 8) {
+  for (int base = 0; base < n; base += 512 * 8) {
     float v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int s = base + 256 * u + tid;
-      v[u] = s < n ? row[s] : -INFINITY;
+      const int p = base + 512 * u + tid;
+      v[u] = p < n ? row[p] : -INFINITY;
     }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mx = fmaxf(mx, v[u]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
+  const int nch = (n + kSoftLChunk - 1) / kSoftLChunk;
+  const int f = tid - 64;  // filling thread index (waves 1..7)
+  auto fill = [&](int c) {
+    const int c0 = c * kSoftLChunk;
+    float v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int s = base + 256 * u + tid;
-      if (s < n) e[s] = v[u];
-      mx = fmaxf(mx, v[u]);
+      const int p = c0 + kSoftLFill * u + f;
+      v[u] = p < n ? row[p] : 0.0f;
     }
-  }
-  mx = block_max256(mx, red);
-  for (int s = tid; s < n; s += 256) {
-    const float d = e[s] - mx;
-    e[s] = (s < n8 * 8) ? rai_exact::schraudolph(d) : rai_exact::expf_glibc(d);
-  }
-  __syncthreads();
-  if (tid < 8) {
-    // Chain j adds e[8i + j] for i = 0..n8-1 in order; loads run 16 ahead.
-    float acc = 0.0f;
-    int i = 0;
-    float bufA[16], bufB[16];
-    if (n8 >= 16) {
+    float *er = &ech[c & 1][(f & 7) * kSoftLStr + (f >> 3)];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) bufA[u] = e[(u)*8 + tid];
-    }
-    for (; i + 32 <= n8; i += 32) {
-#pragma unroll
-      for (int u = 0; u < 16; ++u) bufB[u] = e[(i + 16 + u) * 8 + tid];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) acc = acc + bufA[u];
-      if (i + 48 <= n8) {
-#pragma unroll
-        for (int u = 0; u < 16; ++u) bufA[u] = e[(i + 32 + u) * 8 + tid];
+    for (int u = 0; u < 8; ++u) {
+      const int p = c0 + kSoftLFill * u + f;
+      if (p < body) {
+        const float e = rai_exact::schraudolph(v[u] - mx);
+        er[(kSoftLFill / 8) * u] = e;
+        row[p] = e;
+      } else if (p < n) {
+        const float e = rai_exact::expf_glibc(v[u] - mx);
+        tail[p - body] = e;
+        row[p] = e;
       }
-#pragma unroll
-      for (int u = 0; u < 16; ++u) acc = acc + bufB[u];
     }
-    if (i + 16 <= n8) {
+  };
+  if (wave > 0) fill(0);
+  __syncthreads();
+  float acc = 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    if (wave > 0) {
+      if (c + 1 < nch) fill(c + 1);
+    } else if (tid < 8) {
+      const int cnt = min(kSoftLSteps, n8 - c * kSoftLSteps);  // chain steps in this chunk
+      const float *cr = &ech[c & 1][tid * kSoftLStr];
+      int i = 0;
+      if (cnt >= 32) {
+        float4 cur[8];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) acc = acc + bufA[u];
-      i += 16;
+        for (int u = 0; u < 8; ++u) cur[u] = reinterpret_cast<const float4 *>(cr)[u];
+        for (; i + 32 <= cnt; i += 32) {
+          float4 nxt[8];
+          const int nb = i + 64 <= cnt ? i + 32 : i;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) nxt[u] = reinterpret_cast<const float4 *>(cr + nb)[u];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            acc = acc + cur[u].x;
+            acc = acc + cur[u].y;
+            acc = acc + cur[u].z;
+            acc = acc + cur[u].w;
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+        }
+      }
+      for (; i < cnt; ++i) acc = acc + cr[i];
     }
-    for (; i < n8; ++i) acc = acc + e[i * 8 + tid];
-    red[tid] = acc;
+    __syncthreads();
   }
-  for (int s = tid; s < n; s += 256) row[s] = e[s];
+  if (tid < 8) csum[tid] = acc;
   __syncthreads();
   if (tid == 0) {
-    float sum = ((red[0] + red[4]) + (red[1] + red[5])) + ((red[2] + red[6]) + (red[3] + red[7]));
-    for (int s = n8 * 8; s < n; ++s) sum = sum + e[s];
+    float sum = ((csum[0] + csum[4]) + (csum[1] + csum[5])) + ((csum[2] + csum[6]) + (csum[3] + csum[7]));
+    for (int r = 0; r < n - body; ++r) sum = sum + tail[r];
     row[sstride - 1] = 1.0f / sum;
   }
 }
@@ -1129,25 +1158,20 @@ void set_attention_spin(int polls) { g_pv_spin = polls > 0 ? polls : kPvSpin; }
 
 void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
                       int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
-                      float *out, float *scores, hipStream_t s, const int *st, int *err, int stages) {
-  static size_t sm_configured = 0;
+                      float *out, float *scores, hipStream_t s, const int *st, int *err, int stages,
+                      int span) {
   for (int t0 = 0; t0 < m; t0 += kAttnTokens) {
     const int mt = std::min(kAttnTokens, m - t0);
     const int p0 = pos0 + t0;
-    // With a step record the position is on the device: size for the
-    // capacity, capped at the longest context a forward accepts (so the
-    // register-resident softmax always applies).
-    const int nmax = st ? std::min(cap, kMaxAttnPositions) : p0 + mt;
+    // With a step record the position is on the device: the grids, the
+    // score stride and the softmax kernel are those of the span of
+    // positions the caller gives (by default the first span), so the
+    // launch does not depend on the position.
+    const int nmax = st ? (span > 0 ? std::min(cap, span) : attn_span(cap, 1)) : p0 + mt;
     const int sstride = score_stride(nmax);
     const float *qt = q + (size_t)t0 * q_ld;
     float *ot = out + (size_t)t0 * nh * hd;
     if (stages & 1) launch_scores(qt, q_ld, kc, cap, p0, mt, nh, nkv, hd, scale, scores, sstride, nmax, st, s);
-    const size_t smem = sizeof(float) * (size_t)nmax;
-    if (smem > 48 * 1024 && smem > sm_configured) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_softmax),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      sm_configured = smem;
-    }
     if (!(stages & 2)) {
     } else if (nmax <= 512 * 16) {
       // Chains from registers (k_softmax_c): the chain-major rows hold
@@ -1169,7 +1193,7 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
       const size_t rsm = sizeof(float) * 8 * (size_t)cstr;
       hipLaunchKernelGGL(k_softmax_r<32>, dim3(nh, mt), dim3(512), rsm, s, scores, p0, nh, sstride, cstr, st);
     } else {
-      hipLaunchKernelGGL(k_softmax, dim3(nh, mt), dim3(256), smem, s, scores, p0, nh, sstride, st);
+      hipLaunchKernelGGL(k_softmax_l, dim3(nh, mt), dim3(512), 0, s, scores, p0, nh, sstride, st);
     }
     const size_t total = (size_t)mt * nh * hd;
     const int G = nh / nkv;

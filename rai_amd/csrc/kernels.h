@@ -166,18 +166,30 @@ void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, c
 constexpr int kAttnTokens = 64;
 size_t attention_scores_floats(int m, int nh, int ctx);
 // q rows are q_ld floats apart; out is [m][nh * hd].
-// With a step record `st` (m <= kAttnTokens), grids and the score stride
-// are sized for min(cap, kMaxAttnPositions) so the launch does not depend on
-// the position.  `err` (may be null): bit 0 is set when a PV tile hand-off
-// wait gave up (the output is then wrong and the caller must fail).
-// Longest context (positions) the attention launches accept.
-constexpr int kMaxAttnPositions = 16384;
+// With a step record `st` (m <= kAttnTokens), grids, the score stride and
+// the softmax kernel are sized for a span of positions, min(cap, span), so
+// the launch does not depend on the position (a captured step stays valid
+// for every position below its span).  Spans are kAttnSpan0 << b:
+// attn_span(cap, n) is the span of a step whose last position is n - 1, and
+// attn_span_index its b.  `err` (may be null): bit 0 is set when a PV tile
+// hand-off wait gave up (the output is then wrong and the caller must fail).
+constexpr int kAttnSpan0 = 16384;
+inline int attn_span_index(int n) {
+  int b = 0;
+  while ((kAttnSpan0 << b) < n) ++b;
+  return b;
+}
+inline int attn_span(int cap, int n) {
+  const int s = kAttnSpan0 << attn_span_index(n);
+  return s < cap ? s : cap;
+}
 // `stages` (timing only): bit 0 the score launch, bit 1 the softmax, bit 2
-// PV; a stage left out uses what the buffers already hold.
+// PV; a stage left out uses what the buffers already hold.  `span`: see
+// above (0 = the first span).
 void launch_attention(const float *q, int q_ld, const float *kc, const float *vc, int cap,
                       int vstride, int pos0, int m, int nh, int nkv, int hd, float scale,
                       float *out, float *scores, hipStream_t s, const int *st = nullptr,
-                      int *err = nullptr, int stages = 7);
+                      int *err = nullptr, int stages = 7, int span = 0);
 // Poll limit of the PV tile hand-off waits for launches enqueued from now
 // on (<= 0 restores the default).  Lowering it is for tests of the error
 // path: the waits then give up and report it, and every block still ends.

@@ -31,8 +31,6 @@ void set_last_error(const std::string &m) { g_last_error = m; }
            std::string(#expr) + ": " + hipGetErrorString(e_));                           \
   } while (0)
 
-// Largest attention context the register-resident softmax handles.
-constexpr size_t kMaxAttnContext = kMaxAttnPositions;
 // Tokens per forward chunk (prefill is split into chunks of this size; the
 // per-token arithmetic does not depend on the split).
 constexpr int kChunk = 1024;
@@ -601,7 +599,6 @@ static void forward_check(const rai_model &md, const rai_kv &kv, const Workspace
   const rai_model_config &c = md.cfg;
   if (m <= 0 || m > w.maxm) fail(RAI_E_SHAPE, "batch size exceeds the workspace");
   if (pos0 + m > c.max_context || pos0 + m > kv.cap) fail(RAI_E_RANGE, "batch position exceeds model context");
-  if (pos0 + m > kMaxAttnContext) fail(RAI_E_UNSUPPORTED, "context beyond 16384 positions is not supported");
   for (int l = 0; l < kv.layers; ++l)
     if (pos0 > kv.filled[l])
       fail(RAI_E_WATERMARK, "KV store at position " + std::to_string(pos0) + " would leave a gap (filled " +
@@ -614,9 +611,10 @@ static void forward_commit(rai_kv &kv, int m, size_t pos0) {
 
 // The launches of forward_batch (model.rs:692-963) for m tokens at positions
 // pos0.. whose hidden states are in w.hid.  With a device step record `st`
-// the position-dependent kernels read pos0 from it (graph replay).
+// the position-dependent kernels read pos0 from it (graph replay), and the
+// attention launches are sized for `span` positions (attn_span).
 static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size_t pos0, hipStream_t s,
-                            const int *st) {
+                            const int *st, int span = 0) {
   const rai_model_config &c = md.cfg;
   const int H = c.hidden_size, F = c.intermediate_size, hd = c.head_dim;
   const int nh = c.num_heads, nkv = c.num_kv_heads, qd = nh * hd;
@@ -679,7 +677,7 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
       launch_rope_store(qp, kp, vp, md.rope_cos, md.rope_sin, (int)pos0, m, nh, nkv, hd, kv.kc(li), kv.vc(li),
                         (int)kv.cap, (int)kv.vstride, q_ld, kv_ld, s, st);
     launch_attention(qp, q_ld, kv.kc(li), kv.vc(li), (int)kv.cap, (int)kv.vstride, (int)pos0, m, nh, nkv, hd,
-                     md.attn_scale, w.att.as<float>(), scores, s, st, w.err.as<int>() + 1);
+                     md.attn_scale, w.att.as<float>(), scores, s, st, w.err.as<int>() + 1, 7, span);
     // o_proj with the first residual add (model.rs:858-863) in its epilogue;
     // one token: the GEMV launch quantizes the attention output itself.
     const DLinear &O = L.lin[3];
@@ -833,10 +831,12 @@ struct rai_lookup {
   int *pin = nullptr;     // pinned host mirror of res + tokens (+ the step record at pin[512])
   hipStream_t stream = nullptr;
   // Step graphs: one per verify batch size m (embed, forward, logits,
-  // argmax, accept), replayed with the position in the device step record.
+  // argmax, accept) and attention span (attn_span), replayed with the
+  // position in the device step record.
   DevBuf step;            // int[5] {pos0, len, start, nd, temperature bits}
   bool graphs = false;
-  // Indexed by verify size m, plus kAttnTokens + 1 for exact-sampling steps.
+  // Indexed by verify size m, plus kAttnTokens + 1 for exact-sampling steps,
+  // plus 2 (kAttnTokens + 1) per attention span index.
   std::vector<hipGraphExec_t> graph;
   std::vector<int> graph_uses;
   // Exact sampling: the decoder's StdRng (device), per-row probabilities
@@ -929,11 +929,14 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
   }
   const int m = nd + 1;  // verify [last, draft...] or the single decode_one token
   forward_check(md, d.kv, d.ws, m, pos);
+  // The attention span a graph of this step is captured for: every position
+  // up to it replays the same graph.
+  const int span = attn_span((int)d.kv.cap, (int)pos + m);
   auto enqueue = [&](const int *st) {
     launch_embed(nullptr, d.ctx.as<uint32_t>(), (int)len - 1, start, m, md.emb_codes, md.emb_params,
                  c.vocab_size, c.hidden_size, c.embed_group_size, c.embed_scale, d.ws.hid.as<float>(),
                  d.ws.err.as<int>(), s, st);
-    forward_enqueue(md, d.kv, d.ws, m, pos, s, st);
+    forward_enqueue(md, d.kv, d.ws, m, pos, s, st, span);
     logits(md, d.ws, m, s);
     if (sampled) {
       launch_sample(d.ws.logits.as<float>(), d.probs.as<float>(), c.vocab_size, d.ctx.as<uint32_t>(), (int)len,
@@ -961,7 +964,7 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
     sh[7] = (int)cfg.max_draft;
     HIP_CHECK(hipMemcpyAsync(d.step.p, sh, 8 * sizeof(int), hipMemcpyHostToDevice, s));
     const int *st = d.step.as<int>();
-    const int gi = m + (sampled ? kAttnTokens + 1 : 0);
+    const int gi = m + (sampled ? kAttnTokens + 1 : 0) + 2 * (kAttnTokens + 1) * attn_span_index((int)pos + m);
     if (d.graph[gi]) {
       HIP_CHECK(hipGraphLaunch(d.graph[gi], s));
     } else if (d.graph_uses[gi]++ == 0) {
@@ -1153,6 +1156,9 @@ int rai_kv_read(const rai_kv *kv, size_t layer, size_t head, size_t pos, int whi
     if (pos >= kv->filled[layer])
       rai::fail(RAI_E_WATERMARK, "KV read at unwritten position " + std::to_string(pos) + " (filled " +
                                      std::to_string(kv->filled[layer]) + ")");
+    // The cache is written on the decoders' own (non-blocking) streams:
+    // wait for all of their work before copying.
+    HIP_CHECK(hipDeviceSynchronize());
     if (which == 0) {
       const float *base = kv->kc((int)layer);
       HIP_CHECK(hipMemcpy(out, base + (head * kv->cap + pos) * kv->hd, kv->hd * sizeof(float), hipMemcpyDeviceToHost));
@@ -1265,6 +1271,60 @@ int rai_w4a8_matmul_dev(float *out, const uint8_t *nib, const uint8_t *params, c
                      mm.as<uint8_t>());
     HIP_CHECK(hipGetLastError());
     HIP_CHECK(hipStreamSynchronize(s));  // scratch is freed on return
+  });
+}
+
+// w4a8_fused_qkv / w4a8_fused_gate_up (gemm.rs:1386-1703): the projections'
+// checks (validate_projection, gemm.rs:1215-1226, and the agreement of
+// cols and group_size), one quantization of the input row, then each
+// projection's one-token GEMV on the shared activations.
+static void fused_projections(float *const *outs, const rai_qlinear *const *lin, const char *const *names, int n,
+                              const float *x, void *stream) {
+  if (!x) rai::fail(RAI_E_ARG, "null argument");
+  for (int i = 0; i < n; ++i) {
+    if (!outs[i] || !lin[i] || !lin[i]->nibbles || !lin[i]->params) rai::fail(RAI_E_ARG, "null argument");
+    const rai_qlinear &L = *lin[i];
+    if (L.rows == 0) rai::fail(RAI_E_SHAPE, "rows must be non-zero");
+    if (L.cols == 0 || L.cols % 2) rai::fail(RAI_E_SHAPE, "cols must be non-zero and even");
+    if (L.group_size == 0 || L.group_size % 2) rai::fail(RAI_E_SHAPE, "group_size must be non-zero and even");
+    if (L.rows > INT32_MAX || L.cols > INT32_MAX) rai::fail(RAI_E_SHAPE, "dimensions overflow");
+  }
+  for (int i = 1; i < n; ++i) {
+    if (lin[i]->cols != lin[0]->cols) rai::fail(RAI_E_SHAPE, std::string(names[i]) + " column mismatch");
+    if (lin[i]->group_size != lin[0]->group_size) rai::fail(RAI_E_SHAPE, std::string(names[i]) + " group mismatch");
+  }
+  hipStream_t s = (hipStream_t)stream;
+  const size_t cols = lin[0]->cols, gs = lin[0]->group_size, groups = rai::ceil_div(cols, gs);
+  rai::DevBuf qn, qs, sc, su;
+  qn.alloc(cols);
+  qs.alloc(cols);
+  sc.alloc(groups * 4);
+  su.alloc(groups * 4);
+  rai::launch_quantize(x, 1, (int)cols, (int)gs, qn.as<int8_t>(), qs.as<int8_t>(), sc.as<float>(), su.as<float>(), s);
+  for (int i = 0; i < n; ++i)
+    rai::launch_w4a8(outs[i], nullptr, lin[i]->nibbles, lin[i]->params, x, qn.as<int8_t>(), qs.as<int8_t>(),
+                     sc.as<float>(), su.as<float>(), (int)lin[i]->rows, (int)cols, 1, (int)gs, s, nullptr, nullptr);
+  HIP_CHECK(hipGetLastError());
+  HIP_CHECK(hipStreamSynchronize(s));  // scratch is freed on return
+}
+
+int rai_w4a8_fused_qkv_dev(float *q_out, float *k_out, float *v_out, const rai_qlinear *q, const rai_qlinear *k,
+                           const rai_qlinear *v, const float *x, void *stream) {
+  RAI_API_BODY({
+    float *const outs[3] = {q_out, k_out, v_out};
+    const rai_qlinear *const lin[3] = {q, k, v};
+    const char *const names[3] = {"Q", "Q/K", "Q/V"};
+    fused_projections(outs, lin, names, 3, x, stream);
+  });
+}
+
+int rai_w4a8_fused_gate_up_dev(float *gate_out, float *up_out, const rai_qlinear *gate, const rai_qlinear *up,
+                               const float *x, void *stream) {
+  RAI_API_BODY({
+    float *const outs[2] = {gate_out, up_out};
+    const rai_qlinear *const lin[2] = {gate, up};
+    const char *const names[2] = {"gate", "gate/up"};
+    fused_projections(outs, lin, names, 2, x, stream);
   });
 }
 
@@ -1397,7 +1457,7 @@ int rai_attention_time_dev(const float *q, const float *kc, const float *vc, siz
     if (m == 0 || m > (size_t)rai::kAttnTokens || nkv == 0 || nh % nkv || hd == 0 || hd % 8 || copies == 0 ||
         iters <= 0)
       rai::fail(RAI_E_SHAPE, "invalid attention shape");
-    if (pos + m > cap || cap > (size_t)rai::kMaxAttnPositions) rai::fail(RAI_E_RANGE, "positions exceed the cache");
+    if (pos + m > cap) rai::fail(RAI_E_RANGE, "positions exceed the cache");
     const size_t vstride = (cap + 63) & ~size_t(63);
     const size_t kbytes = nkv * cap * hd, vbytes = nkv * hd * vstride;  // floats per copy
     rai::DevBuf out, scores, err;
@@ -1560,7 +1620,6 @@ int rai_attention_head_dev(float *out, const float *q, const float *k, const flo
   RAI_API_BODY({
     if (!out || !q || !k || !v) rai::fail(RAI_E_ARG, "null argument");
     if (hd == 0 || hd % 8 || hd > 256) rai::fail(RAI_E_SHAPE, "head_dim must be a multiple of 8 up to 256");
-    if (pos + 1 > rai::kMaxAttnContext) rai::fail(RAI_E_UNSUPPORTED, "context beyond 16384 positions");
     // One head: q [hd], cache rows [pos+1][hd] viewed as one kv head with cap = pos+1.
     rai::DevBuf scores;
     scores.alloc(sizeof(float) * rai::attention_scores_floats(1, 1, (int)(pos + 1)));
@@ -1615,8 +1674,9 @@ int rai_lookup_create(rai_model *m, size_t max_ctx, rai_lookup **out) {
     // host to group tokens by expert, which a graph cannot hold).
     const char *env = std::getenv("RAI_STEP_GRAPHS");
     d->graphs = (m->cfg.num_experts == 0 || rai::moe_on_device(*m)) && !(env && env[0] == '0');
-    d->graph.assign(2 * (rai::kAttnTokens + 1), nullptr);
-    d->graph_uses.assign(2 * (rai::kAttnTokens + 1), 0);
+    const size_t spans = (size_t)rai::attn_span_index((int)d->max_ctx) + 1;
+    d->graph.assign(2 * (rai::kAttnTokens + 1) * spans, nullptr);
+    d->graph_uses.assign(2 * (rai::kAttnTokens + 1) * spans, 0);
     d->rng.alloc(sizeof(rai::RngState));
     d->probs.alloc(sizeof(float) * 64 * (size_t)m->cfg.vocab_size);
     d->pscratch.alloc(sizeof(float) * (size_t)m->cfg.vocab_size);
@@ -1749,6 +1809,7 @@ int rai_kv_export(const rai_kv *kv, size_t layer, int which, float *out, size_t 
     if (layer >= (size_t)kv->layers) rai::fail(RAI_E_ARG, "layer index out of range");
     if (npos > kv->filled[layer])
       rai::fail(RAI_E_WATERMARK, "KV export above the watermark (filled " + std::to_string(kv->filled[layer]) + ")");
+    HIP_CHECK(hipDeviceSynchronize());  // as rai_kv_read
     const size_t hd = kv->hd;
     if (which == 0) {
       for (int h = 0; h < kv->nkv; ++h)
@@ -1766,6 +1827,35 @@ int rai_kv_export(const rai_kv *kv, size_t layer, int which, float *out, size_t 
           for (size_t p = 0; p < npos; ++p) dst[p * hd + d] = tmp[d * npos + p];
       }
     }
+  });
+}
+
+int rai_kv_import(rai_kv *kv, size_t layer, int which, const float *rows, size_t npos) {
+  RAI_API_BODY({
+    if (!kv || !rows) rai::fail(RAI_E_ARG, "null argument");
+    if (layer >= (size_t)kv->layers) rai::fail(RAI_E_ARG, "layer index out of range");
+    if (which != 0 && which != 1) rai::fail(RAI_E_ARG, "which must be 0 (K) or 1 (V)");
+    if (npos > kv->cap) rai::fail(RAI_E_RANGE, "KV cache position is out of range");
+    const size_t hd = kv->hd;
+    HIP_CHECK(hipDeviceSynchronize());  // no decoder work may still use the rows
+    if (which == 0) {
+      for (int h = 0; h < kv->nkv; ++h)
+        if (npos)
+          HIP_CHECK(hipMemcpy(kv->kc((int)layer) + (size_t)h * kv->cap * hd, rows + (size_t)h * npos * hd,
+                              sizeof(float) * npos * hd, hipMemcpyHostToDevice));
+    } else {
+      // d-major V [head][hd][vstride]: transpose to [hd][npos], then copy.
+      std::vector<float> tmp(hd * npos);
+      for (int h = 0; h < kv->nkv; ++h) {
+        const float *src = rows + (size_t)h * npos * hd;
+        for (size_t p = 0; p < npos; ++p)
+          for (size_t d = 0; d < hd; ++d) tmp[d * npos + p] = src[p * hd + d];
+        if (npos)
+          HIP_CHECK(hipMemcpy2D(kv->vc((int)layer) + (size_t)h * hd * kv->vstride, kv->vstride * sizeof(float),
+                                tmp.data(), npos * sizeof(float), npos * sizeof(float), hd, hipMemcpyHostToDevice));
+      }
+    }
+    kv->filled[layer] = npos;
   });
 }
 
@@ -1899,9 +1989,23 @@ static void spec_step(rai_spec &d, size_t pos, uint32_t last, const rai_spec_con
     raise_kernel_errors(d.tws, s, e);
   }
   const int acc = d.pin[0], prod = d.pin[1];
-  if (k > 0 && acc == k) decode_on(dm, d.dkv, d.dws, toks + k, pos + k, s);
-  for (auto &x : d.dkv.filled) x = std::min(x, pos + (size_t)prod);
   for (auto &x : d.tkv.filled) x = std::min(x, pos + (size_t)prod);
+  if (k > 0 && acc == k) {
+    // Every draft accepted: the draft model's catch-up step on its last
+    // draft token (row pos + k of the draft cache), finished before the
+    // step returns so that the draft cache is whole for a caller that reads
+    // it next.  If its attention wait gave up, that row stays above the
+    // watermark and the step fails.
+    decode_on(dm, d.dkv, d.dws, toks + k, pos + k, s);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipMemcpyAsync(f, d.dws.err.p, sizeof(f), hipMemcpyDeviceToHost, s));
+    HIP_CHECK(hipStreamSynchronize(s));
+    if (f[0] || f[1]) {
+      for (auto &x : d.dkv.filled) x = std::min(x, pos + (size_t)k);
+      raise_kernel_errors(d.dws, s, f);
+    }
+  }
+  for (auto &x : d.dkv.filled) x = std::min(x, pos + (size_t)prod);
   for (int i = 0; i < prod; ++i) out[i] = (uint32_t)d.pin[2 + i];
   met.accepted = (size_t)acc;
   met.drafted = (size_t)k;

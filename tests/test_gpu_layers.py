@@ -55,10 +55,11 @@ def test_attention_head_bit_exact(rai, ora, hd, pos):
 
 
 @pytest.mark.parametrize("hd", [64, 128])
-@pytest.mark.parametrize("pos", [2047, 2048, 4100, 8191, 9000, 16383])
+@pytest.mark.parametrize("pos", [2047, 2048, 4100, 8191, 9000, 16383, 16384, 20002, 32767, 40001])
 def test_attention_head_long_context_bit_exact(rai, ora, hd, pos):
     """Contexts that select each register depth of the softmax (up to 2048,
-    4096, 8192 and 16384 positions), with tails of 0..7 positions past the
+    4096, 8192 and 16384 positions) and the chunked softmax past them (one
+    to twelve 3584-position chunks), with tails of 0..7 positions past the
     last 8-block and chains long enough for the prefetched LDS reads."""
     rng = np.random.default_rng(hd * 7 + pos)
     q = rng.normal(size=hd).astype(np.float32)
