@@ -104,6 +104,7 @@ def lib():
         "ora_softmax_probabilities": (c_int, [P, c_int, c_float, P]),
         "ora_sample_token": (c_int, [P, c_int, c_float, P, POINTER(c_int)]),
         "ora_sampled_accept": (c_int, [P, c_int, P, c_int, c_float, P, P, POINTER(c_int), POINTER(c_int)]),
+        "ora_spec_accept": (c_int, [P, P, c_int, P, c_int, c_float, P, P, POINTER(c_int), POINTER(c_int)]),
         "ora_spec_create": (c_int, [P, P, c_int, POINTER(c_void_p)]),
         "ora_spec_free": (None, [P]),
         "ora_spec_prefill": (c_int, [P, P, c_int, POINTER(c_int)]),
@@ -418,6 +419,19 @@ def sample_token(logits, temperature: float, rng: Rng) -> int:
     t = c_int()
     _check(lib().ora_sample_token(_ptr(x), x.size, temperature, rng.h, ctypes.byref(t)))
     return t.value
+
+
+def spec_accept(target_logits, draft_logits, draft, temperature: float, rng: Rng):
+    """SpeculativeDecoder::step's acceptance (speculative.rs:300-370) with
+    sample_correction (speculative.rs:478-513): target rows [k + 1][V],
+    draft rows [k][V], draft tokens [k] -> (tokens, accepted)."""
+    tl, dl = f32(target_logits), f32(draft_logits)
+    d = np.ascontiguousarray(draft, np.int32)
+    out = np.zeros(d.size + 1, np.int32)
+    prod, acc = c_int(), c_int()
+    _check(lib().ora_spec_accept(_ptr(tl), _ptr(dl), tl.shape[1], _ptr(d), d.size, temperature, rng.h, _ptr(out),
+                                 ctypes.byref(prod), ctypes.byref(acc)))
+    return out[:prod.value].tolist(), acc.value
 
 
 def sampled_accept(logits, draft, temperature: float, rng: Rng):

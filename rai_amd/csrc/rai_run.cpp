@@ -10,8 +10,11 @@
 // Modes as run.rs: --draft (draft-model speculation) and --lookup-k
 // (prompt lookup) are mutually exclusive; without either, plain decoding
 // (greedy: sampling without speculation, with top-k / top-p / repetition
-// penalty, is not part of this library).  Generated ids go to stdout, one
-// line; the statistics to stderr.
+// penalty, is not part of this library).  One deliberate extension: the
+// reference refuses the speculative modes at --temperature <= 1e-6
+// (run.rs:205-213); here they select greedy acceptance, whose tokens equal
+// plain greedy decoding.  Generated ids go to stdout, one line; the
+// statistics to stderr.
 #include <chrono>
 #include <cmath>
 #include <cstdio>

@@ -124,3 +124,42 @@ def test_bonus_token_follows_the_last_row():
         counts[toks[1]] += 1
     chi2 = ((counts - n * p) ** 2 / (n * p)).sum()
     assert chi2 < 22.0, (counts / n, p)
+
+
+@pytest.mark.parametrize("t", [0.6, 1.0])
+def test_draft_model_acceptance_preserves_the_target_distribution(t):
+    """SpeculativeDecoder's acceptance (speculative.rs:329-350) with
+    sample_correction's residual max(0, p - q) (speculative.rs:478-513),
+    with a draft distribution q that is not a point mass: the draft token is
+    drawn from q, and the first emitted token must follow p =
+    softmax(target / T) (chi-squared over 20000 draws), with the draft
+    accepted at the rate sum(min(p, q)).  The same checks have the power to
+    reject two plausible mistakes: a correction drawn from p instead of the
+    residual, and an acceptance test against p_target instead of
+    p_target / p_draft."""
+    target = np.array([[1.0, 0.2, 2.0, -1.0, 0.5], [0.3, -0.4, 1.1, 0.0, 0.9]], np.float32)
+    draft = np.array([[0.1, 1.5, 1.8, 0.4, -0.3]], np.float32)
+    p = ora.softmax_probabilities(target[0], t).astype(np.float64)
+    q = ora.softmax_probabilities(draft[0], t).astype(np.float64)
+    q /= q.sum()
+    pick = np.random.default_rng(int(t * 100))
+    rng = ora.Rng(seed=int(t * 1000) + 3)
+    n = 20000
+    counts = np.zeros(5)
+    accepted = 0
+    for _ in range(n):
+        d = int(pick.choice(5, p=q))
+        toks, acc = ora.spec_accept(target, draft, [d], t, rng)
+        assert (acc == 1) == (toks[0] == d) and len(toks) == 1 + acc
+        counts[toks[0]] += 1
+        accepted += acc
+    limit = 25.0  # 4 degrees of freedom: p < 1e-4 for a correct rule
+    chi2 = ((counts - n * p) ** 2 / (n * p)).sum()
+    assert chi2 < limit, (counts / n, p)
+    beta = np.minimum(p, q).sum()
+    sigma = np.sqrt(n * beta * (1 - beta))
+    assert abs(accepted - n * beta) < 5 * sigma, (accepted / n, beta)
+    # Power: the expected statistic of each mistaken rule is far past the limits.
+    wrong_correction = np.minimum(p, q) + (1.0 - beta) * p
+    assert n * ((wrong_correction - p) ** 2 / p).sum() > 4 * limit
+    assert abs(n * (q * p).sum() - n * beta) > 20 * sigma

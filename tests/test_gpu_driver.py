@@ -7,7 +7,9 @@
 - rai-run, the `rai run` generate loop (run.rs:242-633) over the C ABI,
   prints the same tokens as the library's own loops for prompt lookup
   (greedy and sampled, same seed), draft-model speculation and plain
-  greedy decoding.
+  greedy decoding, and the same tokens as the CPU oracle's decoders on the
+  same file;
+- the path-loaded model's logits equal the oracle's on the file's bytes.
 """
 import os
 import subprocess
@@ -129,3 +131,85 @@ def test_rai_run_rejects_bad_arguments(model_file):
     r = subprocess.run([RUN, path, "--prompt-ids", "1,2", "--temperature", "0.5"], capture_output=True, text=True,
                        timeout=60)
     assert r.returncode == 2
+
+
+def _oracle(ora, path):
+    with open(path, "rb") as f:
+        return ora.Model(f.read(), 0)
+
+
+def test_load_from_path_matches_oracle(rai, ora, model_file):
+    """RaiModel::load (format.rs:557-637) of a file: embedding rows, hidden
+    states and logits equal the oracle's reading of the same bytes."""
+    path, draft = model_file
+    for p in (path, draft):
+        g, o = rai.RaiModel.load(p), _oracle(ora, p)
+        toks = [3, 9, 27, 81, 243, 599]
+        for t in toks[:2]:
+            assert np.array_equal(_bits(g.embed_token(t)), _bits(o.embed_token(t)))
+        h = np.stack([o.embed_token(t) for t in toks])
+        gh = g.forward_batch(h, np.arange(6), g.create_kv_cache(16))
+        oh = o.forward_batch(h, np.arange(6), o.create_kv(16))
+        assert np.array_equal(_bits(gh), _bits(oh))
+        assert np.array_equal(_bits(g.hidden_to_logits_batch(gh, 6)), _bits(o.hidden_to_logits_batch(oh, 6)))
+
+
+def test_rai_run_plain_greedy_matches_oracle(rai, ora, model_file):
+    """`rai run` without speculation at temperature 0 (run.rs:640-735:
+    prefill of the first N - 1 tokens, then one decode per token) prints the
+    oracle's greedy decode of the same file."""
+    path, _ = model_file
+    prompt = copy_heavy_prompt(50, 600, seed=21)
+    ids = ",".join(str(int(t)) for t in prompt)
+    got = _run([path, "--prompt-ids", ids, "--max-tokens", "32", "--temperature", "0"])
+    want = _oracle(ora, path).greedy_generate(prompt.astype(np.int32), 32, 512).tolist()
+    assert got == want
+
+
+@pytest.mark.parametrize("temperature", [0.0, 0.8])
+def test_rai_run_lookup_matches_oracle(rai, ora, model_file, temperature):
+    """`rai run --lookup-k 6` (run.rs:517-633) prints the oracle
+    LookupDecoder's tokens: greedy, and sampled with the oracle's StdRng
+    seeded as the driver seeds the decoder's (run.rs:345)."""
+    path, _ = model_file
+    prompt = copy_heavy_prompt(60, 600, seed=8)
+    ids = ",".join(str(int(t)) for t in prompt)
+    got = _run([path, "--prompt-ids", ids, "--max-tokens", "40", "--lookup-k", "6", "--lookup-ngram", "3",
+                "--lookup-min-ngram", "1", "--temperature", str(temperature), "--seed", "5"])
+    od = ora.LookupDecoder(_oracle(ora, path), 512)
+    rng = ora.Rng(seed=5)
+    pos = od.prefill(prompt.astype(np.int32))
+    ctx = prompt.tolist()
+    want = []
+    while len(want) < 40:
+        if temperature > 0:
+            toks, met = od.step_sampled(pos, ctx, 6, 1, 3, temperature, rng)
+        else:
+            toks, met = od.step(pos, ctx, 6, 1, 3)
+        take = toks[:40 - len(want)]
+        want += take
+        ctx += take
+        pos += len(take)
+    assert got == want
+
+
+@pytest.mark.parametrize("temperature", [0.0, 0.9])
+def test_rai_run_draft_matches_oracle(rai, ora, model_file, temperature):
+    """`rai run --draft` (run.rs:405-517) prints the oracle
+    SpeculativeDecoder's tokens for the same seed."""
+    path, draft = model_file
+    prompt = copy_heavy_prompt(30, 600, seed=9)
+    ids = ",".join(str(int(t)) for t in prompt)
+    got = _run([path, "--prompt-ids", ids, "--max-tokens", "24", "--draft", draft, "--draft-k", "4",
+                "--temperature", str(temperature), "--seed", "11"])
+    od = ora.SpecDecoder(_oracle(ora, draft), _oracle(ora, path), 512)
+    rng = ora.Rng(seed=11)
+    pos = od.prefill(prompt.astype(np.int32))
+    last, want = int(prompt[-1]), []
+    while len(want) < 24:
+        toks, met = od.step(pos, last, 4, temperature, rng)
+        take = toks[:24 - len(want)]
+        want += take
+        pos += len(take)
+        last = take[-1]
+    assert got == want

@@ -73,3 +73,53 @@ def test_speculative_errors(rai):
         d.step(pos, 5, 0, 0.5)  # draft_k = 0
     with pytest.raises(rai.RaiError):
         d.step(pos, 900, 2, 0.5)  # token outside the vocabulary
+
+
+def test_greedy_speculation_equals_greedy_decoding(rai, ora):
+    """The greedy variant of draft-model speculation emits the target's own
+    greedy continuation whatever the draft (accepted drafts are the target's
+    argmax, the first rejection emits it): its tokens equal the oracle's
+    plain greedy decode of the target (decode_one, lookup.rs:428-455)."""
+    d, t = _models(rai, ora)
+    (gd_m, _), (gt_m, ot_m) = d, t
+    prompt = copy_heavy_prompt(40, 600, seed=77)
+    dec = rai.SpeculativeDecoder(gd_m, gt_m, 256)
+    pos = dec.prefill(prompt)
+    last, got = int(prompt[-1]), []
+    while len(got) < 48:
+        toks, _ = dec.step(pos, last, 5, 0.0)
+        got += toks
+        pos += len(toks)
+        last = toks[-1]
+    want = ot_m.greedy_generate(prompt.astype(np.int32), 48, 256).tolist()
+    assert got[:48] == want
+
+
+@pytest.mark.parametrize("temperature", [0.0, 0.9])
+def test_draft_cache_is_whole_after_an_all_accepted_step(rai, ora, temperature):
+    """After a step in which every draft is accepted, the draft model's
+    catch-up row (position pos + k) is in the draft cache when the step
+    returns: with the target as its own draft, the draft cache's K and V rows
+    0..pos+k equal the oracle's for the same tokens, read right after the
+    step through rai_kv_export."""
+    _, (gm, om) = _models(rai, ora)
+    prompt = copy_heavy_prompt(40, 600, seed=12)
+    dec = rai.SpeculativeDecoder(gm, gm, 256)
+    dec.seed(4)
+    pos = dec.prefill(prompt)
+    toks, met = dec.step(pos, int(prompt[-1]), 6, temperature)
+    assert met["accepted"] == 6
+    n = pos + 7  # rows 0 .. pos + k
+    assert dec.draft_kv.filled(0) == n
+    seq = prompt.tolist() + toks
+    okv = om.create_kv(256)
+    h = np.stack([om.embed_token(int(x)) for x in seq[:n]])
+    om.forward_batch(h, np.arange(n), okv)
+    cfg = om.cfg
+    for layer in range(cfg.num_layers):
+        for which in (0, 1):
+            got = dec.draft_kv.export(layer, which, n, cfg.num_kv_heads, cfg.head_dim)
+            get = okv.get_k if which == 0 else okv.get_v
+            want = np.stack([np.stack([get(layer, hh, p, cfg.head_dim) for p in range(n)])
+                             for hh in range(cfg.num_kv_heads)])
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (layer, which)
