@@ -201,7 +201,7 @@ int rai_w4a8_fused_gate_up_dev(float *gate_out, float *up_out, const rai_qlinear
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * Same arguments, arithmetic and results; the quantized activations live in
- * a fixed per-GPU scratch array held until the process ends (about 4.5 MiB),
+ * a fixed per-GPU scratch array held until the process ends (8 MiB),
  * so the call is asynchronous on `stream` and calls no allocator.  Limits:
  * m * cols <= 1048576 and m * ceil(cols / group_size) <= 65536, else
  * RAI_E_SHAPE.  Every call on one GPU shares that GPU's scratch: calls that

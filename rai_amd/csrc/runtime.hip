@@ -1336,12 +1336,15 @@ int rai_w4a8_fused_gate_up_dev(float *gate_out, float *up_out, const rai_qlinear
 // address hipGetSymbolAddress returns on each device, looked up once per
 // device on the first call there.  Layout (bytes): q_nat [m*cols], q_split
 // [m*cols], scales [m*groups] f32, sums [m*groups] f32, matrix-core
-// activations.
+// activations (2..64 tokens), the matrix-core GEMM's activation records
+// (more than 64 tokens at group 32: at most ceil(m/32) * cols/32 * 2304
+// bytes, which for m > 64 and m * cols <= 2^20 stays below 3/65 * 72 * 2^20).
 namespace rai {
 constexpr size_t kNaTokenCols = size_t(1) << 20;  // m * cols
 constexpr size_t kNaGroups = size_t(1) << 16;     // m * ceil(cols / gs)
 constexpr size_t kNaQaBytes = size_t(2) << 20;
-constexpr size_t kNaScratchBytes = 2 * kNaTokenCols + 8 * kNaGroups + kNaQaBytes;
+constexpr size_t kNaMmBytes = size_t(7) << 19;  // 3.5 MiB
+constexpr size_t kNaScratchBytes = 2 * kNaTokenCols + 8 * kNaGroups + kNaQaBytes + kNaMmBytes;
 constexpr int kNaMaxDevices = 64;
 }  // namespace rai
 
@@ -1386,12 +1389,16 @@ int rai_w4a8_matmul_noalloc_dev(float *out, const uint8_t *nib, const uint8_t *p
     const bool mfma = rai::w4a8_mfma_path((int)rows, (int)cols, (int)m, (int)gs);
     if (mfma && sizeof(_Float16) * rai::qa_pack_halves((int)m, (int)cols) > rai::kNaQaBytes)
       rai::fail(RAI_E_SHAPE, "activation tile exceeds the allocation-free scratch");
+    const bool mm = rai::w4a8_mm_path((int)rows, (int)cols, (int)m, (int)gs);
+    if (mm && rai::mm_pack_bytes((int)m, (int)cols) > rai::kNaMmBytes)
+      rai::fail(RAI_E_SHAPE, "activation records exceed the allocation-free scratch");
     uint8_t *base = rai::noalloc_scratch();
     int8_t *qn = reinterpret_cast<int8_t *>(base);
     int8_t *qs = reinterpret_cast<int8_t *>(base + rai::kNaTokenCols);
     float *sc = reinterpret_cast<float *>(base + 2 * rai::kNaTokenCols);
     float *su = sc + rai::kNaGroups;
     _Float16 *qa = reinterpret_cast<_Float16 *>(base + 2 * rai::kNaTokenCols + 8 * rai::kNaGroups);
+    uint8_t *mmp = base + 2 * rai::kNaTokenCols + 8 * rai::kNaGroups + rai::kNaQaBytes;
     hipStream_t s = (hipStream_t)stream;
     // Every scratch byte a kernel reads is written earlier in this call (the
     // pack writes the padding rows of the last token group as zeros), so the
@@ -1399,7 +1406,7 @@ int rai_w4a8_matmul_noalloc_dev(float *out, const uint8_t *nib, const uint8_t *p
     rai::launch_quantize(x, (int)m, (int)cols, (int)gs, qn, qs, sc, su, s);
     if (mfma) rai::launch_qa_pack(qs, (int)m, (int)cols, qa, s);
     rai::launch_w4a8(out, nullptr, nib, params, x, qn, qs, sc, su, (int)rows, (int)cols, (int)m, (int)gs, s,
-                     mfma ? qa : nullptr);
+                     mfma ? qa : nullptr, mm ? mmp : nullptr);
     HIP_CHECK(hipGetLastError());
   });
 }

@@ -2,7 +2,8 @@
 rai_w4a8_matmul_dev, through the C ABI: bit-identical outputs on two calls in
 a row on the same device buffers, the second with fewer tokens and a smaller
 matrix (the shared scratch keeps the first call's contents), the matrix-core
-and the one-token paths, and the size limit."""
+verify path, the matrix-core GEMM past 64 tokens, the one-token path, and
+the size limit."""
 import ctypes
 
 import numpy as np
@@ -28,6 +29,7 @@ def _run(rai, fn, nib, params, x, rows, cols, m, gs):
     [(2000, 4096, 16, 32), (300, 512, 1, 32)],      # then the one-token path
     [(512, 14336, 3, 32), (96, 1024, 2, 64)],       # long rows, then group 64
     [(1000, 8192, 128, 128), (64, 256, 17, 32)],    # many tokens, then the tiled path
+    [(4096, 4096, 200, 32), (1024, 2048, 70, 32)],  # the matrix-core GEMM (> 64 tokens), twice
 ])
 def test_noalloc_matches_allocating_entry_point(rai, calls):
     for i, (rows, cols, m, gs) in enumerate(calls):
