@@ -323,10 +323,17 @@ int rai_lookup_generate(rai_lookup *dec, const uint32_t *prompt, size_t n, size_
 int rai_lookup_decode(rai_lookup *dec, const uint32_t *context, size_t len, size_t pos,
                       size_t max_tokens, const rai_lookup_config *cfg, uint32_t *out_tokens,
                       size_t out_cap, size_t *n_out, rai_generate_stats *stats);
-/* Plain greedy decode (sampler.rs:61-64 argmax after decode_one), used for the
- * token-identity check: prefill, then `steps` single-token steps. */
+/* Plain greedy decode (sampler.rs:61-64 argmax after decode_one,
+ * lookup.rs:428-455): prefill, then `steps` single-token steps (the `rai run`
+ * loop without speculation at temperature 0, run.rs:640-735).  Also the
+ * token-identity check of the lookup decoder. */
 int rai_greedy_generate(rai_lookup *dec, const uint32_t *prompt, size_t n, size_t steps,
                         uint32_t *out_tokens);
+/* The same decode loop from a prefilled state: context[len - 1] is the token
+ * at position pos (the KV cache holds positions 0..pos-1); `steps` tokens to
+ * out_tokens.  The steps replay the decoder's one-token step graph. */
+int rai_greedy_decode(rai_lookup *dec, const uint32_t *context, size_t len, size_t pos, size_t steps,
+                      uint32_t *out_tokens);
 
 /* ------------------------------------------------------------------ misc -- */
 /* Synthetic .raimodel writer (the build's stand-in for the exporter).

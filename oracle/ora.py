@@ -79,6 +79,7 @@ def lib():
         "ora_kv_filled": (c_int, [P, c_int]),
         "ora_kv_read": (c_int, [P, c_int, c_int, c_int, c_int, P]),
         "ora_kv_import": (c_int, [P, c_int, c_int, P, c_int]),
+        "ora_lookup_decode_one": (c_int, [P, c_int, c_int, P]),
         "ora_route_experts": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P]),
         "ora_embed_token": (c_int, [P, c_int, P]),
         "ora_forward_from_hidden": (c_int, [P, P, P, c_int, c_int]),
@@ -479,6 +480,12 @@ class LookupDecoder:
 
     def kv_filled(self) -> int:
         return lib().ora_lookup_kv_filled(self.h)
+
+    def decode_one(self, pos: int, token: int) -> int:
+        """decode_one (lookup.rs:428-455) with argmax."""
+        out = np.zeros(1, np.int32)
+        _check(lib().ora_lookup_decode_one(self.h, pos, token, _ptr(out)))
+        return int(out[0])
 
     def import_kv(self, layer: int, which: int, rows: np.ndarray) -> None:
         """Set one layer's K (0) or V (1) cache rows [nkv][npos][head_dim]."""

@@ -617,6 +617,23 @@ int ora_lookup_import_kv(ora_lookup *dd, int layer, int which, const float *rows
 }
 int ora_lookup_kv_filled(const ora_lookup *d) { return d->d.kv.filled.at(0); }
 
+// decode_one (lookup.rs:428-455) with argmax: the plain greedy step of the
+// `rai run` loop without speculation.
+int ora_lookup_decode_one(ora_lookup *dd, int pos, int token, int32_t *out) {
+  ORA_TRY({
+    Lookup &d = dd->d;
+    const Model &m = *d.m;
+    const int H = m.cfg.hidden_size, V = m.cfg.vocab_size;
+    if (pos < 0 || pos >= d.max_ctx) fail("decode position exceeds the context window");
+    if (token < 0 || token >= V) fail("token id is out of model vocabulary");
+    std::vector<float> h(H), lg(V);
+    embed(m, token, h.data());
+    forward(m, d.kv, h.data(), &pos, 1);
+    logits(m, h.data(), lg.data(), 1);
+    *out = (int32_t)argmax(lg.data(), V);
+  });
+}
+
 // LookupDecoder::prefill (lookup.rs:219-247).
 int ora_lookup_prefill(ora_lookup *dd, const int32_t *prompt, int n, int *pos_out) {
   ORA_TRY({

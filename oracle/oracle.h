@@ -145,6 +145,9 @@ int ora_lookup_step_sampled(ora_lookup *d, int pos, const int32_t *context, int 
                             int min_ngram, int max_ngram, float temperature, ora_rng *rng,
                             int32_t *out_tokens, ora_metrics *metrics);
 int ora_lookup_kv_filled(const ora_lookup *d);
+/* decode_one (lookup.rs:428-455) with argmax: embed `token` at `pos`,
+ * forward, logits, argmax into *out. */
+int ora_lookup_decode_one(ora_lookup *d, int pos, int token, int32_t *out);
 /* SpeculativeDecoder (speculative.rs:79-391); temperature <= 1e-6 is the
  * greedy variant (argmax drafts, argmax acceptance). */
 int ora_spec_create(const ora_model *draft, const ora_model *target, int max_ctx, ora_spec **out);

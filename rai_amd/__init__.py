@@ -149,6 +149,7 @@ def lib():
         "rai_kv_export": (c_int, [P, S, c_int, P, S]),
         "rai_kv_import": (c_int, [P, S, c_int, P, S]),
         "rai_greedy_generate": (c_int, [P, P, S, S, P]),
+        "rai_greedy_decode": (c_int, [P, P, S, S, S, P]),
         "rai_synth_model": (c_int, [POINTER(SynthConfig), c_uint64, c_char_p,
                                     POINTER(c_void_p), POINTER(c_size_t)]),
         "rai_free_image": (None, [P]),
@@ -684,6 +685,13 @@ class LookupDecoder:
         p = _u32(prompt)
         out = np.zeros(steps, np.uint32)
         _check(lib().rai_greedy_generate(self.h, _ptr(p), p.size, steps, _ptr(out)))
+        return out.tolist()
+
+    def greedy_decode(self, context, pos: int, steps: int):
+        """Plain greedy decoding from a prefilled state (KV holds context[:-1])."""
+        c = _u32(context)
+        out = np.zeros(steps, np.uint32)
+        _check(lib().rai_greedy_decode(self.h, _ptr(c), c.size, pos, steps, _ptr(out)))
         return out.tolist()
 
     def __del__(self):

@@ -201,17 +201,23 @@ int main(int argc, char **argv) {
     if (a.temperature > 1e-6f)
       die("plain decoding samples with top-k / top-p / repetition penalty, which this library does not "
           "implement; use --temperature 0, --lookup-k or --draft");
+    // Prefill of the first N - 1 tokens, then one decode step per token
+    // (run.rs:640-735).
     rai_lookup *dec = nullptr;
     check(rai_lookup_create(model, max_ctx, &dec), "creating the decoder");
-    const size_t steps = std::min(a.max_tokens, max_ctx - a.prompt.size() + 1);
-    std::vector<uint32_t> out(steps);
     const auto t0 = std::chrono::steady_clock::now();
-    check(rai_greedy_generate(dec, a.prompt.data(), a.prompt.size(), steps, out.data()), "decoding");
-    const double ms = ms_since(t0);
-    size_t pos = a.prompt.size() - 1;
+    size_t pos = 0;
+    check(rai_lookup_prefill(dec, a.prompt.data(), a.prompt.size(), &pos), "prefill");
+    const double pms = ms_since(t0);
+    std::fprintf(stderr, "\nPrefill: %zu tokens in %.1fms (%.1f tok/s)\n", a.prompt.size(), pms,
+                 a.prompt.size() / (pms / 1e3));
+    const size_t steps = std::min(a.max_tokens, max_ctx - pos);
+    std::vector<uint32_t> out(steps);
+    const auto t1 = std::chrono::steady_clock::now();
+    check(rai_greedy_decode(dec, a.prompt.data(), a.prompt.size(), pos, steps, out.data()), "decoding");
+    const double ms = ms_since(t1);
     emit(out.data(), out.size(), pos);
-    std::fprintf(stderr, "\n--- Stats ---\nTokens: %zu, %.2f tok/s (prefill included)\n", generated,
-                 generated / (ms / 1e3));
+    std::fprintf(stderr, "\n--- Stats ---\nTokens: %zu, %.2f tok/s\n", generated, generated / (ms / 1e3));
     rai_lookup_free(dec);
   }
   for (size_t i = a.prompt.size(); i < all.size(); ++i)

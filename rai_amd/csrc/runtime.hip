@@ -886,9 +886,13 @@ static bool sync_context(rai_lookup &d, const uint32_t *ctx, size_t len) {
   return same == len;
 }
 
-// One decode step: LookupDecoder::step (lookup.rs:260-425) in greedy mode.
+// One decode step: LookupDecoder::step (lookup.rs:260-425).  With
+// search = false the n-gram search is skipped and the step is decode_one
+// (lookup.rs:428-455): the plain decode loop of `rai run` (run.rs:692-735),
+// on the same one-token step graph.
 static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size_t len,
-                        const rai_lookup_config &cfg, uint32_t *out, size_t cap, rai_lookup_metrics &met) {
+                        const rai_lookup_config &cfg, uint32_t *out, size_t cap, rai_lookup_metrics &met,
+                        bool search = true) {
   rai_model &md = *d.model;
   const rai_model_config &c = md.cfg;
   // validate_lookup_config (lookup.rs:457-475), greedy variant.
@@ -916,7 +920,7 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
   const size_t budget = d.max_ctx > pos + 1 ? d.max_ctx - pos - 1 : 0;
   int *res = d.res.as<int>();
   int nd = 0, start = 0, ngram = 0;
-  if (budget > 0) {
+  if (budget > 0 && search) {
     if (!prefetched) {
       launch_ngram(d.ctx.as<uint32_t>(), (int)len, (int)cfg.min_ngram, (int)cfg.max_ngram,
                    (int)std::min(cfg.max_draft, budget), res, s);
@@ -1866,30 +1870,43 @@ int rai_kv_import(rai_kv *kv, size_t layer, int which, const float *rows, size_t
   });
 }
 
+namespace rai {
+
+// The plain greedy decode loop from a prefilled state (context[len - 1] is
+// the token at pos): decode_one per token (lookup.rs:428-455) with argmax
+// sampling, as run.rs:692-735 at temperature 0.
+static void greedy_decode(rai_lookup &d, const uint32_t *context, size_t len, size_t pos, size_t steps,
+                          uint32_t *out) {
+  const rai_lookup_config plain{1, 1, 1, 0.0f};  // search parameters unused (no search)
+  std::vector<uint32_t> ctx(context, context + len);
+  ctx.reserve(len + steps);
+  uint32_t tok[2];
+  for (size_t i = 0; i < steps; ++i) {
+    if (pos >= d.max_ctx) fail(RAI_E_RANGE, "generation exceeds the context window");
+    rai_lookup_metrics met{};
+    lookup_step(d, pos, ctx.data(), ctx.size(), plain, tok, 2, met, false);
+    out[i] = tok[0];
+    ctx.push_back(tok[0]);
+    ++pos;
+  }
+}
+
+}  // namespace rai
+
 int rai_greedy_generate(rai_lookup *d, const uint32_t *prompt, size_t n, size_t steps, uint32_t *out) {
   RAI_API_BODY({
     if (!d || !prompt || !out) rai::fail(RAI_E_ARG, "null argument");
     size_t pos = 0;
     rai::lookup_prefill(*d, prompt, n, pos);
-    std::vector<uint32_t> ctx(prompt, prompt + n);
-    rai_model &md = *d->model;
-    for (size_t i = 0; i < steps; ++i) {
-      if (pos >= d->max_ctx) rai::fail(RAI_E_RANGE, "generation exceeds the context window");
-      // decode_one (lookup.rs:428-455) with argmax sampling.
-      rai::sync_context(*d, ctx.data(), ctx.size());
-      launch_embed(nullptr, d->ctx.as<uint32_t>(), (int)ctx.size() - 1, 0, 1, md.emb_codes, md.emb_params,
-                   md.cfg.vocab_size, md.cfg.hidden_size, md.cfg.embed_group_size, md.cfg.embed_scale,
-                   d->ws.hid.as<float>(), d->ws.err.as<int>(), d->stream);
-      rai::forward(md, d->kv, d->ws, 1, pos, d->stream);
-      rai::logits(md, d->ws, 1, d->stream);
-      launch_argmax(d->ws.logits.as<float>(), 1, md.cfg.vocab_size, d->ws.am.as<uint32_t>(), d->stream);
-      uint32_t tok = 0;
-      HIP_CHECK(hipMemcpyAsync(&tok, d->ws.am.p, 4, hipMemcpyDeviceToHost, d->stream));
-      rai::check_kernel_error(d->ws, d->stream);
-      out[i] = tok;
-      ctx.push_back(tok);
-      ++pos;
-    }
+    rai::greedy_decode(*d, prompt, n, pos, steps, out);
+  });
+}
+
+int rai_greedy_decode(rai_lookup *d, const uint32_t *context, size_t len, size_t pos, size_t steps, uint32_t *out) {
+  RAI_API_BODY({
+    if (!d || !context || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (len == 0 || pos + 1 != len) rai::fail(RAI_E_ARG, "context[len - 1] must be the token at pos");
+    rai::greedy_decode(*d, context, len, pos, steps, out);
   });
 }
 

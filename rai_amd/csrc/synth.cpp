@@ -24,6 +24,13 @@
 #include "format.h"
 
 namespace rai {
+
+// A synthetic image in malloc'd memory (freed with std::free).
+struct SynthImage {
+  uint8_t *data = nullptr;
+  size_t size = 0;
+};
+
 namespace {
 
 constexpr double kMinF16Scale = 5.9604644775390625e-08;  // 2^-24 (raimodel.py:65)
@@ -92,17 +99,6 @@ struct Lcg {  // gen_convert_fixture.py:53-71
   float norm() { return (float)(1.0 + ((double)(next() % 201) - 100.0) / 1024.0); }
 };
 
-struct Writer {
-  std::vector<uint8_t> buf;
-  void u32(uint32_t v) { raw(&v, 4); }
-  void f32(float v) { raw(&v, 4); }
-  void u16(uint16_t v) { raw(&v, 2); }
-  void raw(const void *p, size_t n) {
-    const uint8_t *b = (const uint8_t *)p;
-    buf.insert(buf.end(), b, b + n);
-  }
-};
-
 // Asymmetric min/max params for one row group (compute_group_params).
 void minmax_params(const float *w, int n, int levels, uint16_t &s16, uint16_t &z16, double &s64,
                    double &z64) {
@@ -118,15 +114,65 @@ void minmax_params(const float *w, int n, int levels, uint16_t &s16, uint16_t &z
   z64 = f16_bits_to_f32(z16);
 }
 
-// Quantize one [rows][cols] weight matrix and append it as a linear
-// ([u32 rows][u32 cols][params][nibbles], raimodel.py:518-526).
-void put_linear(Writer &w, const std::vector<float> &wt, int rows, int cols, int gs, bool sym) {
+int synth_threads() { return std::max(1, std::min<int>((int)std::thread::hardware_concurrency(), 16)); }
+
+// fn(r0, r1) over [0, rows) split across the worker threads.
+template <class F>
+void parallel_rows(size_t rows, F fn) {
+  const int nt = (int)std::min<size_t>(synth_threads(), std::max<size_t>(rows, 1));
+  std::vector<std::thread> th;
+  for (int i = 0; i < nt; ++i) th.emplace_back(fn, rows * i / nt, rows * (i + 1) / nt);
+  for (auto &t : th) t.join();
+}
+
+// The weights of one tensor, row by row: N(0, std) from the counter hash
+// (element j = r * cols + c of tensor `tid`; pairs of elements share one
+// Box-Muller draw, so both come from one log / sqrt / sincos), or rows of a
+// tensor generated up front (the fixture LCG).
+struct Source {
+  uint64_t seed = 0, tid = 0;
+  float stdv = 0.0f;
+  const float *pre = nullptr;  // pre-generated [rows][cols], or null
+  void row(size_t r, size_t cols, float *out) const {
+    if (pre) {
+      std::memcpy(out, pre + r * cols, cols * sizeof(float));
+      return;
+    }
+    size_t j = r * cols, c = 0;
+    if (j & 1) out[c++] = gauss(seed, tid, j++, stdv);
+    for (; c + 1 < cols; c += 2, j += 2) {
+      const uint64_t h = splitmix(seed ^ splitmix(tid * 0x100000001B3ull + (j >> 1)));
+      const uint64_t h2 = splitmix(h);
+      const double u1 = ((h >> 11) + 1.0) * (1.0 / 9007199254740993.0);
+      const double u2 = (h2 >> 11) * (1.0 / 9007199254740992.0);
+      const double rr = std::sqrt(-2.0 * std::log(u1));
+      out[c] = (float)(stdv * (rr * std::cos(6.283185307179586 * u2)));
+      out[c + 1] = (float)(stdv * (rr * std::sin(6.283185307179586 * u2)));
+    }
+    if (c < cols) out[c] = gauss(seed, tid, j, stdv);
+  }
+};
+
+// Bytes of one linear record ([u32 rows][u32 cols][params][nibbles],
+// raimodel.py:518-526).
+size_t linear_bytes(size_t rows, size_t cols, int gs) {
+  return 8 + rows * ((cols + gs - 1) / gs) * 4 + rows * cols / 2;
+}
+
+// Quantize a [rows][cols] weight matrix row by row into its linear record at
+// dst (int4 codes, symmetric or min/max RTN per group).
+void put_linear(uint8_t *dst, const Source &src, int rows, int cols, int gs, bool sym) {
+  if (cols % 2) fail(RAI_E_ARG, "synthetic linear needs an even column count");
   const int groups = (cols + gs - 1) / gs;
-  std::vector<uint16_t> params((size_t)rows * groups * 2);
-  std::vector<uint8_t> codes((size_t)rows * cols);
-  auto work = [&](int r0, int r1) {
-    for (int r = r0; r < r1; ++r) {
-      const float *row = &wt[(size_t)r * cols];
+  const uint32_t hdr[2] = {(uint32_t)rows, (uint32_t)cols};
+  std::memcpy(dst, hdr, 8);
+  uint8_t *params = dst + 8;
+  uint8_t *nib = params + (size_t)rows * groups * 4;
+  parallel_rows(rows, [&](size_t r0, size_t r1) {
+    std::vector<float> row(cols);
+    std::vector<uint8_t> codes(cols);
+    for (size_t r = r0; r < r1; ++r) {
+      src.row(r, cols, row.data());
       for (int g = 0; g < groups; ++g) {
         const int c0 = g * gs, c1 = std::min(cols, c0 + gs);
         uint16_t s16, z16;
@@ -139,58 +185,68 @@ void put_linear(Writer &w, const std::vector<float> &wt, int rows, int cols, int
           z16 = f64_to_f16(-8.0 * s64);
           for (int c = c0; c < c1; ++c) {
             const double q = std::min(7.0, std::max(-8.0, std::nearbyint((double)row[c] / s64)));
-            codes[(size_t)r * cols + c] = (uint8_t)((int)q + 8);
+            codes[c] = (uint8_t)((int)q + 8);
           }
         } else {
-          minmax_params(row + c0, c1 - c0, 16, s16, z16, s64, z64);
+          minmax_params(row.data() + c0, c1 - c0, 16, s16, z16, s64, z64);
           for (int c = c0; c < c1; ++c) {
             const double q = std::min(15.0, std::max(0.0, std::nearbyint(((double)row[c] - z64) / s64)));
-            codes[(size_t)r * cols + c] = (uint8_t)q;
+            codes[c] = (uint8_t)q;
           }
         }
-        params[((size_t)r * groups + g) * 2] = s16;
-        params[((size_t)r * groups + g) * 2 + 1] = z16;
+        const uint16_t p2[2] = {s16, z16};
+        std::memcpy(params + (r * groups + g) * 4, p2, 4);
       }
+      uint8_t *nr = nib + r * (size_t)cols / 2;
+      for (int i = 0; i < cols / 2; ++i) nr[i] = (uint8_t)((codes[2 * i] & 0x0F) | ((codes[2 * i + 1] & 0x0F) << 4));
     }
-  };
-  const int nt = std::max(1, std::min<int>((int)std::thread::hardware_concurrency(), 16));
-  std::vector<std::thread> th;
-  for (int i = 0; i < nt; ++i) th.emplace_back(work, rows * i / nt, rows * (i + 1) / nt);
-  for (auto &t : th) t.join();
-  w.u32(rows);
-  w.u32(cols);
-  w.raw(params.data(), params.size() * 2);
-  const size_t base = w.buf.size();
-  w.buf.resize(base + (size_t)rows * cols / 2);
-  for (size_t i = 0; i < (size_t)rows * cols / 2; ++i)
-    w.buf[base + i] = (uint8_t)((codes[2 * i] & 0x0F) | ((codes[2 * i + 1] & 0x0F) << 4));
+  });
 }
 
-void put_embedding(Writer &w, const std::vector<float> &wt, int vocab, int hidden, int egs) {
+// The 8-bit min/max embedding (quantize_embedding_8bit): params
+// [vocab][groups] x (scale, zero) f16, then codes [vocab][hidden].
+size_t embedding_bytes(size_t vocab, size_t hidden, int egs) {
+  return vocab * ((hidden + egs - 1) / egs) * 4 + vocab * hidden;
+}
+
+void put_embedding(uint8_t *dst, const Source &src, int vocab, int hidden, int egs) {
   const int groups = (hidden + egs - 1) / egs;
-  std::vector<uint16_t> params((size_t)vocab * groups * 2);
-  std::vector<uint8_t> codes((size_t)vocab * hidden);
-  for (int v = 0; v < vocab; ++v)
-    for (int g = 0; g < groups; ++g) {
-      const int c0 = g * egs, c1 = std::min(hidden, c0 + egs);
-      uint16_t s16, z16;
-      double s64, z64;
-      minmax_params(&wt[(size_t)v * hidden + c0], c1 - c0, 256, s16, z16, s64, z64);
-      params[((size_t)v * groups + g) * 2] = s16;
-      params[((size_t)v * groups + g) * 2 + 1] = z16;
-      for (int c = c0; c < c1; ++c) {
-        const double q = std::min(
-            255.0, std::max(0.0, std::nearbyint(((double)wt[(size_t)v * hidden + c] - z64) / s64)));
-        codes[(size_t)v * hidden + c] = (uint8_t)q;
+  uint8_t *params = dst;
+  uint8_t *codes = dst + (size_t)vocab * groups * 4;
+  parallel_rows(vocab, [&](size_t v0, size_t v1) {
+    std::vector<float> row(hidden);
+    for (size_t v = v0; v < v1; ++v) {
+      src.row(v, hidden, row.data());
+      for (int g = 0; g < groups; ++g) {
+        const int c0 = g * egs, c1 = std::min(hidden, c0 + egs);
+        uint16_t s16, z16;
+        double s64, z64;
+        minmax_params(row.data() + c0, c1 - c0, 256, s16, z16, s64, z64);
+        const uint16_t p2[2] = {s16, z16};
+        std::memcpy(params + (v * groups + g) * 4, p2, 4);
+        for (int c = c0; c < c1; ++c) {
+          const double q = std::min(255.0, std::max(0.0, std::nearbyint(((double)row[c] - z64) / s64)));
+          codes[v * hidden + c] = (uint8_t)q;
+        }
       }
     }
-  w.raw(params.data(), params.size() * 2);
-  w.raw(codes.data(), codes.size());
+  });
+}
+
+// A raw f32 tensor (router) or a norm vector of ones.
+void put_f32(uint8_t *dst, const Source &src, int rows, int cols) {
+  parallel_rows(rows, [&](size_t r0, size_t r1) {
+    for (size_t r = r0; r < r1; ++r) src.row(r, cols, reinterpret_cast<float *>(dst) + r * cols);
+  });
 }
 
 }  // namespace
 
-std::vector<uint8_t> synth_model(const rai_synth_config &c, uint64_t seed) {
+// The image is assembled in place: the section sizes follow from the shape,
+// so one buffer is allocated and every tensor is quantized straight into its
+// slot, row by row on the worker threads.  Tensor ids (the generator's
+// streams) are taken in file order, as the reference exporter writes them.
+SynthImage synth_model(const rai_synth_config &c, uint64_t seed) {
   if (c.mode > 2) fail(RAI_E_ARG, "unknown synth mode");
   if (c.num_experts != 0 && c.mode == 2) fail(RAI_E_ARG, "the LCG fixture mode is dense only");
   const int H = c.hidden_size, F = c.intermediate_size, V = c.vocab_size, L = c.num_layers;
@@ -200,105 +256,118 @@ std::vector<uint8_t> synth_model(const rai_synth_config &c, uint64_t seed) {
     fail(RAI_E_ARG, "invalid synthetic model shape");
   const bool sym = c.mode == 0;
   const bool v2 = c.num_experts > 0;
-  Lcg lcg{0x20260813ull};
-  uint64_t tid = 0;
-  auto tensor = [&](size_t rows, size_t cols, bool is_norm = false) {
-    std::vector<float> t(rows * cols);
-    if (c.mode == 2) {
-      for (auto &x : t) x = is_norm ? lcg.norm() : lcg.weight();
-    } else if (is_norm) {
-      std::fill(t.begin(), t.end(), 1.0f);
-    } else {
-      const uint64_t id = ++tid;
-      const size_t n = t.size();
-      const int nt = std::max(1, std::min<int>((int)std::thread::hardware_concurrency(), 16));
-      std::vector<std::thread> th;
-      for (int i = 0; i < nt; ++i)
-        th.emplace_back([&, i] {
-          for (size_t j = n * i / nt; j < n * (i + 1) / nt; ++j) t[j] = gauss(seed, id, j, c.weight_std);
-        });
-      for (auto &x : th) x.join();
-    }
-    return t;
-  };
-  std::vector<std::vector<uint8_t>> sections;
-  {
-    Writer w;
-    put_embedding(w, tensor(V, H), V, H, egs);
-    sections.push_back(std::move(w.buf));
-  }
   const int dims[7][2] = {{qd, H}, {kvd, H}, {kvd, H}, {H, qd}, {F, H}, {F, H}, {H, F}};
-  for (int l = 0; l < L; ++l) {
-    Writer w;
-    for (int p = 0; p < 7; ++p) put_linear(w, tensor(dims[p][0], dims[p][1]), dims[p][0], dims[p][1], gs, sym);
-    if (v2) {
-      std::vector<float> router = tensor(c.num_experts, H);
-      w.raw(router.data(), router.size() * 4);
-      for (uint32_t e = 1; e < c.num_experts; ++e)
-        for (int p = 4; p < 7; ++p)
-          put_linear(w, tensor(dims[p][0], dims[p][1]), dims[p][0], dims[p][1], gs, sym);
-    }
-    std::vector<float> n1 = tensor(1, H, true), n2 = tensor(1, H, true);
-    w.raw(n1.data(), H * 4);
-    w.raw(n2.data(), H * 4);
-    sections.push_back(std::move(w.buf));
-  }
-  {
-    std::vector<float> fn = tensor(1, H, true);
-    Writer w;
-    w.raw(fn.data(), H * 4);
-    sections.push_back(std::move(w.buf));
-  }
-  if (!c.tied) {
-    Writer w;
-    put_linear(w, tensor(V, H), V, H, gs, sym);
-    sections.push_back(std::move(w.buf));
-  }
-  // Header (raimodel.py:558-579; v2 capability block per format.rs:21-40).
-  Writer out;
-  const size_t hsz = v2 ? 128 : 64;
-  out.buf.assign(hsz, 0);
-  std::memcpy(out.buf.data(), "RAIM", 4);
-  auto put32 = [&](size_t off, uint32_t v) { std::memcpy(out.buf.data() + off, &v, 4); };
-  auto putf = [&](size_t off, float v) { std::memcpy(out.buf.data() + off, &v, 4); };
-  put32(4, v2 ? 2 : 1);
-  put32(8, H);
-  put32(12, L);
-  put32(16, c.num_heads);
-  put32(20, c.num_kv_heads);
-  put32(24, c.head_dim);
-  put32(28, F);
-  put32(32, V);
-  put32(36, c.max_context);
-  putf(40, c.rope_theta);
-  putf(44, c.norm_eps);
-  out.buf[48] = 4;
-  out.buf[49] = (uint8_t)gs;
-  out.buf[50] = 8;
-  out.buf[51] = (uint8_t)egs;
-  put32(52, (uint32_t)sections.size());
+  // Section sizes.
+  std::vector<size_t> sec;
+  sec.push_back(embedding_bytes(V, H, egs));
+  size_t layer = 0;
+  for (int p = 0; p < 7; ++p) layer += linear_bytes(dims[p][0], dims[p][1], gs);
   if (v2) {
-    putf(84, 1.0f);  // embed_scale
-    const uint16_t ne = (uint16_t)c.num_experts;
-    std::memcpy(out.buf.data() + 105, &ne, 2);
-    out.buf[107] = (uint8_t)c.experts_per_token;
-    out.buf[108] = c.norm_topk_prob ? 1 : 0;
+    layer += (size_t)c.num_experts * H * 4;
+    for (uint32_t e = 1; e < c.num_experts; ++e)
+      for (int p = 4; p < 7; ++p) layer += linear_bytes(dims[p][0], dims[p][1], gs);
   }
-  uint64_t off = hsz + sections.size() * 16;
-  for (auto &s : sections) {
-    const uint64_t sz = s.size();
-    out.raw(&off, 8);
-    out.raw(&sz, 8);
-    off += sz;
+  layer += 2 * (size_t)H * 4;
+  for (int l = 0; l < L; ++l) sec.push_back(layer);
+  sec.push_back((size_t)H * 4);
+  if (!c.tied) sec.push_back(linear_bytes(V, H, gs));
+  const size_t hsz = v2 ? 128 : 64;
+  size_t total = hsz + sec.size() * 16;
+  for (size_t b : sec) total += b;
+  SynthImage img;
+  img.data = static_cast<uint8_t *>(std::malloc(total));
+  if (!img.data) fail(RAI_E_OOM, "image allocation failed");
+  img.size = total;
+  uint8_t *const out = img.data;
+  try {
+    // Header (raimodel.py:558-579; v2 capability block per format.rs:21-40).
+    std::memset(out, 0, hsz);
+    std::memcpy(out, "RAIM", 4);
+    auto put32 = [&](size_t off, uint32_t v) { std::memcpy(out + off, &v, 4); };
+    auto putf = [&](size_t off, float v) { std::memcpy(out + off, &v, 4); };
+    put32(4, v2 ? 2 : 1);
+    put32(8, H);
+    put32(12, L);
+    put32(16, c.num_heads);
+    put32(20, c.num_kv_heads);
+    put32(24, c.head_dim);
+    put32(28, F);
+    put32(32, V);
+    put32(36, c.max_context);
+    putf(40, c.rope_theta);
+    putf(44, c.norm_eps);
+    out[48] = 4;
+    out[49] = (uint8_t)gs;
+    out[50] = 8;
+    out[51] = (uint8_t)egs;
+    put32(52, (uint32_t)sec.size());
+    if (v2) {
+      putf(84, 1.0f);  // embed_scale
+      const uint16_t ne = (uint16_t)c.num_experts;
+      std::memcpy(out + 105, &ne, 2);
+      out[107] = (uint8_t)c.experts_per_token;
+      out[108] = c.norm_topk_prob ? 1 : 0;
+    }
+    uint64_t off = hsz + sec.size() * 16;
+    for (size_t i = 0; i < sec.size(); ++i) {
+      const uint64_t sz = sec[i];
+      std::memcpy(out + hsz + 16 * i, &off, 8);
+      std::memcpy(out + hsz + 16 * i + 8, &sz, 8);
+      off += sz;
+    }
+    uint8_t *w = out + hsz + sec.size() * 16;
+    Lcg lcg{0x20260813ull};
+    uint64_t tid = 0;
+    std::vector<float> pre;  // the LCG mode's tensor, generated in file order
+    auto source = [&](size_t rows, size_t cols) {
+      Source s;
+      if (c.mode == 2) {
+        pre.resize(rows * cols);
+        for (auto &x : pre) x = lcg.weight();
+        s.pre = pre.data();
+      } else {
+        s.seed = seed;
+        s.tid = ++tid;
+        s.stdv = c.weight_std;
+      }
+      return s;
+    };
+    auto norm = [&](uint8_t *dst) {
+      float *f = reinterpret_cast<float *>(dst);
+      for (int i = 0; i < H; ++i) f[i] = c.mode == 2 ? lcg.norm() : 1.0f;
+    };
+    put_embedding(w, source(V, H), V, H, egs);
+    w += sec[0];
+    for (int l = 0; l < L; ++l) {
+      for (int p = 0; p < 7; ++p) {
+        put_linear(w, source(dims[p][0], dims[p][1]), dims[p][0], dims[p][1], gs, sym);
+        w += linear_bytes(dims[p][0], dims[p][1], gs);
+      }
+      if (v2) {
+        put_f32(w, source(c.num_experts, H), c.num_experts, H);
+        w += (size_t)c.num_experts * H * 4;
+        for (uint32_t e = 1; e < c.num_experts; ++e)
+          for (int p = 4; p < 7; ++p) {
+            put_linear(w, source(dims[p][0], dims[p][1]), dims[p][0], dims[p][1], gs, sym);
+            w += linear_bytes(dims[p][0], dims[p][1], gs);
+          }
+      }
+      norm(w);
+      norm(w + (size_t)H * 4);
+      w += 2 * (size_t)H * 4;
+    }
+    norm(w);
+    w += (size_t)H * 4;
+    if (!c.tied) {
+      put_linear(w, source(V, H), V, H, gs, sym);
+      w += linear_bytes(V, H, gs);
+    }
+    if ((size_t)(w - out) != total) fail(RAI_E_ARG, "synthetic image size mismatch");
+  } catch (...) {
+    std::free(img.data);
+    throw;
   }
-  size_t total = out.buf.size();
-  for (auto &s : sections) total += s.size();
-  out.buf.reserve(total);
-  for (auto &s : sections) {
-    out.raw(s.data(), s.size());
-    std::vector<uint8_t>().swap(s);
-  }
-  return std::move(out.buf);
+  return img;
 }
 
 }  // namespace rai
@@ -307,21 +376,22 @@ extern "C" int rai_synth_model(const rai_synth_config *cfg, uint64_t seed, const
                                uint8_t **image, size_t *image_len) {
   RAI_API_BODY({
     if (!cfg) rai::fail(RAI_E_ARG, "null config");
-    std::vector<uint8_t> img = rai::synth_model(*cfg, seed);
+    if (!path && (!image || !image_len)) rai::fail(RAI_E_ARG, "image output pointers are null");
+    rai::SynthImage img = rai::synth_model(*cfg, seed);
     if (path) {
       FILE *f = std::fopen(path, "wb");
-      if (!f) rai::fail(RAI_E_IO, std::string("cannot open ") + path);
-      const size_t n = std::fwrite(img.data(), 1, img.size(), f);
+      if (!f) {
+        std::free(img.data);
+        rai::fail(RAI_E_IO, std::string("cannot open ") + path);
+      }
+      const size_t n = std::fwrite(img.data, 1, img.size, f);
       const int rc = std::fclose(f);
-      if (n != img.size() || rc != 0) rai::fail(RAI_E_IO, std::string("short write to ") + path);
-      if (image_len) *image_len = img.size();
+      std::free(img.data);
+      if (n != img.size || rc != 0) rai::fail(RAI_E_IO, std::string("short write to ") + path);
+      if (image_len) *image_len = img.size;
     } else {
-      if (!image || !image_len) rai::fail(RAI_E_ARG, "image output pointers are null");
-      uint8_t *p = (uint8_t *)std::malloc(img.size());
-      if (!p) rai::fail(RAI_E_OOM, "image allocation failed");
-      std::memcpy(p, img.data(), img.size());
-      *image = p;
-      *image_len = img.size();
+      *image = img.data;  // the caller frees it with rai_free_image
+      *image_len = img.size;
     }
   });
 }

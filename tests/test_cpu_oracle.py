@@ -401,6 +401,15 @@ def test_oracle_greedy_lookup_equals_greedy_decode(ora, rai):
         assert dec.kv_filled() == pos
     assert got[:steps] == want
     assert drafted > 0
+    # decode_one from the prefilled state gives the same stream.
+    dec1 = ora.LookupDecoder(m, 256)
+    pos = dec1.prefill(prompt)
+    last, plain = int(prompt[-1]), []
+    for _ in range(steps):
+        last = dec1.decode_one(pos, last)
+        plain.append(last)
+        pos += 1
+    assert plain == want
 
 
 # ------------------------------------------------------- product, host side --
