@@ -38,9 +38,18 @@ an exact-sampling generation (temperature 0.7, the decoder's StdRng), the
 forced k = 8 verify step, the 4095-token prefill, every W4A8 shape of the
 model step at 1 and 9 tokens, the prefill GEMM at M = 512 (the matrix-core
 kernel; its integer-op rate against the 5 POPS int8 dense peak and its f32
-epilogue rate against the VALU peak), and config 5: the OLMoE-1B-7B-shaped
-MoE decoder with a 2048-token copy-heavy prompt and 128 generated tokens
-(grouped-expert GEMVs on the device).
+epilogue rate against the VALU peak), and the other configurations:
+  config 1  TinyLlama-1.1B shape, 128-token uniform prompt, greedy decode of
+            128 tokens without speculation (tok/s, GB/s, HBM fraction, CPU);
+  config 2  the same model, 2048-token copy-heavy prompt, prompt lookup n=3
+            k=8 greedy, 256 tokens (acceptance, tokens/step, steps drafted,
+            tok/s, token identity, CPU);
+  config 3  the W4A8 sweep: M in {1, 5, 9, 17} on the four sweep shapes
+            (µs, GB/s, HBM fraction) and M = 512 (integer-op rate against the
+            int8 peak, epilogue rate against the VALU peak);
+  config 5  the OLMoE-1B-7B-shaped MoE decoder, 2048-token copy-heavy prompt,
+            128 tokens (grouped-expert GEMVs on the device; tok/s, plain
+            decode HBM fraction, token identity, CPU).
 
 `--gpus N` with N > 1 is refused: this build runs on one GPU.
 """
@@ -223,7 +232,6 @@ def olmoe_line(args) -> dict:
                               s["intermediate_size"], s["vocab_size"], 4096, group_size=32,
                               num_experts=s["num_experts"], experts_per_token=s["experts_per_token"], seed=77)
     model = rai_amd.RaiModel.from_bytes(img, max_groups=1024)
-    del img
     log(f"olmoe: synthetic model and upload in {time.perf_counter() - t0:.1f}s")
     cfg = rai_amd.LookupConfig(max_draft=8, min_ngram=3, max_ngram=3, temperature=0.0)
     dec = rai_amd.LookupDecoder(model, 4096)
@@ -244,11 +252,28 @@ def olmoe_line(args) -> dict:
     el = time.perf_counter() - t0
     tok_s = runs * st["generated"] / el
     dec.kv_cache.truncate(pos)
+    greedy = dec.greedy_decode(prompt, pos, len(toks))  # the last lookup step may overshoot ntok
+    # Plain greedy decoding from the same state: its rate gives the decode
+    # step's HBM fraction (active weights + the mean context's K and V).
+    t0 = time.perf_counter()
+    for _ in range(runs):
+        dec.kv_cache.truncate(pos)
+        dec.greedy_decode(prompt, pos, ntok)
+    plain_tok_s = runs * ntok / (time.perf_counter() - t0)
+    wb = model.weight_bytes()
+    kvpp = s["num_layers"] * 2 * s["num_kv_heads"] * s["head_dim"] * 4
+    step_bytes = wb + kvpp * (pos + 1 + (ntok - 1) / 2.0)
+    plain_gbs = step_bytes * plain_tok_s / 1e9
+    dec.kv_cache.truncate(pos)
     vt, _ = forced_verify_steps(dec, list(prompt), pos, cfg, 18)
     vms = 1e3 * float(np.mean(vt[2:]))
-    wb = model.weight_bytes()
-    log(f"olmoe: {tok_s:.1f} tok/s ({st['steps_with_draft']} steps drafted), verify step {vms:.3f} ms, "
-        f"prefill {prefill_s:.2f}s")
+    ref_threads, _ = reference_threads()
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(img, s, dec, prompt, pos, toks, args.cpu_seconds / 2, ref_threads)
+    log(f"olmoe: {tok_s:.1f} tok/s ({st['steps_with_draft']} steps drafted), plain decode {plain_tok_s:.1f} tok/s "
+        f"({plain_gbs / HBM_PEAK_GBS:.3f} of HBM), identical to greedy: {greedy == toks}, verify step {vms:.3f} ms, "
+        f"prefill {prefill_s:.2f}s" + (f", cpu {cpu[0]:.2f} tok/s" if cpu else ""))
     return {"workload": "olmoe-1b-7b-shaped W4A8 g32, 64 experts top-8, 2048-token copy-heavy prompt, "
                         "prompt-lookup n=3 k=8 greedy, 128 tokens, batch 1",
             "value_tok_s": round(tok_s, 2), "generations": runs,
@@ -256,8 +281,14 @@ def olmoe_line(args) -> dict:
             "accepted_draft_tokens": st["accepted"],
             "acceptance_rate": round(st["accepted"] / st["drafted"], 4) if st["drafted"] else None,
             "verify_step_ms": round(vms, 4), "prefill_seconds": round(prefill_s, 4),
+            "token_identical_to_greedy": greedy == toks,
+            "plain_decode_tok_s": round(plain_tok_s, 2),
+            "plain_decode_bytes_per_token": int(step_bytes), "plain_decode_gbs": round(plain_gbs, 1),
+            "plain_decode_hbm_frac": round(plain_gbs / HBM_PEAK_GBS, 4),
             "decode_weight_bytes_per_token": wb,
-            "decode_weight_gbs": round(wb * st["generated"] / (el / runs) / 1e9, 1)}
+            "decode_weight_gbs": round(wb * st["generated"] / (el / runs) / 1e9, 1),
+            "cpu_baseline": cpu_entry(cpu, ref_threads, f"greedy lookup n=3 k=8 from the GPU's state after the "
+                                                        f"{pos}-token prefill") if cpu else None}
 
 
 def attention_kernels(rai, shape, pos: int, cap: int) -> dict:
@@ -320,10 +351,11 @@ def host_cpu() -> tuple[str, int]:
     return name, n
 
 
-def cpu_baseline(img, shape, dec, context, pos, gpu_tokens, seconds: float, threads: int):
-    """The oracle's greedy lookup steps from the GPU decoder's state after the
-    prefill (every layer's K/V rows copied over), at the workload's context
-    length, for about `seconds`.  Returns (tok/s, tokens, seconds, matches):
+def cpu_baseline(img, shape, dec, context, pos, gpu_tokens, seconds: float, threads: int, lookup: bool = True):
+    """The oracle's greedy lookup steps (n=3, k=8), or with lookup=False its
+    plain decode_one steps, from the GPU decoder's state after the prefill
+    (every layer's K/V rows copied over), at the workload's context length,
+    for about `seconds`.  Returns (tok/s, tokens, seconds, matches):
     `matches` is whether the oracle's tokens equal the GPU's."""
     from oracle import ora
     ora.set_threads(threads)
@@ -337,14 +369,149 @@ def cpu_baseline(img, shape, dec, context, pos, gpu_tokens, seconds: float, thre
     produced = 0
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds and produced < len(gpu_tokens):
-        toks, met = od.step(pos, ctx, 8, 3, 3)
+        if lookup:
+            toks, met = od.step(pos, ctx, 8, 3, 3)
+            n = met.produced
+        else:
+            toks, n = [od.decode_one(pos, ctx[-1])], 1
         ctx += toks
-        pos += met.produced
-        produced += met.produced
+        pos += n
+        produced += n
     dt = time.perf_counter() - t0
     got = ctx[len(context):]
     matches = got == list(gpu_tokens[:len(got)])
     return produced / dt, produced, dt, matches
+
+
+def reference_threads() -> tuple[int, int]:
+    """(the reference's default thread count, the one-GPU share of the host):
+    configure_thread_pool (gemm.rs:1746-1761) uses max(cpus/2 + 1, 2)."""
+    _, ncpu = host_cpu()
+    share = min(ncpu, 16)
+    return max(share // 2 + 1, 2), share
+
+
+def cpu_entry(res, threads: int, what: str) -> dict:
+    cv, cprod, cdt, cmatch = res
+    return {"value": round(cv, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle, {threads} threads: {what}; {cprod} tokens in {cdt:.1f}s",
+            "tokens_equal_gpu": cmatch}
+
+
+def config3_sweep(rai) -> dict:
+    """Config 3: the isolated W4A8 sweep on the four sweep shapes (int4 g32,
+    f16 scales; N(0, 1) activations quantized per group).  M in {1, 5, 9, 17}:
+    HBM-bound, µs / GB/s / fraction of 8 TB/s with the weights streamed from
+    HBM (rotating copies).  M = 512: the matrix-core GEMM, its integer-op rate
+    against the 5 POPS int8 dense peak and its epilogue's f32 operation rate
+    (11 ordered operations per row, token and group) against the VALU peak."""
+    from rai_amd.workload import GEMV_SHAPES, gemv_operands
+    out = {}
+    for n, k in GEMV_SHAPES:
+        nib, params, x = gemv_operands(n, k, 512, 32, seed=n + k)
+        copies = max(1, int(-(-ROTATE_BYTES // (nib.nbytes + params.nbytes))))
+        t = rai.GemvTimer(nib, params, n, k, 32, copies)
+        ent = {}
+        for m in (1, 5, 9, 17):
+            ms = float(np.median([t.time(x[:m], m, iters=30) for _ in range(3)]))
+            b = gemv_algorithmic_bytes(n, k, m, 32)
+            gbs = b / (ms * 1e-3) / 1e9
+            ent[f"m{m}"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        ms = t.time(x, 512, iters=10)
+        tops = 2.0 * n * k * 512 / (ms * 1e-3) / 1e12
+        valu = 11.0 * n * (k // 32) * 512 / (ms * 1e-3) / 1e9
+        ent["m512"] = {"us": round(ms * 1e3, 1), "int_tops": round(tops, 1),
+                       "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                       "epilogue_valu_frac": round(valu / VALU_PEAK_GOPS, 4)}
+        out[f"{n}x{k}"] = ent
+        del t
+    log("config 3: " + "; ".join(f"{sh} " + ", ".join(f"{m} {v.get('frac', v.get('frac_of_int8_peak'))}"
+                                                       for m, v in e.items()) for sh, e in out.items()))
+    return out
+
+
+def tinyllama_configs(args) -> tuple[dict, dict]:
+    """Configs 1 and 2 on the TinyLlama-1.1B shape (22 layers, hidden 2048,
+    FFN 5632, 32 q-heads / 4 kv-heads of 64, vocab 32000), random-init W4A8
+    g32.  Config 1: a 128-token uniform-random prompt, greedy decoding of 128
+    tokens, speculation off.  Config 2: a 2048-token copy-heavy prompt,
+    prompt lookup n=3 k=8 greedy, 256 tokens.  Each with the CPU oracle on the
+    same decoder state (KV copied from the GPU) and token identity."""
+    import rai_amd
+    from rai_amd.workload import TINYLLAMA, copy_heavy_prompt, uniform_prompt
+    s = TINYLLAMA
+    max_ctx = 4096
+    t0 = time.perf_counter()
+    img = rai_amd.synth_model(s["hidden_size"], s["num_layers"], s["num_heads"], s["num_kv_heads"], s["head_dim"],
+                              s["intermediate_size"], s["vocab_size"], max_ctx, group_size=32, seed=2025)
+    model = rai_amd.RaiModel.from_bytes(img, max_groups=1024)
+    log(f"tinyllama: synthetic model and upload in {time.perf_counter() - t0:.1f}s")
+    wb = model.weight_bytes()
+    kvpp = s["num_layers"] * 2 * s["num_kv_heads"] * s["head_dim"] * 4
+    ref_threads, _ = reference_threads()
+    runs = 5
+
+    # Config 1.
+    p1 = uniform_prompt(128, s["vocab_size"], seed=128)
+    dec = rai_amd.LookupDecoder(model, max_ctx)
+    t0 = time.perf_counter()
+    pos = dec.prefill(p1)
+    prefill1 = time.perf_counter() - t0
+    n1 = 128
+    dec.greedy_decode(p1, pos, n1)  # warm-up (step graphs)
+    rai_amd.lib().rai_device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(runs):
+        dec.kv_cache.truncate(pos)
+        toks1 = dec.greedy_decode(p1, pos, n1)
+    el = time.perf_counter() - t0
+    tok_s1 = runs * n1 / el
+    step_bytes = wb + kvpp * (pos + 1 + (n1 - 1) / 2.0)  # weights + the mean context's K and V
+    gbs1 = step_bytes * tok_s1 / 1e9
+    c1 = cpu_baseline(img, s, dec, p1, pos, toks1, args.cpu_seconds / 2, ref_threads, lookup=False)
+    log(f"config 1: {tok_s1:.1f} tok/s, {gbs1:.0f} GB/s ({gbs1 / HBM_PEAK_GBS:.3f} of HBM); cpu {c1[0]:.2f} tok/s "
+        f"(tokens equal: {c1[3]})")
+    cfg1 = {"workload": "tinyllama-1.1b-shaped W4A8 g32, 128-token uniform prompt, greedy decode of 128 tokens, "
+                        "speculation off, batch 1",
+            "value_tok_s": round(tok_s1, 2), "generations": runs, "prefill_seconds": round(prefill1, 4),
+            "bytes_per_token": int(step_bytes), "gbs": round(gbs1, 1), "hbm_frac": round(gbs1 / HBM_PEAK_GBS, 4),
+            "cpu_baseline": cpu_entry(c1, ref_threads, f"plain greedy decode_one from the GPU's state after the "
+                                                       f"{pos}-token prefill")}
+    del dec
+
+    # Config 2.
+    p2 = copy_heavy_prompt(2048, s["vocab_size"], seed=2048)
+    dec = rai_amd.LookupDecoder(model, max_ctx)
+    t0 = time.perf_counter()
+    pos = dec.prefill(p2)
+    prefill2 = time.perf_counter() - t0
+    cfg = rai_amd.LookupConfig(max_draft=8, min_ngram=3, max_ngram=3, temperature=0.0)
+    n2 = 256
+    dec.decode(p2, pos, n2, cfg)  # warm-up
+    rai_amd.lib().rai_device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(runs):
+        dec.kv_cache.truncate(pos)
+        toks2, st = dec.decode(p2, pos, n2, cfg)
+    el = time.perf_counter() - t0
+    tok_s2 = runs * st["generated"] / el
+    dec.kv_cache.truncate(pos)
+    greedy2 = dec.greedy_decode(p2, pos, len(toks2))
+    c2 = cpu_baseline(img, s, dec, p2, pos, toks2, args.cpu_seconds / 2, ref_threads)
+    log(f"config 2: {tok_s2:.1f} tok/s, {st['accepted']}/{st['drafted']} accepted, {st['steps_with_draft']}/"
+        f"{st['steps']} steps drafted; identical to greedy: {greedy2 == toks2}; cpu {c2[0]:.2f} tok/s")
+    cfg2 = {"workload": "tinyllama-1.1b-shaped W4A8 g32, 2048-token copy-heavy prompt, prompt-lookup n=3 k=8 "
+                        "greedy, 256 tokens, batch 1",
+            "value_tok_s": round(tok_s2, 2), "generations": runs, "prefill_seconds": round(prefill2, 4),
+            "decoder_steps": st["steps"], "steps_with_draft": st["steps_with_draft"],
+            "pct_steps_drafted": round(100.0 * st["steps_with_draft"] / max(st["steps"], 1), 2),
+            "draft_tokens": st["drafted"], "accepted_draft_tokens": st["accepted"],
+            "acceptance_rate": round(st["accepted"] / st["drafted"], 4) if st["drafted"] else None,
+            "tokens_per_step": round(st["generated"] / max(st["steps"], 1), 4),
+            "token_identical_to_greedy": greedy2 == toks2,
+            "cpu_baseline": cpu_entry(c2, ref_threads, f"greedy lookup n=3 k=8 from the GPU's state after the "
+                                                       f"{pos}-token prefill")}
+    return cfg1, cfg2
 
 
 def forced_verify_steps(dec, context, pos: int, cfg, n_steps: int):
@@ -378,6 +545,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-olmoe", action="store_true", help="skip the config-5 (OLMoE) measurement")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations' figures (configs 1, 2, 3 and 5)")
     ap.add_argument("--roofline-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--profile", choices=["prefill", "greedy", "sampled", "olmoe", "gemm512", "gemv9"],
                     help="run one workload alone (for rocprofv3) and print no JSON line")
@@ -513,9 +682,8 @@ def main() -> int:
 
     cpu, cpu_all, cpu_name = None, None, None
     if not args.no_cpu:
-        cpu_name, ncpu = host_cpu()
-        share = min(ncpu, 16)  # one GPU's share of the host
-        ref_threads = max(share // 2 + 1, 2)  # configure_thread_pool, gemm.rs:1746-1761
+        cpu_name, _ = host_cpu()
+        ref_threads, share = reference_threads()
         res = {}
         for th in (ref_threads, share):
             res[th] = cpu_baseline(img, shape, dec, prompt, pos, toks, args.cpu_seconds, th)
@@ -531,11 +699,21 @@ def main() -> int:
         cpu_all = {"value": round(res[share][0], 3), "threads": share, "tokens_equal_gpu": res[share][3]}
     del img
     del dec, model
-    cfg5 = None
-    if not args.no_olmoe:
+    cfg1 = cfg2 = cfg3 = cfg5 = None
+    if not args.no_configs:
+        # Secondary figures: a failure is reported, and does not fail the line.
+        try:
+            cfg3 = config3_sweep(rai_amd)
+        except Exception as e:
+            log(f"config 3 measurement failed: {e}")
+        try:
+            cfg1, cfg2 = tinyllama_configs(args)
+        except Exception as e:
+            log(f"configs 1 and 2 measurement failed: {e}")
+    if not args.no_olmoe and not args.no_configs:
         try:
             cfg5 = olmoe_line(args)
-        except Exception as e:  # a secondary figure: report, do not fail the line
+        except Exception as e:
             log(f"config 5 measurement failed: {e}")
 
     line = {
@@ -570,6 +748,9 @@ def main() -> int:
                                 "the whole context and never repeats a prompt span, so drafts are rarely "
                                 "accepted and the step is plain decoding plus the occasional failed verify"),
             "prefill_gemm_m512": prefill_gemm,
+            "config1_tinyllama_greedy": cfg1,
+            "config2_tinyllama_lookup": cfg2,
+            "config3_w4a8_sweep": cfg3,
             "config5_olmoe": cfg5,
             "verify_step_ms": round(verify_step_ms, 4),
             "verify_step_note": (f"{len(vt) - 2} timed decoder steps with a forced k=8 draft ({vdrafted} drafted "

@@ -332,6 +332,30 @@ def w4a8_time(nibbles, params, x, rows: int, cols: int, num_tokens: int, group_s
     return ms.value
 
 
+class GemvTimer:
+    """rai_w4a8_time_dev over weights uploaded once: `copies` device copies
+    of one W4A8 matrix, timed at any number of tokens."""
+
+    def __init__(self, nibbles, params, rows: int, cols: int, group_size: int, copies: int = 1):
+        nib = np.ascontiguousarray(nibbles, np.uint8)
+        par = np.ascontiguousarray(params, np.uint8)
+        self.dn = DeviceArray(nib.nbytes * copies)
+        self.dp = DeviceArray(par.nbytes * copies)
+        for c in range(copies):
+            _check(lib().rai_memcpy_h2d(c_void_p(self.dn.ptr + c * nib.nbytes), _ptr(nib), nib.nbytes))
+            _check(lib().rai_memcpy_h2d(c_void_p(self.dp.ptr + c * par.nbytes), _ptr(par), par.nbytes))
+        self.rows, self.cols, self.gs, self.copies = rows, cols, group_size, copies
+
+    def time(self, x, num_tokens: int, iters: int = 50) -> float:
+        """Average device time (ms) of one launch at num_tokens rows of x."""
+        dx = DeviceArray.from_host(_f32(x))
+        do = DeviceArray(num_tokens * self.rows * 4)
+        ms = c_float()
+        _check(lib().rai_w4a8_time_dev(do.ptr, self.dn.ptr, self.dp.ptr, dx.ptr, self.rows, self.cols, num_tokens,
+                                       self.gs, self.copies, iters, ctypes.byref(ms)))
+        return ms.value
+
+
 def w4a8_lane_sums(nibbles, x, rows: int, cols: int, num_tokens: int,
                    group_size: int) -> np.ndarray:
     """Integer accumulators of the W4A8 kernel: [tokens][rows][groups][12]."""
