@@ -37,6 +37,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "kernels.h"
 
@@ -562,44 +563,37 @@ __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, c
   typedef u32x4 u4;
   typedef f32x4 f4;
   const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  // Step -1: zero results, scales and parameters (its epilogue adds +0 to
-  // the +0 accumulators).
+  // MFMA results and staged scales of the previous step (each step runs the
+  // epilogue of the one before; step 0 has none, so nothing is zeroed).
   f4 D[NG][4], as4[NG], xs4[NG];
-#pragma unroll
-  for (int t = 0; t < NG; ++t) {
-    as4[t] = zero4;
-    xs4[t] = zero4;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) D[t][b] = zero4;
-  }
   // Lane offsets of the single-token group's A slots and scale slot.
   auto aoff = [&](int t, int b) { return L1 && t == NG - 1 ? l1off[b] : 0; };
   auto soff = [&](int t) { return L1 && t == NG - 1 ? -hs : 0; };
   u4 avc[4], avn[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) avc[b] = la[b * 17 + aoff(0, b)];
-  for (int q0 = 0; q0 < nq; q0 += NQ) {
+  // One step q in ring slot s; FIRST: step 0, without an epilogue.
+  auto step = [&](const int q, const int s, auto first) {
+    constexpr bool FIRST = decltype(first)::value;
+    const int sp = (s + NQ - 1) % NQ;
+    // Refill step, clamped to the last one (a repeated read the cache
+    // serves; never used); the uniform part of the offset goes to the
+    // SGPR offset.
+    const int qr = min(q - 1 + NQ, nq - 1);
+    h8 bq[4];
 #pragma unroll
-    for (int s = 0; s < NQ; ++s) {
-      const int q = q0 + s;
-      const int sp = (s + NQ - 1) % NQ;
-      // Refill step, clamped to the last one (a repeated read the cache
-      // serves; never used); the uniform part of the offset goes to the
-      // SGPR offset.
-      const int qr = min(q - 1 + NQ, nq - 1);
-      h8 bq[4];
+    for (int b = 0; b < 4; ++b) bq[b] = SUB ? unpack_codes_sub(rc[s][b]) : unpack_codes(rc[s][b]);
+    rc[sp] = __builtin_amdgcn_raw_buffer_load_b128(rcs, (int)vc0, qr * 64, 0);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) bq[b] = SUB ? unpack_codes_sub(rc[s][b]) : unpack_codes(rc[s][b]);
-      rc[sp] = __builtin_amdgcn_raw_buffer_load_b128(rcs, (int)vc0, qr * 64, 0);
+    for (int t = 0; t < NG; ++t) {
+      {
+        const int tn = t + 1 < NG ? t + 1 : 0;
+        const int qn = t + 1 < NG ? q : min(q + 1, nq - 1);
 #pragma unroll
-      for (int t = 0; t < NG; ++t) {
-        {
-          const int tn = t + 1 < NG ? t + 1 : 0;
-          const int qn = t + 1 < NG ? q : min(q + 1, nq - 1);
-#pragma unroll
-          for (int b = 0; b < 4; ++b) avn[b] = la[((tn * nq + qn) * 4 + b) * 17 + aoff(tn, b)];
-        }
-        const bool one = L1 && t == NG - 1;
+        for (int b = 0; b < 4; ++b) avn[b] = la[((tn * nq + qn) * 4 + b) * 17 + aoff(tn, b)];
+      }
+      const bool one = L1 && t == NG - 1;
+      if constexpr (!FIRST) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float cs = mul_h16<false>(rp[sp][r], as4[t][r], nz);
@@ -611,24 +605,32 @@ __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, c
           }
           zc[t] = zc[t] + mul_h16<true>(rp[sp][r], xs4[t][r], nz);
         }
-        as4[t] = lsc[(t * nq + q) * 4 + soff(t)];
-        xs4[t] = lsu[(t * nq + q) * 4 + soff(t)];
-        if (one) {
-          D[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[0]), bq[0], zero4, 0, 0, 0);
-#pragma unroll
-          for (int b = 1; b < 4; ++b)
-            D[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[b]), bq[b], D[t][0], 0, 0, 0);
-        } else {
-#pragma unroll
-          for (int b = 0; b < 4; ++b)
-            D[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[b]), bq[b], zero4, 0, 0, 0);
-        }
-#pragma unroll
-        for (int b = 0; b < 4; ++b) avc[b] = avn[b];
       }
-      rp[sp] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, qr * 16, 0);
-      __builtin_amdgcn_sched_barrier(0);
+      as4[t] = lsc[(t * nq + q) * 4 + soff(t)];
+      xs4[t] = lsu[(t * nq + q) * 4 + soff(t)];
+      if (one) {
+        D[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[0]), bq[0], zero4, 0, 0, 0);
+#pragma unroll
+        for (int b = 1; b < 4; ++b)
+          D[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[b]), bq[b], D[t][0], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          D[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, avc[b]), bq[b], zero4, 0, 0, 0);
+      }
+#pragma unroll
+      for (int b = 0; b < 4; ++b) avc[b] = avn[b];
     }
+    rp[sp] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, qr * 16, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // The first NQ steps (step 0 peeled), then the rest NQ at a time.
+  step(0, 0, std::true_type{});
+#pragma unroll
+  for (int s = 1; s < NQ; ++s) step(s, s, std::false_type{});
+  for (int q0 = NQ; q0 < nq; q0 += NQ) {
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) step(q0 + s, s, std::false_type{});
   }
   // Epilogue of the last step (slot NQ - 1: nq is a multiple of NQ).
 #pragma unroll
@@ -883,20 +885,24 @@ bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const ui
   // Kernel and tiling per shape, measured on 4096..32000 x 2048..14336 and
   // M = 2..64 with the weights streamed from HBM.  The register-pipelined
   // kernel: for K <= 4096 three token groups per wave, or two, when that
-  // still gives at least 192 blocks of four waves (64 rows), else one (an
-  // odd count of token groups runs in pairs, the last pair's second group
-  // a clamped duplicate whose outputs are not stored); eight waves per
-  // block for three groups from 16384 rows.  For longer K (K / 128 a
+  // still gives at least 192 blocks of four waves (64 rows), else one (a
+  // count of token groups that the wave's groups do not divide runs the
+  // last block with clamped duplicate groups whose outputs are not stored);
+  // eight waves per block for three groups from 16384 rows.  For longer K (K / 128 a
   // multiple of 4, at most 14336) one token group per block.
   constexpr int Q = kRpMaxCols / 128, Q1 = kRpMaxColsOne / 128;
   if (gemv_rp_ok(rows, cols)) {
     const int rb = (rows + 63) / 64;
     auto blocks = [&](int tgw) { return rb * ((ntg + tgw - 1) / tgw); };
+    // Three token groups per wave for 3, 5 or 6 and more groups (the
+    // duplicates past an odd count cost less than a third pass over the
+    // weights), two for four.
+    const bool three = ntg >= 3 && ntg != 4;
     if (cols > kRpMaxCols)
       launch_rp<1, 4, Q1>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (ntg == 3 && rows >= 16384)
+    else if (three && rows >= 16384)
       launch_rp<3, 8, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (ntg == 3 && blocks(3) >= 192)
+    else if (three && blocks(3) >= 192)
       launch_rp<3, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
     else if (ntg >= 2 && blocks(2) >= 192)
       launch_rp<2, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
