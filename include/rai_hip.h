@@ -76,6 +76,17 @@ typedef struct rai_lookup_config {
                          decoder's StdRng; <= 1e-6: greedy acceptance */
 } rai_lookup_config;
 
+/* SamplerConfig (sampler.rs:17-42) with the repetition penalty `rai run`
+ * applies over the context (run.rs:720): temperature (<= 1e-6 or non-finite:
+ * argmax), top_k (0 = off), top_p (1 = off; NaN = 1), repetition_penalty
+ * (1 = off). */
+typedef struct rai_sampler_config {
+  float temperature;
+  size_t top_k;
+  float top_p;
+  float repetition_penalty;
+} rai_sampler_config;
+
 /* SpeculativeConfig (speculative.rs:25-45): draft_k and the sampler's
  * temperature (top_k 0, top_p 1, no repetition penalty: the exact
  * configuration).  temperature <= 1e-6 selects the greedy variant (argmax
@@ -334,6 +345,21 @@ int rai_greedy_generate(rai_lookup *dec, const uint32_t *prompt, size_t n, size_
  * out_tokens.  The steps replay the decoder's one-token step graph. */
 int rai_greedy_decode(rai_lookup *dec, const uint32_t *context, size_t len, size_t pos, size_t steps,
                       uint32_t *out_tokens);
+/* The `rai run` decode loop without speculation with a sampler (run.rs:692-735):
+ * from a prefilled state as rai_greedy_decode, each token chosen by
+ * apply_repetition_penalty over the whole context (sampler.rs:185-199) and
+ * sample_token with the config (sampler.rs:47-182), drawing from the
+ * decoder's StdRng (rai_lookup_seed).  Ties of equal probabilities in the
+ * top-p order are taken lowest index first (the reference's unstable sort
+ * leaves their order unspecified). */
+int rai_sample_decode(rai_lookup *dec, const uint32_t *context, size_t len, size_t pos, size_t steps,
+                      const rai_sampler_config *cfg, uint32_t *out_tokens);
+/* apply_repetition_penalty over recent[0..n_recent) then sample_token with
+ * the config (sampler.rs:47-199) on one host logit row, `draws` times in a
+ * row (each on the unchanged row) from StdRng::seed_from_u64(seed): the
+ * device sampler alone, for checks against another implementation. */
+int rai_sample_tokens(const float *logits, size_t vocab, const uint32_t *recent, size_t n_recent,
+                      const rai_sampler_config *cfg, uint64_t seed, size_t draws, uint32_t *out_tokens);
 
 /* ------------------------------------------------------------------ misc -- */
 /* Synthetic .raimodel writer (the build's stand-in for the exporter).

@@ -80,6 +80,8 @@ def lib():
         "ora_kv_read": (c_int, [P, c_int, c_int, c_int, c_int, P]),
         "ora_kv_import": (c_int, [P, c_int, c_int, P, c_int]),
         "ora_lookup_decode_one": (c_int, [P, c_int, c_int, P]),
+        "ora_lookup_decode_sample": (c_int, [P, c_int, c_int, P, c_int, c_float, c_int64, c_float, c_float, P, P]),
+        "ora_sample_plain": (c_int, [P, c_int, P, c_int, c_float, c_int64, c_float, c_float, P, POINTER(c_int)]),
         "ora_route_experts": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P]),
         "ora_embed_token": (c_int, [P, c_int, P]),
         "ora_forward_from_hidden": (c_int, [P, P, P, c_int, c_int]),
@@ -415,6 +417,17 @@ def softmax_probabilities(logits, temperature: float) -> np.ndarray:
     return out
 
 
+def sample_plain(logits, recent, temperature: float, top_k: int, top_p: float, penalty: float, rng: Rng) -> int:
+    """apply_repetition_penalty over `recent`, then sample_token with the whole
+    SamplerConfig (sampler.rs:47-199)."""
+    x = f32(logits)
+    r = np.ascontiguousarray(recent, np.int32)
+    t = c_int()
+    _check(lib().ora_sample_plain(_ptr(x), x.size, _ptr(r) if r.size else None, r.size, temperature, top_k, top_p,
+                                  penalty, rng.h, ctypes.byref(t)))
+    return t.value
+
+
 def sample_token(logits, temperature: float, rng: Rng) -> int:
     x = f32(logits)
     t = c_int()
@@ -480,6 +493,15 @@ class LookupDecoder:
 
     def kv_filled(self) -> int:
         return lib().ora_lookup_kv_filled(self.h)
+
+    def decode_sample(self, pos: int, token: int, context, temperature: float, top_k: int, top_p: float,
+                      penalty: float, rng: "Rng") -> int:
+        """The plain sampled step of `rai run` (run.rs:692-735)."""
+        c = np.ascontiguousarray(context, np.int32)
+        out = np.zeros(1, np.int32)
+        _check(lib().ora_lookup_decode_sample(self.h, pos, token, _ptr(c), c.size, temperature, top_k, top_p,
+                                              penalty, rng.h, _ptr(out)))
+        return int(out[0])
 
     def decode_one(self, pos: int, token: int) -> int:
         """decode_one (lookup.rs:428-455) with argmax."""

@@ -617,6 +617,29 @@ int ora_lookup_import_kv(ora_lookup *dd, int layer, int which, const float *rows
 }
 int ora_lookup_kv_filled(const ora_lookup *d) { return d->d.kv.filled.at(0); }
 
+// The plain sampled step of the `rai run` loop without speculation
+// (run.rs:692-735): decode_one's forward of `token` at `pos`, then the
+// repetition penalty over ctx[0..len) and sample_token with the whole
+// SamplerConfig (sampler.rs:47-199), drawing from `rng`.
+int ora_lookup_decode_sample(ora_lookup *dd, int pos, int token, const int32_t *ctx, int len, float temperature,
+                             int64_t top_k, float top_p, float penalty, ora_rng *rng, int32_t *out) {
+  ORA_TRY({
+    Lookup &d = dd->d;
+    const Model &m = *d.m;
+    const int H = m.cfg.hidden_size, V = m.cfg.vocab_size;
+    if (pos < 0 || pos >= d.max_ctx) fail("decode position exceeds the context window");
+    if (token < 0 || token >= V) fail("token id is out of model vocabulary");
+    std::vector<float> h(H), lg(V);
+    embed(m, token, h.data());
+    forward(m, d.kv, h.data(), &pos, 1);
+    logits(m, h.data(), lg.data(), 1);
+    int tok = 0;
+    if (ora_sample_plain(lg.data(), V, ctx, len, temperature, top_k, top_p, penalty, rng, &tok))
+      fail("sample_token failed");
+    *out = tok;
+  });
+}
+
 // decode_one (lookup.rs:428-455) with argmax: the plain greedy step of the
 // `rai run` loop without speculation.
 int ora_lookup_decode_one(ora_lookup *dd, int pos, int token, int32_t *out) {

@@ -11,20 +11,31 @@
 //     f64 = (u64 >> 11) * 2^-53.
 //   - softmax_probabilities and sample_correction (speculative.rs:414-513),
 //     sample_token with top_k = 0, top_p = 1 (sampler.rs:47-182), and the
-//     accept / correct / bonus loop of LookupDecoder::step (lookup.rs:359-403).
+//     accept / correct / bonus loop of LookupDecoder::step (lookup.rs:359-403);
+//   - apply_repetition_penalty and sample_token with the whole SamplerConfig
+//     (sampler.rs:47-199), the token of `rai run` without speculation.
 // Pins: the block function and the buffering order are checked against the
 // RFC 7539 A.1 keystream vectors (20 rounds) and the RFC 8439 2.3.2 block;
 // seed_from_u64 and the float conversions have no published vector and are
 // parity-unpinned beyond their published algorithm.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <utility>
 #include <vector>
 
 #include "ora_internal.h"
 #include "oracle.h"
 
 namespace ora {
+
+// f32::total_cmp order as an unsigned key (larger key = larger value).
+static inline uint32_t total_key(float x) {
+  uint32_t b;
+  std::memcpy(&b, &x, 4);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
 
 static inline uint32_t rotl(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
 
@@ -176,6 +187,129 @@ static int sample_token(std::vector<float> v, float temperature, StdRng &rng) {
   return (int)argmax(v.data(), n);
 }
 
+// SamplerConfig (sampler.rs:17-42).
+struct SamplerCfg {
+  float temperature;
+  int64_t top_k;
+  float top_p;
+};
+
+// apply_repetition_penalty (sampler.rs:185-199): each distinct token of
+// `recent` inside the vocabulary once: a positive logit divided by the
+// penalty, any other multiplied; a non-finite, non-positive or ~1 penalty
+// changes nothing.
+static void apply_repetition_penalty(float *logits, int n, const int32_t *recent, int nr, float penalty) {
+  if (!std::isfinite(penalty) || penalty <= 0.0f || std::fabs(penalty - 1.0f) < 1e-6f) return;
+  std::vector<char> seen(n, 0);
+  for (int i = 0; i < nr; ++i) {
+    const int t = recent[i];
+    if (t < 0 || t >= n || seen[t]) continue;
+    seen[t] = 1;
+    if (logits[t] > 0.0f)
+      logits[t] /= penalty;
+    else
+      logits[t] *= penalty;
+  }
+}
+
+// sample_token (sampler.rs:47-182) with the whole SamplerConfig, in its
+// order: NaN -> -inf; greedy at T <= 1e-6 (or non-finite T); x * (1/T);
+// top-k keeps x >= the k-th largest value (f32::total_cmp order for the
+// selection, the plain comparison for the filter); the softmax (+inf
+// entries share the mass, all -inf is uniform, exp and an f32 sum in index
+// order, multiply by 1/sum, a degenerate sum is uniform); top-p (clamped to
+// [0, 1], NaN = 1) keeps the candidates p > 1e-10 sorted by p descending up
+// to the first cumulative f32 sum >= top_p, zeroes the rest and divides by
+// the f32 sum in index order; then the cumulative search of one f32 draw,
+// argmax as the fallback.  Ties of equal probabilities in the top-p order
+// are taken lowest index first (the reference sorts with sort_unstable_by,
+// which leaves their order unspecified).
+static int sample_token_cfg(std::vector<float> v, const SamplerCfg &cfg, StdRng &rng) {
+  const int n = (int)v.size();
+  if (n == 0) return 0;
+  for (float &x : v)
+    if (std::isnan(x)) x = -INFINITY;
+  if (!std::isfinite(cfg.temperature) || cfg.temperature <= 1e-6f) return (int)argmax(v.data(), n);
+  const float inv_temp = 1.0f / cfg.temperature;
+  for (float &x : v) x *= inv_temp;
+  if (cfg.top_k > 0 && cfg.top_k < n) {
+    std::vector<float> vals(v);
+    const size_t k = (size_t)cfg.top_k;
+    std::nth_element(vals.begin(), vals.begin() + (k - 1), vals.end(), [](float a, float b) {
+      return total_key(a) > total_key(b);
+    });
+    const float threshold = vals[k - 1];
+    for (float &x : v)
+      if (x < threshold) x = -INFINITY;
+  }
+  int pinf = 0;
+  for (float x : v) pinf += x == INFINITY;
+  if (pinf > 0) {
+    const float p = 1.0f / (float)pinf;
+    for (float &x : v) x = x == INFINITY ? p : 0.0f;
+  } else {
+    float mx = -INFINITY;
+    for (float x : v) mx = std::fmax(mx, x);
+    if (mx == -INFINITY) {
+      for (float &x : v) x = 1.0f / (float)n;
+    } else {
+      float sum = 0.0f;
+      for (float &x : v) {
+        x = std::exp(x - mx);
+        sum += x;
+      }
+      if (std::isfinite(sum) && sum > 0.0f) {
+        const float inv = 1.0f / sum;
+        for (float &x : v) x *= inv;
+      } else {
+        for (float &x : v) x = 1.0f / (float)n;
+      }
+    }
+  }
+  const float top_p = std::isfinite(cfg.top_p) ? std::fmin(std::fmax(cfg.top_p, 0.0f), 1.0f) : 1.0f;
+  if (top_p < 1.0f) {
+    std::vector<std::pair<int, float>> cand;
+    for (int i = 0; i < n; ++i)
+      if (v[i] > 1e-10f) cand.emplace_back(i, v[i]);
+    std::stable_sort(cand.begin(), cand.end(), [](const std::pair<int, float> &a, const std::pair<int, float> &b) {
+      return total_key(a.second) > total_key(b.second);
+    });
+    float cum = 0.0f;
+    size_t cutoff = cand.size();
+    for (size_t r = 0; r < cand.size(); ++r) {
+      cum += cand[r].second;
+      if (cum >= top_p) {
+        cutoff = r + 1;
+        break;
+      }
+    }
+    for (float &x : v) x = 0.0f;
+    for (size_t r = 0; r < cutoff; ++r) v[cand[r].first] = cand[r].second;
+    float sum = 0.0f;
+    for (float x : v) sum += x;
+    if (sum > 0.0f) {
+      const float inv = 1.0f / sum;
+      for (float &x : v) x *= inv;
+    }
+  }
+  const float r = rng.gen_f32();
+  float cum = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    cum += v[i];
+    if (r < cum) return i;
+  }
+  return (int)argmax(v.data(), n);
+}
+
+// The `rai run` plain decode token (run.rs:720-721): the penalty over the
+// whole context, then sample_token.
+int sample_plain(const float *logits, int n, const int32_t *ctx, int len, float temperature, int64_t top_k,
+                 float top_p, float penalty, StdRng &rng) {
+  std::vector<float> v(logits, logits + n);
+  apply_repetition_penalty(v.data(), n, ctx, len, penalty);
+  return sample_token_cfg(std::move(v), SamplerCfg{temperature, top_k, top_p}, rng);
+}
+
 // sample_correction (speculative.rs:479-513) against a point-mass draft on
 // `draft` (all other draft logits -inf).
 static int sample_correction(const float *target, int n, int draft, float temperature, StdRng &rng) {
@@ -314,6 +448,10 @@ void ora_rng_key(const ora_rng *r, uint32_t *key) { std::memcpy(key, r->r.key, 3
 
 int ora_sample_token(const float *logits, int n, float temperature, ora_rng *r, int *token) {
   ORA_TRY(*token = sample_token(std::vector<float>(logits, logits + n), temperature, r->r));
+}
+int ora_sample_plain(const float *logits, int n, const int32_t *ctx, int len, float temperature, int64_t top_k,
+                     float top_p, float penalty, ora_rng *r, int *token) {
+  ORA_TRY(*token = sample_plain(logits, n, ctx, len, temperature, top_k, top_p, penalty, r->r));
 }
 int ora_softmax_probabilities(const float *logits, int n, float temperature, float *out) {
   ORA_TRY({

@@ -148,6 +148,14 @@ int ora_lookup_kv_filled(const ora_lookup *d);
 /* decode_one (lookup.rs:428-455) with argmax: embed `token` at `pos`,
  * forward, logits, argmax into *out. */
 int ora_lookup_decode_one(ora_lookup *d, int pos, int token, int32_t *out);
+/* The plain sampled step (run.rs:692-735): forward of `token` at `pos`, the
+ * repetition penalty over ctx[0..len), sample_token with the config. */
+int ora_lookup_decode_sample(ora_lookup *d, int pos, int token, const int32_t *ctx, int len, float temperature,
+                             int64_t top_k, float top_p, float penalty, ora_rng *rng, int32_t *out);
+/* apply_repetition_penalty (sampler.rs:185-199) over ctx[0..len), then
+ * sample_token (sampler.rs:47-182) with the whole SamplerConfig. */
+int ora_sample_plain(const float *logits, int n, const int32_t *ctx, int len, float temperature, int64_t top_k,
+                     float top_p, float penalty, ora_rng *r, int *token);
 /* SpeculativeDecoder (speculative.rs:79-391); temperature <= 1e-6 is the
  * greedy variant (argmax drafts, argmax acceptance). */
 int ora_spec_create(const ora_model *draft, const ora_model *target, int max_ctx, ora_spec **out);

@@ -33,6 +33,16 @@ class RaiError(RuntimeError):
         self.status = _STATUS.get(status, str(status))
 
 
+class SamplerConfig(ctypes.Structure):
+    """rai_sampler_config: SamplerConfig (sampler.rs:17-42) and the repetition
+    penalty; the defaults are `rai run`'s (run.rs:40-56)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", c_size_t), ("top_p", ctypes.c_float),
+                ("repetition_penalty", ctypes.c_float)]
+
+    def __init__(self, temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.1):
+        super().__init__(temperature, top_k, top_p, repetition_penalty)
+
+
 class QLinear(ctypes.Structure):
     """rai_qlinear: QuantizedLinear (format.rs:361-367) with device pointers."""
     _fields_ = [("nibbles", c_void_p), ("params", c_void_p), ("rows", c_size_t), ("cols", c_size_t),
@@ -150,6 +160,8 @@ def lib():
         "rai_kv_import": (c_int, [P, S, c_int, P, S]),
         "rai_greedy_generate": (c_int, [P, P, S, S, P]),
         "rai_greedy_decode": (c_int, [P, P, S, S, S, P]),
+        "rai_sample_decode": (c_int, [P, P, S, S, S, POINTER(SamplerConfig), P]),
+        "rai_sample_tokens": (c_int, [P, S, P, S, POINTER(SamplerConfig), ctypes.c_uint64, S, P]),
         "rai_synth_model": (c_int, [POINTER(SynthConfig), c_uint64, c_char_p,
                                     POINTER(c_void_p), POINTER(c_size_t)]),
         "rai_free_image": (None, [P]),
@@ -276,6 +288,18 @@ def _fused(fn: str, projections, x) -> list[np.ndarray]:
     args = [o.ptr for o in outs] + [ctypes.byref(q) for q in lins] + [dx.ptr, None]
     _check(getattr(lib(), fn)(*args))
     return [o.to_host(np.float32, p[2]) for o, p in zip(outs, projections)]
+
+
+def sample_tokens(logits, recent, config: SamplerConfig, seed: int, draws: int) -> list[int]:
+    """The device sampler alone: apply_repetition_penalty over `recent` then
+    sample_token (sampler.rs:47-199), `draws` times from
+    StdRng::seed_from_u64(seed)."""
+    lg = _f32(np.asarray(logits).reshape(-1))
+    r = _u32(recent)
+    out = np.zeros(max(draws, 1), np.uint32)
+    _check(lib().rai_sample_tokens(_ptr(lg), lg.size, _ptr(r) if r.size else None, r.size, ctypes.byref(config),
+                                   seed, draws, _ptr(out)))
+    return out[:draws].tolist()
 
 
 def w4a8_fused_qkv(q, k, v, x) -> list[np.ndarray]:
@@ -709,6 +733,14 @@ class LookupDecoder:
         p = _u32(prompt)
         out = np.zeros(steps, np.uint32)
         _check(lib().rai_greedy_generate(self.h, _ptr(p), p.size, steps, _ptr(out)))
+        return out.tolist()
+
+    def sample_decode(self, context, pos: int, steps: int, config: "SamplerConfig"):
+        """The `rai run` decode loop without speculation (run.rs:692-735) from a
+        prefilled state: repetition penalty + sample_token per token."""
+        c = _u32(context)
+        out = np.zeros(steps, np.uint32)
+        _check(lib().rai_sample_decode(self.h, _ptr(c), c.size, pos, steps, ctypes.byref(config), _ptr(out)))
         return out.tolist()
 
     def greedy_decode(self, context, pos: int, steps: int):

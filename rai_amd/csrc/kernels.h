@@ -251,6 +251,14 @@ void launch_draw(const float *row, int V, float T, RngState *rng, float *keep, f
                  hipStream_t s);
 // n draws (kinds: 0 u32, 1 u64, 2 f32, 3 f64) from the device generator.
 void launch_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *out, hipStream_t s);
+// apply_repetition_penalty over ctx[0..len), then sample_token with the whole
+// SamplerConfig (sampler.rs:47-199) for one logit row: the token goes to
+// tok_out (ctx[len] when null), res (may be null) = {0, 1}.  work: V floats;
+// flags: V words, zero on entry and on exit.  With a step record, len, T
+// and the options come from st[1], st[4], st[8..10].
+void launch_sample_plain(const float *logits, int V, uint32_t *ctx, int len, float T, int top_k, float top_p,
+                         float penalty, RngState *rng, float *work, uint32_t *flags, uint32_t *tok_out, int *res,
+                         hipStream_t s, const int *st = nullptr);
 
 // Device MoE (moe.hip): group 32/64/128, hidden and FFN multiples of 256,
 // at most 1024 experts.

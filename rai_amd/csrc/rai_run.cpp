@@ -3,18 +3,20 @@
 // (the tokenizer and chat templates sit outside this path).
 //
 //   rai-run MODEL --prompt-ids 1,2,3 [--max-tokens 64] [--temperature 0.7]
+//           [--top-k 40] [--top-p 0.9] [--repetition-penalty 1.1]
 //           [--seed 42] [--max-context N] [--eos ID] [--max-groups G] [--verbose]
 //           [--lookup-k K --lookup-ngram 3 --lookup-min-ngram 1]
 //           [--draft DRAFT.raimodel --draft-k 6]
 //
 // Modes as run.rs: --draft (draft-model speculation) and --lookup-k
-// (prompt lookup) are mutually exclusive; without either, plain decoding
-// (greedy: sampling without speculation, with top-k / top-p / repetition
-// penalty, is not part of this library).  One deliberate extension: the
-// reference refuses the speculative modes at --temperature <= 1e-6
-// (run.rs:205-213); here they select greedy acceptance, whose tokens equal
-// plain greedy decoding.  Generated ids go to stdout, one line; the
-// statistics to stderr.
+// (prompt lookup) are mutually exclusive and need --top-k 0 --top-p 1
+// --repetition-penalty 1; without either, plain decoding, each token by the
+// repetition penalty over the context and sample_token (sampler.rs:47-199).
+// One deliberate extension: the reference refuses the speculative modes at
+// --temperature <= 1e-6 (run.rs:205-213); here they select greedy
+// acceptance, whose tokens equal plain greedy decoding.  Generated ids go to
+// stdout, one line; the statistics to stderr.
+#include <cfloat>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -31,7 +33,8 @@ struct Args {
   std::string model, draft;
   std::vector<uint32_t> prompt;
   size_t max_tokens = 64, max_context = 0, draft_k = 6, lookup_k = 0, lookup_ngram = 3, lookup_min_ngram = 1;
-  float temperature = 0.7f;
+  float temperature = 0.7f, top_p = 0.9f, repetition_penalty = 1.1f;  // run.rs:40-56
+  size_t top_k = 40;
   uint64_t seed = 42;
   long eos = -1;
   int max_groups = 0;  // 0: the reference's MAX_GROUPS (gemm.rs:1167)
@@ -72,6 +75,9 @@ Args parse(int argc, char **argv) {
     if (k == "--prompt-ids") a.prompt = parse_ids(val());
     else if (k == "--max-tokens") a.max_tokens = std::strtoull(val(), nullptr, 10);
     else if (k == "--temperature") a.temperature = std::strtof(val(), nullptr);
+    else if (k == "--top-k") a.top_k = std::strtoull(val(), nullptr, 10);
+    else if (k == "--top-p") a.top_p = std::strtof(val(), nullptr);
+    else if (k == "--repetition-penalty") a.repetition_penalty = std::strtof(val(), nullptr);
     else if (k == "--seed") a.seed = std::strtoull(val(), nullptr, 10);
     else if (k == "--max-context") a.max_context = std::strtoull(val(), nullptr, 10);
     else if (k == "--eos") a.eos = std::strtol(val(), nullptr, 10);
@@ -91,6 +97,9 @@ Args parse(int argc, char **argv) {
   if (a.max_tokens == 0) die("--max-tokens must be greater than zero");
   if (!(std::isfinite(a.temperature) && a.temperature >= 0.0f && a.temperature <= 2.0f))
     die("--temperature must be within [0, 2]");
+  if (!(std::isfinite(a.top_p) && a.top_p >= FLT_MIN && a.top_p <= 1.0f)) die("--top-p must be within (0, 1]");
+  if (!(std::isfinite(a.repetition_penalty) && a.repetition_penalty >= 0.01f && a.repetition_penalty <= 4.0f))
+    die("--repetition-penalty must be within [0.01, 4]");
   if (!a.draft.empty() && a.lookup_k > 0) die("--draft and --lookup-k are mutually exclusive");
   // MAX_SPECULATIVE_TOKENS = 32, MAX_LOOKUP_NGRAM = 16 (run.rs:25-29).
   if (!a.draft.empty() && (a.draft_k < 1 || a.draft_k > 32)) die("--draft-k must be between 1 and 32");
@@ -99,6 +108,10 @@ Args parse(int argc, char **argv) {
     die("--lookup-ngram must be between 1 and 16");
   if (a.lookup_k > 0 && (a.lookup_min_ngram < 1 || a.lookup_min_ngram > a.lookup_ngram))
     die("--lookup-min-ngram must be between 1 and --lookup-ngram");
+  // Verification compares against the exact sampled distribution.
+  if ((!a.draft.empty() || a.lookup_k > 0) &&
+      !(a.top_k == 0 && a.top_p == 1.0f && std::fabs(a.repetition_penalty - 1.0f) < FLT_EPSILON))
+    die("speculative decoding requires --top-k 0, --top-p 1 and --repetition-penalty 1");
   return a;
 }
 
@@ -198,13 +211,11 @@ int main(int argc, char **argv) {
                  100.0 * with_draft / (steps ? steps : 1), (double)generated / (steps ? steps : 1));
     rai_lookup_free(dec);
   } else {
-    if (a.temperature > 1e-6f)
-      die("plain decoding samples with top-k / top-p / repetition penalty, which this library does not "
-          "implement; use --temperature 0, --lookup-k or --draft");
-    // Prefill of the first N - 1 tokens, then one decode step per token
-    // (run.rs:640-735).
+    // Prefill of the first N - 1 tokens, then one decode step per token, each
+    // token by the repetition penalty and sample_token (run.rs:640-735).
     rai_lookup *dec = nullptr;
     check(rai_lookup_create(model, max_ctx, &dec), "creating the decoder");
+    check(rai_lookup_seed(dec, a.seed), "seeding");
     const auto t0 = std::chrono::steady_clock::now();
     size_t pos = 0;
     check(rai_lookup_prefill(dec, a.prompt.data(), a.prompt.size(), &pos), "prefill");
@@ -214,7 +225,8 @@ int main(int argc, char **argv) {
     const size_t steps = std::min(a.max_tokens, max_ctx - pos);
     std::vector<uint32_t> out(steps);
     const auto t1 = std::chrono::steady_clock::now();
-    check(rai_greedy_decode(dec, a.prompt.data(), a.prompt.size(), pos, steps, out.data()), "decoding");
+    const rai_sampler_config sc{a.temperature, a.top_k, a.top_p, a.repetition_penalty};
+    check(rai_sample_decode(dec, a.prompt.data(), a.prompt.size(), pos, steps, &sc, out.data()), "decoding");
     const double ms = ms_since(t1);
     emit(out.data(), out.size(), pos);
     std::fprintf(stderr, "\n--- Stats ---\nTokens: %zu, %.2f tok/s\n", generated, generated / (ms / 1e3));

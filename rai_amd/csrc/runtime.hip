@@ -835,13 +835,15 @@ struct rai_lookup {
   // position in the device step record.
   DevBuf step;            // int[5] {pos0, len, start, nd, temperature bits}
   bool graphs = false;
-  // Indexed by verify size m, plus kAttnTokens + 1 for exact-sampling steps,
-  // plus 2 (kAttnTokens + 1) per attention span index.
+  // Indexed by verify size m, plus (kAttnTokens + 1) times the mode (0
+  // greedy, 1 exact-sampling lookup, 2 the plain sampler), plus
+  // 3 (kAttnTokens + 1) per attention span index.
   std::vector<hipGraphExec_t> graph;
   std::vector<int> graph_uses;
   // Exact sampling: the decoder's StdRng (device), per-row probabilities
   // [64][V] and one row of scratch.
   DevBuf rng, probs, pscratch;
+  DevBuf flags;  // [V] words for the plain sampler, zero between calls
   ~rai_lookup() {
     for (hipGraphExec_t g : graph)
       if (g) (void)hipGraphExecDestroy(g);
@@ -889,10 +891,12 @@ static bool sync_context(rai_lookup &d, const uint32_t *ctx, size_t len) {
 // One decode step: LookupDecoder::step (lookup.rs:260-425).  With
 // search = false the n-gram search is skipped and the step is decode_one
 // (lookup.rs:428-455): the plain decode loop of `rai run` (run.rs:692-735),
-// on the same one-token step graph.
+// on the same one-token step graph; `plain` (then) selects the token with
+// the repetition penalty and sample_token's whole SamplerConfig
+// (sampler.rs:47-199) instead of argmax.
 static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size_t len,
                         const rai_lookup_config &cfg, uint32_t *out, size_t cap, rai_lookup_metrics &met,
-                        bool search = true) {
+                        bool search = true, const rai_sampler_config *plain = nullptr) {
   rai_model &md = *d.model;
   const rai_model_config &c = md.cfg;
   // validate_lookup_config (lookup.rs:457-475), greedy variant.
@@ -942,7 +946,12 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
                  d.ws.err.as<int>(), s, st);
     forward_enqueue(md, d.kv, d.ws, m, pos, s, st, span);
     logits(md, d.ws, m, s);
-    if (sampled) {
+    if (plain) {
+      launch_sample_plain(d.ws.logits.as<float>(), c.vocab_size, d.ctx.as<uint32_t>(), (int)len,
+                          plain->temperature, (int)std::min<size_t>(plain->top_k, INT32_MAX), plain->top_p,
+                          plain->repetition_penalty, d.rng.as<RngState>(), d.pscratch.as<float>(),
+                          d.flags.as<uint32_t>(), nullptr, res + 4, s, st);
+    } else if (sampled) {
       launch_sample(d.ws.logits.as<float>(), d.probs.as<float>(), c.vocab_size, d.ctx.as<uint32_t>(), (int)len,
                     start, nd, cfg.temperature, d.rng.as<RngState>(), d.pscratch.as<float>(), res + 4, s, st, m);
     } else {
@@ -966,9 +975,14 @@ static void lookup_step(rai_lookup &d, size_t pos, const uint32_t *context, size
     sh[5] = (int)cfg.min_ngram;
     sh[6] = (int)cfg.max_ngram;
     sh[7] = (int)cfg.max_draft;
-    HIP_CHECK(hipMemcpyAsync(d.step.p, sh, 8 * sizeof(int), hipMemcpyHostToDevice, s));
+    sh[8] = plain ? (int)std::min<size_t>(plain->top_k, INT32_MAX) : 0;
+    std::memcpy(&sh[9], plain ? &plain->top_p : &cfg.temperature, sizeof(float));
+    std::memcpy(&sh[10], plain ? &plain->repetition_penalty : &cfg.temperature, sizeof(float));
+    if (plain) std::memcpy(&sh[4], &plain->temperature, sizeof(float));
+    HIP_CHECK(hipMemcpyAsync(d.step.p, sh, 11 * sizeof(int), hipMemcpyHostToDevice, s));
     const int *st = d.step.as<int>();
-    const int gi = m + (sampled ? kAttnTokens + 1 : 0) + 2 * (kAttnTokens + 1) * attn_span_index((int)pos + m);
+    const int mode = plain ? 2 : sampled ? 1 : 0;
+    const int gi = m + (kAttnTokens + 1) * mode + 3 * (kAttnTokens + 1) * attn_span_index((int)pos + m);
     if (d.graph[gi]) {
       HIP_CHECK(hipGraphLaunch(d.graph[gi], s));
     } else if (d.graph_uses[gi]++ == 0) {
@@ -1686,11 +1700,13 @@ int rai_lookup_create(rai_model *m, size_t max_ctx, rai_lookup **out) {
     const char *env = std::getenv("RAI_STEP_GRAPHS");
     d->graphs = (m->cfg.num_experts == 0 || rai::moe_on_device(*m)) && !(env && env[0] == '0');
     const size_t spans = (size_t)rai::attn_span_index((int)d->max_ctx) + 1;
-    d->graph.assign(2 * (rai::kAttnTokens + 1) * spans, nullptr);
-    d->graph_uses.assign(2 * (rai::kAttnTokens + 1) * spans, 0);
+    d->graph.assign(3 * (rai::kAttnTokens + 1) * spans, nullptr);
+    d->graph_uses.assign(3 * (rai::kAttnTokens + 1) * spans, 0);
     d->rng.alloc(sizeof(rai::RngState));
     d->probs.alloc(sizeof(float) * 64 * (size_t)m->cfg.vocab_size);
     d->pscratch.alloc(sizeof(float) * (size_t)m->cfg.vocab_size);
+    d->flags.alloc(sizeof(uint32_t) * (size_t)m->cfg.vocab_size);
+    HIP_CHECK(hipMemset(d->flags.p, 0, sizeof(uint32_t) * (size_t)m->cfg.vocab_size));
     rai::RngState r;
     rai::rng_seed_from_u64(r, 0);
     HIP_CHECK(hipMemcpy(d->rng.p, &r, sizeof(r), hipMemcpyHostToDevice));
@@ -1872,11 +1888,13 @@ int rai_kv_import(rai_kv *kv, size_t layer, int which, const float *rows, size_t
 
 namespace rai {
 
-// The plain greedy decode loop from a prefilled state (context[len - 1] is
-// the token at pos): decode_one per token (lookup.rs:428-455) with argmax
-// sampling, as run.rs:692-735 at temperature 0.
+// The plain decode loop from a prefilled state (context[len - 1] is the
+// token at pos): decode_one per token (lookup.rs:428-455), the token by
+// argmax (sampler = null: run.rs:692-735 at temperature 0 without a
+// repetition penalty) or by the repetition penalty and sample_token with
+// the sampler's config (run.rs:720-721).
 static void greedy_decode(rai_lookup &d, const uint32_t *context, size_t len, size_t pos, size_t steps,
-                          uint32_t *out) {
+                          uint32_t *out, const rai_sampler_config *sampler = nullptr) {
   const rai_lookup_config plain{1, 1, 1, 0.0f};  // search parameters unused (no search)
   std::vector<uint32_t> ctx(context, context + len);
   ctx.reserve(len + steps);
@@ -1884,7 +1902,7 @@ static void greedy_decode(rai_lookup &d, const uint32_t *context, size_t len, si
   for (size_t i = 0; i < steps; ++i) {
     if (pos >= d.max_ctx) fail(RAI_E_RANGE, "generation exceeds the context window");
     rai_lookup_metrics met{};
-    lookup_step(d, pos, ctx.data(), ctx.size(), plain, tok, 2, met, false);
+    lookup_step(d, pos, ctx.data(), ctx.size(), plain, tok, 2, met, false, sampler);
     out[i] = tok[0];
     ctx.push_back(tok[0]);
     ++pos;
@@ -1907,6 +1925,47 @@ int rai_greedy_decode(rai_lookup *d, const uint32_t *context, size_t len, size_t
     if (!d || !context || !out) rai::fail(RAI_E_ARG, "null argument");
     if (len == 0 || pos + 1 != len) rai::fail(RAI_E_ARG, "context[len - 1] must be the token at pos");
     rai::greedy_decode(*d, context, len, pos, steps, out);
+  });
+}
+
+int rai_sample_decode(rai_lookup *d, const uint32_t *context, size_t len, size_t pos, size_t steps,
+                      const rai_sampler_config *cfg, uint32_t *out) {
+  RAI_API_BODY({
+    if (!d || !context || !cfg || !out) rai::fail(RAI_E_ARG, "null argument");
+    if (len == 0 || pos + 1 != len) rai::fail(RAI_E_ARG, "context[len - 1] must be the token at pos");
+    rai::greedy_decode(*d, context, len, pos, steps, out, cfg);
+  });
+}
+
+int rai_sample_tokens(const float *logits, size_t vocab, const uint32_t *recent, size_t n_recent,
+                      const rai_sampler_config *cfg, uint64_t seed, size_t draws, uint32_t *out) {
+  RAI_API_BODY({
+    if (!logits || !cfg || !out || (n_recent && !recent)) rai::fail(RAI_E_ARG, "null argument");
+    if (vocab == 0 || vocab > INT32_MAX || n_recent > INT32_MAX) rai::fail(RAI_E_SHAPE, "invalid vocabulary size");
+    hipStream_t s;
+    HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    rai::DevBuf dl, dc, dw, df, dr, dout;
+    dl.alloc(sizeof(float) * vocab);
+    dc.alloc(sizeof(uint32_t) * (n_recent + 1));
+    dw.alloc(sizeof(float) * vocab);
+    df.alloc(sizeof(uint32_t) * vocab);
+    dr.alloc(sizeof(rai::RngState));
+    dout.alloc(sizeof(uint32_t) * std::max<size_t>(draws, 1));
+    rai::RngState r;
+    rai::rng_seed_from_u64(r, seed);
+    HIP_CHECK(hipMemcpyAsync(dl.p, logits, sizeof(float) * vocab, hipMemcpyHostToDevice, s));
+    if (n_recent) HIP_CHECK(hipMemcpyAsync(dc.p, recent, sizeof(uint32_t) * n_recent, hipMemcpyHostToDevice, s));
+    HIP_CHECK(hipMemcpyAsync(dr.p, &r, sizeof(r), hipMemcpyHostToDevice, s));
+    HIP_CHECK(hipMemsetAsync(df.p, 0, sizeof(uint32_t) * vocab, s));
+    const int top_k = (int)std::min<size_t>(cfg->top_k, INT32_MAX);
+    for (size_t i = 0; i < draws; ++i)
+      rai::launch_sample_plain(dl.as<float>(), (int)vocab, dc.as<uint32_t>(), (int)n_recent, cfg->temperature, top_k,
+                               cfg->top_p, cfg->repetition_penalty, dr.as<rai::RngState>(), dw.as<float>(),
+                               df.as<uint32_t>(), dout.as<uint32_t>() + i, nullptr, s);
+    HIP_CHECK(hipGetLastError());
+    if (draws) HIP_CHECK(hipMemcpyAsync(out, dout.p, sizeof(uint32_t) * draws, hipMemcpyDeviceToHost, s));
+    HIP_CHECK(hipStreamSynchronize(s));
+    HIP_CHECK(hipStreamDestroy(s));
   });
 }
 

@@ -21,6 +21,7 @@
 // 2^-24, f64 = (u64 >> 11) * 2^-53.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstdint>
 
 #include "exact_math.h"
@@ -339,6 +340,30 @@ __device__ void row_probs(const float *row, int V, float T, float *out, float *r
   __syncthreads();
 }
 
+// argmax (sampler.rs:201-208): f32::total_cmp order, the last maximum wins
+// (block-wide; every thread returns it).
+__device__ int block_argmax(const float *p, int V) {
+  __shared__ long long best[16];
+  long long b = LLONG_MIN;
+  for (int i = threadIdx.x; i < V; i += blockDim.x) {
+    const int32_t bits = __float_as_int(p[i]);
+    const int32_t key = bits ^ (int32_t)(((uint32_t)(bits >> 31)) >> 1);
+    const long long k = ((long long)key << 32) | (uint32_t)i;
+    b = k > b ? k : b;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const long long x = __shfl_xor(b, o, 64);
+    b = x > b ? x : b;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) best[threadIdx.x >> 6] = b;
+  __syncthreads();
+  long long r = best[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = best[w] > r ? best[w] : r;
+  __syncthreads();
+  return (int)(r & 0xFFFFFFFFll);
+}
+
 // sample_token's draw over the probabilities p (block-wide; thread 0 draws).
 __device__ int draw_token(const float *p, int V, Gen &g, int *ires) {
   __shared__ float rr;
@@ -346,28 +371,8 @@ __device__ int draw_token(const float *p, int V, Gen &g, int *ires) {
   __syncthreads();
   int tok = seq_search(p, V, rr);
   (void)ires;
-  if (tok < 0) {
-    // Fallback: argmax of the probabilities (sampler.rs:201-208, last
-    // maximum wins).
-    __shared__ long long best[16];
-    long long b = LLONG_MIN;
-    for (int i = threadIdx.x; i < V; i += blockDim.x) {
-      const int32_t bits = __float_as_int(p[i]);
-      const int32_t key = bits ^ (int32_t)(((uint32_t)(bits >> 31)) >> 1);
-      const long long k = ((long long)key << 32) | (uint32_t)i;
-      b = k > b ? k : b;
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-      const long long x = __shfl_xor(b, o, 64);
-      b = x > b ? x : b;
-    }
-    if ((threadIdx.x & 63) == 0) best[threadIdx.x >> 6] = b;
-    __syncthreads();
-    long long r = best[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = best[w] > r ? best[w] : r;
-    tok = (int)(r & 0xFFFFFFFFll);
-    __syncthreads();
-  }
+  // Fallback: argmax of the probabilities.
+  if (tok < 0) tok = block_argmax(p, V);
   return tok;
 }
 
@@ -506,6 +511,391 @@ __global__ void k_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *ou
   }
 }
 
+// ------------------------------------------------------------ plain sampler --
+//
+// apply_repetition_penalty (sampler.rs:185-199) over ctx[0..len), then
+// sample_token (sampler.rs:47-182) with the whole SamplerConfig: the token
+// of the `rai run` loop without speculation (run.rs:720-721).  One block of
+// kSampleThreads; x [V] is the working row, flags [V] are zero on entry and
+// on exit (they mark the penalised tokens, then the top-p nucleus).
+
+// f32::total_cmp order as an unsigned key, and back.
+__device__ __forceinline__ uint32_t total_key(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float total_val(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Block-wide exclusive prefix sum of one count per thread; *total gets the
+// block's sum.
+__device__ int block_excl_scan(int v, int *total) {
+  __shared__ int wsum[16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int inc = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += y;
+  }
+  __syncthreads();
+  if (lane == 63) wsum[w] = inc;
+  __syncthreads();
+  int base = 0, tot = 0;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) {
+    if (i < w) base += wsum[i];
+    tot += wsum[i];
+  }
+  *total = tot;
+  return base + inc - v;
+}
+
+// Stage chunk [c0, c0 + cn) of x compactly in index order: its non-zero
+// values to vbuf (and their indices to ibuf), padded with +0 to a multiple
+// of 64; returns the count.  (kStage = 4 x kSampleThreads.)
+__device__ int stage_nonzero(const float *x, int c0, int cn, float *vbuf, int *ibuf) {
+  float v[4];
+  int k = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = 4 * threadIdx.x + u;
+    v[u] = i < cn ? x[c0 + i] : 0.0f;
+    k += v[u] != 0.0f;
+  }
+  int tot;
+  int o = block_excl_scan(k, &tot);
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (v[u] != 0.0f) {
+      vbuf[o] = v[u];
+      if (ibuf) ibuf[o] = c0 + 4 * threadIdx.x + u;
+      ++o;
+    }
+  const int padded = (tot + 63) & ~63;
+  for (int i = tot + threadIdx.x; i < padded; i += blockDim.x) vbuf[i] = 0.0f;
+  __syncthreads();
+  return tot;
+}
+
+// seq_sum over the non-zero entries only: the values are >= +0, so adding
+// a zero leaves every partial sum unchanged.
+__device__ float seq_sum_nz(const float *x, int n) {
+  __shared__ __align__(16) float buf[kStage];
+  __shared__ float res;
+  float c = 0.0f;
+  for (int c0 = 0; c0 < n; c0 += kStage) {
+    const int tot = stage_nonzero(x, c0, min(kStage, n - c0), buf, nullptr);
+    if (threadIdx.x < 64) {
+      for (int i = 0; i < tot; i += 32) {
+        f4v v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f4v *>(&buf[i + 4 * u]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          c = c + v[u][0];
+          c = c + v[u][1];
+          c = c + v[u][2];
+          c = c + v[u][3];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) res = c;
+  __syncthreads();
+  return res;
+}
+
+// seq_search over the non-zero entries only: the running sum does not move
+// at a zero entry, so the first index where r < sum is a non-zero one.
+__device__ int seq_search_nz(const float *x, int n, float r) {
+  __shared__ __align__(16) float buf[kStage];
+  __shared__ int bidx[kStage];
+  __shared__ int res;
+  const int lane = threadIdx.x & 63;
+  float c = 0.0f;
+  int found = -1;
+  for (int c0 = 0; c0 < n && found < 0; c0 += kStage) {
+    const int tot = stage_nonzero(x, c0, min(kStage, n - c0), buf, bidx);
+    if (threadIdx.x < 64) {
+      for (int i = 0; i < tot && found < 0; i += 64) {
+        f4v v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = *reinterpret_cast<const f4v *>(&buf[i + 4 * u]);
+        const float cstart = c;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) c = c + v[u][w];
+        }
+        if (!(c <= r)) {
+          float cc = cstart, pref = 0.0f;
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              cc = cc + v[u][w];
+              pref = lane == 4 * u + w ? cc : pref;
+            }
+          }
+          const uint64_t hit = __ballot(r < pref && i + lane < tot);
+          if (hit) found = bidx[i + __ffsll((unsigned long long)hit) - 1];
+        }
+      }
+    }
+    if (threadIdx.x == 0) res = found;
+    __syncthreads();
+    found = res;
+  }
+  return found;
+}
+
+// The key of descending rank `rank` (0-based) under total_cmp among the
+// entries i of x with elig(i) (rank < their count): a four-pass radix
+// selection over the key bytes.  *eq_before: how many entries with that key
+// rank before it (so rank - *eq_before entries have larger keys).
+template <class E>
+__device__ uint32_t select_desc(const float *x, int V, int rank, E elig, int *eq_before) {
+  __shared__ unsigned hist[256];
+  __shared__ uint32_t sh_prefix;
+  __shared__ int sh_rank;
+  uint32_t prefix = 0, hmask = 0;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < V; i += blockDim.x)
+      if (elig(i)) {
+        const uint32_t k = total_key(x[i]);
+        if ((k & hmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+      }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int r = rank, d = 255;
+      for (; d > 0; --d) {
+        if (r < (int)hist[d]) break;
+        r -= (int)hist[d];
+      }
+      sh_prefix = prefix | ((uint32_t)d << shift);
+      sh_rank = r;
+    }
+    __syncthreads();
+    prefix = sh_prefix;
+    rank = sh_rank;
+    hmask |= 255u << shift;
+  }
+  *eq_before = rank;
+  return prefix;
+}
+
+// Top-p (sampler.rs:129-167) over the probabilities x: the candidates
+// p > 1e-10 in descending p (ties lowest index first), the shortest prefix
+// whose f32 running sum from +0 reaches tp, everything else zeroed, then the
+// division by the f32 sum in index order.  The candidates are taken 1024 at
+// a time: the 1024 largest not taken yet (a radix selection, equal keys by
+// index), sorted in LDS (bitonic), and thread 0 continues the running sum
+// over them in order; the taken ones are marked 2 in flags.
+__device__ void top_p_nucleus(float *x, int V, float tp, uint32_t *flags, int *redi) {
+  constexpr int B = kSampleThreads;
+  __shared__ uint32_t skey[B];
+  __shared__ int sidx[B];
+  __shared__ int sh_cnt, sh_cut, sh_done;
+  __shared__ float sh_cum;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  auto cand = [&](int i) { return x[i] > 1e-10f && flags[i] != 2u; };
+  int remaining = 0;
+  for (int i = tid; i < V; i += nt) remaining += cand(i);
+  remaining = block_sum_i(remaining, redi);
+  if (tid == 0) sh_cum = 0.0f;
+  bool done = false;
+  while (!done && remaining > 0) {
+    const int take = min(B, remaining);
+    const bool all = take == remaining;
+    uint32_t kth = 0;
+    int need_eq = 0;
+    if (!all) {
+      int before;
+      kth = select_desc(x, V, take - 1, cand, &before);
+      need_eq = before + 1;
+    }
+    if (tid == 0) sh_cnt = 0;
+    for (int i = tid; i < B; i += nt) {
+      skey[i] = 0u;
+      sidx[i] = INT_MAX;
+    }
+    __syncthreads();
+    for (int i = tid; i < V; i += nt)
+      if (cand(i)) {
+        const uint32_t k = total_key(x[i]);
+        if (all || k > kth) {
+          const int slot = atomicAdd(&sh_cnt, 1);
+          skey[slot] = k;
+          sidx[slot] = i;
+        }
+      }
+    __syncthreads();
+    if (!all) {
+      // The entries equal to the k-th key, lowest index first.
+      int got = 0;
+      for (int c0 = 0; c0 < V && got < need_eq; c0 += nt) {
+        const int i = c0 + tid;
+        const int eq = i < V && cand(i) && total_key(x[i]) == kth;
+        int tot;
+        const int off = block_excl_scan(eq, &tot);
+        if (eq && got + off < need_eq) {
+          skey[take - need_eq + got + off] = kth;
+          sidx[take - need_eq + got + off] = i;
+        }
+        got += tot;
+      }
+      __syncthreads();
+    }
+    // Bitonic sort: descending key, then ascending index.
+    for (int k = 2; k <= B; k <<= 1)
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const int i = tid, ixj = i ^ j;
+        if (ixj > i) {
+          const uint32_t ka = skey[i], kb = skey[ixj];
+          const int ia = sidx[i], ib = sidx[ixj];
+          const bool a_first = ka > kb || (ka == kb && ia < ib);
+          const bool up = (i & k) == 0;
+          if (up ? !a_first : a_first) {
+            skey[i] = kb;
+            skey[ixj] = ka;
+            sidx[i] = ib;
+            sidx[ixj] = ia;
+          }
+        }
+        __syncthreads();
+      }
+    if (tid == 0) {
+      float c = sh_cum;
+      int cut = take, fin = 0;
+      for (int j = 0; j < take; ++j) {
+        c = c + total_val(skey[j]);
+        if (c >= tp) {
+          cut = j + 1;
+          fin = 1;
+          break;
+        }
+      }
+      sh_cum = c;
+      sh_cut = cut;
+      sh_done = fin;
+    }
+    __syncthreads();
+    for (int j = tid; j < sh_cut; j += nt) flags[sidx[j]] = 2u;
+    __syncthreads();
+    done = sh_done != 0;
+    remaining -= take;
+  }
+  for (int i = tid; i < V; i += nt) {
+    const bool keep = flags[i] == 2u;
+    x[i] = keep ? x[i] : 0.0f;
+    flags[i] = 0u;
+  }
+  __syncthreads();
+  const float sum = seq_sum_nz(x, V);
+  if (sum > 0.0f) {
+    const float is = 1.0f / sum;
+    for (int i = tid; i < V; i += nt) x[i] = x[i] * is;
+  }
+  __syncthreads();
+}
+
+// The plain token: writes it to tok_out (ctx + len when null) and, when res
+// is given, res = {0 accepted, 1 produced}.  With a step record, len, T and
+// the sampler options come from st[1], st[4], st[8..10].
+__global__ __launch_bounds__(kSampleThreads) void k_sample_plain(
+    const float *__restrict__ logits, int V, uint32_t *__restrict__ ctx, int len, float T, int top_k, float top_p,
+    float pen, RngState *rng, float *__restrict__ x, uint32_t *__restrict__ flags, uint32_t *tok_out, int *res,
+    const int *__restrict__ st) {
+  if (st) {
+    len = st[1];
+    T = __int_as_float(st[4]);
+    top_k = st[8];
+    top_p = __int_as_float(st[9]);
+    pen = __int_as_float(st[10]);
+  }
+  __shared__ float redf[16];
+  __shared__ int redi[16];
+  __shared__ float rr;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  // apply_repetition_penalty: each distinct token once.
+  const bool penal = isfinite(pen) && pen > 0.0f && fabsf(pen - 1.0f) >= 1e-6f;
+  if (penal)
+    for (int i = tid; i < len; i += nt) {
+      const uint32_t t = ctx[i];
+      if (t < (uint32_t)V) flags[t] = 1u;
+    }
+  __syncthreads();
+  for (int i = tid; i < V; i += nt) {
+    float v = logits[i];
+    if (penal && flags[i]) {
+      v = v > 0.0f ? v / pen : v * pen;
+      flags[i] = 0u;
+    }
+    x[i] = isnan(v) ? -INFINITY : v;
+  }
+  __syncthreads();
+  int tok;
+  if (!isfinite(T) || T <= 1e-6f) {
+    tok = block_argmax(x, V);
+  } else {
+    const float inv_t = 1.0f / T;
+    for (int i = tid; i < V; i += nt) x[i] = x[i] * inv_t;
+    __syncthreads();
+    if (top_k > 0 && top_k < V) {
+      int before;
+      const float thr = total_val(select_desc(x, V, top_k - 1, [](int) { return true; }, &before));
+      for (int i = tid; i < V; i += nt)
+        if (x[i] < thr) x[i] = -INFINITY;
+      __syncthreads();
+    }
+    int pinf = 0;
+    float mx = -INFINITY;
+    for (int i = tid; i < V; i += nt) {
+      pinf += x[i] == INFINITY;
+      mx = fmaxf(mx, x[i]);
+    }
+    pinf = block_sum_i(pinf, redi);
+    mx = block_max(mx, redf);
+    if (pinf > 0) {
+      const float p = 1.0f / (float)pinf;
+      for (int i = tid; i < V; i += nt) x[i] = x[i] == INFINITY ? p : 0.0f;
+    } else if (mx == -INFINITY) {
+      for (int i = tid; i < V; i += nt) x[i] = 1.0f / (float)V;
+    } else {
+      for (int i = tid; i < V; i += nt) x[i] = rai_exact::expf_glibc(x[i] - mx);
+      __syncthreads();
+      const float sum = seq_sum_nz(x, V);
+      if (isfinite(sum) && sum > 0.0f) {
+        const float is = 1.0f / sum;
+        for (int i = tid; i < V; i += nt) x[i] = x[i] * is;
+      } else {
+        for (int i = tid; i < V; i += nt) x[i] = 1.0f / (float)V;
+      }
+    }
+    __syncthreads();
+    const float tp = isfinite(top_p) ? fminf(fmaxf(top_p, 0.0f), 1.0f) : 1.0f;
+    if (tp < 1.0f) top_p_nucleus(x, V, tp, flags, redi);
+    if (tid == 0) {
+      Gen g{rng};
+      rr = g.gen_f32();
+    }
+    __syncthreads();
+    tok = seq_search_nz(x, V, rr);
+    if (tok < 0) tok = block_argmax(x, V);
+  }
+  if (tid == 0) {
+    uint32_t *o = tok_out ? tok_out : ctx + len;
+    *o = (uint32_t)tok;
+    if (res) {
+      res[0] = 0;
+      res[1] = 1;
+    }
+  }
+}
+
 }  // namespace
 
 void rng_seed_from_u64(RngState &r, uint64_t state) {
@@ -543,6 +933,13 @@ void launch_spec_sample(const float *tlogits, float *tprobs, const float *dlogit
 void launch_draw(const float *row, int V, float T, RngState *rng, float *keep, float *scratch, uint32_t *out,
                  hipStream_t s) {
   hipLaunchKernelGGL(k_draw, dim3(1), dim3(kSampleThreads), 0, s, row, V, T, rng, keep, scratch, out);
+}
+
+void launch_sample_plain(const float *logits, int V, uint32_t *ctx, int len, float T, int top_k, float top_p,
+                         float penalty, RngState *rng, float *work, uint32_t *flags, uint32_t *tok_out, int *res,
+                         hipStream_t s, const int *st) {
+  hipLaunchKernelGGL(k_sample_plain, dim3(1), dim3(kSampleThreads), 0, s, logits, V, ctx, len, T, top_k, top_p,
+                     penalty, rng, work, flags, tok_out, res, st);
 }
 
 void launch_rng_draws(RngState *rng, const int *kinds, int n, uint64_t *out, hipStream_t s) {

@@ -163,3 +163,104 @@ def test_draft_model_acceptance_preserves_the_target_distribution(t):
     wrong_correction = np.minimum(p, q) + (1.0 - beta) * p
     assert n * ((wrong_correction - p) ** 2 / p).sum() > 4 * limit
     assert abs(n * (q * p).sum() - n * beta) > 20 * sigma
+
+
+# ---- sample_token with the whole SamplerConfig and the repetition penalty --
+# (sampler.rs:47-199: the `rai run` token without speculation)
+
+def _softmax64(x):
+    z = np.asarray(x, np.float64)
+    e = np.exp(z - z.max())
+    return e / e.sum()
+
+
+def test_sampler_reference_tests_mirrored():
+    """sampler.rs:216-317: greedy pick, low temperature concentration, the
+    penalty on one token (and once per distinct token), top-k = 2 keeping
+    only the two largest, non-finite logits, non-finite options falling back
+    (T NaN = greedy, top_p NaN = 1, penalty NaN = none)."""
+    rng = ora.Rng(seed=42)
+    assert ora.sample_plain([1.0, 5.0, 2.0, 3.0], [], 0.0, 40, 0.9, 1.0, rng) == 1
+    counts = np.zeros(3, int)
+    for _ in range(100):
+        counts[ora.sample_plain([1.0, 2.0, 3.0], [], 0.1, 0, 1.0, 1.0, rng)] += 1
+    assert counts[2] > 90
+    # [1, 2, 3, 4] with token 3 penalised by 2 -> [1, 2, 3, 2]: greedy picks 2.
+    assert ora.sample_plain([1.0, 2.0, 3.0, 4.0], [3], 0.0, 0, 1.0, 2.0, rng) == 2
+    # once per distinct token: [1, 4] -> [1, 2] (argmax 1), not [1, 0.5].
+    assert ora.sample_plain([1.0, 4.0], [1, 1, 1], 0.0, 0, 1.0, 2.0, rng) == 1
+    # a negative logit is multiplied: [-1, -3] with token 0 penalised by 4 -> [-4, -3].
+    assert ora.sample_plain([-1.0, -3.0], [0], 0.0, 0, 1.0, 4.0, rng) == 1
+    counts = np.zeros(5, int)
+    for _ in range(200):
+        counts[ora.sample_plain([1.0, 5.0, 3.0, 4.0, 2.0], [], 1.0, 2, 1.0, 1.0, rng)] += 1
+    assert counts[0] == counts[2] == counts[4] == 0 and counts[1] > 0 and counts[3] > 0
+    assert ora.sample_plain([np.nan, 1.0, 2.0], [], 0.0, 40, 0.9, 1.1, rng) == 2
+    for _ in range(32):
+        assert ora.sample_plain([np.inf, np.inf, 0.0, np.nan], [], 0.7, 40, 0.9, 1.0, rng) < 2
+    assert ora.sample_plain([np.nan, -np.inf], [], 0.7, 40, 0.9, 1.0, rng) < 2
+    assert ora.sample_plain([1.0, 3.0, 2.0], [], np.nan, (1 << 62), np.nan, np.nan, rng) == 1
+    # penalty NaN changes nothing: [1, 4] stays, greedy 1.
+    assert ora.sample_plain([1.0, 4.0], [1], 0.0, 0, 1.0, np.nan, rng) == 1
+
+
+def _nucleus(p, top_p):
+    order = sorted(range(len(p)), key=lambda i: (-p[i], i))
+    keep, cum = [], 0.0
+    for i in order:
+        keep.append(i)
+        cum += p[i]
+        if cum >= top_p:
+            break
+    q = np.zeros(len(p))
+    q[keep] = p[keep]
+    return q / q.sum()
+
+
+@pytest.mark.parametrize("t,top_k,top_p,penalty", [(0.8, 3, 1.0, 1.0), (1.0, 0, 0.6, 1.0), (0.7, 5, 0.9, 1.3),
+                                                   (1.3, 0, 0.95, 0.5)])
+def test_sampler_distribution_against_float64(t, top_k, top_p, penalty):
+    """The draws follow the distribution the config defines, computed here
+    in float64 from the definitions (penalty on the distinct recent tokens,
+    x / T, the k largest, softmax, the smallest descending prefix reaching
+    top_p, renormalised): chi-squared over 20000 draws.  Keeping one
+    nucleus token too many, or filtering k + 1 tokens, moves the expected
+    statistic far past the limit (checked here)."""
+    logits = np.array([1.2, -0.4, 2.0, 0.3, 1.7, -1.5, 0.9, 2.4, 0.0, 1.1], np.float32)
+    recent = [7, 2, 7, 5]
+    x = logits.astype(np.float64).copy()
+    if abs(penalty - 1.0) >= 1e-6:
+        for tkn in set(recent):
+            x[tkn] = x[tkn] / penalty if x[tkn] > 0 else x[tkn] * penalty
+    x = x / t
+    if 0 < top_k < len(x):
+        thr = np.sort(x)[::-1][top_k - 1]
+        x = np.where(x < thr, -np.inf, x)
+    p = _softmax64(x)
+    q = _nucleus(p, top_p) if top_p < 1 else p
+    rng = ora.Rng(seed=int(1000 * t) + top_k)
+    n = 20000
+    counts = np.zeros(len(logits))
+    for _ in range(n):
+        counts[ora.sample_plain(logits, recent, t, top_k, top_p, penalty, rng)] += 1
+    assert np.all(counts[q == 0] == 0), (counts, q)
+    live = q > 0
+    chi2 = ((counts[live] - n * q[live]) ** 2 / (n * q[live])).sum()
+    dof = int(live.sum()) - 1
+    limit = dof + 8 * np.sqrt(2 * dof) + 10
+    assert chi2 < limit, (chi2, counts / n, q)
+    # Power against plausible mistakes.
+    if top_p < 1:
+        order = sorted(range(len(p)), key=lambda i: (-p[i], i))
+        k_in = int((q > 0).sum())
+        if k_in < int((p > 0).sum()):
+            wrong = np.zeros(len(p))
+            wrong[order[:k_in + 1]] = p[order[:k_in + 1]]
+            wrong /= wrong.sum()
+            assert n * (((wrong - q) ** 2)[live] / q[live]).sum() + n * wrong[~live].sum() > 4 * limit
+    if 0 < top_k < len(x) - 1 and top_p >= 1 and abs(penalty - 1.0) < 1e-6:
+        # Filtering at the (k + 1)-th value instead of the k-th: the extra
+        # token would show up in the draws about this often.
+        z = np.asarray(logits, np.float64) / t
+        wrong = _softmax64(np.where(z < np.sort(z)[::-1][top_k], -np.inf, z))
+        assert n * wrong[~live].sum() > 50

@@ -72,6 +72,12 @@ def test_kv_clear_resets_watermarks(rai, model_file):
     assert kv.filled(1) == 1
 
 
+# Speculative modes need the neutral sampler options (run.rs:134-215); so do
+# comparisons with plain greedy decoding, which the default penalty of 1.1
+# would change.
+NEUTRAL = ["--top-k", "0", "--top-p", "1", "--repetition-penalty", "1"]
+
+
 def _run(args):
     r = subprocess.run([RUN] + args, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
@@ -84,7 +90,7 @@ def test_rai_run_lookup_equals_library(rai, model_file, temperature):
     prompt = copy_heavy_prompt(60, 600, seed=8)
     ids = ",".join(str(int(t)) for t in prompt)
     got = _run([path, "--prompt-ids", ids, "--max-tokens", "40", "--lookup-k", "6", "--lookup-ngram", "3",
-                "--lookup-min-ngram", "1", "--temperature", str(temperature), "--seed", "5"])
+                "--lookup-min-ngram", "1", "--temperature", str(temperature), "--seed", "5"] + NEUTRAL)
     m = rai.RaiModel.load(path)
     dec = rai.LookupDecoder(m, 512)
     dec.seed(5)
@@ -106,7 +112,7 @@ def test_rai_run_draft_and_plain_equal_library(rai, model_file):
     prompt = copy_heavy_prompt(30, 600, seed=9)
     ids = ",".join(str(int(t)) for t in prompt)
     got = _run([path, "--prompt-ids", ids, "--max-tokens", "24", "--draft", draft, "--draft-k", "4",
-                "--temperature", "0.9", "--seed", "11"])
+                "--temperature", "0.9", "--seed", "11"] + NEUTRAL)
     t, d = rai.RaiModel.load(path), rai.RaiModel.load(draft)
     dec = rai.SpeculativeDecoder(d, t, 512)
     dec.seed(11)
@@ -119,7 +125,7 @@ def test_rai_run_draft_and_plain_equal_library(rai, model_file):
         pos += len(take)
         last = take[-1]
     assert got == want
-    plain = _run([path, "--prompt-ids", ids, "--max-tokens", "16", "--temperature", "0"])
+    plain = _run([path, "--prompt-ids", ids, "--max-tokens", "16", "--temperature", "0"] + NEUTRAL)
     assert plain == rai.LookupDecoder(t, 512).greedy_generate(prompt, 16)
 
 
@@ -128,9 +134,12 @@ def test_rai_run_rejects_bad_arguments(model_file):
     r = subprocess.run([RUN, path, "--prompt-ids", "1,2", "--lookup-k", "2", "--draft", draft],
                        capture_output=True, text=True, timeout=60)
     assert r.returncode == 2 and "mutually exclusive" in r.stderr
-    r = subprocess.run([RUN, path, "--prompt-ids", "1,2", "--temperature", "0.5"], capture_output=True, text=True,
-                       timeout=60)
-    assert r.returncode == 2
+    # Speculation with the default top-k / top-p / penalty, and options out
+    # of range.
+    for bad in (["--lookup-k", "2"], ["--draft", draft, "--top-k", "0", "--top-p", "1"], ["--top-p", "0"],
+                ["--repetition-penalty", "5"], ["--temperature", "2.5"]):
+        r = subprocess.run([RUN, path, "--prompt-ids", "1,2"] + bad, capture_output=True, text=True, timeout=60)
+        assert r.returncode == 2, bad
 
 
 def _oracle(ora, path):
@@ -161,7 +170,7 @@ def test_rai_run_plain_greedy_matches_oracle(rai, ora, model_file):
     path, _ = model_file
     prompt = copy_heavy_prompt(50, 600, seed=21)
     ids = ",".join(str(int(t)) for t in prompt)
-    got = _run([path, "--prompt-ids", ids, "--max-tokens", "32", "--temperature", "0"])
+    got = _run([path, "--prompt-ids", ids, "--max-tokens", "32", "--temperature", "0"] + NEUTRAL)
     want = _oracle(ora, path).greedy_generate(prompt.astype(np.int32), 32, 512).tolist()
     assert got == want
 
@@ -175,7 +184,7 @@ def test_rai_run_lookup_matches_oracle(rai, ora, model_file, temperature):
     prompt = copy_heavy_prompt(60, 600, seed=8)
     ids = ",".join(str(int(t)) for t in prompt)
     got = _run([path, "--prompt-ids", ids, "--max-tokens", "40", "--lookup-k", "6", "--lookup-ngram", "3",
-                "--lookup-min-ngram", "1", "--temperature", str(temperature), "--seed", "5"])
+                "--lookup-min-ngram", "1", "--temperature", str(temperature), "--seed", "5"] + NEUTRAL)
     od = ora.LookupDecoder(_oracle(ora, path), 512)
     rng = ora.Rng(seed=5)
     pos = od.prefill(prompt.astype(np.int32))
@@ -201,7 +210,7 @@ def test_rai_run_draft_matches_oracle(rai, ora, model_file, temperature):
     prompt = copy_heavy_prompt(30, 600, seed=9)
     ids = ",".join(str(int(t)) for t in prompt)
     got = _run([path, "--prompt-ids", ids, "--max-tokens", "24", "--draft", draft, "--draft-k", "4",
-                "--temperature", str(temperature), "--seed", "11"])
+                "--temperature", str(temperature), "--seed", "11"] + NEUTRAL)
     od = ora.SpecDecoder(_oracle(ora, draft), _oracle(ora, path), 512)
     rng = ora.Rng(seed=11)
     pos = od.prefill(prompt.astype(np.int32))
