@@ -31,6 +31,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "exact_math.h"
 #include "kernels.h"
@@ -81,7 +82,7 @@ size_t dec_smem(int cols, bool fused) {
   return act + std::max(waves, fused ? sizeof(float) * (size_t)rms_scratch_floats(cols) : size_t(0));
 }
 
-constexpr int kEpiPlain = 0, kEpiGlu = 1, kEpiRope = 2, kEpiMoe = 3;
+constexpr int kEpiPlain = 0, kEpiGlu = 1, kEpiRope = 2, kEpiMoe = 3, kEpiMoeGlu = 4;
 
 // rope_store of one rotation pair (x0 at head element i, x1 at i + hd/2)
 // as k_rope_store does it (layers.rs:561-726): q and k rotated in the qkv
@@ -125,25 +126,37 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
                                                   DecMoe moe) {
   using C = DecCfg<R>;
   constexpr int IPL = C::IPL, LSTR = C::LSTR;
-  constexpr bool GLU = EPI == kEpiGlu, ROPE = EPI == kEpiRope, MOE = EPI == kEpiMoe;
-  static_assert(!GLU || (R == 8 && ST == 0), "a gate|up block: 4 waves x 8 rows, fused input norm");
+  // MOE: one grid row per MoE entry; GLU: the block's gate|up output group
+  // through silu_mul and its quantization (both for an entry's experts).
+  constexpr bool MOE = EPI == kEpiMoe || EPI == kEpiMoeGlu, GLU = EPI == kEpiGlu || EPI == kEpiMoeGlu;
+  constexpr bool ROPE = EPI == kEpiRope;
+  static_assert(EPI != kEpiGlu || (R == 8 && ST == 0), "a gate|up block: 4 waves x 8 rows, fused input norm");
+  static_assert(EPI != kEpiMoeGlu || R == 8, "an entry's gate|up block: 4 waves x 8 rows");
   static_assert(!ROPE || R == 8, "a rope tile: 4 rows of each half of a head");
   static_assert(!MOE || (ST >= 1 && ST <= 4), "an entry row: quantized activations staged from memory");
   extern __shared__ __align__(16) unsigned char smem[];
   const int groups = cols / 32;
   if constexpr (MOE) {
-    // Grid row = MoE entry: its expert's matrix, its activation row and its
-    // output row (the whole block leaves together past the last entry).
+    // Grid row = MoE entry (token, slot): its expert's matrix, its
+    // activation row and its output row (the whole block leaves together
+    // for an empty slot).
     const int ent = blockIdx.y;
-    if (ent >= moe.off[moe.E]) return;
-    const int x = moe.ent_exp[ent];
+    const int x = moe.sel[ent];
+    if (x < 0 || x >= moe.E) return;
     nib = moe.nib_tab[(size_t)x * moe.tstride];
     params = moe.par_tab[(size_t)x * moe.tstride];
-    const int ar = moe.act_row ? moe.act_row[ent] : ent;
+    const int ar = moe.tok_rows ? ent / moe.K : ent;
     q_split += (size_t)ar * cols;
     scales += (size_t)ar * groups;
     sums += (size_t)ar * groups;
-    out += (size_t)ent * moe.ld;
+    if constexpr (EPI == kEpiMoeGlu) {
+      const int fo = rows / 2;  // the entry's silu_mul row: fo values, fo / 32 groups
+      moe.qo += (size_t)ent * fo;
+      moe.so += (size_t)ent * (fo / 32);
+      moe.uo += (size_t)ent * (fo / 32);
+    } else {
+      out += (size_t)ent * moe.ld;
+    }
   }
   const int nchunks = (groups + kDecChunk - 1) / kDecChunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -417,7 +430,7 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
     // silu_mul_inplace (layers.rs:850-883) of the block's 32 outputs and
     // their quantization (gemm.rs:147-374) as k_silu_quant does; the
     // quantized group goes to q_split / scales / sums, which are outputs
-    // here.
+    // here (to the entry's row of moe.qo / so / uo for an expert).
     __syncthreads();  // every wave is done with the staged activations
     float *glu = reinterpret_cast<float *>(smem);
     if (lane < R) {
@@ -434,8 +447,11 @@ __global__ __launch_bounds__(256) void k_w4a8_dec(float *out, const float *add, 
         const float e = rai_exact::schraudolph(xv * -1.0f);
         v[c] = (xv / (1.0f + e)) * glu[32 + 8 * c + j];
       }
-      quantize_group8_to<4>(v, j, lane < 8, const_cast<int8_t *>(q_split) + 32 * b, nullptr,
-                            const_cast<float *>(scales) + b, const_cast<float *>(sums) + b);
+      if constexpr (MOE)
+        quantize_group8_to<4>(v, j, lane < 8, moe.qo + 32 * b, nullptr, moe.so + b, moe.uo + b);
+      else
+        quantize_group8_to<4>(v, j, lane < 8, const_cast<int8_t *>(q_split) + 32 * b, nullptr,
+                              const_cast<float *>(scales) + b, const_cast<float *>(sums) + b);
     }
   }
 }
@@ -545,15 +561,17 @@ bool launch_w4a8_dec(float *out, const float *add, const uint8_t *nib, const uin
   return true;
 }
 
-// 4-row tiles, 4-chunk ring; per entry about 1024 / entries blocks (at
-// least 8, at most one tile per wave), a multiple of 8 so that the blocks of
-// consecutive entries - the entries of one expert are consecutive - fall on
-// the same XCD and share its L2.
+// 4-row tiles, 4-chunk ring; per entry about 2304 / entries blocks rounded
+// up to a multiple of 8 (at least 8, at most one tile per wave): block x of
+// every entry then falls on XCD x mod 8, so the entries of one expert read
+// each row tile through the same L2.  Measured on the OLMoE expert shapes
+// (2048 x 2048 gate|up, 2048 x 1024 down) at 72 entries: 8, 16, 24, 32 and
+// 64 blocks per entry gave a 2.29, 2.17, 2.19, 2.14 and 2.21 ms verify step.
 bool launch_w4a8_dec_moe(float *out, const DecMoe &moe, const int8_t *q_split, const float *scales,
                          const float *sums, int rows, int cols, int gs, int max_entries, hipStream_t s) {
   if (!w4a8_dec_path(rows, cols, gs) || max_entries <= 0 || max_entries > 65535 || cols > 16 * 1024) return false;
   const int tiles = (rows + 3) / 4, full = (tiles + kDecWaves - 1) / kDecWaves;
-  int blocks = std::max(8, (1024 / max_entries) & ~7);
+  int blocks = std::max(8, (2304 / max_entries + 7) & ~7);
   blocks = std::min(blocks, full);
   if (cols <= 16 * 256)
     launch_dec_moe_t<4, 4, 1>(out, moe, q_split, scales, sums, rows, cols, blocks, max_entries, s);
@@ -561,6 +579,36 @@ bool launch_w4a8_dec_moe(float *out, const DecMoe &moe, const int8_t *q_split, c
     launch_dec_moe_t<4, 4, 2>(out, moe, q_split, scales, sums, rows, cols, blocks, max_entries, s);
   else
     launch_dec_moe_t<4, 4, 4>(out, moe, q_split, scales, sums, rows, cols, blocks, max_entries, s);
+  return true;
+}
+
+// The experts' gate|up with silu_mul and the quantization fused: grid
+// (F / 32 output groups, entries), the entry's quantized silu_mul row into
+// moe.qo / so / uo (F = rows / 2 values per entry).
+bool launch_w4a8_dec_moe_glu(const DecMoe &moe, const int8_t *q_split, const float *scales, const float *sums,
+                             int rows, int cols, int gs, int max_entries, hipStream_t s) {
+  if (!w4a8_dec_path(rows, cols, gs) || rows % 64 != 0 || max_entries <= 0 || max_entries > 65535 ||
+      cols > 16 * 1024 || !moe.qo || !moe.so || !moe.uo)
+    return false;
+  const size_t smem = dec_smem<8>(cols, false);
+  auto go = [&](auto st) {
+    constexpr int ST = decltype(st)::value;
+    static size_t configured = 0;
+    if (smem > configured) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4a8_dec<8, 3, ST, kEpiMoeGlu>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      configured = smem;
+    }
+    hipLaunchKernelGGL((k_w4a8_dec<8, 3, ST, kEpiMoeGlu>), dim3(rows / 64, max_entries), dim3(256), smem, s,
+                       nullptr, nullptr, nullptr, nullptr, q_split, scales, sums, rows, cols, 2, nullptr, nullptr,
+                       0.0f, DecRope{}, moe);
+  };
+  if (cols <= 16 * 256)
+    go(std::integral_constant<int, 1>{});
+  else if (cols <= 16 * 512)
+    go(std::integral_constant<int, 2>{});
+  else
+    go(std::integral_constant<int, 4>{});
   return true;
 }
 

@@ -72,19 +72,31 @@ bool launch_w4a8_qkv_rope1(float *out, const uint8_t *nib, const uint8_t *params
                            const float *norm_w, float eps, int rows, int cols, int gs, const DecRope &rope,
                            hipStream_t s);
 
-// Grouped expert GEMV (one-token kernel, one grid row per MoE entry): entry
-// e < off[E] of expert x = ent_exp[e] runs matrix (nib_tab[x * tstride],
-// par_tab[x * tstride]) against activation row act_row[e] (row e when
-// act_row is null) of q_split / scales / sums and writes out + e * ld.
-// Entry rows up to max_entries; those past off[E] are left as they are.
+// Expert GEMVs (one-token kernel, one grid row per MoE entry): entry
+// i = t * K + k is slot k of token t; with expert x = sel[i] in [0, E) it
+// runs matrix (nib_tab[x * tstride], par_tab[x * tstride]) against
+// activation row t (tok_rows) or i of q_split / scales / sums and writes
+// out + i * ld; an empty slot (sel[i] < 0) leaves its row as it is.
 struct DecMoe {
   const uint8_t *const *nib_tab, *const *par_tab;
   int tstride;
-  const int *off, *ent_exp, *act_row;
+  const int *sel;
+  int K;
+  bool tok_rows;
   int E, ld;
+  // Outputs of launch_w4a8_dec_moe_glu: per entry the quantized silu_mul
+  // row (rows / 2 int8 in the block-split order), its scales and sums.
+  int8_t *qo = nullptr;
+  float *so = nullptr, *uo = nullptr;
 };
 bool launch_w4a8_dec_moe(float *out, const DecMoe &moe, const int8_t *q_split, const float *scales,
                          const float *sums, int rows, int cols, int gs, int max_entries, hipStream_t s);
+// The experts' gate|up (rows = 2 F, gate rows first) with silu_mul_inplace
+// and the quantization of its output fused (as launch_silu_quant): one block
+// per (32-value output group, entry); false when the shape is outside the
+// one-token kernel's (or rows % 64 != 0).
+bool launch_w4a8_dec_moe_glu(const DecMoe &moe, const int8_t *q_split, const float *scales, const float *sums,
+                             int rows, int cols, int gs, int max_entries, hipStream_t s);
 
 // Matrix-core W4A8 (gemv.hip): group 32, K a multiple of 256, 2..64 tokens
 // (past 64 the GEMM of gemm_mm.hip is faster on every measured shape).
@@ -273,6 +285,10 @@ void launch_moe_gemv(float *out, int ld, const uint8_t *const *nibp, const uint8
                      hipStream_t s);
 void launch_moe_combine(float *hid, const float *eo, const float *wts, const int *ent_of, int m, int K, int H,
                         hipStream_t s);
+// The combine with entries in (token, slot) order (entry t * K + k), empty
+// slots marked by sel < 0.
+void launch_moe_combine_sel(float *hid, const float *eo, const float *wts, const int *sel, int m, int K, int H,
+                            hipStream_t s);
 
 }  // namespace rai
 

@@ -1231,13 +1231,13 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_logits(const float *_
 // row_shr:1 moves each chain to lane q + 1 of its row, so the dot from -0.0
 // is one sequence of dependent adds with no memory access between them;
 // lane 15 of each row ends with its expert's logit.
+// One wave's four chains: expert e (lane row c = lane / 16) of token t;
+// returns the logit on lane 15 of each row.
 template <int S>
-__global__ __launch_bounds__(64) void k_router_logits_r(const float *__restrict__ x,
-                                                        const float *__restrict__ router, int experts,
-                                                        float *__restrict__ logits) {
+__device__ __forceinline__ float router_chain_r(const float *__restrict__ x, const float *__restrict__ router, int t,
+                                                int e) {
   constexpr int hidden = 16 * S;
-  const int t = blockIdx.x, lane = threadIdx.x, c = lane >> 4, q = lane & 15;
-  const int e = min((int)blockIdx.y * 4 + c, experts - 1);
+  const int q = threadIdx.x & 15;
   const float4 *rr = reinterpret_cast<const float4 *>(router + (size_t)e * hidden + S * q);
   const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)t * hidden + S * q);
   float p[S];
@@ -1268,7 +1268,17 @@ __global__ __launch_bounds__(64) void k_router_logits_r(const float *__restrict_
       acc = q == ph + 1 ? moved : acc;
     }
   }
-  if (q == 15 && (int)blockIdx.y * 4 + c < experts) logits[(size_t)t * experts + blockIdx.y * 4 + c] = acc;
+  return acc;
+}
+
+template <int S>
+__global__ __launch_bounds__(64) void k_router_logits_r(const float *__restrict__ x,
+                                                        const float *__restrict__ router, int experts,
+                                                        float *__restrict__ logits) {
+  const int t = blockIdx.x, lane = threadIdx.x, c = lane >> 4;
+  const int e = min((int)blockIdx.y * 4 + c, experts - 1);
+  const float acc = router_chain_r<S>(x, router, t, e);
+  if ((lane & 15) == 15 && (int)blockIdx.y * 4 + c < experts) logits[(size_t)t * experts + blockIdx.y * 4 + c] = acc;
 }
 
 // route_experts for at most 64 experts, one wave per token, expert e on
@@ -1277,11 +1287,11 @@ __global__ __launch_bounds__(64) void k_router_logits_r(const float *__restrict_
 // wave maximum over the untaken finite probabilities and the lowest lane
 // holding it (a ballot), which is k_router's strict-> scan with the lowest
 // index winning a tie; NaN probabilities are never picked.
-__global__ __launch_bounds__(64) void k_router64(const float *__restrict__ logits, int experts, int topk,
-                                                 int norm_topk, int *__restrict__ sel, float *__restrict__ wts) {
-  const int t = blockIdx.x, lane = threadIdx.x;
+__device__ __forceinline__ void route64_wave(float lg_in, int t, int experts, int topk, int norm_topk,
+                                             int *__restrict__ sel, float *__restrict__ wts) {
+  const int lane = threadIdx.x & 63;
   const bool live = lane < experts;
-  const float lg = live ? logits[(size_t)t * experts + lane] : -INFINITY;
+  const float lg = live ? lg_in : -INFINITY;
   const float mx = wave_max_dpp(lg);
   const float ex = live ? rai_exact::expf_glibc(lg - mx) : 0.0f;
   const int exi = __float_as_int(ex);
@@ -1313,6 +1323,12 @@ __global__ __launch_bounds__(64) void k_router64(const float *__restrict__ logit
     if (norm_topk && total > 0.0f)
       for (int k = 0; k < cnt; ++k) wts[t * topk + k] = __fdiv_exact(wts[t * topk + k], total);
   }
+}
+
+__global__ __launch_bounds__(64) void k_router64(const float *__restrict__ logits, int experts, int topk,
+                                                 int norm_topk, int *__restrict__ sel, float *__restrict__ wts) {
+  const int t = blockIdx.x, lane = threadIdx.x;
+  route64_wave(lane < experts ? logits[(size_t)t * experts + lane] : 0.0f, t, experts, topk, norm_topk, sel, wts);
 }
 
 // route_experts (layers.rs:1808-1870) after the logits: softmax over all

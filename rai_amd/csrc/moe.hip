@@ -2,8 +2,19 @@
 // mlp_block (model.rs:208-261) for m tokens with no host round trip, so a
 // verify step that crosses a sparse layer stays one stream of launches.
 //
-//   k_router (kernels.hip)  softmax over all experts, top-k by selection
-//                           (route_experts, layers.rs:1808-1870)
+//   k_route64 / k_router (kernels.hip)
+//                           router logits, softmax over all experts, top-k
+//                           by selection (route_experts, layers.rs:1808-1870)
+// Group 32 with the experts' gate|up stored as one matrix: entry t * K + k
+// is slot k of token t, with no plan -
+//   k_w4a8_dec (decode_gemv.hip), one grid row per entry: the block reads
+//                           its expert from the router's picks (an empty
+//                           slot leaves), gate|up against the token's row
+//   k_silu_quant (fused.hip) over the entries
+//   k_w4a8_dec              down, against the entry's row
+//   k_moe_combine_sel       out = sum over slots, in slot order from +0, of
+//                           fl(weight * expert value), then hidden += out
+// Otherwise, entries grouped by expert -
 //   k_moe_plan              per-expert entry counts and offsets; entry
 //                           (token, slot) pairs listed expert by expert
 //   k_moe_gather            the token's quantized input row, scales and sums
@@ -15,8 +26,7 @@
 //                           matrix against all of its entries (gate and up
 //                           share a launch)
 //   k_silu_quant (fused.hip) over the entries
-//   k_moe_combine           out = sum over slots, in slot order from +0, of
-//                           fl(weight * expert value), then hidden += out
+//   k_moe_combine           as k_moe_combine_sel through the plan's entry rows
 //
 // Each entry's arithmetic is the one-token W4A8 arithmetic (matmul ==
 // matvec, gemm.rs:1774-1919), so the grouping changes no bit.
@@ -230,6 +240,40 @@ __global__ void k_moe_combine(float *__restrict__ hid, const float *__restrict__
   hid[(size_t)t * H + c] = hid[(size_t)t * H + c] + acc;
 }
 
+// The same sum with the entries in (token, slot) order (entry t * K + k is
+// slot k of token t; the slots past the router's last pick hold -1): the
+// slots' weights and expert values are loaded eight at a time before the
+// sum, which then runs in slot order from +0.
+__global__ void k_moe_combine_sel(float *__restrict__ hid, const float *__restrict__ eo,
+                                  const float *__restrict__ wts, const int *__restrict__ sel, int K, int H) {
+  const int t = blockIdx.y;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= H) return;
+  float acc = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    const int nk = min(8, K - k0);
+    bool ok[8];
+    float w[8], v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = t * K + k0 + min(j, nk - 1);
+      ok[j] = j < nk && sel[i] >= 0;
+      w[j] = wts[i];
+      v[j] = eo[(size_t)i * H + c];
+    }
+    // The slots with a pick come first; the sum stops at the first empty one.
+    int run = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (run == j && ok[j]) ++run;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < run) acc = acc + w[j] * v[j];
+    if (run < nk) break;
+  }
+  hid[(size_t)t * H + c] = hid[(size_t)t * H + c] + acc;
+}
+
 }  // namespace
 
 bool moe_device_path(int hidden, int ffn, int gs, int experts) {
@@ -271,6 +315,11 @@ void launch_moe_gemv(float *out, int ld, const uint8_t *const *nibp, const uint8
 void launch_moe_combine(float *hid, const float *eo, const float *wts, const int *ent_of, int m, int K, int H,
                         hipStream_t s) {
   hipLaunchKernelGGL(k_moe_combine, dim3((H + 255) / 256, m), dim3(256), 0, s, hid, eo, wts, ent_of, K, H);
+}
+
+void launch_moe_combine_sel(float *hid, const float *eo, const float *wts, const int *sel, int m, int K, int H,
+                            hipStream_t s) {
+  hipLaunchKernelGGL(k_moe_combine_sel, dim3((H + 255) / 256, m), dim3(256), 0, s, hid, eo, wts, sel, K, H);
 }
 
 }  // namespace rai

@@ -462,24 +462,36 @@ static void moe_block_device(const rai_model &md, int li, Workspace &w, int m, h
   const uint8_t *const *tab = md.moe_tab.as<const uint8_t *>() + (size_t)6 * E * li;
   launch_router(w.normed.as<float>(), L.router, m, H, E, K, c.norm_topk_prob, w.sel.as<int>(),
                 w.wts.as<float>(), w.mlogit.as<float>(), s);
-  launch_moe_plan(w.sel.as<int>(), m, K, E, w.moff.as<int>(), w.ment_of.as<int>(), w.ment_tok.as<int>(),
-                  w.ment_exp.as<int>(), s);
-  // Entry GEMVs: every expert's gate|up one matrix, each entry's rows through
-  // the one-token kernel, the token's quantized row read in place.
+  // Entry GEMVs: every expert's gate|up one matrix, entry t * K + k (slot k
+  // of token t) through the one-token kernel, the token's quantized row read
+  // in place; no plan: each block reads its entry's expert from the router's
+  // picks, and the combine walks the slots in order.
   if (L.experts_gu && w4a8_dec_path(2 * F, H, gs) && w4a8_dec_path(H, F, gs)) {
-    const DecMoe gu{tab, tab + 2 * E, 2, w.moff.as<int>(), w.ment_exp.as<int>(), w.ment_tok.as<int>(), E, 2 * F};
-    const DecMoe dn{tab + 4 * E, tab + 5 * E, 1, w.moff.as<int>(), w.ment_exp.as<int>(), nullptr, E, H};
-    if (launch_w4a8_dec_moe(w.mgu.as<float>(), gu, w.q_split.as<int8_t>(), w.qscale.as<float>(),
-                            w.qsum.as<float>(), 2 * F, H, gs, ne, s)) {
+    DecMoe gu{tab, tab + 2 * E, 2, w.sel.as<int>(), K, true, E, 2 * F};
+    const DecMoe dn{tab + 4 * E, tab + 5 * E, 1, w.sel.as<int>(), K, false, E, H};
+    gu.qo = w.mq.as<int8_t>();
+    gu.so = w.msc.as<float>();
+    gu.uo = w.msu.as<float>();
+    // gate|up with silu_mul and the quantization of the entry rows fused,
+    // else the two steps apart.
+    bool done = launch_w4a8_dec_moe_glu(gu, w.q_split.as<int8_t>(), w.qscale.as<float>(), w.qsum.as<float>(),
+                                        2 * F, H, gs, ne, s);
+    if (!done && launch_w4a8_dec_moe(w.mgu.as<float>(), gu, w.q_split.as<int8_t>(), w.qscale.as<float>(),
+                                     w.qsum.as<float>(), 2 * F, H, gs, ne, s)) {
       launch_silu_quant(w.mgu.as<float>(), w.mgu.as<float>() + F, ne, F, 2 * F, gs, w.mq.as<int8_t>(), nullptr,
                         w.msc.as<float>(), w.msu.as<float>(), s, nullptr);
+      done = true;
+    }
+    if (done) {
       if (!launch_w4a8_dec_moe(w.eo.as<float>(), dn, w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), H,
                                F, gs, ne, s))
         fail(RAI_E_UNSUPPORTED, "expert down projection shape");
-      launch_moe_combine(w.hid.as<float>(), w.eo.as<float>(), w.wts.as<float>(), w.ment_of.as<int>(), m, K, H, s);
+      launch_moe_combine_sel(w.hid.as<float>(), w.eo.as<float>(), w.wts.as<float>(), w.sel.as<int>(), m, K, H, s);
       return;
     }
   }
+  launch_moe_plan(w.sel.as<int>(), m, K, E, w.moff.as<int>(), w.ment_of.as<int>(), w.ment_tok.as<int>(),
+                  w.ment_exp.as<int>(), s);
   launch_moe_gather(w.q_split.as<int8_t>(), w.qscale.as<float>(), w.qsum.as<float>(), w.ment_tok.as<int>(),
                     w.moff.as<int>(), E, ne, H, H / gs, w.mq.as<int8_t>(), w.msc.as<float>(), w.msu.as<float>(), s);
   launch_moe_gemv(w.mgu.as<float>(), 2 * F, tab, tab + 2 * E, 2, F, H, gs, E, w.mq.as<int8_t>(), w.msc.as<float>(),
