@@ -2,7 +2,7 @@
 // mlp_block (model.rs:208-261) for m tokens with no host round trip, so a
 // verify step that crosses a sparse layer stays one stream of launches.
 //
-//   k_route64 / k_router (kernels.hip)
+//   k_router_logits_r, k_router64 / k_router (kernels.hip)
 //                           router logits, softmax over all experts, top-k
 //                           by selection (route_experts, layers.rs:1808-1870)
 // Group 32 with the experts' gate|up stored as one matrix: entry t * K + k
