@@ -256,14 +256,24 @@ __device__ __forceinline__ void score_chunks(std::integer_sequence<int, Cs...>, 
 // chunk outer, so each key value read serves PB dot products (pairs past the end repeat the
 // last one and store nothing).  HD = 0: rows hd + 1 floats apart, queries
 // from global memory, one pair at a time.  With a step record the token
-// positions start at st[0] + toff.
+// positions start at st[0] + toff.  grid.z splits the m tokens into groups
+// of mb (the LDS holds one group's query rows): group z takes tokens
+// z * mb.. as a launch of its own would.
 template <int HD, int PB>
 __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int q_ld,
                                                 const float *__restrict__ kc, int cap, int pos0,
                                                 int m, int nh, int nkv, int hd_rt, float scale,
                                                 float *__restrict__ S, int sstride,
-                                                const int *__restrict__ st, int toff) {
+                                                const int *__restrict__ st, int toff, int mb) {
   extern __shared__ float ks[];
+  {
+    const int u0 = (int)blockIdx.z * mb;
+    m = min(mb, m - u0);
+    q += (size_t)u0 * q_ld;
+    S += (size_t)u0 * nh * sstride;
+    pos0 += u0;
+    toff += u0;
+  }
   if (st) pos0 = st[0] + toff;
   const int hd = HD > 0 ? HD : hd_rt;
   const int kstride = HD > 0 ? HD + 4 : hd + 1;
@@ -377,7 +387,8 @@ __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int
 
 template <int HD, int PB>
 void launch_scores_t(dim3 sg, size_t ksm, hipStream_t s, const float *q, int q_ld, const float *kc, int cap, int p0,
-                     int m, int nh, int nkv, float scale, float *scores, int sstride, const int *st, int toff) {
+                     int m, int nh, int nkv, float scale, float *scores, int sstride, const int *st, int toff,
+                     int mb) {
   static bool configured = false;
   if (!configured) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_scores<HD, PB>),
@@ -386,25 +397,25 @@ void launch_scores_t(dim3 sg, size_t ksm, hipStream_t s, const float *q, int q_l
     configured = true;
   }
   hipLaunchKernelGGL((k_scores<HD, PB>), sg, dim3(256), ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, HD, scale, scores,
-                     sstride, st, toff);
+                     sstride, st, toff, mb);
 }
 
 template <int HD>
 void launch_scores_hd(dim3 sg, size_t ksm, int npw, hipStream_t s, const float *q, int q_ld, const float *kc, int cap,
                       int p0, int m, int nh, int nkv, float scale, float *scores, int sstride, const int *st,
-                      int toff) {
+                      int toff, int mb) {
   // Pairs per wave at once: all of them up to three, nine for the verify
   // batch, else four at a time.
   if (npw <= 1)
-    launch_scores_t<HD, 1>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+    launch_scores_t<HD, 1>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
   else if (npw == 2)
-    launch_scores_t<HD, 2>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+    launch_scores_t<HD, 2>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
   else if (npw == 3)
-    launch_scores_t<HD, 3>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+    launch_scores_t<HD, 3>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
   else if (npw <= 4 || npw > 9)
-    launch_scores_t<HD, 4>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+    launch_scores_t<HD, 4>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
   else
-    launch_scores_t<HD, 9>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff);
+    launch_scores_t<HD, 9>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
 }
 
 // Score launches for tokens [0, m): the compile-time head dims in sub-batches
@@ -414,20 +425,19 @@ void launch_scores(const float *q, int q_ld, const float *kc, int cap, int p0, i
   static size_t sc_configured = 0;
   const int G = nh / nkv;
   if (hd == 128 || hd == 64) {
+    // Groups of mb tokens (their query rows next to the keys in LDS, at
+    // most 64 KB of them) in one launch, grid.z = group; the grid's x covers
+    // the last group's positions and earlier groups' blocks past their own
+    // positions leave at once.
     const int mb = std::max(1, std::min(16, 16384 / (G * hd)));
-    for (int u0 = 0; u0 < m; u0 += mb) {
-      const int mm = std::min(mb, m - u0);
-      const int nmax_u = st ? nmax : p0 + u0 + mm;
-      const dim3 sg((nmax_u + kScoreTile - 1) / kScoreTile, nkv);
-      const size_t ksm = sizeof(float) * ((size_t)kScoreTile * (hd + 4) + (size_t)G * mm * hd);
-      const int npw = (G * mm + 3) / 4;
-      if (hd == 128)
-        launch_scores_hd<128>(sg, ksm, npw, s, q + (size_t)u0 * q_ld, q_ld, kc, cap, p0 + u0, mm, nh, nkv, scale,
-                              scores + (size_t)u0 * nh * sstride, sstride, st, u0);
-      else
-        launch_scores_hd<64>(sg, ksm, npw, s, q + (size_t)u0 * q_ld, q_ld, kc, cap, p0 + u0, mm, nh, nkv, scale,
-                             scores + (size_t)u0 * nh * sstride, sstride, st, u0);
-    }
+    const int nz = (m + mb - 1) / mb;
+    const dim3 sg((nmax + kScoreTile - 1) / kScoreTile, nkv, nz);
+    const size_t ksm = sizeof(float) * ((size_t)kScoreTile * (hd + 4) + (size_t)G * std::min(mb, m) * hd);
+    const int npw = (G * std::min(mb, m) + 3) / 4;
+    if (hd == 128)
+      launch_scores_hd<128>(sg, ksm, npw, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, 0, mb);
+    else
+      launch_scores_hd<64>(sg, ksm, npw, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, 0, mb);
     return;
   }
   const dim3 sg((nmax + kScoreTile - 1) / kScoreTile, nkv);
@@ -438,7 +448,7 @@ void launch_scores(const float *q, int q_ld, const float *kc, int cap, int p0, i
     sc_configured = ksm;
   }
   hipLaunchKernelGGL((k_scores<0, 1>), sg, dim3(256), ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, hd, scale, scores,
-                     sstride, st, 0);
+                     sstride, st, 0, m);
 }
 
 // The softmax of rows of any length (used past the register-resident
@@ -756,14 +766,14 @@ __global__ __launch_bounds__(512) void k_softmax_c(float *__restrict__ S, int po
 // probabilities per 16-byte LDS read, 32 positions ahead of the chain.  The
 // chunks run to the block's longest token.  No block barrier in the chunk
 // loop: LDS flags hand each tile over (k_pv_flag).
-template <int DL, int G, int CP, int TM, int NL>
+template <int DL, int G, int CP, int TM, int NL, int TPL = 1>
 struct PvCfg {
-  static constexpr int NCW = TM * G * DL / 64;       // compute waves
+  static constexpr int NCW = TM * G * DL / (64 * TPL);  // compute waves (TPL tokens per lane)
   static constexpr int NT = 64 * (NCW + NL);         // threads
   static constexpr int NV = DL * CP / 256;           // V float4 per loader lane per chunk
   static constexpr int NP = (TM * G * CP / 4 + 63) / 64;  // P float4 per loader lane per chunk
   static constexpr int STR = CP + 4;                 // LDS row stride (floats)
-  static_assert(TM * G * DL % 64 == 0, "whole compute waves");
+  static_assert(TM * G * DL % (64 * TPL) == 0 && TM % TPL == 0, "whole compute waves");
 };
 
 
@@ -890,11 +900,64 @@ __device__ __forceinline__ float pv_chunk(const float4 *__restrict__ vr, const f
   return acc;
 }
 
-template <int DL, int G, int CP, int TM, int NL>
-__global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
+// Two chains at once (tokens t and t + 1 of the lane's head and dim): each
+// V read feeds both, so a wave issues two independent FMAs per position
+// and the dependent latency of one hides behind the other.  Groups of 16
+// positions (4 V and 2 x 4 probability reads), read one group ahead with one
+// wait per group.
+template <int CP>
+__device__ __forceinline__ void pv_chunk2(const float4 *__restrict__ vr, const float4 *__restrict__ pr0,
+                                          const float4 *__restrict__ pr1, int nvalid, float &acc0, float &acc1) {
+  constexpr int NG = CP / 16;
+  static_assert(CP % 64 == 0, "whole 64-position quarters");
+  float4 rv[2][4], r0[2][4], r1[2][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    rv[0][u] = vr[u];
+    r0[0][u] = pr0[u];
+    r1[0][u] = pr1[u];
+  }
+#pragma unroll
+  for (int q = 0; q < NG / 4; ++q) {
+    if (64 * q >= nvalid) break;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      const int b = 4 * q + bb;
+      if (b + 1 < NG) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          rv[(b + 1) & 1][u] = vr[4 * (b + 1) + u];
+          r0[(b + 1) & 1][u] = pr0[4 * (b + 1) + u];
+          r1[(b + 1) & 1][u] = pr1[4 * (b + 1) + u];
+        }
+        wait_lgkm<12>();
+      } else {
+        wait_lgkm<0>();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4 v4 = rv[b & 1][u], p4 = r0[b & 1][u], q4 = r1[b & 1][u];
+        acc0 = __fmaf_rn(p4.x, v4.x, acc0);
+        acc1 = __fmaf_rn(q4.x, v4.x, acc1);
+        acc0 = __fmaf_rn(p4.y, v4.y, acc0);
+        acc1 = __fmaf_rn(q4.y, v4.y, acc1);
+        acc0 = __fmaf_rn(p4.z, v4.z, acc0);
+        acc1 = __fmaf_rn(q4.z, v4.z, acc1);
+        acc0 = __fmaf_rn(p4.w, v4.w, acc0);
+        acc1 = __fmaf_rn(q4.w, v4.w, acc1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+template <int DL, int G, int CP, int TM, int NL, int TPL = 1>
+__global__ __launch_bounds__(TM * G * DL / TPL + 64 * NL) void k_pv_flag(
     const float *__restrict__ P, const float *__restrict__ vt_g, int vstride, int pos0, int m, int nh, int hd,
     int sstride, float *__restrict__ out, const int *__restrict__ st, int *__restrict__ err, int spin) {
-  using C = PvCfg<DL, G, CP, TM, NL>;
+  using C = PvCfg<DL, G, CP, TM, NL, TPL>;
+  static_assert(TPL == 1 || TPL == 2, "one or two tokens per compute lane");
   if (st) pos0 = st[0];
   constexpr int NCW = C::NCW, NV = C::NV, NP = C::NP, STR = C::STR;
   constexpr int Q4 = CP / 4;  // float4 per tile row
@@ -978,14 +1041,19 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
   }
   __syncthreads();
   const int L = wave * 64 + lane;
-  const int tl = L / (G * DL), g = (L / DL) % G, dd = L % DL;
-  float acc = 0.0f;
+  // Lane L runs tokens tl .. tl + TPL - 1 of head g, dim dd.
+  const int tl = TPL * (L / (G * DL)), g = (L / DL) % G, dd = L % DL;
+  float acc = 0.0f, acc1 = 0.0f;
   for (int k = 0; k < nchunks; ++k) {
     if (wave < NCW) {
       if (lds_wait_ge<false>(&ready[k & 1], k, spin) < k) pv_wait_failed(err);
       const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
       const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][(tl * G + g) * STR]);
-      acc = pv_chunk<CP>(vr, pr, nmax - k * CP, acc);
+      if constexpr (TPL == 2)
+        pv_chunk2<CP>(vr, pr, reinterpret_cast<const float4 *>(&pt[k & 1][((tl + 1) * G + g) * STR]), nmax - k * CP,
+                      acc, acc1);
+      else
+        acc = pv_chunk<CP>(vr, pr, nmax - k * CP, acc);
       // The release orders this chunk's tile reads before the post.
       __hip_atomic_store(&done[wave], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     } else if (k + 1 < nchunks && lw == (k + 1) % NL) {
@@ -1000,14 +1068,15 @@ __global__ __launch_bounds__(TM * G * DL + 64 * NL) void k_pv_flag(
     }
   }
   if (wave < NCW && tl < tn) out[((size_t)(t0 + tl) * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc;
+  if (TPL == 2 && wave < NCW && tl + 1 < tn) out[((size_t)(t0 + tl + 1) * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc1;
 }
 
-template <int DL, int G, int CP, int TM, int NL>
+template <int DL, int G, int CP, int TM, int NL, int TPL = 1>
 void launch_pv_flag(const float *scores, const float *vc, int vstride, int p0, int m, int nh, int nkv, int hd,
                     int sstride, float *out, const int *st, int *err, int spin, hipStream_t s) {
   const dim3 pg(nkv * (hd / DL), (m + TM - 1) / TM);
-  hipLaunchKernelGGL((k_pv_flag<DL, G, CP, TM, NL>), pg, dim3(PvCfg<DL, G, CP, TM, NL>::NT), 0, s, scores, vc,
-                     vstride, p0, m, nh, hd, sstride, out, st, err, spin);
+  hipLaunchKernelGGL((k_pv_flag<DL, G, CP, TM, NL, TPL>), pg, dim3(PvCfg<DL, G, CP, TM, NL, TPL>::NT), 0, s, scores,
+                     vc, vstride, p0, m, nh, hd, sstride, out, st, err, spin);
 }
 
 // PV for any head_dim: thread per output element, same chain order.  V
@@ -1209,7 +1278,9 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
       // 256 and four; the loaders' registers spill from 640 positions or four
       // loaders at 512; three tokens: 256 and three).
       if (G == 4 && mt > 12)
-        launch_pv_flag<16, 4, 128, 4, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
+        // Prefill batches: eight tokens per block, two per compute lane.
+        launch_pv_flag<16, 4, 128, 8, 4, 2>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin,
+                                            s);
       else if (G == 4 && mt > 2)
         launch_pv_flag<16, 4, 256, 3, 3>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin, s);
       else if (G == 4)
