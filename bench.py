@@ -127,11 +127,12 @@ def profile_workload(which: str) -> int:
                 4096-token prefill, then 12 verify steps with 8 forced drafts;
     sampled   - the same at temperature 0.7 (seed 42);
     olmoe     - OLMoE-1B-7B shape, 2048-token prompt, as greedy;
+    tinyllama - TinyLlama-1.1B shape, 2048-token prompt, as greedy;
     gemm512   - the prefill GEMM alone: 28672 x 4096 W4A8 g32 at M = 512;
     gemv9     - the five verify-step GEMV shapes alone at M = 9.
     Step graphs are off so the trace shows every kernel launch."""
     import rai_amd
-    from rai_amd.workload import MISTRAL_7B, OLMOE, copy_heavy_prompt
+    from rai_amd.workload import MISTRAL_7B, OLMOE, TINYLLAMA, copy_heavy_prompt
     if which == "gemm512":
         n, k, _ = roofline_shape()
         ms, _, _ = measure_gemv(rai_amd, n, k, 512, 32, iters=20)
@@ -145,8 +146,8 @@ def profile_workload(which: str) -> int:
             log(f"{n}x{k} M=9: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
         return 0
     os.environ["RAI_STEP_GRAPHS"] = "0"
-    s = OLMOE if which == "olmoe" else MISTRAL_7B
-    ctx, plen = (4096, 2048) if which == "olmoe" else (8192, 4096)
+    s = OLMOE if which == "olmoe" else TINYLLAMA if which == "tinyllama" else MISTRAL_7B
+    ctx, plen = (4096, 2048) if which in ("olmoe", "tinyllama") else (8192, 4096)
     img = rai_amd.synth_model(s["hidden_size"], s["num_layers"], s["num_heads"], s["num_kv_heads"], s["head_dim"],
                               s["intermediate_size"], s["vocab_size"], ctx, group_size=32,
                               num_experts=s.get("num_experts", 0), experts_per_token=s.get("experts_per_token", 0),
@@ -548,7 +549,7 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other configurations' figures (configs 1, 2, 3 and 5)")
     ap.add_argument("--roofline-only", action="store_true", help=argparse.SUPPRESS)
-    ap.add_argument("--profile", choices=["prefill", "greedy", "sampled", "olmoe", "gemm512", "gemv9"],
+    ap.add_argument("--profile", choices=["prefill", "greedy", "sampled", "olmoe", "tinyllama", "gemm512", "gemv9"],
                     help="run one workload alone (for rocprofv3) and print no JSON line")
     args = ap.parse_args()
     if args.roofline_only:
