@@ -646,8 +646,9 @@ static void forward_enqueue(rai_model &md, rai_kv &kv, Workspace &w, int m, size
     }
   };
   // One token: the projections behind a norm normalise and quantize the
-  // row inside the GEMV launch.
-  const bool norm1 = m == 1 && c.num_experts == 0;
+  // row inside the GEMV launch (a sparse layer's MLP norm stays a launch of
+  // its own: the router reads the normalised row).
+  const bool norm1 = m == 1;
   for (int li = 0; li < (int)c.num_layers; ++li) {
     const DLayer &L = md.layers[li];
     const bool qkv1 = norm1 && L.qkv.rows && w4a8_norm1_path(L.qkv.rows, L.qkv.cols, L.qkv.gs);
