@@ -404,15 +404,19 @@ template <int HD>
 void launch_scores_hd(dim3 sg, size_t ksm, int npw, hipStream_t s, const float *q, int q_ld, const float *kc, int cap,
                       int p0, int m, int nh, int nkv, float scale, float *scores, int sstride, const int *st,
                       int toff, int mb) {
-  // Pairs per wave at once: all of them up to three, nine for the verify
-  // batch, else four at a time.
+  // Pairs per wave at once: all of them up to three, four for four, nine
+  // for the verify batch (5..9), eight at a time beyond.
   if (npw <= 1)
     launch_scores_t<HD, 1>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
   else if (npw == 2)
     launch_scores_t<HD, 2>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
   else if (npw == 3)
     launch_scores_t<HD, 3>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
-  else if (npw <= 4 || npw > 9)
+  else if (npw > 9)
+    // Prefill groups: eight pairs per key read (0.577 against 0.584 s for
+    // the 4095-token Mistral-7B prefill with four).
+    launch_scores_t<HD, 8>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
+  else if (npw <= 4)
     launch_scores_t<HD, 4>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
   else
     launch_scores_t<HD, 9>(sg, ksm, s, q, q_ld, kc, cap, p0, m, nh, nkv, scale, scores, sstride, st, toff, mb);
