@@ -956,12 +956,63 @@ __device__ __forceinline__ void pv_chunk2(const float4 *__restrict__ vr, const f
   }
 }
 
+// Four chains at once (tokens t .. t + 3 of the lane's head and dim, token
+// rows PS4 float4 apart): each V read feeds four independent FMAs per
+// position.  Groups of 8 positions (2 V and 4 x 2 probability reads), read
+// one group ahead with one wait per group.
+template <int CP, int PS4>
+__device__ __forceinline__ void pv_chunk4(const float4 *__restrict__ vr, const float4 *__restrict__ pr, int nvalid,
+                                          float (&acc)[4]) {
+  constexpr int NG = CP / 8;
+  static_assert(CP % 64 == 0, "whole 64-position quarters");
+  float4 rv[2][2], rp[2][4][2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    rv[0][u] = vr[u];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) rp[0][t][u] = pr[t * PS4 + u];
+  }
+#pragma unroll
+  for (int q = 0; q < NG / 8; ++q) {
+    if (64 * q >= nvalid) break;
+#pragma unroll
+    for (int bb = 0; bb < 8; ++bb) {
+      const int b = 8 * q + bb;
+      if (b + 1 < NG) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          rv[(b + 1) & 1][u] = vr[2 * (b + 1) + u];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) rp[(b + 1) & 1][t][u] = pr[t * PS4 + 2 * (b + 1) + u];
+        }
+        wait_lgkm<10>();
+      } else {
+        wait_lgkm<0>();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const float4 v4 = rv[b & 1][u];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = __fmaf_rn(rp[b & 1][t][u].x, v4.x, acc[t]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = __fmaf_rn(rp[b & 1][t][u].y, v4.y, acc[t]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = __fmaf_rn(rp[b & 1][t][u].z, v4.z, acc[t]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = __fmaf_rn(rp[b & 1][t][u].w, v4.w, acc[t]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 template <int DL, int G, int CP, int TM, int NL, int TPL = 1>
 __global__ __launch_bounds__(TM * G * DL / TPL + 64 * NL) void k_pv_flag(
     const float *__restrict__ P, const float *__restrict__ vt_g, int vstride, int pos0, int m, int nh, int hd,
     int sstride, float *__restrict__ out, const int *__restrict__ st, int *__restrict__ err, int spin) {
   using C = PvCfg<DL, G, CP, TM, NL, TPL>;
-  static_assert(TPL == 1 || TPL == 2, "one or two tokens per compute lane");
+  static_assert(TPL == 1 || TPL == 2 || TPL == 4, "one, two or four tokens per compute lane");
   if (st) pos0 = st[0];
   constexpr int NCW = C::NCW, NV = C::NV, NP = C::NP, STR = C::STR;
   constexpr int Q4 = CP / 4;  // float4 per tile row
@@ -1011,6 +1062,18 @@ __global__ __launch_bounds__(TM * G * DL / TPL + 64 * NL) void k_pv_flag(
       const int f = 64 * u + lane;
       *reinterpret_cast<f4 *>(&vt[b][(f / Q4) * STR + 4 * (f % Q4)]) = fv[u];
     }
+    if (tn == TM && s0 + CP <= pos0 + t0 + 1) {
+      // Every row of the block covers the whole chunk: nothing to mask.
+#pragma unroll
+      for (int r = 0; r < NP; ++r) {
+        const int f = 64 * r + lane;
+        if (f < TM * G * Q4) {
+          const int rr = f / Q4;
+          *reinterpret_cast<f4 *>(&pt[b][rr * STR + 4 * (f % Q4)]) = fp[r] * pinv[rr];
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < NP; ++r) {
       const int f = 64 * r + lane;
@@ -1047,32 +1110,41 @@ __global__ __launch_bounds__(TM * G * DL / TPL + 64 * NL) void k_pv_flag(
   const int L = wave * 64 + lane;
   // Lane L runs tokens tl .. tl + TPL - 1 of head g, dim dd.
   const int tl = TPL * (L / (G * DL)), g = (L / DL) % G, dd = L % DL;
-  float acc = 0.0f, acc1 = 0.0f;
-  for (int k = 0; k < nchunks; ++k) {
-    if (wave < NCW) {
+  // One loop per role (the role is wave-uniform), so the loaders' in-flight
+  // tiles are not live in the compute loop's registers.
+  if (wave < NCW) {
+    float acc[TPL];
+#pragma unroll
+    for (int t = 0; t < TPL; ++t) acc[t] = 0.0f;
+    for (int k = 0; k < nchunks; ++k) {
       if (lds_wait_ge<false>(&ready[k & 1], k, spin) < k) pv_wait_failed(err);
       const float4 *vr = reinterpret_cast<const float4 *>(&vt[k & 1][dd * STR]);
       const float4 *pr = reinterpret_cast<const float4 *>(&pt[k & 1][(tl * G + g) * STR]);
-      if constexpr (TPL == 2)
-        pv_chunk2<CP>(vr, pr, reinterpret_cast<const float4 *>(&pt[k & 1][((tl + 1) * G + g) * STR]), nmax - k * CP,
-                      acc, acc1);
+      if constexpr (TPL == 4)
+        pv_chunk4<CP, G * STR / 4>(vr, pr, nmax - k * CP, acc);
+      else if constexpr (TPL == 2)
+        pv_chunk2<CP>(vr, pr, pr + G * STR / 4, nmax - k * CP, acc[0], acc[1]);
       else
-        acc = pv_chunk<CP>(vr, pr, nmax - k * CP, acc);
+        acc[0] = pv_chunk<CP>(vr, pr, nmax - k * CP, acc[0]);
       // The release orders this chunk's tile reads before the post.
       __hip_atomic_store(&done[wave], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    } else if (k + 1 < nchunks && lw == (k + 1) % NL) {
-      // Tile half (k + 1) & 1 held chunk k - 1: wait until every compute
-      // wave has consumed it.
+    }
+#pragma unroll
+    for (int t = 0; t < TPL; ++t)
+      if (tl + t < tn) out[((size_t)(t0 + tl + t) * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc[t];
+  } else {
+    // Loader lw publishes chunks lw, lw + NL, ... (loader 0 published chunk 0
+    // above and holds chunk NL).  Tile half c & 1 held chunk c - 2: wait
+    // until every compute wave has consumed it.
+    for (int c = lw == 0 ? NL : lw; c < nchunks; c += NL) {
 #pragma unroll
       for (int w = 0; w < NCW; ++w)
-        if (lds_wait_ge<true>(&done[w], k, spin) < k) pv_wait_failed(err);
-      publish(k + 1);
-      __hip_atomic_store(&ready[(k + 1) & 1], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (k + 1 + NL < nchunks) issue(k + 1 + NL);
+        if (lds_wait_ge<true>(&done[w], c - 1, spin) < c - 1) pv_wait_failed(err);
+      publish(c);
+      __hip_atomic_store(&ready[c & 1], c, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (c + NL < nchunks) issue(c + NL);
     }
   }
-  if (wave < NCW && tl < tn) out[((size_t)(t0 + tl) * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc;
-  if (TPL == 2 && wave < NCW && tl + 1 < tn) out[((size_t)(t0 + tl + 1) * nh + (size_t)kvh * G + g) * hd + d0 + dd] = acc1;
 }
 
 template <int DL, int G, int CP, int TM, int NL, int TPL = 1>
@@ -1281,8 +1353,16 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
       // token: 512-position tiles and two loaders, 21.0 -> 20.0 us against
       // 256 and four; the loaders' registers spill from 640 positions or four
       // loaders at 512; three tokens: 256 and three).
-      if (G == 4 && mt > 12)
-        // Prefill batches: eight tokens per block, two per compute lane.
+      if (G == 4 && mt > 12 && hd % 32 == 0)
+        // Prefill batches: 32-dim slices, eight tokens per block, four per
+        // compute lane (each V read feeds four chains; a kv head's
+        // probability rows are read by four slice blocks instead of eight):
+        // 0.517 s per 4095-token Mistral-7B prefill against 0.552-0.559 with
+        // 16-dim slices and two tokens per lane (two to four loaders within
+        // 0.002 s).
+        launch_pv_flag<32, 4, 128, 8, 2, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin,
+                                            s);
+      else if (G == 4 && mt > 12)
         launch_pv_flag<16, 4, 128, 8, 4, 2>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin,
                                             s);
       else if (G == 4 && mt > 2)

@@ -104,20 +104,24 @@ def test_single_token_fused_norm_bit_exact(rai, ora, kw):
                               _bits(om.hidden_to_logits_batch(oh, 1))), p
 
 
-def test_multi_token_attention_batches_bit_exact(rai, ora):
-    """Batches of 13, 40 and 9 tokens continuing from earlier positions with
-    four query heads per kv head and head_dim 128: the PV kernel's
-    several-token blocks (three and four tokens per block, the last block
-    partial) against the oracle's per-token chains, bit for bit."""
-    img = _small_synth(rai, hidden_size=1024, num_layers=2, num_heads=8, num_kv_heads=2, head_dim=128,
+@pytest.mark.parametrize("hd", [128, 96, 80])
+def test_multi_token_attention_batches_bit_exact(rai, ora, hd):
+    """Batches of 300, 13, 40 and 9 tokens continuing from earlier positions
+    with four query heads per kv head: the PV kernel's several-token blocks
+    (three tokens per block for nine, eight per block beyond twelve, the
+    last block partial, several 128-position tiles) against the oracle's
+    per-token chains, bit for bit.  head_dim 128 and 96 take the 32-dim
+    slices with four tokens per compute lane, 80 the 16-dim slices with
+    two."""
+    img = _small_synth(rai, hidden_size=1024, num_layers=2, num_heads=8, num_kv_heads=2, head_dim=hd,
                        intermediate_size=1024, vocab_size=500, max_context=512, seed=23)
     om = ora.Model(img, 0)
     gm = rai.RaiModel.from_bytes(img, max_groups=1024)
-    toks = _token_sequence(om.cfg.vocab_size, 62)
+    toks = _token_sequence(om.cfg.vocab_size, 362)
     hs = np.stack([om.embed_token(t) for t in toks])
-    okv, gkv = om.create_kv(128), gm.create_kv_cache(128)
+    okv, gkv = om.create_kv(512), gm.create_kv_cache(512)
     p = 0
-    for n in (13, 40, 9):
+    for n in (300, 13, 40, 9):
         oh = om.forward_batch(hs[p:p + n], np.arange(p, p + n), okv)
         gh = gm.forward_batch(hs[p:p + n], np.arange(p, p + n), gkv)
         assert np.array_equal(_bits(gh), _bits(oh)), (p, n)
