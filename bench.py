@@ -68,8 +68,11 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA
-# Non-packed f32 VALU lane operations per second: 256 CUs x 64 lanes x 2.4 GHz.
-VALU_PEAK_GOPS = 256 * 64 * 2.4
+# f32 VALU lane operations per second at MI355X's published FP32 vector peak
+# (157.3 TFLOP/s, 78.6 T fused multiply-adds): 256 CUs x 128 lanes x 2.4 GHz.
+# Independent v_fmac_f32 measured on the device sustain 51.6 T/s (eight waves
+# per SIMD), above the 64-lane-per-CU figure once used here.
+VALU_PEAK_GOPS = 256 * 128 * 2.4
 
 
 def log(msg: str) -> None:
