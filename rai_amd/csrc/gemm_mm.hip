@@ -53,34 +53,42 @@ constexpr int kMmRec = 2304;  // bytes per (token tile, group)
 constexpr int kMmP = 16;      // groups per LDS stage
 constexpr int kMmWR = 4;      // waves (32-row tiles) per block
 
-// One thread per (token tile, group, block b, lane): the lane's four f16
-// A values; lanes < 32 of blocks 0 and 1 also write the tile's scales and
-// input sums.  Tokens past m are zero.
-__global__ void k_mm_pack(const int8_t *__restrict__ q_split, const float *__restrict__ scales,
-                          const float *__restrict__ sums, int m, int cols, int groups, int ntt,
-                          uint8_t *__restrict__ rec) {
-  const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= (size_t)ntt * groups * 256) return;
-  const int l = (int)(id & 63), b = (int)((id >> 6) & 3);
-  const size_t tg = id >> 8;  // tile * groups + group
-  const int g = (int)(tg % groups), tt = (int)(tg / groups);
-  const int i = l & 31, h = l >> 5;
-  const int t = tt * 32 + i;
-  uint8_t *r = rec + tg * kMmRec;
-  h4 a = {(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
-  if (t < m) {
+// One block per (token tile, four consecutive groups), 256 threads.  The
+// tile's 32 rows of those 128 columns are read with whole-line loads (eight
+// lanes of 16 bytes per row) into LDS; then thread (b, lane) of pass g
+// writes the lane's four f16 A values of block b of group g, and one
+// thread per (group, token) its scale or input sum.  Tokens past m are
+// zero.
+__global__ __launch_bounds__(256) void k_mm_pack(const int8_t *__restrict__ q_split,
+                                                 const float *__restrict__ scales, const float *__restrict__ sums,
+                                                 int m, int cols, int groups, uint8_t *__restrict__ rec) {
+  constexpr int QS = 128 + 16;  // LDS row stride (bytes)
+  __shared__ __align__(16) int8_t qs[32 * QS];
+  const int tid = threadIdx.x, gq = blockIdx.x, tt = blockIdx.y;
+  {
+    const int row = tid >> 3, seg = tid & 7, t = tt * 32 + row;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (t < m) v = *reinterpret_cast<const uint4 *>(q_split + (size_t)t * cols + 128 * gq + 16 * seg);
+    *reinterpret_cast<uint4 *>(qs + row * QS + 16 * seg) = v;
+  }
+  __syncthreads();
+  uint8_t *r0 = rec + ((size_t)tt * groups + 4 * gq) * kMmRec;
+  const int l = tid & 63, b = tid >> 6, i = l & 31, h = l >> 5;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
     // q_split block: four even columns, then four odd ones.
-    const uint2 q = *reinterpret_cast<const uint2 *>(q_split + (size_t)t * cols + 32 * g + 8 * b);
-    const int8_t *e = reinterpret_cast<const int8_t *>(&q);
+    const int8_t *e = qs + i * QS + 32 * g + 8 * b;
+    h4 a;
     a[0] = (_Float16)(float)e[h];
     a[1] = (_Float16)(float)e[h + 2];
     a[2] = (_Float16)((float)e[4 + h] * 0.0625f);
     a[3] = (_Float16)((float)e[6 + h] * 0.0625f);
+    *reinterpret_cast<h4 *>(r0 + g * kMmRec + b * 512 + l * 8) = a;
   }
-  *reinterpret_cast<h4 *>(r + b * 512 + l * 8) = a;
-  if (l < 32 && b < 2) {
-    const float v = t < m ? (b == 0 ? scales : sums)[(size_t)t * groups + g] : 0.0f;
-    reinterpret_cast<float *>(r + 2048 + b * 128)[i] = v;
+  {
+    const int g = tid >> 6, which = (tid >> 5) & 1, t = tt * 32 + i;
+    const float v = t < m ? (which ? sums : scales)[(size_t)t * groups + 4 * gq + g] : 0.0f;
+    reinterpret_cast<float *>(r0 + g * kMmRec + 2048 + which * 128)[i] = v;
   }
 }
 
@@ -253,9 +261,7 @@ void launch_w4a8_mm(float *out, const float *add, const uint8_t *nib, const uint
                     const float *scales, const float *sums, int rows, int cols, int m, uint8_t *pack,
                     hipStream_t s) {
   const int groups = cols / 32, ntt = (m + 31) / 32;
-  const size_t n = (size_t)ntt * groups * 256;
-  hipLaunchKernelGGL(k_mm_pack, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, q_split, scales, sums, m, cols,
-                     groups, ntt, pack);
+  hipLaunchKernelGGL(k_mm_pack, dim3(groups / 4, ntt), dim3(256), 0, s, q_split, scales, sums, m, cols, groups, pack);
   const dim3 grid((rows + 32 * kMmWR - 1) / (32 * kMmWR), ntt);
   hipLaunchKernelGGL((k_w4a8_mm<kMmWR, kMmP>), grid, dim3(64 * kMmWR), 0, s, out, add, nib, params, pack, rows,
                      cols, m);
