@@ -1598,14 +1598,16 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
       // 256 and four; the loaders' registers spill from 640 positions or four
       // loaders at 512; three tokens: 256 and three).
       if (G == 4 && mt > 12 && hd % 32 == 0)
-        // Prefill batches: 32-dim slices, eight tokens per block, four per
-        // compute lane (each V read feeds four chains; a kv head's
-        // probability rows are read by four slice blocks instead of eight):
-        // 0.517 s per 4095-token Mistral-7B prefill against 0.552-0.559 with
-        // 16-dim slices and two tokens per lane (two to four loaders within
-        // 0.002 s).
-        launch_pv_flag<32, 4, 128, 8, 2, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin,
-                                            s);
+        // Prefill batches (128 tokens per launch): 32-dim slices, eight
+        // tokens per block, four per compute lane (each V read feeds four
+        // chains; a kv head's probability rows are read by four slice
+        // blocks instead of eight), 64-position tiles and two loaders, whose
+        // registers (126 per lane) let two blocks share a CU: 0.483 s per
+        // 4095-token Mistral-7B prefill against 0.491 with 128-position
+        // tiles (236 registers, one block per CU) and 0.506 with 64-token
+        // launches.
+        launch_pv_flag<32, 4, 64, 8, 2, 4>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin,
+                                           s);
       else if (G == 4 && mt > 12)
         launch_pv_flag<16, 4, 128, 8, 4, 2>(scores, vc, vstride, p0, mt, nh, nkv, hd, sstride, ot, st, err, g_pv_spin,
                                             s);

@@ -175,7 +175,7 @@ void launch_rope_store(float *q, float *k, const float *v, const float *cos_t, c
 // V cache d-major [nkv][hd][vstride] when vstride > 0, else [nkv][cap][hd].
 // `scores` is scratch of attention_scores_floats(m, nh, pos0 + m) floats;
 // tokens are processed in groups of kAttnTokens.
-constexpr int kAttnTokens = 64;
+constexpr int kAttnTokens = 128;
 size_t attention_scores_floats(int m, int nh, int ctx);
 // q rows are q_ld floats apart; out is [m][nh * hd].
 // With a step record `st` (m <= kAttnTokens), grids, the score stride and
