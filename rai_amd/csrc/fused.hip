@@ -1388,6 +1388,143 @@ void launch_pv_flag(const float *scores, const float *vc, int vstride, int p0, i
                      vc, vstride, p0, m, nh, hd, sstride, out, st, err, spin);
 }
 
+// One-token attention over a short context in one launch: one block per kv
+// head and G * HD = 512 threads, with k_scores', k_softmax_w's and
+// pv_chunk's arithmetic and orders.  The block requests the kv head's V rows
+// (positions up to n rounded up to 64) into registers, then wave w computes
+// the scores of positions 64 w + lane for the G query heads from the lane's
+// key row in registers (query values through DPP row_newbcast, as
+// k_scores) and the V rows go to LDS; wave g runs head g's softmax (the row
+// in registers, DPP maximum, Schraudolph on the first 8 floor(n/8)
+// positions, expf on the tail; chain j on lane j over the position-major row
+// at stride 8, the zeros past 8 floor(n/8) leaving it unchanged) and stores
+// p = e * (1/sum) over the scores; thread (g, d) then runs the PV chain of
+// head g, dim d.  Positions up to NMAX.
+template <int HD, int G, int NMAX>
+__global__ __launch_bounds__(512) void k_attn1s(const float *__restrict__ q, const float *__restrict__ kc,
+                                                const float *__restrict__ vc, int cap, int vstride, int pos0,
+                                                float scale, float *__restrict__ out, const int *__restrict__ st) {
+  constexpr int NT = 512, STR = NMAX + 4, KSTR = HD + 4, KV4 = HD * (NMAX / 4) / NT;
+  static_assert(G * HD == NT && NMAX % 64 == 0 && NMAX <= 64 * (NT / 64), "a lane per position and chain");
+  static_assert(KV4 * NT == HD * (NMAX / 4), "whole V and key float4s per thread");
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  // The key rows [position][HD + 4], then the V rows [dim][position].
+  constexpr int XF = (NMAX * KSTR > HD * STR) ? NMAX * KSTR : HD * STR;
+  __shared__ __align__(16) float xs[XF];
+  __shared__ __align__(16) float ps[G * STR];  // scores, then probabilities [head][position]
+  __shared__ __align__(16) float qs[G * HD];
+  if (st) pos0 = st[0];
+  const int n = pos0 + 1, n8x8 = n & ~7, nv = (n + 63) & ~63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kvh = blockIdx.x;
+  // Key float4 i = tid + 512 k: position i / (HD / 4), clamped to the last;
+  // V float4 i: dim i / (NMAX / 4), positions 4 (i % (NMAX / 4)).., clamped
+  // to the row.  Both requested before any is used.
+  f4 kr[KV4], vr[KV4];
+  const float *kb = kc + (size_t)kvh * cap * HD;
+  const float *vb = vc + (size_t)kvh * HD * vstride;
+#pragma unroll
+  for (int k = 0; k < KV4; ++k) {
+    const int i = tid + NT * k, r = i / (HD / 4), c4 = i % (HD / 4);
+    if (r < nv) kr[k] = reinterpret_cast<const f4 *>(kb + (size_t)min(r, n - 1) * HD)[c4];
+  }
+#pragma unroll
+  for (int k = 0; k < KV4; ++k) {
+    const int i = tid + NT * k, d = i / (NMAX / 4), p = 4 * (i % (NMAX / 4));
+    if (p < nv) vr[k] = *reinterpret_cast<const f4 *>(vb + (size_t)d * vstride + min(p, vstride - 4));
+  }
+  if (tid < G * HD / 4)
+    reinterpret_cast<f4 *>(qs)[tid] = reinterpret_cast<const f4 *>(q + (size_t)kvh * G * HD)[tid];
+#pragma unroll
+  for (int k = 0; k < KV4; ++k) {
+    const int i = tid + NT * k, r = i / (HD / 4), c4 = i % (HD / 4);
+    if (r < nv) *reinterpret_cast<f4 *>(xs + r * KSTR + 4 * c4) = kr[k];
+  }
+  __syncthreads();
+  // Scores of position s = 64 wave + lane for the G heads.
+  const int s = 64 * wave + lane;
+  if (64 * wave < n) {
+    float qb[G][HD / 16];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int mm = 0; mm < HD / 16; ++mm) qb[g][mm] = qs[g * HD + 16 * mm + (lane & 15)];
+    float a[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[g][i] = 0.0f;
+    score_chunks<HD, G>(std::make_integer_sequence<int, HD / 8>{}, reinterpret_cast<const sf4 *>(xs + s * KSTR),
+                        qb, a);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float d = ((a[g][0] + a[g][4]) + (a[g][1] + a[g][5])) + ((a[g][2] + a[g][6]) + (a[g][3] + a[g][7]));
+      if (s < n) ps[g * STR + s] = d * scale;
+    }
+  }
+  __syncthreads();  // the key rows are read: the region takes the V rows
+#pragma unroll
+  for (int k = 0; k < KV4; ++k) {
+    const int i = tid + NT * k, d = i / (NMAX / 4), p = 4 * (i % (NMAX / 4));
+    if (p < nv) *reinterpret_cast<f4 *>(xs + d * STR + p) = vr[k];
+  }
+  __syncthreads();
+  if (wave < G) {
+    float *row = ps + wave * STR;
+    constexpr int NB = NMAX / 64;
+    float v[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) v[k] = row[min(lane + 64 * k, n - 1)];
+    const float xt = row[min(n8x8 + (lane & 7), n - 1)];  // tail value (lanes < n - n8x8)
+    float mx = v[0];
+#pragma unroll
+    for (int k = 1; k < NB; ++k) mx = fmaxf(mx, v[k]);
+    mx = wave_max_dpp(mx);
+    // schraudolph(-inf) is +0: positions from 8 floor(n/8) on hold 0.
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int p = lane + 64 * k;
+      v[k] = rai_exact::schraudolph(p < n8x8 ? v[k] - mx : -INFINITY);
+      row[p] = v[k];
+    }
+    const float et = lane < n - n8x8 ? rai_exact::expf_glibc(xt - mx) : 0.0f;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // Chain j on lane j: e_{8i+j} for i < NMAX / 8 in order (+0 past n / 8).
+    float acc = 0.0f;
+    if (lane < 8) {
+      float r[NMAX / 8];
+#pragma unroll
+      for (int i = 0; i < NMAX / 8; ++i) r[i] = row[8 * i + lane];
+#pragma unroll
+      for (int i = 0; i < NMAX / 8; ++i) acc = acc + r[i];
+    }
+    float c[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) c[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), k));
+    float sum = ((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7]));
+#pragma unroll
+    for (int k = 0; k < 7; ++k)
+      if (k < n - n8x8) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(et), k));
+    const float inv = 1.0f / sum;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int k = 0; k < NB; ++k) row[lane + 64 * k] = v[k] * inv;
+    if (lane < n - n8x8) row[n8x8 + lane] = et * inv;
+  }
+  __syncthreads();
+  {
+    const int g = tid / HD, d = tid % HD;
+    const float acc = pv_chunk<NMAX>(reinterpret_cast<const float4 *>(xs + d * STR),
+                                     reinterpret_cast<const float4 *>(ps + g * STR), n, 0.0f);
+    out[(size_t)(kvh * G + g) * HD + d] = acc;
+  }
+}
+
 // PV for any head_dim: thread per output element, same chain order.  V
 // layout: DMAJOR [kv][hd][vstride], else [kv][cap][hd].
 template <bool DMAJOR>
@@ -1549,6 +1686,15 @@ void launch_attention(const float *q, int q_ld, const float *kc, const float *vc
     const int sstride = score_stride(nmax);
     const float *qt = q + (size_t)t0 * q_ld;
     float *ot = out + (size_t)t0 * nh * hd;
+    if (stages == 7 && mt == 1 && nh == 8 * nkv && hd == 64 && nmax <= 384 && vstride > 0 && vstride % 64 == 0) {
+      // One token over a short context: scores, softmax and PV in one launch
+      // (11.0 against 3.5 + 4.0 + 4.7 us at 128-256 positions for the
+      // TinyLlama shape; the block's key and V loads, 4 CUs for 4 kv heads,
+      // take 2.6 of them).
+      hipLaunchKernelGGL((k_attn1s<64, 8, 384>), dim3(nkv), dim3(512), 0, s, qt, kc, vc, cap, vstride, p0, scale, ot,
+                         st);
+      continue;
+    }
     if (stages & 1) launch_scores(qt, q_ld, kc, cap, p0, mt, nh, nkv, hd, scale, scores, sstride, nmax, st, s);
     if (!(stages & 2)) {
     } else if (mt > 12 && nmax <= 4096) {

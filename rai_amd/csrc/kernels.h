@@ -185,7 +185,7 @@ size_t attention_scores_floats(int m, int nh, int ctx);
 // attn_span(cap, n) is the span of a step whose last position is n - 1, and
 // attn_span_index its b.  `err` (may be null): bit 0 is set when a PV tile
 // hand-off wait gave up (the output is then wrong and the caller must fail).
-constexpr int kAttnSpan0 = 16384;
+constexpr int kAttnSpan0 = 256;
 inline int attn_span_index(int n) {
   int b = 0;
   while ((kAttnSpan0 << b) < n) ++b;

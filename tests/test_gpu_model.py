@@ -151,6 +151,43 @@ def test_hidden_3072_norm_chains_bit_exact(rai, ora):
         p += n
 
 
+def test_single_token_short_context_one_launch_bit_exact(rai, ora):
+    """One-token steps at every position from 0 to 389 with eight query
+    heads per kv head and head_dim 64: up to 384 positions the scores, the
+    softmax and PV run as one launch per kv head (fewer than 8 positions, a
+    multiple of 8, every tail length 1..7), past it the separate kernels;
+    hidden states bit for bit against the oracle."""
+    img = _small_synth(rai, hidden_size=1024, num_layers=1, num_heads=16, num_kv_heads=2, head_dim=64,
+                       intermediate_size=1024, vocab_size=500, max_context=512, seed=37)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    toks = _token_sequence(om.cfg.vocab_size, 390)
+    hs = np.stack([om.embed_token(t) for t in toks])
+    okv, gkv = om.create_kv(512), gm.create_kv_cache(512)
+    for p in range(390):
+        oh = om.forward_batch(hs[p:p + 1], np.arange(p, p + 1), okv)
+        gh = gm.forward_batch(hs[p:p + 1], np.arange(p, p + 1), gkv)
+        assert np.array_equal(_bits(gh), _bits(oh)), p
+
+
+@pytest.mark.parametrize("graphs", ["1", "0"])
+def test_short_context_greedy_lookup_equals_oracle(rai, ora, monkeypatch, graphs):
+    """Greedy lookup decoding from a 40-token prompt through position 300
+    with eight query heads per kv head and head_dim 64 (one-launch attention
+    for one-token steps, step graphs captured per 256-position span), token
+    for token against the oracle's decoder."""
+    monkeypatch.setenv("RAI_STEP_GRAPHS", graphs)
+    img = _small_synth(rai, hidden_size=1024, num_layers=2, num_heads=16, num_kv_heads=2, head_dim=64,
+                       intermediate_size=1024, vocab_size=600, max_context=1024, seed=53)
+    om = ora.Model(img, 0)
+    gm = rai.RaiModel.from_bytes(img, max_groups=1024)
+    prompt = copy_heavy_prompt(40, 600, seed=9)
+    cfg = rai.LookupConfig(max_draft=8, min_ngram=1, max_ngram=3)
+    toks, _ = rai.LookupDecoder(gm, 1024).generate(prompt, 260, cfg)
+    want = om.greedy_generate(prompt.astype(np.int32), len(toks), 1024).tolist()
+    assert toks == want
+
+
 def test_single_token_attention_long_context_bit_exact(rai, ora):
     """One-token steps after 1100 positions with four query heads per kv
     head and head_dim 128: the softmax's sum chains past their read-ahead,
