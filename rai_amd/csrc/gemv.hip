@@ -554,7 +554,7 @@ __device__ __forceinline__ float mul_h16(uint32_t w, float x, float nz) {
 // zero).  The lane runs that token's block-h chain, its cs and its zc chain
 // (5 operations per group instead of 11); l1off[b] moves the lane's A slot
 // to the one block b needs, hs moves its scale slot to the token's.
-template <int NG, int NQ, bool SUB, bool L1>
+template <int NG, int NQ, bool SUB, bool L1, int PSB>
 __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, const __amdgpu_buffer_rsrc_t rps,
                                              uint32_t vc0, uint32_t vp0, const u32x4 *__restrict__ la,
                                              const f32x4 *__restrict__ lsc, const f32x4 *__restrict__ lsu,
@@ -621,7 +621,7 @@ __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, c
 #pragma unroll
       for (int b = 0; b < 4; ++b) avc[b] = avn[b];
     }
-    rp[sp] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, qr * 16, 0);
+    rp[sp] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, qr * PSB, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
   // The first NQ steps (step 0 peeled), then the rest NQ at a time.
@@ -652,7 +652,11 @@ __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, c
 
 // Block of WPB waves = 16 * WPB rows and TGW token groups (blockIdx.y picks
 // the token groups); requires K <= 128 * MAXQ and (K / 128) % NQ == 0.
-template <int TGW, int NQ, int WPB, int MAXQ>
+// TMP: the parameters in the 16-row tile layout of k_params_tile16 (rows a
+// multiple of 16), where one step's parameters of a wave's 16 rows are 256
+// contiguous bytes (two cache lines) instead of 16 bytes in each of 16
+// rows: the same values, fewer lines per load.
+template <int TGW, int NQ, int WPB, int MAXQ, bool TMP>
 __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
     float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
     const _Float16 *__restrict__ qa, const float *__restrict__ scales, const float *__restrict__ sums, int rows,
@@ -684,7 +688,9 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
   const __amdgpu_buffer_rsrc_t rqa =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(qa), 0, ntg * nq * 1024, 0x00020000);
   const uint32_t vc0 = (uint32_t)rowc * (cols / 2) + h * 16;
-  const uint32_t vp0 = (uint32_t)rowc * groups * 4;
+  constexpr int PSB = TMP ? 256 : 16;  // parameter bytes between steps
+  const uint32_t vp0 =
+      TMP ? (uint32_t)(rowc >> 4) * groups * 64 + (rowc & 15) * 16 : (uint32_t)rowc * groups * 4;
 
   // Activations, scales and sums first (fixed counts, clamped duplicates
   // past the end, all issued before any wait), then the ring.
@@ -712,7 +718,7 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
 #pragma unroll
   for (int s = 0; s < NQ - 1; ++s) {
     rc[s] = __builtin_amdgcn_raw_buffer_load_b128(rcs, (int)vc0, s * 64, 0);
-    rp[s] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, s * 16, 0);
+    rp[s] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, s * PSB, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
   // Unconditional stores (clamped duplicates write the same values); the
@@ -768,16 +774,16 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
 #pragma unroll
     for (int s = 0; s < NQ - 1; ++s) {
       rch[s] = __builtin_amdgcn_raw_buffer_load_b128(rcs, (int)vc0, s * 64, 0);
-      rph[s] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, s * 16, 0);
+      rph[s] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, s * PSB, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    gemv_rp_main<TGW, NQ, false, false>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rch, rph, f, zc,
+    gemv_rp_main<TGW, NQ, false, false, PSB>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rch, rph, f, zc,
                                         l1off, h);
   } else if (l1) {
-    gemv_rp_main<TGW, NQ, true, true>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rc, rp, f, zc,
+    gemv_rp_main<TGW, NQ, true, true, PSB>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rc, rp, f, zc,
                                       l1off, h);
   } else {
-    gemv_rp_main<TGW, NQ, true, false>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rc, rp, f, zc,
+    gemv_rp_main<TGW, NQ, true, false, PSB>(rcs, rps, vc0, vp0, la + aslot, lsc + h, lsu + h, nq, nz, rc, rp, f, zc,
                                        l1off, h);
   }
   // Single-token group: lane (j, h) holds block chain h; lane (j, 0) sums
@@ -858,27 +864,68 @@ bool gemv_rp_ok(int rows, int cols) {
          (int64_t)rows * (cols / 2) < ((int64_t)1 << 31);
 }
 
-template <int TGW, int WPB, int MAXQ, int NQ = kRpRing>
+template <int TGW, int WPB, int MAXQ, bool TMP, int NQ = kRpRing>
 void launch_rp(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                const float *scales, const float *sums, int rows, int cols, int m, int ntg, hipStream_t s) {
   constexpr size_t kStepBytes = 68 * 16 + 2 * 4 * 16;  // A blocks, scales, sums of one (group, step)
   static bool configured = false;
   if (!configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_rp<TGW, NQ, WPB, MAXQ>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_rp<TGW, NQ, WPB, MAXQ, TMP>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)(TGW * MAXQ * kStepBytes));
     configured = true;
   }
   const size_t smem = TGW * (size_t)(cols / 128) * kStepBytes;
   const dim3 grid((rows + 16 * WPB - 1) / (16 * WPB), (ntg + TGW - 1) / TGW);
-  hipLaunchKernelGGL((k_gemv_rp<TGW, NQ, WPB, MAXQ>), grid, dim3(64 * WPB), smem, s, out, add, nib, params, qa,
+  hipLaunchKernelGGL((k_gemv_rp<TGW, NQ, WPB, MAXQ, TMP>), grid, dim3(64 * WPB), smem, s, out, add, nib, params, qa,
                      scales, sums, rows, cols, m, ntg);
+}
+
+template <bool TMP>
+void launch_rp_shape(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
+                     const float *scales, const float *sums, int rows, int cols, int m, int ntg, hipStream_t s) {
+  constexpr int Q = kRpMaxCols / 128, Q1 = kRpMaxColsOne / 128;
+  const int rb = (rows + 63) / 64;
+  auto blocks = [&](int tgw) { return rb * ((ntg + tgw - 1) / tgw); };
+  // Three token groups per wave for 3, 5 or 6 and more groups (the
+  // duplicates past an odd count cost less than a third pass over the
+  // weights), two for four.
+  const bool three = ntg >= 3 && ntg != 4;
+  if (cols > kRpMaxCols)
+    launch_rp<1, 4, Q1, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+  else if (three && rows >= 16384)
+    launch_rp<3, 8, Q, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+  else if (three && blocks(3) >= 192)
+    launch_rp<3, 4, Q, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+  else if (ntg >= 2 && blocks(2) >= 192)
+    launch_rp<2, 4, Q, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+  else
+    launch_rp<1, 4, Q, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+}
+
+// One thread per 16 bytes (four groups' parameters of one row).
+__global__ void k_params_tile16(const u32x4 *__restrict__ params, int rows, int nq, u32x4 *__restrict__ tiled) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * nq) return;
+  const int row = i / nq, q = i - row * nq;
+  tiled[((size_t)(row >> 4) * nq + q) * 16 + (row & 15)] = params[i];
 }
 
 }  // namespace
 
+bool params_tile16_ok(int rows, int cols, int gs) {
+  return gs == 32 && rows % 16 == 0 && cols % 128 == 0 && (int64_t)rows * (cols / 32) * 4 < ((int64_t)1 << 31);
+}
+
+void launch_params_tile16(const uint8_t *params, int rows, int cols, uint8_t *tiled, hipStream_t s) {
+  const int nq = cols / 128;
+  const int n = rows * nq;
+  hipLaunchKernelGGL(k_params_tile16, dim3((n + 255) / 256), dim3(256), 0, s,
+                     reinterpret_cast<const u32x4 *>(params), rows, nq, reinterpret_cast<u32x4 *>(tiled));
+}
+
 bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                       const float *scales, const float *sums, int rows, int cols, int m, int gs,
-                      hipStream_t s) {
+                      hipStream_t s, const uint8_t *params_tiled) {
   if (!qa || !w4a8_mfma_path(rows, cols, m, gs)) return false;
   const int ntg = (m + 3) / 4;
   const int groups = cols / 32;
@@ -889,25 +936,15 @@ bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const ui
   // count of token groups that the wave's groups do not divide runs the
   // last block with clamped duplicate groups whose outputs are not stored);
   // eight waves per block for three groups from 16384 rows.  For longer K (K / 128 a
-  // multiple of 4, at most 14336) one token group per block.
-  constexpr int Q = kRpMaxCols / 128, Q1 = kRpMaxColsOne / 128;
+  // multiple of 4, at most 14336) one token group per block.  With the
+  // parameters also in the 16-row tile layout, that copy is read instead
+  // (o_proj 4096x4096 at 9 tokens 10.9 -> 9.3 us, down 4096x14336 31.8 ->
+  // 26.6, gate|up 28672x4096 27.5 -> 26.6).
   if (gemv_rp_ok(rows, cols)) {
-    const int rb = (rows + 63) / 64;
-    auto blocks = [&](int tgw) { return rb * ((ntg + tgw - 1) / tgw); };
-    // Three token groups per wave for 3, 5 or 6 and more groups (the
-    // duplicates past an odd count cost less than a third pass over the
-    // weights), two for four.
-    const bool three = ntg >= 3 && ntg != 4;
-    if (cols > kRpMaxCols)
-      launch_rp<1, 4, Q1>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (three && rows >= 16384)
-      launch_rp<3, 8, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (three && blocks(3) >= 192)
-      launch_rp<3, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
-    else if (ntg >= 2 && blocks(2) >= 192)
-      launch_rp<2, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    if (params_tiled && params_tile16_ok(rows, cols, gs))
+      launch_rp_shape<true>(out, add, nib, params_tiled, qa, scales, sums, rows, cols, m, ntg, s);
     else
-      launch_rp<1, 4, Q>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+      launch_rp_shape<false>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
     return true;
   }
   // Longer K: the register-streamed kernel for many rows (one wave keeps up

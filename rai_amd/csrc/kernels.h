@@ -25,10 +25,12 @@ void launch_quantize(const float *x, int m, int k, int gs, int8_t *q_nat, int8_t
 // enables the matrix-core kernel for 2..kMfmaMaxTokens tokens at group 32.
 // `mm` (may be null): mm_pack_bytes(m, cols) bytes of scratch, which
 // enables the matrix-core GEMM for more than kMfmaMaxTokens tokens.
+// `params_tiled` (may be null): launch_params_tile16's copy of `params`,
+// which the matrix-core GEMV then reads.
 void launch_w4a8(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const float *x,
                  const int8_t *q_nat, const int8_t *q_split, const float *scales,
                  const float *sums, int rows, int cols, int m, int gs, hipStream_t s,
-                 const _Float16 *qa = nullptr, uint8_t *mm = nullptr);
+                 const _Float16 *qa = nullptr, uint8_t *mm = nullptr, const uint8_t *params_tiled = nullptr);
 
 // One token: rms_norm(x) * norm_w (layers.rs:325-376), its group-32
 // quantization and the W4A8 GEMV in one launch; each block normalises and
@@ -107,9 +109,18 @@ size_t qa_pack_halves(int m, int cols);
 // Packs block-split int8 activations [m][cols] into the MFMA A-operand
 // layout (f16, zero rows for the padding tokens of the last 4-token group).
 void launch_qa_pack(const int8_t *q_split, int m, int cols, _Float16 *qa, hipStream_t s);
+// `params_tiled` (may be null): the same parameters in the layout of
+// launch_params_tile16, read instead of `params` where it applies.
 bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
                       const float *scales, const float *sums, int rows, int cols, int m, int gs,
-                      hipStream_t s);
+                      hipStream_t s, const uint8_t *params_tiled = nullptr);
+// The parameter array of a group-32 matrix (rows x cols/32 dwords, f16
+// scale and zero point per row and group) rearranged in 16-row tiles:
+// [rows / 16][cols / 128][16 rows][4 groups] dwords, the layout the
+// matrix-core GEMV reads in one 256-byte piece per step and wave.  Same
+// size as the input; requires params_tile16_ok.
+bool params_tile16_ok(int rows, int cols, int gs);
+void launch_params_tile16(const uint8_t *params, int rows, int cols, uint8_t *tiled, hipStream_t s);
 // Matrix-core W4A8 GEMM (gemm_mm.hip): group 32, K a multiple of 512,
 // more than kMfmaMaxTokens tokens.  Packs the block-split activations into
 // `pack` (mm_pack_bytes(m, cols) bytes), then runs the GEMM.

@@ -58,6 +58,9 @@ struct DevBuf {
 struct DLinear {
   int rows = 0, cols = 0, gs = 0;
   const uint8_t *nib = nullptr, *params = nullptr;
+  // The parameters again in 16-row tiles (launch_params_tile16), read by
+  // the matrix-core GEMV of 2..64 tokens; null where that does not apply.
+  const uint8_t *params_tiled = nullptr;
 };
 
 struct DLayer {
@@ -94,6 +97,7 @@ struct rai_model {
   // Sparse layers: per layer 6 * num_experts device pointers, the code and
   // parameter arrays of gate|up (expert-major, gate then up), then of down.
   DevBuf moe_tab;
+  DevBuf tiled;  // the params_tiled copies
   ~rai_model();
 };
 
@@ -405,6 +409,38 @@ static void upload_model(rai_model &m, const uint8_t *img, size_t len, int max_g
     HIP_CHECK(hipMemcpy(m.moe_tab.p, tab.data(), sizeof(void *) * tab.size(), hipMemcpyHostToDevice));
   }
   HIP_CHECK(hipStreamCreateWithFlags(&m.stream, hipStreamNonBlocking));
+  // Tile-layout copies of the parameters of the matrices the batched
+  // forward runs through the matrix-core GEMV (about a fifth of the weight
+  // bytes again; decode reads only the originals).
+  {
+    std::vector<DLinear *> tl;
+    for (DLayer &D : m.layers) {
+      if (D.qkv.rows) tl.push_back(&D.qkv);
+      else for (int p : {0, 1, 2}) tl.push_back(&D.lin[p]);
+      tl.push_back(&D.lin[3]);
+      if (c.num_experts == 0) {
+        if (D.gate_up.rows) tl.push_back(&D.gate_up);
+        else for (int p : {4, 5}) tl.push_back(&D.lin[p]);
+        tl.push_back(&D.lin[6]);
+      }
+    }
+    if (!m.tied) tl.push_back(&m.lm_head);
+    size_t tb = 0;
+    for (DLinear *L : tl)
+      if (params_tile16_ok(L->rows, L->cols, L->gs)) tb += ((size_t)L->rows * (L->cols / 32) * 4 + 255) & ~size_t(255);
+    if (tb) {
+      m.tiled.alloc(tb);
+      uint8_t *p = m.tiled.as<uint8_t>();
+      for (DLinear *L : tl) {
+        if (!params_tile16_ok(L->rows, L->cols, L->gs)) continue;
+        launch_params_tile16(L->params, L->rows, L->cols, p, m.stream);
+        L->params_tiled = p;
+        p += ((size_t)L->rows * (L->cols / 32) * 4 + 255) & ~size_t(255);
+      }
+      HIP_CHECK(hipGetLastError());
+      HIP_CHECK(hipStreamSynchronize(m.stream));
+    }
+  }
 }
 
 // ------------------------------------------------------------- forward --
@@ -413,7 +449,7 @@ static void linear(const DLinear &L, const float *x, const Workspace &w, float *
                    hipStream_t s, const float *add = nullptr) {
   launch_w4a8(out, add, L.nib, L.params, x, w.q_nat.as<int8_t>(), w.q_split.as<int8_t>(),
               w.qscale.as<float>(), w.qsum.as<float>(), L.rows, L.cols, m, L.gs, s,
-              w.qa.as<_Float16>(), w.qmm.as<uint8_t>());
+              w.qa.as<_Float16>(), w.qmm.as<uint8_t>(), L.params_tiled);
 }
 
 // After any quantization of m rows of k columns into the workspace: pack
@@ -1469,10 +1505,20 @@ int rai_w4a8_time_dev(float *out, const uint8_t *nib, const uint8_t *params, con
     }
     if (rai::w4a8_mm_path((int)rows, (int)cols, (int)m, (int)gs)) mm.alloc(rai::mm_pack_bytes((int)m, (int)cols));
     const size_t nib_bytes = rows * cols / 2, par_bytes = rows * groups * 4;
+    // The parameters' tile-layout copies, as a loaded model holds them.
+    rai::DevBuf tiled;
+    if (mfma && rai::params_tile16_ok((int)rows, (int)cols, (int)gs)) {
+      tiled.alloc(copies * par_bytes);
+      for (size_t c = 0; c < copies; ++c)
+        rai::launch_params_tile16(params + c * par_bytes, (int)rows, (int)cols, tiled.as<uint8_t>() + c * par_bytes,
+                                  s);
+      HIP_CHECK(hipGetLastError());
+    }
     auto run = [&](size_t c) {
       rai::launch_w4a8(out, nullptr, nib + c * nib_bytes, params + c * par_bytes, x, qn.as<int8_t>(),
                        qs.as<int8_t>(), sc.as<float>(), su.as<float>(), (int)rows, (int)cols, (int)m, (int)gs, s,
-                       mfma ? qa.as<_Float16>() : nullptr, mm.as<uint8_t>());
+                       mfma ? qa.as<_Float16>() : nullptr, mm.as<uint8_t>(),
+                       tiled.p ? tiled.as<uint8_t>() + c * par_bytes : nullptr);
     };
     run(0);  // warm-up
     HIP_CHECK(hipEventRecord(e0, s));
