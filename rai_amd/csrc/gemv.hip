@@ -534,6 +534,30 @@ size_t gemv_rs_smem(int tgw, int nq_chunk) {
 // the parameter dword directly.  With subnormal codes the staged activation
 // scales carry the 2^24 (as * 2^24 is exact below 2^104): fl(ws * (as *
 // 2^24)) = fl((ws * 2^24) * as).
+// One 16-byte piece of block-split int8 activations (blocks b and b + 1 of
+// one token and group; per block the even columns c0 c2 c4 c6, then the odd
+// ones c1 c3 c5 c7) as the two f16 A slots of those blocks: K order (0, 4,
+// 1, 5, 2, 6, 3, 7), odd columns divided by 16, as k_qa_pack4 writes them.
+// A byte x ^ 0x80 = x + 128 placed under 0x64 is the f16 1152 + x; minus
+// 1152 gives x, and times 1/16 then minus 72 gives x / 16, every step exact.
+__device__ __forceinline__ void a_slots_from_i8(u32x4 v, u32x4 &a0, u32x4 &a1) {
+  const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  const h2 sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const h2 off = {(_Float16)-72.0f, (_Float16)-72.0f};
+  auto slot = [&](uint32_t ev, uint32_t od) {
+    ev ^= 0x80808080u;
+    od ^= 0x80808080u;
+    const h2 e01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, ev, 0x04020400u)) + bias;
+    const h2 e45 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, ev, 0x04030401u)) + bias;
+    const h2 e23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, od, 0x04020400u)) * sixteenth + off;
+    const h2 e67 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, od, 0x04030401u)) * sixteenth + off;
+    return u32x4{__builtin_bit_cast(uint32_t, e01), __builtin_bit_cast(uint32_t, e23),
+                 __builtin_bit_cast(uint32_t, e45), __builtin_bit_cast(uint32_t, e67)};
+  };
+  a0 = slot(v[0], v[1]);
+  a1 = slot(v[2], v[3]);
+}
+
 constexpr int kRpMaxCols = 4096, kRpMaxColsOne = 14336;
 
 template <bool HI>
@@ -656,17 +680,21 @@ __device__ __forceinline__ void gemv_rp_main(const __amdgpu_buffer_rsrc_t rcs, c
 // multiple of 16), where one step's parameters of a wave's 16 rows are 256
 // contiguous bytes (two cache lines) instead of 16 bytes in each of 16
 // rows: the same values, fewer lines per load.
+//
+// The A operands are built in the prologue from the block-split int8
+// activations (half the bytes of their f16 form, which matters: every CU
+// pulls the whole activation block through its L1 before the first step).
 template <int TGW, int NQ, int WPB, int MAXQ, bool TMP>
 __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
     float *out, const float *add, const uint8_t *__restrict__ nib, const uint8_t *__restrict__ params,
-    const _Float16 *__restrict__ qa, const float *__restrict__ scales, const float *__restrict__ sums, int rows,
+    const int8_t *__restrict__ q_split, const float *__restrict__ scales, const float *__restrict__ sums, int rows,
     int cols, int m, int ntg) {
   typedef u32x4 u4;
   typedef f32x4 f4;
   constexpr int NT = 64 * WPB;
-  constexpr int PA = MAXQ * 64 / NT;             // A u4 per thread and token group
+  constexpr int PB = MAXQ * 32 / NT;             // 16-byte int8 pieces per thread and token group
   constexpr int PS = (MAXQ * 4 + NT - 1) / NT;   // scale / sum f4 per thread and token group
-  static_assert(PA * NT == MAXQ * 64, "whole A loads per thread");
+  static_assert(PB * NT == MAXQ * 32, "whole activation loads per thread");
   extern __shared__ __align__(16) unsigned char smem[];
   const int groups = cols / 32, nq = groups / 4;
   // LDS: A [TGW][nq][4 blocks][17 slots] u4 (slot 16 zero) | scales, sums
@@ -685,24 +713,34 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(nib), 0, rows * (cols / 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rps =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(params), 0, rows * groups * 4, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rqa =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(qa), 0, ntg * nq * 1024, 0x00020000);
+  // Rows of tokens past m read as zeros (past the range).
+  const __amdgpu_buffer_rsrc_t rqs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(q_split), 0, m * cols, 0x00020000);
   const uint32_t vc0 = (uint32_t)rowc * (cols / 2) + h * 16;
   constexpr int PSB = TMP ? 256 : 16;  // parameter bytes between steps
   const uint32_t vp0 =
       TMP ? (uint32_t)(rowc >> 4) * groups * 64 + (rowc & 15) * 16 : (uint32_t)rowc * groups * 4;
 
-  // Activations, scales and sums first (fixed counts, clamped duplicates
-  // past the end, all issued before any wait), then the ring.
-  u4 sa[TGW][PA];
+  // Activations (16-byte int8 pieces), scales and sums first (fixed counts,
+  // clamped duplicates past the end, all issued before any wait), then the
+  // ring.  Piece i of a token group: its token t = i / (nq * 8), bytes
+  // 16 w.. of that token's row (w = i % (nq * 8)), which hold blocks
+  // 2 (w & 1) and 2 (w & 1) + 1 of group w / 2.
+  const int npr = nq * 8;  // pieces per token row
+  auto piece = [&](int i, int &t, int &w) {
+    t = (i >= npr) + (i >= 2 * npr) + (i >= 3 * npr);
+    w = i - t * npr;
+  };
+  u4 sq[TGW][PB];
   f4 ssc[TGW][PS], ssu[TGW][PS];
 #pragma unroll
   for (int tg = 0; tg < TGW; ++tg) {
-    const int tgo = min(tg0 + tg, ntg - 1) * nq * 1024;
+    const int tgc = min(tg0 + tg, ntg - 1);
 #pragma unroll
-    for (int u = 0; u < PA; ++u) {
-      const int ic = min(tid + NT * u, nq * 64 - 1);
-      sa[tg][u] = __builtin_amdgcn_raw_buffer_load_b128(rqa, ic * 16, tgo, 0);
+    for (int u = 0; u < PB; ++u) {
+      int t, w;
+      piece(min(tid + NT * u, nq * 32 - 1), t, w);
+      sq[tg][u] = __builtin_amdgcn_raw_buffer_load_b128(rqs, (4 * tgc + t) * cols + 16 * w, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < PS; ++u) {
@@ -728,9 +766,14 @@ __global__ __launch_bounds__(64 * WPB, 8 / WPB) void k_gemv_rp(
 #pragma unroll
   for (int tg = 0; tg < TGW; ++tg) {
 #pragma unroll
-    for (int u = 0; u < PA; ++u) {
-      const int ic = min(tid + NT * u, nq * 64 - 1);
-      la[tg * nq * 68 + ic + (ic >> 4)] = sa[tg][u];
+    for (int u = 0; u < PB; ++u) {
+      int t, w;
+      piece(min(tid + NT * u, nq * 32 - 1), t, w);
+      u4 a0, a1;
+      a_slots_from_i8(sq[tg][u], a0, a1);
+      u4 *d = la + tg * nq * 68 + ((w >> 3) * 4 + 2 * (w & 1)) * 17 + 4 * t + ((w >> 1) & 3);
+      d[0] = a0;
+      d[17] = a1;
     }
 #pragma unroll
     for (int u = 0; u < PS; ++u) {
@@ -865,7 +908,7 @@ bool gemv_rp_ok(int rows, int cols) {
 }
 
 template <int TGW, int WPB, int MAXQ, bool TMP, int NQ = kRpRing>
-void launch_rp(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
+void launch_rp(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                const float *scales, const float *sums, int rows, int cols, int m, int ntg, hipStream_t s) {
   constexpr size_t kStepBytes = 68 * 16 + 2 * 4 * 16;  // A blocks, scales, sums of one (group, step)
   static bool configured = false;
@@ -876,12 +919,12 @@ void launch_rp(float *out, const float *add, const uint8_t *nib, const uint8_t *
   }
   const size_t smem = TGW * (size_t)(cols / 128) * kStepBytes;
   const dim3 grid((rows + 16 * WPB - 1) / (16 * WPB), (ntg + TGW - 1) / TGW);
-  hipLaunchKernelGGL((k_gemv_rp<TGW, NQ, WPB, MAXQ, TMP>), grid, dim3(64 * WPB), smem, s, out, add, nib, params, qa,
-                     scales, sums, rows, cols, m, ntg);
+  hipLaunchKernelGGL((k_gemv_rp<TGW, NQ, WPB, MAXQ, TMP>), grid, dim3(64 * WPB), smem, s, out, add, nib, params,
+                     q_split, scales, sums, rows, cols, m, ntg);
 }
 
 template <bool TMP>
-void launch_rp_shape(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
+void launch_rp_shape(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                      const float *scales, const float *sums, int rows, int cols, int m, int ntg, hipStream_t s) {
   constexpr int Q = kRpMaxCols / 128, Q1 = kRpMaxColsOne / 128;
   const int rb = (rows + 63) / 64;
@@ -891,15 +934,15 @@ void launch_rp_shape(float *out, const float *add, const uint8_t *nib, const uin
   // weights), two for four.
   const bool three = ntg >= 3 && ntg != 4;
   if (cols > kRpMaxCols)
-    launch_rp<1, 4, Q1, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    launch_rp<1, 4, Q1, TMP>(out, add, nib, params, q_split, scales, sums, rows, cols, m, ntg, s);
   else if (three && rows >= 16384)
-    launch_rp<3, 8, Q, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    launch_rp<3, 8, Q, TMP>(out, add, nib, params, q_split, scales, sums, rows, cols, m, ntg, s);
   else if (three && blocks(3) >= 192)
-    launch_rp<3, 4, Q, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    launch_rp<3, 4, Q, TMP>(out, add, nib, params, q_split, scales, sums, rows, cols, m, ntg, s);
   else if (ntg >= 2 && blocks(2) >= 192)
-    launch_rp<2, 4, Q, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    launch_rp<2, 4, Q, TMP>(out, add, nib, params, q_split, scales, sums, rows, cols, m, ntg, s);
   else
-    launch_rp<1, 4, Q, TMP>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+    launch_rp<1, 4, Q, TMP>(out, add, nib, params, q_split, scales, sums, rows, cols, m, ntg, s);
 }
 
 // One thread per 16 bytes (four groups' parameters of one row).
@@ -924,8 +967,8 @@ void launch_params_tile16(const uint8_t *params, int rows, int cols, uint8_t *ti
 }
 
 bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
-                      const float *scales, const float *sums, int rows, int cols, int m, int gs,
-                      hipStream_t s, const uint8_t *params_tiled) {
+                      const int8_t *q_split, const float *scales, const float *sums, int rows, int cols, int m,
+                      int gs, hipStream_t s, const uint8_t *params_tiled) {
   if (!qa || !w4a8_mfma_path(rows, cols, m, gs)) return false;
   const int ntg = (m + 3) / 4;
   const int groups = cols / 32;
@@ -940,11 +983,11 @@ bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const ui
   // parameters also in the 16-row tile layout, that copy is read instead
   // (o_proj 4096x4096 at 9 tokens 10.9 -> 9.3 us, down 4096x14336 31.8 ->
   // 26.6, gate|up 28672x4096 27.5 -> 26.6).
-  if (gemv_rp_ok(rows, cols)) {
+  if (q_split && gemv_rp_ok(rows, cols)) {
     if (params_tiled && params_tile16_ok(rows, cols, gs))
-      launch_rp_shape<true>(out, add, nib, params_tiled, qa, scales, sums, rows, cols, m, ntg, s);
+      launch_rp_shape<true>(out, add, nib, params_tiled, q_split, scales, sums, rows, cols, m, ntg, s);
     else
-      launch_rp_shape<false>(out, add, nib, params, qa, scales, sums, rows, cols, m, ntg, s);
+      launch_rp_shape<false>(out, add, nib, params, q_split, scales, sums, rows, cols, m, ntg, s);
     return true;
   }
   // Longer K: the register-streamed kernel for many rows (one wave keeps up

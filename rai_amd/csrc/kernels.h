@@ -111,9 +111,12 @@ size_t qa_pack_halves(int m, int cols);
 void launch_qa_pack(const int8_t *q_split, int m, int cols, _Float16 *qa, hipStream_t s);
 // `params_tiled` (may be null): the same parameters in the layout of
 // launch_params_tile16, read instead of `params` where it applies.
+// `q_split` (may be null): the block-split int8 activations the packed
+// `qa` was made from, from which the register-pipelined kernel builds its
+// A operands itself.
 bool launch_w4a8_mfma(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const _Float16 *qa,
-                      const float *scales, const float *sums, int rows, int cols, int m, int gs,
-                      hipStream_t s, const uint8_t *params_tiled = nullptr);
+                      const int8_t *q_split, const float *scales, const float *sums, int rows, int cols, int m,
+                      int gs, hipStream_t s, const uint8_t *params_tiled = nullptr);
 // The parameter array of a group-32 matrix (rows x cols/32 dwords, f16
 // scale and zero point per row and group) rearranged in 16-row tiles:
 // [rows / 16][cols / 128][16 rows][4 groups] dwords, the layout the

@@ -1457,7 +1457,7 @@ void launch_w4a8(float *out, const float *add, const uint8_t *nib, const uint8_t
                  const float *sums, int rows, int cols, int m, int gs, hipStream_t s,
                  const _Float16 *qa, uint8_t *mm, const uint8_t *params_tiled) {
   const int groups = (cols + gs - 1) / gs;
-  if (launch_w4a8_mfma(out, add, nib, params, qa, scales, sums, rows, cols, m, gs, s, params_tiled)) return;
+  if (launch_w4a8_mfma(out, add, nib, params, qa, q_split, scales, sums, rows, cols, m, gs, s, params_tiled)) return;
   if (mm && q_split && w4a8_mm_path(rows, cols, m, gs)) {
     launch_w4a8_mm(out, add, nib, params, q_split, scales, sums, rows, cols, m, mm, s);
     return;
