@@ -8,9 +8,16 @@
 // 32-column group, so D[token][row] is the reference's lane sum S_b (the
 // PMADDUBSW/PMADDWD sum of 8 code x activation products, gemm.rs:606-614)
 // for 32 tokens x 32 rows, with no block-diagonal padding.  Codes 0..15
-// enter as f16 1024 + n minus 1024 (odd columns as 16 n), activations as
-// f16 a (odd columns a / 16); every product and partial sum is an integer
-// below 2^24, so the f32 accumulators hold S exactly in any order.  The
+// enter as f16 subnormals n 2^-24 (odd columns 16 n 2^-24: one mask per
+// pair), activations as f16 a (odd columns a / 16); every product and
+// partial sum is an integer times 2^-24 below 2^-10, so the f32
+// accumulators hold S 2^-24 exactly in any order, and the records carry the
+// activation scales times 2^24, so that fl(S 2^-24 * fl(ws * as 2^24)) =
+// fl(S * fl(ws * as)) (power-of-two scaling commutes with rounding in the
+// normal range; ws * as is zero or above 2^-24 * 1e-10 / 127).  A quad of
+// groups whose 32 tokens include a scale of 2^88 or more (where as 2^24
+// could overflow the product) keeps its scales as they are, is flagged,
+// and runs with the codes as f16 1024 + n minus 1024 (S itself).  The
 // f16 instruction is used rather than an int8 one because it returns S
 // already as f32: an i32 result would cost one VALU conversion per S, and
 // the VALU epilogue, not the matrix core, bounds this kernel.
@@ -27,7 +34,9 @@
 //
 // Data: activations are packed once per GEMM input by k_mm_pack into
 // 2304-byte records per (32-token tile, group): four 512-byte A operands
-// (lane-ordered), then 32 scales and 32 input sums.  A block of WR waves
+// (lane-ordered), then 32 scales (times 2^24 unless flagged) and 32 input
+// sums; after the records one int per (token tile, quad of groups), nonzero
+// for a flagged quad.  A block of WR waves
 // (32 rows each) shares one token tile; the records of P groups are copied
 // to LDS by DMA (global_load_lds), double-buffered.  Each lane streams its
 // row's codes (16 B per group) and parameters (16 B per four groups)
@@ -35,6 +44,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "kernels.h"
 
@@ -88,7 +98,10 @@ __global__ __launch_bounds__(256) void k_mm_pack(const int8_t *__restrict__ q_sp
   {
     const int g = tid >> 6, which = (tid >> 5) & 1, t = tt * 32 + i;
     const float v = t < m ? (which ? sums : scales)[(size_t)t * groups + 4 * gq + g] : 0.0f;
-    reinterpret_cast<float *>(r0 + g * kMmRec + 2048 + which * 128)[i] = v;
+    const float av = fabsf(v);
+    const bool huge = __syncthreads_or(which == 0 && av >= 0x1p88f && av < INFINITY) != 0;
+    reinterpret_cast<float *>(r0 + g * kMmRec + 2048 + which * 128)[i] = (which == 0 && !huge) ? v * 0x1p24f : v;
+    if (tid == 0) reinterpret_cast<int *>(rec + (size_t)gridDim.y * groups * kMmRec)[tt * (groups / 4) + gq] = huge;
   }
 }
 
@@ -101,9 +114,16 @@ __device__ __forceinline__ float mul_half(uint32_t w, float x, float nz) {
   return __builtin_fmaf((float)hv, x, nz);
 }
 
-// The B operand of block dword w for half h (sh = 8 h).
+// The B operand of block dword w for half h (sh = 8 h): the codes as f16
+// subnormals (SUB), or as 1024 + n minus 1024.
+template <bool SUB>
 __device__ __forceinline__ h4 unpack_half(uint32_t w, uint32_t sh) {
   const uint32_t t = w >> sh;
+  if constexpr (SUB) {
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    const u2 d = {t & 0x000F000Fu, t & 0x00F000F0u};
+    return __builtin_bit_cast(h4, d);
+  }
   const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
   const h2 e0 = __builtin_bit_cast(h2, (t & 0x000F000Fu) | 0x64006400u) - bias;
   const h2 e1 = __builtin_bit_cast(h2, (t & 0x00F000F0u) | 0x64006400u) - bias;
@@ -121,21 +141,25 @@ struct MmLane {
 };
 
 // One group: four MFMAs from the LDS record `rc` and the code dword ring
-// slot `wq`, then the epilogue with parameter dword `pw`.
+// slot `wq`, then the epilogue with parameter dword `pw`.  Codes as f16
+// subnormals (SUB), or as 1024 + n with the record's scales times smul
+// (2^-24 for those stored times 2^24: exact).
+template <bool SUB>
 __device__ __forceinline__ void mm_group(const uint8_t *rc, const u4v &wq, uint32_t pw, uint32_t sh, int lane,
-                                         int h, float nz, MmLane &acc) {
+                                         int h, float nz, float smul, MmLane &acc) {
   const f16v zero = {};
   // Blocks 0 and 1 first; their MFMAs run while the zero-point chain and
   // the combined scales are computed.
   f16v D0 = __builtin_amdgcn_mfma_f32_32x32x8f16(*reinterpret_cast<const h4 *>(rc + lane * 8),
-                                                 unpack_half(wq[0], sh), zero, 0, 0, 0);
+                                                 unpack_half<SUB>(wq[0], sh), zero, 0, 0, 0);
   f16v D1 = __builtin_amdgcn_mfma_f32_32x32x8f16(*reinterpret_cast<const h4 *>(rc + 512 + lane * 8),
-                                                 unpack_half(wq[1], sh), zero, 0, 0, 0);
+                                                 unpack_half<SUB>(wq[1], sh), zero, 0, 0, 0);
   float cs[16];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const f4v xs4 = *reinterpret_cast<const f4v *>(rc + 2176 + (8 * q + 4 * h) * 4);
-    const f4v as4 = *reinterpret_cast<const f4v *>(rc + 2048 + (8 * q + 4 * h) * 4);
+    f4v as4 = *reinterpret_cast<const f4v *>(rc + 2048 + (8 * q + 4 * h) * 4);
+    if constexpr (!SUB) as4 = as4 * smul;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       acc.zc[4 * q + r] = acc.zc[4 * q + r] + mul_half<true>(pw, xs4[r], nz);
@@ -148,9 +172,9 @@ __device__ __forceinline__ void mm_group(const uint8_t *rc, const u4v &wq, uint3
     acc.f[1][v] = acc.f[1][v] + D1[v] * cs[v];
   }
   D0 = __builtin_amdgcn_mfma_f32_32x32x8f16(*reinterpret_cast<const h4 *>(rc + 1024 + lane * 8),
-                                            unpack_half(wq[2], sh), zero, 0, 0, 0);
+                                            unpack_half<SUB>(wq[2], sh), zero, 0, 0, 0);
   D1 = __builtin_amdgcn_mfma_f32_32x32x8f16(*reinterpret_cast<const h4 *>(rc + 1536 + lane * 8),
-                                            unpack_half(wq[3], sh), zero, 0, 0, 0);
+                                            unpack_half<SUB>(wq[3], sh), zero, 0, 0, 0);
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     acc.f[2][v] = acc.f[2][v] + D0[v] * cs[v];
@@ -210,31 +234,48 @@ __global__ __launch_bounds__(64 * WR, 2) void k_w4a8_mm(float *out, const float 
   }
   __syncthreads();
 
-  // The P groups of stage kt from LDS buffer `buf`, eight at a time (two
-  // parameter quads, so the parameter registers alternate statically).
-  auto stage = [&](const uint8_t *buf, int kt) {
-    for (int g8 = 0; g8 < P; g8 += 8) {
+  // Quad flags of this token tile: any set (rare) runs the whole block with
+  // the codes as 1024 + n, and the unflagged quads' scales times 2^-24.
+  const int *qflag = reinterpret_cast<const int *>(rec + (size_t)gridDim.y * groups * kMmRec) +
+                     (size_t)blockIdx.y * (groups / 4);
+  int fl = 0;
+  for (int i = lane; i < groups / 4; i += 64) fl |= qflag[i];
+  const bool anybig = __builtin_amdgcn_ballot_w64(fl != 0) != 0;
+
+  auto run = [&](auto sub) __attribute__((always_inline)) {
+    constexpr bool SUB = decltype(sub)::value;
+    // The P groups of stage kt from LDS buffer `buf`, eight at a time (two
+    // parameter quads, so the parameter registers alternate statically).
+    auto stage = [&](const uint8_t *buf, int kt) __attribute__((always_inline)) {
+      for (int g8 = 0; g8 < P; g8 += 8) {
 #pragma unroll
-      for (int gi = 0; gi < 8; ++gi) {
-        const int g = kt * P + g8 + gi;
-        const int slot = gi & 3, quad = gi >> 2;
-        mm_group(buf + (g8 + gi) * kMmRec, wr[slot], pr[quad][gi & 3], sh, lane, h, nz, acc);
-        wr[slot] = __builtin_amdgcn_raw_buffer_load_b128(rcs, (int)vc0, min(g + 4, groups - 1) * 16, 0);
-        if ((gi & 3) == 3)
-          pr[quad] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, min(g + 5, groups - 4) * 4, 0);
+        for (int gi = 0; gi < 8; ++gi) {
+          const int g = kt * P + g8 + gi;
+          const int slot = gi & 3, quad = gi >> 2;
+          float smul = 1.0f;
+          if constexpr (!SUB) smul = __builtin_amdgcn_readfirstlane(qflag[g >> 2]) ? 1.0f : 0x1p-24f;
+          mm_group<SUB>(buf + (g8 + gi) * kMmRec, wr[slot], pr[quad][gi & 3], sh, lane, h, nz, smul, acc);
+          wr[slot] = __builtin_amdgcn_raw_buffer_load_b128(rcs, (int)vc0, min(g + 4, groups - 1) * 16, 0);
+          if ((gi & 3) == 3)
+            pr[quad] = __builtin_amdgcn_raw_buffer_load_b128(rps, (int)vp0, min(g + 5, groups - 4) * 4, 0);
+        }
+      }
+    };
+    for (int kt = 0; kt < ntile; kt += 2) {
+      if (kt + 1 < ntile) dma(bufB, kt + 1);
+      stage(bufA, kt);
+      __syncthreads();
+      if (kt + 1 < ntile) {
+        if (kt + 2 < ntile) dma(bufA, kt + 2);
+        stage(bufB, kt + 1);
+        __syncthreads();
       }
     }
   };
-  for (int kt = 0; kt < ntile; kt += 2) {
-    if (kt + 1 < ntile) dma(bufB, kt + 1);
-    stage(bufA, kt);
-    __syncthreads();
-    if (kt + 1 < ntile) {
-      if (kt + 2 < ntile) dma(bufA, kt + 2);
-      stage(bufB, kt + 1);
-      __syncthreads();
-    }
-  }
+  if (anybig)
+    run(std::false_type{});
+  else
+    run(std::true_type{});
   if (row < rows) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -255,7 +296,10 @@ bool w4a8_mm_path(int rows, int cols, int m, int gs) {
          (int64_t)rows * (cols / 2) < ((int64_t)1 << 31);
 }
 
-size_t mm_pack_bytes(int m, int cols) { return (size_t)((m + 31) / 32) * (cols / 32) * kMmRec; }
+size_t mm_pack_bytes(int m, int cols) {
+  const size_t ntt = (size_t)((m + 31) / 32);
+  return ntt * (cols / 32) * kMmRec + ntt * (cols / 128) * sizeof(int);
+}
 
 void launch_w4a8_mm(float *out, const float *add, const uint8_t *nib, const uint8_t *params, const int8_t *q_split,
                     const float *scales, const float *sums, int rows, int cols, int m, uint8_t *pack,
