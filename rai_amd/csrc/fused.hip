@@ -246,6 +246,34 @@ __device__ __forceinline__ void score_chunks(std::integer_sequence<int, Cs...>, 
   (score_chunk<HD, PB, Cs>(kr4, qb, a), ...);
 }
 
+// The same with the next chunk's keys requested before this chunk's FMAs
+// (k0, k1 hold chunk C's keys on entry, chunk C + 1's on exit).
+template <int HD, int PB, int C>
+__device__ __forceinline__ void score_chunk_p(const sf4 *kr4, const float (&qb)[PB][HD / 16], float (&a)[PB][8],
+                                              sf4 &k0, sf4 &k1) {
+  sf4 n0 = k0, n1 = k1;
+  if constexpr (C + 1 < HD / 8) {
+    n0 = kr4[2 * C + 2];
+    n1 = kr4[2 * C + 3];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+  for (int p = 0; p < PB; ++p)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[p][i] = fma_bcast_n((8 * C + i) & 15, qb[p][C >> 1], kv[i], a[p][i]);
+  __builtin_amdgcn_sched_barrier(0);
+  k0 = n0;
+  k1 = n1;
+}
+
+template <int HD, int PB, int... Cs>
+__device__ __forceinline__ void score_chunks_pipe(std::integer_sequence<int, Cs...>, const sf4 *kr4,
+                                                  const float (&qb)[PB][HD / 16], float (&a)[PB][8]) {
+  sf4 k0 = kr4[0], k1 = kr4[1];
+  (score_chunk_p<HD, PB, Cs>(kr4, qb, a, k0, k1), ...);
+}
+
 // grid (ceil(nmax / 64), nkv), 256 threads.  The block stages its 64 key
 // rows in LDS; each wave takes (token, head) pairs of the kv group, lane =
 // position.  HD > 0 (compile-time head_dim): key rows HD + 4 floats apart
@@ -393,7 +421,7 @@ __global__ __launch_bounds__(256) void k_scores(const float *__restrict__ q, int
 // ... of the group; wave w takes the tile's pairs w, w + 8, ..., PB at a
 // time.  ns is chosen so that the grid's blocks are about one per CU.
 template <int HD, int PB>
-__global__ __launch_bounds__(512) void k_scores_mt(const float *__restrict__ q, int q_ld,
+__global__ __launch_bounds__(512, 1) void k_scores_mt(const float *__restrict__ q, int q_ld,
                                                    const float *__restrict__ kc, int cap, int pos0, int m, int nh,
                                                    int nkv, float scale, float *__restrict__ S, int sstride,
                                                    const int *__restrict__ st, int mb, int ns) {
@@ -469,7 +497,9 @@ __global__ __launch_bounds__(512) void k_scores_mt(const float *__restrict__ q, 
       for (int p = 0; p < PB; ++p)
 #pragma unroll
         for (int i = 0; i < 8; ++i) a[p][i] = 0.0f;
-      score_chunks<HD, PB>(std::make_integer_sequence<int, HD / 8>{}, reinterpret_cast<const sf4 *>(kr4), qb, a);
+      // The batch's query values all read before its FMAs.
+      __builtin_amdgcn_sched_barrier(0);
+      score_chunks_pipe<HD, PB>(std::make_integer_sequence<int, HD / 8>{}, reinterpret_cast<const sf4 *>(kr4), qb, a);
 #pragma unroll
       for (int p = 0; p < PB; ++p) {
         const int pi = wave + 8 * (b0 + p);
