@@ -131,7 +131,10 @@ int rai_device_info(char *name, size_t name_len, int *compute_units);
  * reads and validates the whole file with the reference's rules
  * (format.rs:1098-1521), then uploads it to HBM.  max_groups replaces the
  * reference's MAX_GROUPS = 128 (gemm.rs:1167); pass 0 for the reference value
- * 128, or a larger bound for group-32 models with K > 4096. */
+ * 128, or a larger bound for group-32 models with K > 4096.  Device memory:
+ * the file's bytes, RoPE tables, and for group-32 dense matrices a second
+ * copy of their scale/zero parameters in 16-row tiles (about a fifth of the
+ * quantized weight bytes), which the 2..64-token GEMVs read. */
 int rai_model_open(const char *path, int max_groups, rai_model **out);
 /* Same, from a caller-owned in-memory .raimodel image (copied). */
 int rai_model_from_buffer(const void *data, size_t len, int max_groups, rai_model **out);
