@@ -372,12 +372,18 @@ class GemvTimer:
 
     def time(self, x, num_tokens: int, iters: int = 50) -> float:
         """Average device time (ms) of one launch at num_tokens rows of x."""
+        return self.run(x, num_tokens, iters)[0]
+
+    def run(self, x, num_tokens: int, iters: int = 1):
+        """(average ms, outputs [num_tokens][rows] of the last launch): the
+        launches read the parameters' 16-row tile copy where it applies, as a
+        loaded model's batched forward does."""
         dx = DeviceArray.from_host(_f32(x))
         do = DeviceArray(num_tokens * self.rows * 4)
         ms = c_float()
         _check(lib().rai_w4a8_time_dev(do.ptr, self.dn.ptr, self.dp.ptr, dx.ptr, self.rows, self.cols, num_tokens,
                                        self.gs, self.copies, iters, ctypes.byref(ms)))
-        return ms.value
+        return ms.value, do.to_host(np.float32, num_tokens * self.rows).reshape(num_tokens, self.rows)
 
 
 def w4a8_lane_sums(nibbles, x, rows: int, cols: int, num_tokens: int,

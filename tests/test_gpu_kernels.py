@@ -136,6 +136,31 @@ def test_w4a8_register_pipelined_huge_scales_and_subnormal_params(rai, ora, rows
         assert np.array_equal(_bits(got), _bits(want)), (rows, m, scaled)
 
 
+@pytest.mark.parametrize("rows,cols,m", [(1024, 4096, 9), (6144, 4096, 9), (16384, 4096, 9), (4096, 14336, 9),
+                                         (2048, 2560, 5), (16384, 4096, 16)])
+def test_w4a8_tiled_parameters_bit_exact(rai, ora, rows, cols, m):
+    """The register-pipelined kernel reading the parameters' 16-row tile copy
+    (the batched forward's path; the GEMV timer builds the copy as a loaded
+    model does), with and without activation groups past 2^88 (its 1024 + n
+    code form) and with f16 weight scales / zero points that are subnormal or
+    zero."""
+    nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + 3 * m)
+    p = params.copy().view(np.float16).reshape(rows, cols // 32, 2)
+    p[::7, ::3, 0] = np.float16(3e-6)
+    p[::5, 1::4, 1] = np.float16(-2e-6)
+    p[3::11, 2::5, :] = np.float16(0.0)
+    params = p.view(np.uint8).reshape(-1)
+    timer = rai.GemvTimer(nib, params, rows, cols, 32)
+    for scaled in (False, True):
+        xs = x.copy()
+        if scaled:
+            xs[m - 1, 64:96] *= np.float32(1e30)
+        want = np.asarray(ora.w4a8_matmul(nib, params, xs, rows, cols, m, 32)).reshape(m, rows)
+        _, got = timer.run(xs, m)
+        assert np.isfinite(want).all()
+        assert np.array_equal(_bits(got), _bits(want)), (rows, cols, m, scaled)
+
+
 @pytest.mark.parametrize("rows,cols,gs", SHAPES[:6])
 def test_lane_sums_bit_exact(rai, ora, rows, cols, gs):
     nib, _, x = gemv_operands(rows, cols, 3, gs, seed=cols)
