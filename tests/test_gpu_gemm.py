@@ -49,6 +49,26 @@ def test_mm_extreme_scales_and_subnormal_params(rai, ora):
     assert np.array_equal(_bits(got), _bits(want))
 
 
+@pytest.mark.parametrize("rows,cols", [(256, 1024), (1000, 4096)])
+def test_mm_huge_scale_quads_per_token_tile(rai, ora, rows, cols):
+    """Activation scales of 2^88 and more flag their quad of groups: a token
+    tile holding one runs with the 1024 + n codes and rescales its other
+    quads' scales; the other tiles keep the subnormal codes.  Huge groups in
+    the first and in the last, partial, token tile (75 tokens), none in the
+    middle one."""
+    m = 75
+    nib, params, x = gemv_operands(rows, cols, m, 32, seed=rows + 75)
+    x = x.reshape(m, cols // 32, 32).copy()
+    x[5, 3] *= np.float32(1e30)
+    x[70, cols // 32 - 1] *= np.float32(3e29)
+    x[40, 7] *= np.float32(1e-30)
+    x = x.reshape(m, cols)
+    want = ora.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    got = rai.w4a8_matmul(nib, params, x, rows, cols, m, 32)
+    assert np.isfinite(want).all()
+    assert np.array_equal(_bits(got), _bits(want)), (rows, cols)
+
+
 @pytest.mark.parametrize("rows,cols", GEMV_SHAPES)
 def test_cfg3_m512_sweep_shapes_bit_exact(rai, ora, rows, cols):
     """W4A8 sweep at M = 512 (prefill-sized) on the four sweep shapes."""
