@@ -936,7 +936,12 @@ void launch_rp_shape(float *out, const float *add, const uint8_t *nib, const uin
   // tokens 14.3 -> 13.5 us, at 17 tokens 19.3 -> 14.3; o_proj 4096x4096 at
   // 17 tokens 14.3 -> 13.5).
   const bool three = ntg >= 3 && ntg != 4;
-  if (cols > kRpMaxCols)
+  // Past K = 4096 (one token group per block, 3.5 x the steps) a ring of
+  // eight steps where K / 128 allows (down 4096x14336 at 9 tokens 26.9 ->
+  // 26.2 us; shorter K is slower with it).
+  if (cols > kRpMaxCols && (cols / 128) % 8 == 0)
+    launch_rp<1, 4, Q1, TMP, 8>(out, add, nib, params, q_split, scales, sums, rows, cols, m, ntg, s);
+  else if (cols > kRpMaxCols)
     launch_rp<1, 4, Q1, TMP>(out, add, nib, params, q_split, scales, sums, rows, cols, m, ntg, s);
   else if (TMP && rows <= 8192 && ntg <= 5)
     launch_rp<1, 4, Q, TMP>(out, add, nib, params, q_split, scales, sums, rows, cols, m, ntg, s);
