@@ -16,8 +16,10 @@
 //     (sampler.rs:47-199), the token of `rai run` without speculation.
 // Pins: the block function and the buffering order are checked against the
 // RFC 7539 A.1 keystream vectors (20 rounds) and the RFC 8439 2.3.2 block;
-// seed_from_u64 and the float conversions have no published vector and are
-// parity-unpinned beyond their published algorithm.
+// seed_from_u64 against the PCG32 reference demo's outputs (seed 42,
+// sequence 54) through seeds that put its first step on the demo's states;
+// the float conversions have no published vector and are parity-unpinned
+// beyond their published algorithm.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>

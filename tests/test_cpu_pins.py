@@ -218,3 +218,29 @@ def test_expf_restatement_matches_host_libm(tmp_path):
     checked, bad, first = out.split()
     assert int(checked) > 20_000_000
     assert int(bad) == 0, f"first mismatch at {first}"
+
+
+# The PCG32 reference implementation's demo (pcg32_srandom_r(42, 54), then
+# pcg32_random_r): its published first outputs.
+_PCG_DEMO_42_54 = [0xA15C02B7, 0x7B47F409, 0xBA1D3330, 0x83D2F293, 0xBFA4784B, 0xCBED606E]
+
+
+def test_seed_from_u64_against_the_pcg32_reference_vector(ora):
+    """SeedableRng::seed_from_u64 (rand_core 0.6.4) fills the ChaCha key with
+    PCG32 outputs: state = state * 6364136223846793005 + 11634580027462260723,
+    then the XSH RR output of the new state.  The PCG reference demo runs the
+    same multiplier and output function with increment 109 (sequence 54).
+    For each state S_k the demo outputs from, the seed (S_k - increment) /
+    multiplier (mod 2^64) makes the oracle's first step land on S_k, so its
+    first key word must be the demo's k-th output: a wrong output function,
+    multiplier, increment or step order fails it."""
+    m64, mul, inc_rand = 1 << 64, 6364136223846793005, 11634580027462260723
+    inv = pow(mul, -1, m64)
+    inc = (54 << 1) | 1  # pcg32_srandom_r(initstate = 42, initseq = 54)
+    s = (0 * mul + inc) % m64
+    s = (s + 42) % m64
+    s = (s * mul + inc) % m64
+    for k, want in enumerate(_PCG_DEMO_42_54):
+        seed = ((s - inc_rand) * inv) % m64
+        assert int(ora.Rng(seed=seed).key()[0]) == want, k
+        s = (s * mul + inc) % m64
