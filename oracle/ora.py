@@ -103,6 +103,8 @@ def lib():
         "ora_rng_next_u64": (c_uint64, [P]),
         "ora_rng_gen_f32": (c_float, [P]),
         "ora_rng_gen_f64": (c_double, [P]),
+        "ora_standard_f32": (c_float, [ctypes.c_uint32]),
+        "ora_standard_f64": (c_double, [ctypes.c_uint64]),
         "ora_rng_key": (None, [P, P]),
         "ora_softmax_probabilities": (c_int, [P, c_int, c_float, P]),
         "ora_sample_token": (c_int, [P, c_int, c_float, P, POINTER(c_int)]),
@@ -397,6 +399,16 @@ class Rng:
 
     def gen_f64(self) -> float:
         return float(lib().ora_rng_gen_f64(self.h))
+
+    @staticmethod
+    def standard_f32(u: int) -> float:
+        """rand's Standard f32 of one u32 (what gen_f32 applies to next_u32)."""
+        return float(lib().ora_standard_f32(u))
+
+    @staticmethod
+    def standard_f64(u: int) -> float:
+        """rand's Standard f64 of one u64."""
+        return float(lib().ora_standard_f64(u))
 
     def key(self) -> np.ndarray:
         k = np.zeros(8, np.uint32)

@@ -18,8 +18,7 @@
 // RFC 7539 A.1 keystream vectors (20 rounds) and the RFC 8439 2.3.2 block;
 // seed_from_u64 against the PCG32 reference demo's outputs (seed 42,
 // sequence 54) through seeds that put its first step on the demo's states;
-// the float conversions have no published vector and are parity-unpinned
-// beyond their published algorithm.
+// the float conversions against rand 0.8's value-stability vectors.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -70,6 +69,11 @@ void chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, int 
   for (int i = 0; i < 16; ++i) out[i] = s[i] + in[i];
 }
 
+// rand 0.8.6 Standard for f32 / f64 (distributions/float.rs): the top 24 /
+// 53 bits of a u32 / u64 times 2^-24 / 2^-53.
+static float standard_f32(uint32_t u) { return (float)(u >> 8) * (1.0f / 16777216.0f); }
+static double standard_f64(uint64_t u) { return (double)(u >> 11) * (1.0 / 9007199254740992.0); }
+
 struct StdRng {
   uint32_t key[8];
   uint64_t counter = 0;
@@ -103,8 +107,8 @@ struct StdRng {
     index = 1;
     return lo | ((uint64_t)buf[0] << 32);
   }
-  float gen_f32() { return (float)(next_u32() >> 8) * (1.0f / 16777216.0f); }
-  double gen_f64() { return (double)(next_u64() >> 11) * (1.0 / 9007199254740992.0); }
+  float gen_f32() { return standard_f32(next_u32()); }
+  double gen_f64() { return standard_f64(next_u64()); }
 };
 
 static void seed_from_u64(StdRng &r, uint64_t state) {
@@ -446,6 +450,8 @@ uint32_t ora_rng_next_u32(ora_rng *r) { return r->r.next_u32(); }
 uint64_t ora_rng_next_u64(ora_rng *r) { return r->r.next_u64(); }
 float ora_rng_gen_f32(ora_rng *r) { return r->r.gen_f32(); }
 double ora_rng_gen_f64(ora_rng *r) { return r->r.gen_f64(); }
+float ora_standard_f32(uint32_t u) { return standard_f32(u); }
+double ora_standard_f64(uint64_t u) { return standard_f64(u); }
 void ora_rng_key(const ora_rng *r, uint32_t *key) { std::memcpy(key, r->r.key, 32); }
 
 int ora_sample_token(const float *logits, int n, float temperature, ora_rng *r, int *token) {

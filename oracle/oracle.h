@@ -101,6 +101,9 @@ uint32_t ora_rng_next_u32(ora_rng *r);
 uint64_t ora_rng_next_u64(ora_rng *r);
 float ora_rng_gen_f32(ora_rng *r);
 double ora_rng_gen_f64(ora_rng *r);
+/* The Standard f32 / f64 of one u32 / u64, as gen_f32 / gen_f64 apply it. */
+float ora_standard_f32(uint32_t u);
+double ora_standard_f64(uint64_t u);
 void ora_rng_key(const ora_rng *r, uint32_t *key8);
 int ora_softmax_probabilities(const float *logits, int n, float temperature, float *out);
 int ora_sample_token(const float *logits, int n, float temperature, ora_rng *r, int *token);

@@ -244,3 +244,51 @@ def test_seed_from_u64_against_the_pcg32_reference_vector(ora):
         seed = ((s - inc_rand) * inv) % m64
         assert int(ora.Rng(seed=seed).key()[0]) == want, k
         s = (s * mul + inc) % m64
+
+
+class _Pcg32:
+    """rand_pcg 0.3's Lcg64Xsh32 (Pcg32): state and stream words, XSH RR
+    output of the state before each step."""
+
+    MUL = 6364136223846793005
+
+    def __init__(self, state, stream):
+        self.inc = ((stream << 1) | 1) % (1 << 64)
+        self.state = (state + self.inc) % (1 << 64)
+        self._step()
+
+    def _step(self):
+        self.state = (self.state * self.MUL + self.inc) % (1 << 64)
+
+    def next_u32(self):
+        s = self.state
+        self._step()
+        xs = (((s >> 18) ^ s) >> 27) & 0xFFFFFFFF
+        rot = s >> 59
+        return ((xs >> rot) | (xs << ((32 - rot) & 31))) & 0xFFFFFFFF
+
+    def next_u64(self):
+        lo = self.next_u32()
+        return lo | (self.next_u32() << 32)
+
+
+def test_standard_float_conversions_against_rand_value_stability(ora):
+    """rand 0.8's Standard f32 / f64 against that crate's own value-stability
+    vectors (distributions/float.rs), drawn from its test generator
+    Pcg32(0x6f44f5646c2a7334, 11634580027462260723).  The generator is
+    restated here and checked first against the PCG32 reference demo (seed
+    42, sequence 54: pcg32_srandom_r runs the same steps as this
+    constructor), so a wrong conversion in the oracle (bits kept, scale,
+    rounding) is what a mismatch points to."""
+    demo = _Pcg32(42, 54)
+    assert [demo.next_u32() for _ in range(6)] == _PCG_DEMO_42_54
+    rng = _Pcg32(0x6F44F5646C2A7334, 11634580027462260723)
+    f32 = [np.float32(ora.Rng.standard_f32(rng.next_u32())) for _ in range(3)]
+    assert f32 == [np.float32(0.0035963655), np.float32(0.7346052), np.float32(0.09778172)]
+    rng = _Pcg32(0x6F44F5646C2A7334, 11634580027462260723)
+    f64 = [ora.Rng.standard_f64(rng.next_u64()) for _ in range(3)]
+    assert f64 == [0.7346051961657583, 0.20298547462974248, 0.8166436635290655]
+    # gen_f32 / gen_f64 apply the same conversion to the ChaCha stream.
+    a, b = ora.Rng(seed=5), ora.Rng(seed=5)
+    assert a.gen_f32() == np.float32(ora.Rng.standard_f32(b.next_u32()))
+    assert a.gen_f64() == ora.Rng.standard_f64(b.next_u64())
